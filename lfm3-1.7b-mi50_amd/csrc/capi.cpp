@@ -1,0 +1,165 @@
+// extern "C" entry points of libdspark_amd.so (declared in include/dspark.h). Every shape a kernel's grid and
+// indexing assume is checked here, on the host, before anything is launched.
+#include <hip/hip_runtime.h>
+
+#include "dspark.h"
+#include "dspark_internal.h"
+
+using namespace dspark;
+
+namespace {
+
+constexpr int ABI_VERSION = 1;
+constexpr int ATTN_TARGET_WGS = 512;  // two 4-wave workgroups per CU on 256 CUs
+
+hipStream_t S(dspark_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool attn_args_ok(const dspark_attn_args* a) {
+  if (!a || !a->q || !a->k_pages || !a->v_pages) return false;
+  if (!a->out && !a->out_f32) return false;
+  if (a->D != 64 && a->D != 128) return false;
+  if (a->KVH < 1 || a->QH < a->KVH || a->QH % a->KVH != 0) return false;
+  if (a->M < 1 || a->M > DSPARK_MT_MAX) return false;
+  if (a->a < 0 || a->start < 0 || a->window < 0) return false;
+  if (a->start > a->a + a->M - 1) return false;
+  if (a->splits < 0) return false;
+  if ((int64_t)a->QH / a->KVH * a->M > 64 * 16) return false;  // rows per KV head
+  return true;
+}
+
+AttnParams attn_params(const dspark_attn_args* a) {
+  AttnParams p = {};
+  p.q = static_cast<const _Float16*>(a->q);
+  p.kp = static_cast<const _Float16*>(a->k_pages);
+  p.vp = static_cast<const _Float16*>(a->v_pages);
+  p.bt = a->block_table;
+  p.out16 = static_cast<_Float16*>(a->out);
+  p.out32 = a->out_f32;
+  p.gate = a->gate;
+  p.M = a->M;
+  p.QH = a->QH;
+  p.KVH = a->KVH;
+  p.G = a->QH / a->KVH;
+  p.a = a->a;
+  p.start = a->start;
+  p.window = a->window;
+  p.causal = a->causal ? 1 : 0;
+  p.S = a->splits;
+  attn_plan(p, a->D, ATTN_TARGET_WGS);
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dspark_abi_version(void) { return ABI_VERSION; }
+int dspark_page_tokens(void) { return DSPARK_PAGE_TOKENS; }
+int dspark_max_tokens(void) { return DSPARK_MT_MAX; }
+int dspark_state_bytes(void) { return (int)sizeof(dspark_state); }
+
+size_t dspark_verify_attention_workspace(const dspark_attn_args* a) {
+  if (!a || a->M < 1 || a->M > DSPARK_MT_MAX || a->KVH < 1 || a->QH < a->KVH || (a->D != 64 && a->D != 128)) return 0;
+  dspark_attn_args b = *a;
+  if (!b.q) b.q = b.k_pages = b.v_pages = b.out = reinterpret_cast<void*>(1);  // size only
+  if (!attn_args_ok(&b)) return 0;
+  AttnParams p = attn_params(&b);
+  return attn_workspace_bytes(p, a->D);
+}
+
+int dspark_verify_attention(const dspark_attn_args* a, dspark_stream_t stream) {
+  if (!attn_args_ok(a)) return DSPARK_EINVAL;
+  AttnParams p = attn_params(a);
+  const size_t need = attn_workspace_bytes(p, a->D);
+  if (!a->workspace || a->workspace_bytes < need) return DSPARK_ENOSPACE;
+  const size_t slots = (size_t)p.KVH * p.RG * p.S;
+  p.part_acc = static_cast<float*>(a->workspace);
+  // partial (max, sum) pairs after the accumulators, 256-byte aligned
+  const size_t acc_bytes = (slots * p.R * a->D * sizeof(float) + 255) / 256 * 256;
+  p.part_ml = reinterpret_cast<f32x2_t*>(static_cast<char*>(a->workspace) + acc_bytes);
+  if (acc_bytes + slots * p.R * sizeof(f32x2_t) > a->workspace_bytes) return DSPARK_ENOSPACE;
+  return attn_launch(p, a->D, S(stream));
+}
+
+int dspark_kv_write(const void* k, const void* v, int64_t row_stride, void* k_pages, void* v_pages,
+                    const int32_t* block_table, int32_t KVH, int32_t D, int32_t pos0, int32_t n,
+                    dspark_stream_t stream) {
+  if (!k || !v || !k_pages || !v_pages) return DSPARK_EINVAL;
+  if ((D != 64 && D != 128) || KVH < 1 || pos0 < 0 || n < 0 || row_stride < (int64_t)KVH * D || row_stride % 8 != 0)
+    return DSPARK_EINVAL;
+  return kv_write_launch(k, v, row_stride, k_pages, v_pages, block_table, KVH, D, pos0, n, S(stream));
+}
+
+size_t dspark_verify_argmax_workspace(int32_t M, int32_t V) {
+  if (M < 1 || M > DSPARK_MT_MAX || V < 1) return 0;
+  return verify_argmax_ws(M, V);
+}
+
+int dspark_verify_argmax(const void* logits, int32_t logits_f16, int32_t M, int32_t V, const uint32_t* seen,
+                         const dspark_state* st, float rep, float inv_rep, uint64_t* best_keys, void* workspace,
+                         size_t workspace_bytes, dspark_stream_t stream) {
+  if (!logits || !seen || !st || !best_keys || M < 1 || M > DSPARK_MT_MAX || V < 1) return DSPARK_EINVAL;
+  if (!workspace || workspace_bytes < verify_argmax_ws(M, V)) return DSPARK_ENOSPACE;
+  return verify_argmax_launch(logits, logits_f16, M, V, seen, st, rep, inv_rep, best_keys, workspace, S(stream));
+}
+
+int dspark_accept_commit(dspark_state* st, const uint64_t* best_keys, int32_t M, int32_t skip_now, int32_t* out_tokens,
+                         uint32_t* seen, dspark_stream_t stream) {
+  if (!st || !best_keys || !out_tokens || !seen || M < 1 || M > DSPARK_MT_MAX) return DSPARK_EINVAL;
+  return accept_commit_launch(st, best_keys, M, skip_now, out_tokens, seen, S(stream));
+}
+
+size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K) {
+  if (M < 1 || M > 64 || N < 16 || N % 16 || K < 64 || K % 64) return 0;
+  return gemm_ws_bytes(M, N, K);
+}
+
+int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* scale, int32_t N,
+                   int32_t epilogue, float* y_f32, void* y_f16, void* workspace, size_t workspace_bytes,
+                   dspark_stream_t stream) {
+  if (!x || !w || !scale || M < 1 || M > 64 || N < 16 || N % 16 || K < 64 || K % 64) return DSPARK_EINVAL;
+  if (epilogue < 0 || epilogue > 2) return DSPARK_EINVAL;
+  if (epilogue == 0 && !y_f32 && !y_f16) return DSPARK_EINVAL;
+  if (epilogue != 0 && !y_f16) return DSPARK_EINVAL;
+  GemmParams p = {};
+  p.x = static_cast<const _Float16*>(x);
+  p.w = w;
+  p.scale = static_cast<const _Float16*>(scale);
+  p.y32 = epilogue == 0 ? y_f32 : nullptr;
+  p.y16 = static_cast<_Float16*>(y_f16);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.epilogue = epilogue;
+  p.ksplit = gemm_choose_ksplit(N, K, 512);
+  if (p.ksplit > 1) {
+    if (!workspace || workspace_bytes < gemm_ws_bytes(M, N, K)) return DSPARK_ENOSPACE;
+    p.part = static_cast<float*>(workspace);
+  }
+  return gemm_launch(p, true, S(stream));
+}
+
+size_t dspark_head_argmax_workspace(int32_t M, int32_t N) {
+  if (M < 1 || M > 64 || N < 16 || N % 16) return 0;
+  return (size_t)M * (N / 16) * sizeof(uint64_t);
+}
+
+int dspark_head_argmax_f16(const void* x, int32_t M, int32_t K, const void* w, int32_t N, float* y_f32,
+                           uint64_t* best_keys, void* workspace, size_t workspace_bytes, dspark_stream_t stream) {
+  if (!x || !w || !best_keys || M < 1 || M > 64 || N < 16 || N % 16 || K < 64 || K % 64) return DSPARK_EINVAL;
+  if (!workspace || workspace_bytes < dspark_head_argmax_workspace(M, N)) return DSPARK_ENOSPACE;
+  GemmParams p = {};
+  p.x = static_cast<const _Float16*>(x);
+  p.w = w;
+  p.scale = nullptr;
+  p.y32 = y_f32;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ksplit = 1;
+  p.best_part = static_cast<uint64_t*>(workspace);
+  p.best = best_keys;
+  return gemm_launch(p, false, S(stream));
+}
+
+}  // extern "C"

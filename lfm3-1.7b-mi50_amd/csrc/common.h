@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 (CDNA4) DSpark kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dspark {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+constexpr int PAGE = 32;  // tokens per KV page (the reference's BlockTokens)
+
+// D = A(16x32) * B(32x16) + C on the matrix cores. Lane l holds A row l%16 / B column l%16, k = 8*(l/16)+0..7;
+// C/D: column l%16, rows 4*(l/16)+0..3.
+__device__ __forceinline__ f32x4 mfma16x16x32(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half8 as_half8(u32x4 u) {
+  half8 h;
+  __builtin_memcpy(&h, &u, 16);
+  return h;
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  typedef __attribute__((address_space(1))) const T GT;
+  return *(const GT*)p;
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg_nt(const T* p) {
+  typedef __attribute__((address_space(1))) const T GT;
+  return __builtin_nontemporal_load((const GT*)p);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Argmax key (reference dspark.hip:967-971): ordered float bits above, 0xFFFFFFFF - index below. The maximum key is the
+// largest value and, among equal values, the smallest index.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t w = shfl_xor_u64(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+}  // namespace dspark

@@ -1,0 +1,197 @@
+// Verify GEMMs for M <= 64 tokens on the matrix cores: int8 weights (biased u8, one fp16 scale per output row) and the
+// fp16 cropped head with a fused row argmax.
+//
+// Layout. C^T[rows][tokens] = W[rows][K] * X^T[K][tokens] with v_mfma_f32_16x16x32_f16: a wave streams a 16-row strip
+// of W (lane l: row l%16, 16 contiguous bytes per 64-column chunk), X^T comes from the same 16-byte pieces of the
+// token rows. int8 -> fp16 is exact: byte b (= q + 128) placed under 0x64 is the half 1024 + b, minus 1152 gives q
+// (v_perm_b32 + v_pk_add_f16 per two weights). The four waves of a workgroup take interleaved K chunks of one strip
+// and reduce through LDS in a fixed order; long K splits further across workgroups with a fixed-order reduce kernel.
+// Weights are read once per call for all tokens; the kernel is HBM-bound (about 2*M flop per weight byte).
+// Reference: gemv_phase / unit_dot_r (dspark.hip:541-716), head_run<true> (2219-2318), markov argmax (2322-2366).
+#include "common.h"
+#include "dspark.h"
+#include "dspark_internal.h"
+
+namespace dspark {
+
+__device__ __forceinline__ half8 i8x8_to_half8(uint32_t w0, uint32_t w1) {
+  const uint32_t k64 = 0x64646464u;
+  const uint32_t a0 = __builtin_amdgcn_perm(k64, w0, 0x04010400u);
+  const uint32_t a1 = __builtin_amdgcn_perm(k64, w0, 0x04030402u);
+  const uint32_t a2 = __builtin_amdgcn_perm(k64, w1, 0x04010400u);
+  const uint32_t a3 = __builtin_amdgcn_perm(k64, w1, 0x04030402u);
+  u32x4 u = {a0, a1, a2, a3};
+  half8 h = as_half8(u);
+  const half8 bias = {1152, 1152, 1152, 1152, 1152, 1152, 1152, 1152};
+  return h - bias;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+// Epilogue for one lane's 4 rows (row0 + 4g + i) of token t.
+__device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0, int g, f32x4 v) {
+  if (t >= p.M) return;
+  const int r = row0 + 4 * g;
+  if (p.scale) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] *= (float)ldg(p.scale + r + i);
+  }
+  if (p.epilogue == 1) {
+    // rows (2i, 2i+1) = (gate, up): h[t][r/2 + i] = fp16(silu(gate) * up)
+    _Float16* y = p.y16 + (size_t)t * (p.N / 2) + r / 2;
+    y[0] = (_Float16)(silu_f(v[0]) * v[1]);
+    y[1] = (_Float16)(silu_f(v[2]) * v[3]);
+    return;
+  }
+  if (p.y32) *reinterpret_cast<f32x4*>(p.y32 + (size_t)t * p.N + r) = v;
+  if (p.y16) {
+    half4 h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = (_Float16)(p.epilogue == 2 ? silu_f(v[i]) : v[i]);
+    *reinterpret_cast<half4*>(p.y16 + (size_t)t * p.N + r) = h;
+  }
+}
+
+// TB token blocks of 16. I8: weights biased int8, else fp16. Grid: strips * ksplit.
+template <int TB, bool I8>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int strip = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
+  const int row0 = strip * 16;
+  const int chunks = p.K / 64;                 // 64 columns per chunk
+  const int cpk = (chunks + p.ksplit - 1) / p.ksplit;
+  const int c0 = ks * cpk, c1 = min(chunks, c0 + cpk);
+
+  f32x4 acc[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0, 0, 0, 0};
+
+  const uint8_t* wrow = reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K * (I8 ? 1 : 2);
+  for (int c = c0 + wave; c < c1; c += 4) {
+    const int k0 = c * 64;
+    half8 a[2];
+    if (I8) {
+      const u32x4 wv = ldg_nt(reinterpret_cast<const u32x4*>(wrow + k0 + 16 * g));
+      a[0] = i8x8_to_half8(wv[0], wv[1]);
+      a[1] = i8x8_to_half8(wv[2], wv[3]);
+    } else {
+      const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * (k0 + 16 * g));
+      a[0] = as_half8(ldg_nt(wp));
+      a[1] = as_half8(ldg_nt(wp + 1));
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = 16 * tb + n;
+      half8 b0 = {0, 0, 0, 0, 0, 0, 0, 0}, b1 = b0;
+      if (t < p.M) {
+        const u32x4* xp = reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + k0 + 16 * g);
+        b0 = as_half8(ldg(xp));
+        b1 = as_half8(ldg(xp + 1));
+      }
+      acc[tb] = mfma16x16x32(a[0], b0, acc[tb]);
+      acc[tb] = mfma16x16x32(a[1], b1, acc[tb]);
+    }
+  }
+
+  // Fixed-order reduction of the four waves.
+  __shared__ f32x4 red[4][TB][64];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) red[wave][tb][lane] = acc[tb];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) acc[tb] = ((red[0][tb][lane] + red[1][tb][lane]) + red[2][tb][lane]) + red[3][tb][lane];
+
+  if (p.ksplit > 1) {
+    // partial [ks][M][N] fp32, epilogue in the reduce kernel
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = 16 * tb + n;
+      if (t < p.M) *reinterpret_cast<f32x4*>(p.part + ((size_t)ks * p.M + t) * p.N + row0 + 4 * g) = acc[tb];
+    }
+    return;
+  }
+  if (p.best_part) {
+    // Row argmax of this strip per token: lane holds rows row0+4g+i of token n; fold the 4 row groups.
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = 16 * tb + n;
+      uint64_t b = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t k = argmax_key(acc[tb][i], (uint32_t)(row0 + 4 * g + i));
+        b = k > b ? k : b;
+      }
+      uint64_t o = shfl_xor_u64(b, 16);
+      b = o > b ? o : b;
+      o = shfl_xor_u64(b, 32);
+      b = o > b ? o : b;
+      if (g == 0 && t < p.M) p.best_part[(size_t)t * (p.N / 16) + strip] = b;
+    }
+  }
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) gemm_store(p, 16 * tb + n, row0, g, acc[tb]);
+}
+
+// Split-K reduce in index order + epilogue: one thread per 4 rows of one token.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int groups = p.N / 4;
+  if (idx >= p.M * groups) return;
+  const int t = idx / groups, r = (idx % groups) * 4;
+  f32x4 v = {0, 0, 0, 0};
+  for (int ks = 0; ks < p.ksplit; ++ks) v += *reinterpret_cast<const f32x4*>(p.part + ((size_t)ks * p.M + t) * p.N + r);
+  // gemm_store expects the lane's 4 rows at row0 + 4g: pass row0 = r, g = 0.
+  gemm_store(p, t, r, 0, v);
+}
+
+__global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int strips, uint64_t* best) {
+  const int t = blockIdx.x;
+  uint64_t b = 0;
+  for (int c = threadIdx.x; c < strips; c += 64) {
+    const uint64_t k = part[(size_t)t * strips + c];
+    b = k > b ? k : b;
+  }
+  b = wave_max_u64(b);
+  if (threadIdx.x == 0) best[t] = b;
+}
+
+template <bool I8>
+static void launch_gemm(const GemmParams& p, hipStream_t s) {
+  const int tb = (p.M + 15) / 16;
+  const dim3 grid((p.N / 16) * p.ksplit), block(256);
+  switch (tb) {
+    case 1: hipLaunchKernelGGL((gemm_kernel<1, I8>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<2, I8>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_kernel<3, I8>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((gemm_kernel<4, I8>), grid, block, 0, s, p); break;
+  }
+}
+
+int gemm_choose_ksplit(int N, int K, int target_wgs) {
+  const int strips = N / 16, chunks = K / 64;
+  int ks = 1;
+  while (strips * ks < target_wgs && ks * 2 * 4 <= chunks && ks < 16) ks *= 2;
+  return ks;
+}
+
+size_t gemm_ws_bytes(int M, int N, int K) {
+  const int ks = gemm_choose_ksplit(N, K, 512);
+  return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+}
+
+int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
+  if (i8)
+    launch_gemm<true>(p, s);
+  else
+    launch_gemm<false>(p, s);
+  if (p.ksplit > 1) {
+    const int threads = p.M * (p.N / 4);
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, p);
+  }
+  if (p.best_part) hipLaunchKernelGGL(fold_strip_keys, dim3(p.M), dim3(64), 0, s, p.best_part, p.N / 16, p.best);
+  return (int)hipGetLastError();
+}
+
+}  // namespace dspark

@@ -1,0 +1,149 @@
+// Greedy verify argmax over logits and the round's acceptance + commit, on the device State.
+//
+// verify_argmax: one block per (token, vocab chunk) folds the penalised fp16-rounded logits into the argmax key
+// (ordered bits << 32 | 0xFFFFFFFF - index), the second kernel folds the chunks per token. Integer max is order-free,
+// so the result is bit-identical run to run. Reference: head_run<false, M> (dspark.hip:2219-2318), argmax_key
+// (967-971), penalty sign rule (internal/sample/sample.go:75-90; kernel form multiplies by the host's 1/rep,
+// internal/model/dspark.go:575-578).
+//
+// accept_commit: the books of dspark.hip:2848-2913 on one wave.
+#include "common.h"
+#include "dspark.h"
+#include "dspark_internal.h"
+
+namespace dspark {
+
+constexpr int ARGMAX_CHUNK = 4096;  // logits per block
+
+template <bool F16>
+__global__ __launch_bounds__(256) void verify_argmax_partial(const void* logits, int M, int V, const uint32_t* seen,
+                                                             const dspark_state* st, float rep, float inv_rep,
+                                                             uint64_t* part, int nchunks) {
+  const int t = blockIdx.y, chunk = blockIdx.x;
+  // Drafts 1..t that were not seen before this round count as seen for this position (dspark.hip:2226-2232).
+  __shared__ int dt[DSPARK_MT_MAX];
+  __shared__ uint64_t isnew_s;
+  if (threadIdx.x == 0) {
+    uint64_t bits = 0;
+    for (int j = 1; j <= t && j < M; ++j) {
+      dt[j] = st->tokens[j];
+      // a draft outside the vocabulary matches no logit (and is not looked up in seen)
+      if (dt[j] >= 0 && dt[j] < V && ((seen[dt[j] >> 5] >> (dt[j] & 31)) & 1u) == 0) bits |= 1ull << j;
+    }
+    isnew_s = bits;
+  }
+  __syncthreads();
+  const uint64_t isnew = isnew_s;
+  uint64_t best = 0;
+  const int r0 = chunk * ARGMAX_CHUNK, r1 = min(V, r0 + ARGMAX_CHUNK);
+  for (int r = r0 + (int)threadIdx.x; r < r1; r += 256) {
+    float vr;
+    if (F16) {
+      vr = (float)ldg(reinterpret_cast<const _Float16*>(logits) + (size_t)t * V + r);
+    } else {
+      vr = (float)(_Float16)ldg(reinterpret_cast<const float*>(logits) + (size_t)t * V + r);
+    }
+    bool hit = ((ldg(seen + (r >> 5)) >> (r & 31)) & 1u) != 0;
+    if (isnew)
+      for (int j = 1; j <= t; ++j)
+        if (((isnew >> j) & 1) && r == dt[j]) hit = true;
+    const float pv = hit ? (vr > 0.f ? vr * inv_rep : vr * rep) : vr;
+    const uint64_t k = argmax_key(pv, (uint32_t)r);
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  __shared__ uint64_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = red[0];
+    for (int w = 1; w < 4; ++w) b = red[w] > b ? red[w] : b;
+    part[(size_t)t * nchunks + chunk] = b;
+  }
+}
+
+__global__ __launch_bounds__(64) void fold_keys(const uint64_t* part, int nchunks, uint64_t* best) {
+  const int t = blockIdx.x;
+  uint64_t b = 0;
+  for (int c = threadIdx.x; c < nchunks; c += 64) {
+    const uint64_t k = part[(size_t)t * nchunks + c];
+    b = k > b ? k : b;
+  }
+  b = wave_max_u64(b);
+  if (threadIdx.x == 0) best[t] = b;
+}
+
+__device__ __forceinline__ int key_token(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
+
+__global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, const uint64_t* best, int m, int skip_now,
+                                                           int32_t* out_tokens, uint32_t* seen) {
+  if (threadIdx.x != 0) return;
+  int acc = 0;
+  for (int t = 0; t < m - 1; ++t) {
+    if (key_token(best[t]) != st->tokens[t + 1]) break;
+    ++acc;
+  }
+  const int commit = acc + 1;
+  const int bonus = key_token(best[acc]);
+  const int aa = st->a;
+  int count = st->count;
+  for (int i = 1; i <= acc; ++i) out_tokens[count++] = st->tokens[i];
+  out_tokens[count++] = bonus;
+  for (int i = 1; i <= acc; ++i) {
+    const int tk = st->tokens[i];
+    seen[tk >> 5] |= 1u << (tk & 31);
+  }
+  seen[bonus >> 5] |= 1u << (bonus & 31);
+  bool stop = false;
+  if (st->eos >= 0)
+    for (int i = count - commit; i < count; ++i) stop = stop || out_tokens[i] == st->eos;
+  st->count = count;
+  st->ctx_new = commit;
+  st->ctx_pos = aa;
+  st->a = aa + commit;
+  st->anchor = bonus;
+  st->accepted += acc;
+  st->verified += m;
+  if (skip_now > 0) {
+    st->skip -= 1;
+  } else if (acc == 0) {
+    st->miss += 1;
+    if (st->skip_after > 0 && st->miss >= st->skip_after) {
+      st->skip = st->skip_rounds;
+      st->miss = 0;
+    }
+  } else {
+    st->miss = 0;
+  }
+  st->tokens[0] = bonus;
+  st->rounds_done += 1;
+  st->rounds_left -= 1;
+  st->run = (!stop && st->rounds_left > 0 && st->a < st->stop_at && count < st->budget) ? 1 : 0;
+}
+
+size_t verify_argmax_ws(int M, int V) {
+  const int nchunks = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+  return (size_t)M * nchunks * sizeof(uint64_t);
+}
+
+int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32_t* seen, const dspark_state* st,
+                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s) {
+  const int nchunks = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+  uint64_t* part = reinterpret_cast<uint64_t*>(ws);
+  if (f16)
+    hipLaunchKernelGGL(verify_argmax_partial<true>, dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st, rep,
+                       inv_rep, part, nchunks);
+  else
+    hipLaunchKernelGGL(verify_argmax_partial<false>, dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st, rep,
+                       inv_rep, part, nchunks);
+  hipLaunchKernelGGL(fold_keys, dim3(M), dim3(64), 0, s, part, nchunks, best);
+  return (int)hipGetLastError();
+}
+
+int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, uint32_t* seen,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, m, skip_now, out_tokens, seen);
+  return (int)hipGetLastError();
+}
+
+}  // namespace dspark

@@ -1,0 +1,264 @@
+"""Host-side binding of libdspark_amd.so (the C ABI in include/dspark.h).
+
+ctypes over the C ABI; torch is used only for device memory and the current HIP stream. There is no fallback:
+if the library is missing the import fails, and every call raises on a nonzero status.
+
+Mirrors the reference's host path for the DSpark step (internal/model/dspark.go: State words 52-77, draftLaunch
+537-621) at the level the C ABI exposes: per-round attention, argmax, acceptance and commit.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdspark_amd.so")
+
+MT_MAX = 64
+PAGE = 32
+
+STATE_FIELDS = ["a", "anchor", "count", "rounds_left", "limit", "budget", "eos", "M", "ctx_new", "ctx_pos", "ctx_lo",
+                "run", "force_m", "rounds_done", "accepted", "verified", "miss", "skip", "skip_after", "skip_rounds",
+                "stop_at", "ckpt_slot"]
+
+ERRORS = {1001: "DSPARK_EINVAL", 1002: "DSPARK_ENOSPACE", 1003: "DSPARK_EUNSUPPORTED"}
+
+
+class DsparkError(RuntimeError):
+    pass
+
+
+class State(ctypes.Structure):
+    """struct dspark_state (include/dspark.h) = struct State of dspark.hip:134-158 with tokens[64]."""
+    _fields_ = [(n, ctypes.c_int32) for n in STATE_FIELDS] + [("tokens", ctypes.c_int32 * MT_MAX)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("k_pages", ctypes.c_void_p), ("v_pages", ctypes.c_void_p),
+                ("block_table", ctypes.c_void_p), ("out", ctypes.c_void_p), ("out_f32", ctypes.c_void_p),
+                ("gate", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("M", ctypes.c_int32), ("QH", ctypes.c_int32), ("KVH", ctypes.c_int32), ("D", ctypes.c_int32),
+                ("a", ctypes.c_int32), ("start", ctypes.c_int32), ("window", ctypes.c_int32),
+                ("causal", ctypes.c_int32), ("splits", ctypes.c_int32)]
+
+
+_lib = None
+
+_SIGS = {
+    "dspark_abi_version": (ctypes.c_int, []),
+    "dspark_page_tokens": (ctypes.c_int, []),
+    "dspark_max_tokens": (ctypes.c_int, []),
+    "dspark_state_bytes": (ctypes.c_int, []),
+    "dspark_verify_attention_workspace": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
+    "dspark_verify_attention": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "dspark_kv_write": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_verify_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
+    "dspark_verify_argmax": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "dspark_accept_commit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "dspark_gemm_i8_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]),
+    "dspark_gemm_i8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "dspark_head_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
+    "dspark_head_argmax_f16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                              ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_size_t, ctypes.c_void_p]),
+}
+
+
+def lib():
+    """Load libdspark_amd.so; raises if it has not been built (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise DsparkError(f"{LIB_PATH} is missing: run __graft_entry__.build() (make -C {HERE})")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc, what):
+    if rc != 0:
+        raise DsparkError(f"{what} failed: {ERRORS.get(rc, 'hipError %d' % rc)}")
+
+
+# ---------------------------------------------------------------- torch plumbing
+def _torch():
+    import torch
+    return torch
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+class Workspace:
+    """A growable device byte buffer reused across calls (caller-owned memory, as the reference's engine owns
+    every buffer, internal/model/dspark.go:202-223)."""
+
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes):
+        torch = _torch()
+        nbytes = max(int(nbytes), 256)
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+# ---------------------------------------------------------------- KV pages
+def kv_pages_alloc(n_pages, KVH, D, device="cuda"):
+    torch = _torch()
+    k = torch.zeros((n_pages, KVH, PAGE, D), dtype=torch.float16, device=device)
+    v = torch.zeros((n_pages, KVH, D, PAGE), dtype=torch.float16, device=device)
+    return k, v
+
+
+def kv_write(k, v, k_pages, v_pages, pos0, block_table=None, stream=None):
+    """k, v: fp16 [n][KVH][D] (or [n][row] with row >= KVH*D) device tensors."""
+    n = k.shape[0]
+    KVH, D = k_pages.shape[1], k_pages.shape[3]
+    row = k.stride(0)
+    assert v.stride(0) == row and k.dtype == v.dtype == _torch().float16
+    rc = lib().dspark_kv_write(ptr(k), ptr(v), row, ptr(k_pages), ptr(v_pages), ptr(block_table), KVH, D, pos0, n,
+                               stream_handle(stream))
+    check(rc, "dspark_kv_write")
+
+
+def kv_to_pages(k, v, n_pages=None, block_table=None):
+    """Logical fp16 [T][KVH][D] K and V -> freshly allocated page pools (identity table unless given)."""
+    T, KVH, D = k.shape
+    if n_pages is None:
+        n_pages = (T + PAGE - 1) // PAGE
+    kp, vp = kv_pages_alloc(n_pages, KVH, D, device=k.device)
+    kv_write(k.contiguous(), v.contiguous(), kp, vp, 0, block_table)
+    return kp, vp
+
+
+# ---------------------------------------------------------------- verify attention
+def attn_args(q, k_pages, v_pages, a, start=0, window=0, causal=True, out=None, out_f32=None, gate=None,
+              block_table=None, splits=0):
+    M, QH, D = q.shape
+    KVH = k_pages.shape[1]
+    args = AttnArgs()
+    args.q, args.k_pages, args.v_pages = q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr()
+    args.block_table = block_table.data_ptr() if block_table is not None else None
+    args.out = out.data_ptr() if out is not None else None
+    args.out_f32 = out_f32.data_ptr() if out_f32 is not None else None
+    args.gate = gate.data_ptr() if gate is not None else None
+    args.M, args.QH, args.KVH, args.D = M, QH, KVH, D
+    args.a, args.start, args.window, args.causal, args.splits = a, start, window, int(causal), splits
+    return args
+
+
+def verify_attention(q, k_pages, v_pages, a, start=0, window=0, causal=True, out=None, out_f32=None, gate=None,
+                     block_table=None, splits=0, workspace=None, stream=None):
+    """q fp16 [M][QH][D]; pages hold positions 0..a+M-1. Returns (out fp16, out_f32) tensors as given/created."""
+    torch = _torch()
+    M, QH, D = q.shape
+    if out is None and out_f32 is None:
+        out = torch.empty((M, QH, D), dtype=torch.float16, device=q.device)
+    args = attn_args(q, k_pages, v_pages, a, start, window, causal, out, out_f32, gate, block_table, splits)
+    need = lib().dspark_verify_attention_workspace(ctypes.byref(args))
+    if need == 0:
+        raise DsparkError("dspark_verify_attention_workspace rejected the arguments")
+    ws = (workspace or Workspace(q.device)).get(need)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    check(lib().dspark_verify_attention(ctypes.byref(args), stream_handle(stream)), "dspark_verify_attention")
+    return out, out_f32
+
+
+# ---------------------------------------------------------------- argmax / accept
+def state_tensor(device="cuda", **fields):
+    """A device dspark_state initialised from keyword fields (tokens=list)."""
+    torch = _torch()
+    st = State()
+    for k, v in fields.items():
+        if k == "tokens":
+            for i, t in enumerate(v):
+                st.tokens[i] = int(t)
+        else:
+            setattr(st, k, int(v))
+    raw = bytes(st)
+    host = torch.frombuffer(bytearray(raw), dtype=torch.int32).clone()
+    return host.to(device)
+
+
+def state_from_tensor(t):
+    st = State()
+    ctypes.memmove(ctypes.byref(st), bytes(t.cpu().numpy().tobytes()), ctypes.sizeof(State))
+    return st
+
+
+def verify_argmax(logits, seen, st, rep=1.0, inv_rep=None, best=None, workspace=None, stream=None):
+    torch = _torch()
+    M, V = logits.shape
+    f16 = logits.dtype == torch.float16
+    if inv_rep is None:
+        inv_rep = float(torch.tensor(1.0, dtype=torch.float32) / torch.tensor(rep, dtype=torch.float32))
+    if best is None:
+        best = torch.empty(M, dtype=torch.int64, device=logits.device)
+    need = lib().dspark_verify_argmax_workspace(M, V)
+    ws = (workspace or Workspace(logits.device)).get(need)
+    rc = lib().dspark_verify_argmax(ptr(logits), int(f16), M, V, ptr(seen), ptr(st), rep, inv_rep, ptr(best), ptr(ws),
+                                    ws.numel(), stream_handle(stream))
+    check(rc, "dspark_verify_argmax")
+    return best
+
+
+def accept_commit(st, best, M, out_tokens, seen, skip_now=0, stream=None):
+    rc = lib().dspark_accept_commit(ptr(st), ptr(best), M, skip_now, ptr(out_tokens), ptr(seen), stream_handle(stream))
+    check(rc, "dspark_accept_commit")
+
+
+def keys_to_tokens(keys):
+    """u64 keys held in an int64 tensor -> token ids."""
+    torch = _torch()
+    low = keys & 0xFFFFFFFF
+    return (0xFFFFFFFF - low).to(torch.int64)
+
+
+# ---------------------------------------------------------------- GEMMs
+def gemm_i8(x, w_biased, scale, epilogue=0, y_f32=None, y_f16=None, workspace=None, stream=None):
+    torch = _torch()
+    M, K = x.shape
+    N = w_biased.shape[0]
+    if epilogue == 0 and y_f32 is None and y_f16 is None:
+        y_f32 = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    if epilogue != 0 and y_f16 is None:
+        y_f16 = torch.empty((M, N // 2 if epilogue == 1 else N), dtype=torch.float16, device=x.device)
+    need = lib().dspark_gemm_i8_workspace(M, N, K)
+    ws = (workspace or Workspace(x.device)).get(need)
+    rc = lib().dspark_gemm_i8(ptr(x), M, K, ptr(w_biased), ptr(scale), N, epilogue, ptr(y_f32), ptr(y_f16), ptr(ws),
+                              ws.numel(), stream_handle(stream))
+    check(rc, "dspark_gemm_i8")
+    return y_f32 if epilogue == 0 and y_f32 is not None else y_f16
+
+
+def head_argmax(x, w, y_f32=None, best=None, workspace=None, stream=None):
+    torch = _torch()
+    M, K = x.shape
+    N = w.shape[0]
+    if best is None:
+        best = torch.empty(M, dtype=torch.int64, device=x.device)
+    need = lib().dspark_head_argmax_workspace(M, N)
+    ws = (workspace or Workspace(x.device)).get(need)
+    rc = lib().dspark_head_argmax_f16(ptr(x), M, K, ptr(w), N, ptr(y_f32), ptr(best), ptr(ws), ws.numel(),
+                                      stream_handle(stream))
+    check(rc, "dspark_head_argmax_f16")
+    return best

@@ -1,0 +1,73 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what include/dspark.h declares, and the State struct
+keeps the reference's 22 scalar words in order (internal/model/dspark_test.go:8-22 pins the same layout)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT, load_host
+
+HEADER = os.path.join(ROOT, "include", "dspark.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(re.findall(r"\b(dspark_[a-z0-9_]+)\s*\(", text))
+    inline = set(re.findall(r"static inline [^(]*\b(dspark_[a-z0-9_]+)\s*\(", text))
+    return sorted(names - inline)
+
+
+def test_library_exports_every_declared_symbol():
+    host = load_host()
+    lib = host.lib()
+    names = declared_functions()
+    assert len(names) >= 14
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the binding declares a signature for each of them
+    assert sorted(host._SIGS) == names
+
+
+def test_size_queries_and_state_layout():
+    host = load_host()
+    lib = host.lib()
+    assert lib.dspark_abi_version() == 1
+    assert lib.dspark_page_tokens() == 32
+    assert lib.dspark_max_tokens() == 64
+    # 22 scalars (dspark.hip:134-157, dspark.go:52-77 sTokens == 22) then tokens[64]
+    assert lib.dspark_state_bytes() == (22 + 64) * 4 == ctypes.sizeof(host.State)
+    assert [f[0] for f in host.State._fields_][:22] == host.STATE_FIELDS
+    assert host.State.tokens.offset == 22 * 4
+
+
+def test_workspace_queries_reject_bad_shapes():
+    host = load_host()
+    lib = host.lib()
+    args = host.AttnArgs()
+    args.M, args.QH, args.KVH, args.D, args.a = 16, 32, 8, 64, 32768
+    args.causal = 1
+    ws = lib.dspark_verify_attention_workspace(ctypes.byref(args))
+    assert ws > 0
+    args.D = 96
+    assert lib.dspark_verify_attention_workspace(ctypes.byref(args)) == 0
+    args.D, args.M = 64, 65
+    assert lib.dspark_verify_attention_workspace(ctypes.byref(args)) == 0
+    assert lib.dspark_gemm_i8_workspace(16, 8192, 2048) == 0          # one split: no partials
+    assert lib.dspark_gemm_i8_workspace(16, 2048, 8192) > 0           # split K
+    assert lib.dspark_gemm_i8_workspace(16, 2050, 8192) == 0          # N % 16
+    assert lib.dspark_head_argmax_workspace(16, 16384) == 16 * 1024 * 8
+
+
+def test_entry_points_refuse_invalid_arguments_without_launching():
+    """Argument errors are reported before any device work (no GPU is needed to reach them)."""
+    host = load_host()
+    lib = host.lib()
+    args = host.AttnArgs()
+    args.M, args.QH, args.KVH, args.D, args.a = 16, 30, 8, 64, 10   # QH % KVH != 0
+    assert lib.dspark_verify_attention(ctypes.byref(args), None) == 1001
+    assert lib.dspark_kv_write(None, None, 512, None, None, None, 8, 64, 0, 1, None) == 1001
+    assert lib.dspark_gemm_i8(None, 16, 2048, None, None, 8192, 0, None, None, None, 0, None) == 1001
+    assert lib.dspark_accept_commit(None, None, 9, 0, None, None, None) == 1001
+    assert lib.dspark_verify_argmax(None, 0, 9, 65536, None, None, 1.0, 1.0, None, None, 0, None) == 1001

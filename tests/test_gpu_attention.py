@@ -1,0 +1,124 @@
+"""GPU parity of verify attention (through the C ABI) against the fp64 CPU oracle.
+
+Bar: max-abs error <= 2e-3 against the oracle on the same seeded fp16 inputs, plus
+run-to-run bit identity. Shapes cover the configs' geometry (32/8/64), the reference geometry (16/4/128), causal and
+bidirectional blocks, sliding windows, a paged block table, empty and ragged contexts.
+"""
+import numpy as np
+import pytest
+
+from conftest import load_host
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch
+
+
+def f16(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).cuda()
+
+
+def run_case(torch, orc, host, M, QH, KVH, D, a, start=0, window=0, causal=True, seed=100, paged=False, splits=0):
+    print(f"case M={M} QH={QH} KVH={KVH} D={D} a={a} start={start} window={window} causal={causal} paged={paged}",
+          flush=True)
+    T = a + M
+    q = orc.normal_f16(seed, (M, QH, D))
+    k = orc.normal_f16(seed + 1, (T, KVH, D))
+    v = orc.normal_f16(seed + 2, (T, KVH, D))
+    want = orc.verify_attention(q, k, v, a, start, window, causal)
+    npages = (T + 31) // 32
+    bt = None
+    if paged:
+        perm = np.random.default_rng(seed).permutation(npages + 3)[:npages].astype(np.int32)
+        bt = torch.from_numpy(perm).cuda()
+        kp, vp = host.kv_pages_alloc(npages + 3, KVH, D)
+        # cache rows 0..a-1 then the verified tokens' rows a..a+M-1 (the append a verify round does)
+        host.kv_write(f16(torch, k[:a]), f16(torch, v[:a]), kp, vp, 0, bt)
+        host.kv_write(f16(torch, k[a:]), f16(torch, v[a:]), kp, vp, a, bt)
+    else:
+        kp, vp = host.kv_to_pages(f16(torch, k), f16(torch, v))
+    qd = f16(torch, q)
+    out32 = torch.empty((M, QH, D), dtype=torch.float32, device="cuda")
+    out16 = torch.empty((M, QH, D), dtype=torch.float16, device="cuda")
+    host.verify_attention(qd, kp, vp, a, start, window, causal, out=out16, out_f32=out32, block_table=bt,
+                          splits=splits)
+    torch.cuda.synchronize()
+    got = out32.cpu().numpy().astype(np.float64)
+    err = np.max(np.abs(got - want))
+    assert err <= TOL, f"max-abs {err}"
+    err16 = np.max(np.abs(out16.cpu().numpy().astype(np.float64) - want))
+    assert err16 <= TOL, f"fp16 output max-abs {err16}"
+    # bit-identical on a second run
+    out32b = torch.empty_like(out32)
+    host.verify_attention(qd, kp, vp, a, start, window, causal, out_f32=out32b, block_table=bt, splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(out32, out32b)
+    return err
+
+
+@pytest.mark.parametrize("M,QH,KVH,D,a,start,window,causal,paged", [
+    (9, 32, 8, 64, 1024, 0, 0, True, False),      # C1 geometry
+    (16, 32, 8, 64, 4096, 0, 0, True, False),     # C2 shape at a short context
+    (1, 32, 8, 64, 777, 0, 0, True, False),       # single token, ragged context
+    (16, 32, 8, 64, 0, 0, 0, True, False),        # empty cache: causal block only
+    (5, 32, 8, 64, 3000, 2745, 256, True, False), # sliding window (start = a - window + 1)
+    (16, 32, 8, 64, 2000, 300, 0, False, False),  # drafter: ring range, bidirectional block
+    (9, 16, 4, 128, 1500, 0, 0, True, False),     # reference geometry
+    (9, 16, 4, 128, 1000, 745, 256, True, True),  # reference sliding layer, paged
+    (16, 32, 8, 64, 5000, 0, 0, True, True),      # permuted block table
+    (33, 32, 8, 64, 2048, 0, 0, True, False),     # C5 block (M = 33)
+])
+def test_verify_attention_matches_oracle(dev, orc, M, QH, KVH, D, a, start, window, causal, paged):
+    host = load_host()
+    run_case(dev, orc, host, M, QH, KVH, D, a, start, window, causal, paged=paged)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 64])
+def test_verify_attention_split_counts(dev, orc, splits):
+    host = load_host()
+    run_case(dev, orc, host, 16, 32, 8, 64, 3000, splits=splits, seed=300)
+
+
+def test_verify_attention_c2_full_context(dev, orc):
+    """C2 at its real shape: ctx 32768, M = 16, 32/8/64, one layer."""
+    host = load_host()
+    run_case(dev, orc, host, 16, 32, 8, 64, 32768, seed=400)
+
+
+def test_verify_attention_gate(dev, orc):
+    torch = dev
+    host = load_host()
+    M, QH, KVH, D, a = 9, 32, 8, 64, 600
+    q = orc.normal_f16(500, (M, QH, D))
+    k = orc.normal_f16(501, (a + M, KVH, D))
+    v = orc.normal_f16(502, (a + M, KVH, D))
+    gate = np.random.default_rng(5).standard_normal((M, QH)).astype(np.float32)
+    want = orc.verify_attention(q, k, v, a) * (1.0 / (1.0 + np.exp(-gate.astype(np.float64))))[:, :, None]
+    kp, vp = host.kv_to_pages(f16(torch, k), f16(torch, v))
+    out32 = torch.empty((M, QH, D), dtype=torch.float32, device="cuda")
+    host.verify_attention(f16(torch, q), kp, vp, a, out_f32=out32, gate=torch.from_numpy(gate).cuda())
+    torch.cuda.synchronize()
+    assert np.max(np.abs(out32.cpu().numpy() - want)) <= TOL
+
+
+def test_kv_write_layout(dev, orc):
+    """Pages hold K token-major and V transposed; positions beyond the write are untouched."""
+    torch = dev
+    host = load_host()
+    T, KVH, D = 70, 8, 64
+    k = orc.normal_f16(600, (T, KVH, D))
+    v = orc.normal_f16(601, (T, KVH, D))
+    kp, vp = host.kv_to_pages(f16(torch, k), f16(torch, v), n_pages=4)
+    kpn = kp.cpu().numpy().view(np.uint16)
+    vpn = vp.cpu().numpy().view(np.uint16)
+    for pos in (0, 31, 32, 69):
+        pg, sl = divmod(pos, 32)
+        assert np.array_equal(kpn[pg, :, sl, :], k[pos])
+        assert np.array_equal(vpn[pg, :, :, sl], v[pos])
+    assert not kpn[2, :, 6:, :].any() and not kpn[3].any()

@@ -1,0 +1,166 @@
+"""GPU parity of the greedy verify argmax, acceptance/commit, the int8 verify GEMM and the cropped head argmax,
+through the C ABI, against the CPU oracle. Integer/index results (keys, acceptance, commit offsets, emitted tokens)
+must be bit-exact; GEMM values within 2e-3 relative of the fp64 oracle; head argmax exact except where the oracle's
+top two values are within the GEMM's rounding (a near tie, the only exception north_star allows)."""
+import numpy as np
+import pytest
+
+from conftest import load_host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch
+
+
+def f16(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).cuda()
+
+
+def seen_bitmap(V, toks):
+    bits = np.zeros((V + 31) // 32, np.uint32)
+    for t in toks:
+        bits[t >> 5] |= np.uint32(1 << (t & 31))
+    return bits
+
+
+def c1_round(orc, seed, M=9, V=65536, plant=0.5, rep=1.0, nseen=200):
+    """BASELINE config C1's acceptance half: seeded fp16 logits, drafts planted as the previous position's argmax."""
+    rng = np.random.default_rng(seed)
+    logits = orc.f16_to_f32(orc.normal_f16(seed, (M, V)))
+    seen_toks = rng.integers(0, V, nseen)
+    bits = seen_bitmap(V, seen_toks)
+    tokens = np.zeros(M, np.int32)
+    tokens[0] = int(rng.integers(0, V))
+    for t in range(1, M):
+        keys = orc.verify_argmax(logits[:t], bits, tokens[:max(t, 1)], rep=rep)
+        am = int(orc.keys_to_tokens(keys)[t - 1])
+        if rng.random() < plant:
+            tokens[t] = am
+        else:
+            d = int(rng.integers(0, V))
+            tokens[t] = d if d != am else (d + 1) % V
+    return logits, bits, tokens
+
+
+@pytest.mark.parametrize("seed,plant,rep", [(1, 0.5, 1.0), (2, 1.0, 1.0), (3, 0.0, 1.0), (4, 0.5, 1.3), (5, 1.0, 1.3)])
+def test_verify_argmax_and_commit_c1(dev, orc, seed, plant, rep):
+    torch = dev
+    host = load_host()
+    M, V, a = 9, 65536, 1024
+    print(f"case C1 seed={seed} plant={plant} rep={rep}", flush=True)
+    logits, bits, tokens = c1_round(orc, seed, M, V, plant, rep)
+    want_keys = orc.verify_argmax(logits, bits, tokens, rep=rep)
+    for dt in (torch.float32, torch.float16):
+        lg = torch.from_numpy(logits).cuda().to(dt)
+        st = host.state_tensor(a=a, anchor=int(tokens[0]), tokens=tokens, rounds_left=32, budget=512, eos=-1,
+                               stop_at=1056, run=1, skip_rounds=1)
+        seen = torch.from_numpy(bits.view(np.int32)).cuda()
+        best = host.verify_argmax(lg, seen, st, rep=rep)
+        torch.cuda.synchronize()
+        got = best.cpu().numpy().view(np.uint64)
+        assert np.array_equal(got, want_keys), (got, want_keys)
+    # acceptance + commit on the device State, against the oracle's books
+    out = torch.zeros(600, dtype=torch.int32, device="cuda")
+    host.accept_commit(st, best, M, out, seen)
+    torch.cuda.synchronize()
+    gst = host.state_from_tensor(st)
+    ost = orc.new_state(a=a, anchor=int(tokens[0]), tokens=tokens, rounds_left=32, budget=512, eos=-1, stop_at=1056,
+                        run=1, skip_rounds=1)
+    oout = np.zeros(600, np.int32)
+    obits = bits.copy()
+    acc = orc.accept_commit(ost, orc.keys_to_tokens(want_keys), M, oout, obits)
+    for f in host.STATE_FIELDS:
+        assert getattr(gst, f) == getattr(ost, f), f
+    assert list(gst.tokens)[:M] == list(ost.tokens)[:M]
+    assert np.array_equal(out.cpu().numpy(), oout)
+    assert np.array_equal(seen.cpu().numpy().view(np.uint32), obits)
+    assert gst.a == a + acc + 1  # KV commit offset
+    if plant == 1.0 and rep == 1.0:
+        assert acc == M - 1
+    if plant == 0.0:
+        assert acc == 0
+
+
+def test_commit_stop_rules_on_device(dev, orc):
+    torch = dev
+    host = load_host()
+    V = 4096
+    for kw in (dict(eos=11), dict(stop_at=1027), dict(budget=3), dict(rounds_left=1), dict(skip=2)):
+        base = dict(a=1024, anchor=5, tokens=[5, 10, 11, 12], rounds_left=32, budget=512, eos=-1, stop_at=1056,
+                    run=1, skip_rounds=1, skip_after=2, miss=1)
+        base.update(kw)
+        skip_now = 1 if kw.get("skip") else 0
+        keys = np.array([orc.argmax_key(1.0, t) for t in (10, 11, 12, 13)], np.uint64)
+        st = host.state_tensor(**base)
+        best = torch.from_numpy(keys.view(np.int64)).cuda()
+        out = torch.zeros(64, dtype=torch.int32, device="cuda")
+        seen = torch.zeros(V // 32, dtype=torch.int32, device="cuda")
+        host.accept_commit(st, best, 4, out, seen, skip_now=skip_now)
+        torch.cuda.synchronize()
+        gst = host.state_from_tensor(st)
+        ost = orc.new_state(**base)
+        oout = np.zeros(64, np.int32)
+        acc = orc.accept_commit(ost, np.array([10, 11, 12, 13], np.int32), 4, oout, np.zeros(V // 32, np.uint32),
+                                skip_now=skip_now)
+        for f in host.STATE_FIELDS:
+            assert getattr(gst, f) == getattr(ost, f), (kw, f)
+
+
+@pytest.mark.parametrize("M,N,K,epilogue", [(16, 8192, 2048, 0), (16, 2048, 8192, 0), (9, 1024, 2048, 1),
+                                            (16, 512, 1024, 2), (1, 64, 128, 0), (33, 256, 512, 0),
+                                            (64, 128, 256, 0)])
+def test_gemm_i8_matches_oracle(dev, orc, M, N, K, epilogue):
+    torch = dev
+    host = load_host()
+    print(f"case gemm M={M} N={N} K={K} epi={epilogue}", flush=True)
+    x = orc.normal_f16(700 + M, (M, K))
+    w = orc.int8_uniform(701 + N, (N, K))
+    s = orc.f32_to_f16(np.random.default_rng(N).uniform(0.5, 1.5, N).astype(np.float32) / np.float32(127 * np.sqrt(K)))
+    want = orc.gemm_i8(x, w, s)
+    wb = torch.from_numpy((w.astype(np.int16) + 128).astype(np.uint8)).cuda()
+    y = host.gemm_i8(f16(torch, x), wb, f16(torch, s), epilogue=epilogue)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().astype(np.float64)
+    scale = np.max(np.abs(want))
+    if epilogue == 0:
+        assert np.max(np.abs(got - want)) <= 2e-3 * scale
+    elif epilogue == 1:
+        g, u = want[:, 0::2], want[:, 1::2]
+        ref = (g / (1 + np.exp(-g))) * u
+        assert np.max(np.abs(got - ref)) <= 2e-3 * max(1.0, np.max(np.abs(ref)))
+    else:
+        ref = want / (1 + np.exp(-want))
+        assert np.max(np.abs(got - ref)) <= 2e-3 * max(1.0, np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 16384, 2048), (9, 4096, 2048), (33, 1024, 512)])
+def test_head_argmax_matches_oracle(dev, orc, M, N, K):
+    torch = dev
+    host = load_host()
+    print(f"case head M={M} N={N} K={K}", flush=True)
+    x = orc.normal_f16(800 + M, (M, K))
+    w = orc.normal_f16(801 + N, (N, K), scale=float(1 / np.sqrt(K)))
+    want = orc.gemm_f16(x, w)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    best = host.head_argmax(f16(torch, x), f16(torch, w), y_f32=y)
+    torch.cuda.synchronize()
+    got_y = y.cpu().numpy().astype(np.float64)
+    assert np.max(np.abs(got_y - want)) <= 2e-3
+    idx = host.keys_to_tokens(best).cpu().numpy()
+    # the key must be the argmax of the GPU's own fp32 values (bit-exact fold) ...
+    assert idx.tolist() == orc.row_argmax(y.cpu().numpy()).tolist()
+    # ... and match the oracle's argmax unless the oracle's top two are a near tie
+    for t in range(M):
+        o = int(np.argmax(want[t]))
+        if idx[t] != o:
+            top = np.sort(want[t])[-2:]
+            assert top[1] - top[0] < 1e-4, (t, idx[t], o, top)
+    # bit-identical rerun
+    best2 = host.head_argmax(f16(torch, x), f16(torch, w))
+    torch.cuda.synchronize()
+    assert torch.equal(best, best2)
