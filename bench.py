@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the DSpark step's hot path on one MI355X.
+
+Default workload ("C2"): verify attention alone, 6 GQA layers (32 query / 8 KV heads,
+head_dim 64), fp16 K/V cache at context 32768, 16 verify tokens per step, causal inside the drafted block. A step
+runs each layer's verify attention (split pass + combine) over pages that already hold the 16 tokens' own K/V.
+Inputs are synthetic N(0,1) fp16 resident in HBM; two full KV sets (2 x 6 x 64 MiB) alternate between steps so the
+256 MB Infinity Cache cannot serve a step from the previous one.
+
+Prints one JSON line (the driver's contract) with a `roofline` object for the dominant kernel (the split pass,
+`verify_attn_kernel`) timed with HIP events on the library's stream, and a `cpu_baseline` object (the C oracle's
+fp32 multi-threaded restatement timed on a bounded sample of the same workload).
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "lfm3-1.7b-mi50_amd")
+METRIC = "greedy decode tok/s at 1k/32k/128k ctx; verify-attn HBM GB/s vs roofline"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "verify_attn_c2_traffic.txt")
+
+
+def load_host():
+    spec = importlib.util.spec_from_file_location("dspark_amd_host", os.path.join(PKG, "dspark.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def read_traffic():
+    """HBM bytes per launch of verify_attn_kernel from the committed rocprofv3 --pmc summary, if present."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    vals = {}
+    for line in open(TRAFFIC_FILE):
+        if ":" in line:
+            k, _, v = line.partition(":")
+            vals[k.strip()] = v.strip()
+    try:
+        return int(float(vals["hbm_bytes_per_launch"]))
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline_c2(ctx, M, QH, KVH, D, seconds):
+    """The CPU oracle (test infrastructure, used here only as the timed baseline) on layers of the same workload."""
+    import numpy as np
+    from oracle import oracle as orc
+    rng = np.random.default_rng(20261202)
+    q = rng.standard_normal((M, QH, D)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((ctx + M, KVH, D)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((ctx + M, KVH, D)).astype(np.float16).view(np.uint16)
+    threads = cpu_threads()
+    layers = 0
+    t0 = time.perf_counter()
+    while True:
+        orc.verify_attention_f32_mt(q, k, v, ctx, threads=threads)
+        layers += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    layer_bytes = ctx * KVH * D * 2 * 2
+    return {"value": round(layer_bytes * layers / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{layers} layers of the C2 workload (ctx {ctx}, {M} verify tokens, {QH}/{KVH} heads, d{D}) "
+                      f"through the C oracle's fp32 verify attention on {threads} threads, {el:.1f} s"}
+
+
+def bench_c2(args, host, torch):
+    L, ctx, M, QH, KVH, D = 6, 32768, 16, 32, 8, 64
+    SETS = 2
+    lib = host.lib()
+    dev = "cuda"
+    stream = torch.cuda.current_stream()
+    sh = host.stream_handle(stream)
+    n_pages = (ctx + M + 31) // 32
+    g = torch.Generator(device=dev)
+    g.manual_seed(20261201 + 1)
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(torch.float16)
+
+    kv = [[(rnd(n_pages, KVH, 32, D), rnd(n_pages, KVH, D, 32)) for _ in range(L)] for _ in range(SETS)]
+    q = [rnd(M, QH, D) for _ in range(L)]
+    fk = [rnd(M, KVH, D) for _ in range(L)]
+    fv = [rnd(M, KVH, D) for _ in range(L)]
+    out = [torch.empty((M, QH, D), dtype=torch.float16, device=dev) for _ in range(L)]
+    argv = [[host.attn_args(q[l], kv[s][l][0], kv[s][l][1], ctx, out=out[l]) for l in range(L)] for s in range(SETS)]
+    need = lib.dspark_verify_attention_workspace(ctypes.byref(argv[0][0]))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    for s in range(SETS):
+        for l in range(L):
+            argv[s][l].workspace, argv[s][l].workspace_bytes = ws.data_ptr(), ws.numel()
+    kvw = [[(ctypes.c_void_p(fk[l].data_ptr()), ctypes.c_void_p(fv[l].data_ptr()),
+             ctypes.c_void_p(kv[s][l][0].data_ptr()), ctypes.c_void_p(kv[s][l][1].data_ptr())) for l in range(L)]
+           for s in range(SETS)]
+
+    # The verified block's K/V rows go into every layer's pages once (in the full step the kernel that produces them
+    # writes them); each step then re-verifies the same block.
+    for s in range(SETS):
+        for l in range(L):
+            a_, b_, c_, d_ = kvw[s][l]
+            host.check(lib.dspark_kv_write(a_, b_, KVH * D, c_, d_, None, KVH, D, ctx, M, sh), "kv_write")
+
+    def step(i):
+        s = i % SETS
+        for l in range(L):
+            host.check(lib.dspark_verify_attention(ctypes.byref(argv[s][l]), sh), "verify_attention")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = e0.elapsed_time(e1)
+    ms_per_step = total_ms / args.steps
+    layer_bytes = ctx * KVH * D * 2 * 2
+    step_bytes = L * layer_bytes
+
+    # Dominant kernel (the split pass): the same launches back to back, HIP events around the whole run on the
+    # library's stream, average = elapsed / launches (launch gaps included, so this errs low).
+    n_launch = args.steps * L
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record(stream)
+    for i in range(args.steps):
+        for l in range(L):
+            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
+    b1.record(stream)
+    torch.cuda.synchronize()
+    split_avg = b0.elapsed_time(b1) / n_launch
+    # Per-launch brackets (event overhead included, so these err high), split and combine separately.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_launch)]
+    j = 0
+    for i in range(args.steps):
+        for l in range(L):
+            ev[j][0].record(stream)
+            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
+            ev[j][1].record(stream)
+            host.check(lib.dspark_verify_attention_combine(ctypes.byref(argv[i % SETS][l]), sh), "combine")
+            ev[j][2].record(stream)
+            j += 1
+    torch.cuda.synchronize()
+    split_br = sorted(e[0].elapsed_time(e[1]) for e in ev)
+    comb_br = sorted(e[1].elapsed_time(e[2]) for e in ev)
+    achieved = layer_bytes / (split_avg * 1e-3) / 1e9
+    traffic = read_traffic()
+    res = {
+        "metric": METRIC,
+        "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1) fp16 K/V/Q resident in HBM, 2 rotating KV sets",
+        "config": {"workload": "C2 verify attention (BASELINE configs[1]): 6 GQA layers, 32 q / 8 kv heads, head_dim 64, "
+                               "fp16 paged K/V at context 32768, 16 verify tokens causal in block; per layer: split pass + "
+                               "combine (the block's K/V appended once at setup)",
+                   "layers": L, "ctx": ctx, "verify_tokens": M, "q_heads": QH, "kv_heads": KVH, "head_dim": D,
+                   "algorithmic_bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "verify_attn_kernel", "algorithmic_bytes_per_launch": layer_bytes,
+                     "avg_launch_us": round(split_avg * 1e3, 2),
+                     "bracketed_median_us": round(split_br[len(split_br) // 2] * 1e3, 2),
+                     "combine_bracketed_median_us": round(comb_br[len(comb_br) // 2] * 1e3, 2)},
+    }
+    return res
+
+
+def bench_copy(args, torch):
+    """Plain device copy of a known size: the calibration point for rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    nbytes = 512 << 20
+    src = torch.ones(nbytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    return {"workload": "copy", "bytes_per_copy": nbytes, "GBs_read_plus_write": round(2 * nbytes * args.steps / el / 1e9, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", default="c2", choices=["c2", "copy"])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    if args.workload == "copy":
+        print(json.dumps(bench_copy(args, torch)), flush=True)
+        return
+    host = load_host()
+    res = bench_c2(args, host, torch)
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        res["cpu_baseline"] = cpu_baseline_c2(32768, 16, 32, 8, 64, args.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

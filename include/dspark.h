@@ -10,10 +10,13 @@
  *
  * Reference interfaces each entry point replaces are cited as file:line in jwyjohn/lfm3-1.7b-mi50.
  *
- * KV cache format (this library's own, chosen for the matrix cores): per attention layer two page pools,
- *   K pages [n_pages][KVH][32][D]   fp16 (token-major inside a page, one 2*D-byte row per token)
- *   V pages [n_pages][KVH][D][32]   fp16 (transposed inside a page, one 64-byte row per dimension)
- * and an int32 block table mapping logical page (position / 32) to a physical page (NULL = identity).
+ * KV cache format (this library's own, chosen for the matrix cores): per attention layer two page pools of
+ * n_pages x KVH x (32 * D) fp16, and an int32 block table mapping logical page (position / 32) to a physical page
+ * (NULL = identity). Inside a (page, KV head) block:
+ *   K: matrix-core operand order -- for key block b in {0,1} and k-step s < D/32, 64 lanes x 8 halves, lane
+ *      (n = lane % 16, g = lane / 16) holding K[key][32 s + 8 g .. +8] with key = 8 (n / 4) + 4 b + n % 4;
+ *   V: transposed, [D][32 keys].
+ * dspark_kv_write is the one writer of this format (prefill and verify rounds both append through it).
  */
 #ifndef DSPARK_H
 #define DSPARK_H
@@ -64,6 +67,7 @@ typedef struct dspark_attn_args {
   const void* k_pages;         /* fp16 K page pool */
   const void* v_pages;         /* fp16 V page pool (transposed pages) */
   const int32_t* block_table;  /* [ceil((a+M)/32)] logical -> physical page, NULL = identity */
+  int64_t kv_pages;            /* pages in each pool (bounds every page access; pool bytes < 2 GiB) */
   void* out;                   /* fp16 [M][QH][D] or NULL */
   float* out_f32;              /* fp32 [M][QH][D] or NULL */
   const float* gate;           /* fp32 [M][QH] pre-sigmoid gate or NULL (target layers gate the output) */
@@ -76,6 +80,11 @@ typedef struct dspark_attn_args {
 
 size_t dspark_verify_attention_workspace(const dspark_attn_args* args);
 int dspark_verify_attention(const dspark_attn_args* args, dspark_stream_t stream);
+/* The two phases of dspark_verify_attention, for callers that schedule them apart (the reference separates them by a
+ * grid barrier: attention phase, then combine_phase, dspark.hip:2519-2556): the key-split pass writes partials into
+ * the workspace; the combine merges them (same args, same workspace, same stream order). */
+int dspark_verify_attention_splits(const dspark_attn_args* args, dspark_stream_t stream);
+int dspark_verify_attention_combine(const dspark_attn_args* args, dspark_stream_t stream);
 
 /* ---------------------------------------------------------------- KV write (append / commit)
  * Writes K/V rows for positions pos0..pos0+n-1 into the pages: k, v fp16 [n][KVH][D] (row stride `row_stride`

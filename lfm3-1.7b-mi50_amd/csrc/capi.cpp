@@ -10,7 +10,19 @@ using namespace dspark;
 namespace {
 
 constexpr int ABI_VERSION = 1;
-constexpr int ATTN_TARGET_WGS = 512;  // two 4-wave workgroups per CU on 256 CUs
+
+// Compute units of the current device (queried once per device; 256 on MI355X).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 hipStream_t S(dspark_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -23,6 +35,8 @@ bool attn_args_ok(const dspark_attn_args* a) {
   if (a->a < 0 || a->start < 0 || a->window < 0) return false;
   if (a->start > a->a + a->M - 1) return false;
   if (a->splits < 0) return false;
+  if (a->kv_pages < 1 || a->kv_pages * a->KVH * DSPARK_PAGE_TOKENS * a->D * 2 >= (int64_t)1 << 31) return false;
+  if (!a->block_table && a->kv_pages < (a->a + a->M + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS) return false;
   if ((int64_t)a->QH / a->KVH * a->M > 64 * 16) return false;  // rows per KV head
   return true;
 }
@@ -33,6 +47,7 @@ AttnParams attn_params(const dspark_attn_args* a) {
   p.kp = static_cast<const _Float16*>(a->k_pages);
   p.vp = static_cast<const _Float16*>(a->v_pages);
   p.bt = a->block_table;
+  p.k_bytes = p.v_bytes = (uint32_t)(a->kv_pages * a->KVH * DSPARK_PAGE_TOKENS * a->D * 2);
   p.out16 = static_cast<_Float16*>(a->out);
   p.out32 = a->out_f32;
   p.gate = a->gate;
@@ -45,7 +60,7 @@ AttnParams attn_params(const dspark_attn_args* a) {
   p.window = a->window;
   p.causal = a->causal ? 1 : 0;
   p.S = a->splits;
-  attn_plan(p, a->D, ATTN_TARGET_WGS);
+  attn_plan(p, a->D, device_cus());
   return p;
 }
 
@@ -62,12 +77,13 @@ size_t dspark_verify_attention_workspace(const dspark_attn_args* a) {
   if (!a || a->M < 1 || a->M > DSPARK_MT_MAX || a->KVH < 1 || a->QH < a->KVH || (a->D != 64 && a->D != 128)) return 0;
   dspark_attn_args b = *a;
   if (!b.q) b.q = b.k_pages = b.v_pages = b.out = reinterpret_cast<void*>(1);  // size only
+  if (b.kv_pages == 0) b.kv_pages = (b.a + b.M + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS;
   if (!attn_args_ok(&b)) return 0;
   AttnParams p = attn_params(&b);
   return attn_workspace_bytes(p, a->D);
 }
 
-int dspark_verify_attention(const dspark_attn_args* a, dspark_stream_t stream) {
+static int verify_attention_phases(const dspark_attn_args* a, int phases, dspark_stream_t stream) {
   if (!attn_args_ok(a)) return DSPARK_EINVAL;
   AttnParams p = attn_params(a);
   const size_t need = attn_workspace_bytes(p, a->D);
@@ -78,7 +94,17 @@ int dspark_verify_attention(const dspark_attn_args* a, dspark_stream_t stream) {
   const size_t acc_bytes = (slots * p.R * a->D * sizeof(float) + 255) / 256 * 256;
   p.part_ml = reinterpret_cast<f32x2_t*>(static_cast<char*>(a->workspace) + acc_bytes);
   if (acc_bytes + slots * p.R * sizeof(f32x2_t) > a->workspace_bytes) return DSPARK_ENOSPACE;
-  return attn_launch(p, a->D, S(stream));
+  return attn_launch(p, a->D, phases, S(stream));
+}
+
+int dspark_verify_attention(const dspark_attn_args* a, dspark_stream_t stream) {
+  return verify_attention_phases(a, 3, stream);
+}
+int dspark_verify_attention_splits(const dspark_attn_args* a, dspark_stream_t stream) {
+  return verify_attention_phases(a, 1, stream);
+}
+int dspark_verify_attention_combine(const dspark_attn_args* a, dspark_stream_t stream) {
+  return verify_attention_phases(a, 2, stream);
 }
 
 int dspark_kv_write(const void* k, const void* v, int64_t row_stride, void* k_pages, void* v_pages,

@@ -15,6 +15,7 @@ struct AttnParams {
   const _Float16* kp;
   const _Float16* vp;
   const int32_t* bt;
+  uint32_t k_bytes, v_bytes;  // page pool sizes (range of the buffer loads; < 2 GiB)
   float* part_acc;   // [KVH][RG][S][R][D]
   f32x2_t* part_ml;  // [KVH][RG][S][R] (max, sum); max = -inf when the split saw no key of the row
   _Float16* out16;
@@ -23,14 +24,14 @@ struct AttnParams {
   int M, QH, KVH, G;
   int a, start, window, causal;
   int page0, npages, pps, S;  // logical page range and its split
-  int RG, QB, R;              // row groups, 16-row blocks per wave, rows per group
+  int RG, QB, R, OCC;         // row groups, 16-row blocks per wave, rows per group, workgroups per CU
   int full_lo, full_hi;       // pages inside [full_lo, full_hi] need no mask
   float c;                    // log2(e) / sqrt(D)
 };
 
-void attn_plan(AttnParams& p, int D, int target_wgs);
+void attn_plan(AttnParams& p, int D, int cus);
 size_t attn_workspace_bytes(const AttnParams& p, int D);
-int attn_launch(AttnParams& p, int D, hipStream_t s);
+int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);  // phases: 1 split pass, 2 combine, 3 both
 int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt, int KVH,
                     int D, int pos0, int n, hipStream_t s);
 

@@ -33,7 +33,7 @@ class State(ctypes.Structure):
 
 class AttnArgs(ctypes.Structure):
     _fields_ = [("q", ctypes.c_void_p), ("k_pages", ctypes.c_void_p), ("v_pages", ctypes.c_void_p),
-                ("block_table", ctypes.c_void_p), ("out", ctypes.c_void_p), ("out_f32", ctypes.c_void_p),
+                ("block_table", ctypes.c_void_p), ("kv_pages", ctypes.c_int64), ("out", ctypes.c_void_p), ("out_f32", ctypes.c_void_p),
                 ("gate", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
                 ("M", ctypes.c_int32), ("QH", ctypes.c_int32), ("KVH", ctypes.c_int32), ("D", ctypes.c_int32),
                 ("a", ctypes.c_int32), ("start", ctypes.c_int32), ("window", ctypes.c_int32),
@@ -49,6 +49,8 @@ _SIGS = {
     "dspark_state_bytes": (ctypes.c_int, []),
     "dspark_verify_attention_workspace": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "dspark_verify_attention": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "dspark_verify_attention_splits": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "dspark_verify_attention_combine": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_kv_write": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
@@ -140,6 +142,38 @@ def kv_write(k, v, k_pages, v_pages, pos0, block_table=None, stream=None):
     check(rc, "dspark_kv_write")
 
 
+def k_page_index(D):
+    """For a (page, head) K block of 32*D halves: flat index of K[key][d], as a [32][D] int64 array (the operand
+    order documented in include/dspark.h)."""
+    import numpy as np
+    key = np.arange(PAGE)[:, None]
+    d = np.arange(D)[None, :]
+    b = (key >> 2) & 1
+    nrow = 4 * (key >> 3) + (key & 3)
+    s, g, j = d // 32, (d % 32) // 8, d % 8
+    return (((b * (D // 32) + s) * 64 + nrow + 16 * g) * 8 + j).astype(np.int64)
+
+
+def kv_from_pages(k_pages, v_pages, positions, block_table=None):
+    """Read K/V rows of the given positions back from the pages (host copy; for checks and debugging)."""
+    import numpy as np
+    kp = k_pages.detach().cpu().numpy()
+    vp = v_pages.detach().cpu().numpy()
+    n_pages, KVH = kp.shape[0], kp.shape[1]
+    D = kp.size // (n_pages * KVH * PAGE)
+    kflat = kp.reshape(n_pages, KVH, PAGE * D)
+    vflat = vp.reshape(n_pages, KVH, D, PAGE)
+    idx = k_page_index(D)
+    bt = None if block_table is None else block_table.detach().cpu().numpy()
+    ks, vs = [], []
+    for pos in positions:
+        lp, sl = divmod(int(pos), PAGE)
+        pg = lp if bt is None else int(bt[lp])
+        ks.append(kflat[pg][:, idx[sl]])
+        vs.append(vflat[pg][:, :, sl])
+    return np.stack(ks), np.stack(vs)
+
+
 def kv_to_pages(k, v, n_pages=None, block_table=None):
     """Logical fp16 [T][KVH][D] K and V -> freshly allocated page pools (identity table unless given)."""
     T, KVH, D = k.shape
@@ -158,6 +192,7 @@ def attn_args(q, k_pages, v_pages, a, start=0, window=0, causal=True, out=None, 
     args = AttnArgs()
     args.q, args.k_pages, args.v_pages = q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr()
     args.block_table = block_table.data_ptr() if block_table is not None else None
+    args.kv_pages = k_pages.shape[0]
     args.out = out.data_ptr() if out is not None else None
     args.out_f32 = out_f32.data_ptr() if out_f32 is not None else None
     args.gate = gate.data_ptr() if gate is not None else None

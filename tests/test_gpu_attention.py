@@ -108,17 +108,23 @@ def test_verify_attention_gate(dev, orc):
 
 
 def test_kv_write_layout(dev, orc):
-    """Pages hold K token-major and V transposed; positions beyond the write are untouched."""
+    """K pages hold the operand order of include/dspark.h, V pages are transposed; pages past the write stay zero."""
     torch = dev
     host = load_host()
-    T, KVH, D = 70, 8, 64
-    k = orc.normal_f16(600, (T, KVH, D))
-    v = orc.normal_f16(601, (T, KVH, D))
-    kp, vp = host.kv_to_pages(f16(torch, k), f16(torch, v), n_pages=4)
-    kpn = kp.cpu().numpy().view(np.uint16)
-    vpn = vp.cpu().numpy().view(np.uint16)
-    for pos in (0, 31, 32, 69):
-        pg, sl = divmod(pos, 32)
-        assert np.array_equal(kpn[pg, :, sl, :], k[pos])
-        assert np.array_equal(vpn[pg, :, :, sl], v[pos])
-    assert not kpn[2, :, 6:, :].any() and not kpn[3].any()
+    for D in (64, 128):
+        T, KVH = 70, 4
+        k = orc.normal_f16(600 + D, (T, KVH, D))
+        v = orc.normal_f16(601 + D, (T, KVH, D))
+        kp, vp = host.kv_to_pages(f16(torch, k), f16(torch, v), n_pages=4)
+        torch.cuda.synchronize()
+        kpn = kp.cpu().numpy().view(np.uint16).reshape(4, KVH, 32 * D)
+        vpn = vp.cpu().numpy().view(np.uint16).reshape(4, KVH, D, 32)
+        idx = host.k_page_index(D)
+        assert sorted(idx.ravel().tolist()) == list(range(32 * D))  # a permutation of the block
+        for pos in (0, 5, 31, 32, 45, 69):
+            pg, sl = divmod(pos, 32)
+            assert np.array_equal(kpn[pg][:, idx[sl]], k[pos])
+            assert np.array_equal(vpn[pg][:, :, sl], v[pos])
+        kb, vb = host.kv_from_pages(kp, vp, range(T))
+        assert np.array_equal(kb.view(np.uint16), k) and np.array_equal(vb.view(np.uint16), v)
+        assert not kpn[3].any()
