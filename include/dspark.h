@@ -132,6 +132,88 @@ int dspark_head_argmax_f16(const void* x, int32_t M, int32_t K, const void* w, i
                            uint64_t* best_keys, void* workspace, size_t workspace_bytes, dspark_stream_t stream);
 size_t dspark_head_argmax_workspace(int32_t M, int32_t N);
 
+/* ---------------------------------------------------------------- the full DSpark step (engine)
+ * An engine owns one model (target + drafter weights, int8 GEMM weights as biased u8 with one fp16 scale per output
+ * row) and the runtime buffers of one request, all in device memory of the device current at creation. A round is a
+ * fixed launch sequence driven by the device State: context projection of the last round's committed tokens into the
+ * drafter's KV ring, the drafter block [anchor, mask x (block-1)] through the drafter layers, the cropped head and the
+ * Markov/confidence steps (drafts), the verify pass of the target layers over the whole block with the greedy head,
+ * then acceptance + commit. Every kernel reads positions from the State and does nothing once State.run is 0, so
+ * rounds are enqueued back to back with no host round trip (the reference runs up to 32 rounds in one persistent
+ * launch, dspark.hip:2379-2950). Replaces Engine.draftLaunch + dspark_kernel (internal/model/dspark.go:537-621). */
+#define DSPARK_MAX_LAYERS 64
+#define DSPARK_MAX_TAPS 8
+
+typedef struct dspark_model_desc {
+  int32_t hidden;          /* H (multiple of 256) */
+  int32_t ffn;             /* target FFN width I: w13 has 2 I rows (gate, up interleaved) */
+  int32_t vocab;           /* V (multiple of 16) */
+  int32_t n_layers;        /* target layers */
+  int32_t layer_kind[DSPARK_MAX_LAYERS]; /* 0 gated short conv, 1 full attention, 2 sliding attention */
+  int32_t q_heads, kv_heads, head_dim;   /* attention geometry (head_dim 64 or 128) */
+  int32_t conv_kernel;     /* short-conv taps (<= 8) */
+  int32_t window;          /* sliding-window length of kind-2 layers */
+  float rope_base;         /* RoPE base; rope_pairs rotating pairs per head (<= head_dim / 2) */
+  int32_t rope_pairs;
+  int32_t draft_layers;    /* drafter attention layers */
+  int32_t draft_ffn;       /* drafter FFN width */
+  int32_t block;           /* drafter block = max verified tokens per round (<= 64) */
+  int32_t max_drafts;      /* drafts per round (<= block - 1) */
+  int32_t crop_rows;       /* N rows of the cropped head (multiple of 16); row N is the confidence row */
+  int32_t markov_rank;     /* rank of the Markov head (multiple of 16) */
+  int32_t n_taps;          /* tapped target layers feeding the drafter */
+  int32_t tap_layer[DSPARK_MAX_TAPS];
+  int32_t draft_window;    /* drafter attention window over its context ring */
+  int32_t ring_positions;  /* drafter context ring (multiple of 32, > draft_window + block) */
+  int32_t mask_token;
+  float conf_bias, conf_thr;
+  float eps;               /* RMS-norm epsilon */
+} dspark_model_desc;
+
+typedef struct dspark_engine dspark_engine;
+
+/* Allocate weights (uninitialised) and runtime buffers for contexts up to max_context positions. */
+int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dspark_engine** out);
+void dspark_engine_destroy(dspark_engine* e);
+/* Random-initialise every weight on the device from `seed` (synthetic benchmarks; no host copy of the weights). */
+int dspark_engine_init_random(dspark_engine* e, uint64_t seed, dspark_stream_t stream);
+/* Device pointer and size of a named tensor -- weights ("embed", "head.w", "L3.mix.w", "D0.w13.s", ...), caches
+ * ("kv.L2.k", "ring.D1.v", "conv.L0") and runtime state ("state", "seen", "out_tokens", "logits", "base", ...); the
+ * full list is dspark_engine_tensor_name(e, i) for i < dspark_engine_tensor_count(e). */
+int dspark_engine_tensor(dspark_engine* e, const char* name, void** ptr, size_t* bytes);
+int dspark_engine_tensor_count(dspark_engine* e);
+const char* dspark_engine_tensor_name(dspark_engine* e, int32_t i);
+/* Enqueue one round on `stream`. force_m > 0 skips the drafter and verifies tokens[0..force_m) of the State as they
+ * are (the reference's force_m debug mode, dspark.hip:147, 2442-2451). The first call for a (force_m, plan) records
+ * the round as a HIP graph; later calls replay it. `plan_a` is the position the attention plan is tuned for (any
+ * run-time a is correct; the plan is re-recorded when plan_a moves to another 4096-position bucket). */
+int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream);
+
+/* draftLaunch: run rounds from the sequence's last token to the next 32-position block boundary (the State fields
+ * a, anchor, limit, budget, eos, stop_at are set from the arguments as internal/model/dspark.go:543-566 does), then
+ * copy the State and the emitted tokens back. Synchronous on `stream`. */
+typedef struct dspark_launch_args {
+  int32_t a;               /* position of the anchor (= len(tokens) - 1) */
+  int32_t anchor;          /* token at position a */
+  int32_t budget;          /* tokens this launch may emit (capped at 512) */
+  int32_t eos;             /* stop token or -1 */
+  float rep;               /* repetition penalty (1 = none) */
+  int32_t rounds;          /* rounds per launch (the reference uses 32) */
+  int32_t ctx_new, ctx_pos, ctx_lo;  /* drafter context bookkeeping carried between launches */
+  int32_t force_m;         /* > 0: verify-only rounds of the State's tokens (the tokens array below) */
+  int32_t tokens[DSPARK_MT_MAX];
+} dspark_launch_args;
+
+typedef struct dspark_launch_result {
+  int32_t count;           /* tokens emitted */
+  int32_t rounds, accepted, verified;
+  int32_t boundary;        /* the block boundary the launch ran to */
+  dspark_state state;      /* State after the launch */
+} dspark_launch_result;
+
+int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* args, int32_t* out_tokens, int32_t max_out,
+                         dspark_launch_result* result, dspark_stream_t stream);
+
 /* token id of an argmax key */
 static inline int32_t dspark_key_token(uint64_t key) { return (int32_t)(0xFFFFFFFFu - (uint32_t)key); }
 

@@ -20,6 +20,7 @@
 // float atomics), applies the optional sigmoid gate and stores fp16/fp32. Reference: dspark.hip:1070-1412
 // (attention_pass), 1488-2120 (attention_v2/v3), 2132-2185 (combine_phase); masks 975-978, 1308-1312, 2006-2012.
 #include "common.h"
+#include "dspark.h"
 #include "dspark_internal.h"
 
 namespace dspark {
@@ -135,8 +136,34 @@ __device__ __forceinline__ void tile_step(const AttnParams& p, const Tile<D>& tl
   }
 }
 
+// Page range, pages per split and unmasked range from a (the host plan evaluated with the State's a at run time).
+__device__ void attn_range(AttnParams& p) {
+  const int a = p.st->a;
+  p.a = a;
+  if (p.drafter) {
+    // drafter ring: context [max(ctx_lo, a - window), a) for every block token, block keys in both directions
+    p.start = max(p.st->ctx_lo, a - p.window);
+    p.window = 0;
+    p.causal = 0;
+  } else if (p.window > 0) {
+    p.start = max(0, a - p.window + 1);
+  }
+  const int lo0 = max(p.start, p.window > 0 ? a - p.window + 1 : 0);
+  const int lo_last = max(p.start, p.window > 0 ? a + p.M - p.window : 0);
+  const int hi_last = a + p.M - 1;
+  p.full_lo = lo_last;
+  p.full_hi = p.causal ? a : hi_last;
+  p.page0 = lo0 / PAGE;
+  p.npages = hi_last / PAGE - p.page0 + 1;
+  p.pps = (p.npages + p.S - 1) / p.S;
+}
+
 template <int D, int QB, int PF, int OCC, bool QLDS>
 __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
+  if (p.st) {
+    if (p.st->run == 0) return;
+    attn_range(p);
+  }
   constexpr int R = 16 * QB;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: page indices stay scalar
@@ -260,6 +287,7 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
 // One wave per output row (KV head h, row r = t*G + j); lanes over D. Splits merge in index order.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
+  if (p.st && p.st->run == 0) return;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rows = p.G * p.M;
   const int task = blockIdx.x * 4 + wave;

@@ -6,11 +6,17 @@
 #include <algorithm>
 #include <cmath>
 
+struct dspark_state;
+
 namespace dspark {
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
+constexpr int CONV_RING = 128;  // conv history positions kept per layer (>= max verify tokens + kernel - 1)
+
 struct AttnParams {
+  const struct ::dspark_state* st;  // when set: a (and the drafter's ctx_lo) come from the State at run time
+  int drafter;                      // with st: start = max(ctx_lo, a - window), no per-token window
   const _Float16* q;
   const _Float16* kp;
   const _Float16* vp;
@@ -30,12 +36,76 @@ struct AttnParams {
 };
 
 void attn_plan(AttnParams& p, int D, int cus);
+// The same plan evaluated on the device from the State's a: page range, pages per split, unmasked range.
+__device__ void attn_range(AttnParams& p);
+
+struct ResNormParams {
+  const struct ::dspark_state* st;
+  const float* h_old;           // [groups][M][H] or nullptr (zero)
+  const float* v;               // bands of [M][H], v_band_stride apart, or nullptr
+  int bands;
+  size_t v_band_stride;
+  const _Float16* post_w;       // [H] or nullptr (1)
+  const _Float16* norm_w;       // [groups][H]
+  size_t norm_w_stride;
+  int sandwich;
+  float eps;
+  float* dst;                   // h_new [groups][M][H] or nullptr
+  float* tap;                   // [M][H] or nullptr
+  _Float16* x16;                // [groups][M][x_row]
+  size_t group_stride, x_group_stride;
+  int x_row;
+  int H;
+};
+
+struct QkRopeParams {
+  const struct ::dspark_state* st;
+  const float* mix;             // per token: q [QH*D] | k [KVH*D] | v [KVH*D] | gate [QH]   (q absent when !q16)
+  int row;                      // floats per token row
+  int M, QH, KVH, D, rot;
+  const _Float16* q_norm;
+  const _Float16* k_norm;
+  const _Float16* rope;         // [positions][D]: cos | sin
+  float eps;
+  _Float16* q16;                // [M][QH][D] or nullptr (context projection: K/V only)
+  float* gate;                  // [M][QH] or nullptr
+  int gate_in_mix;
+  _Float16* kp;                 // K/V page pools and block table
+  _Float16* vp;
+  const int32_t* bt;
+  int pos_from_ctx, count_from_ctx;  // positions st->ctx_pos + t, tokens t < st->ctx_new (context projection)
+};
+
+struct MarkovParams {
+  struct ::dspark_state* st;
+  const float* base;            // [block][stride] crop-head outputs; column N is the confidence term
+  int stride, N, rank, block, max_drafts;
+  const int8_t* w2q;            // [N][rank]
+  const float* w2s;             // [N]
+  const int8_t* w1q;            // [vocab][rank]
+  const float* w1s;             // [vocab]
+  const float* c2;              // [vocab]
+  const int32_t* crop_ids;      // [N]
+  uint64_t* best;               // [block] argmax keys (cleared by round_begin)
+  float conf_bias, conf_thr;
+};
+
+int embed_launch(const void* embed, const struct ::dspark_state* st, int mode, int mask_token, int M, int H, int V, float* h,
+                 hipStream_t s);
+int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s);
+int conv_launch(const float* mix, const void* conv_w, void* ring, const struct ::dspark_state* st, int M, int H, int K,
+                void* y, hipStream_t s);
+int qkrope_launch(const QkRopeParams& p, hipStream_t s);
+int markov_launch(const MarkovParams& p, hipStream_t s);
+int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, hipStream_t s);
+int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);
 size_t attn_workspace_bytes(const AttnParams& p, int D);
 int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);  // phases: 1 split pass, 2 combine, 3 both
 int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt, int KVH,
                     int D, int pos0, int n, hipStream_t s);
 
 struct GemmParams {
+  const struct ::dspark_state* st;  // when set, a stopped round (run == 0) skips the launch's work
   const _Float16* x;        // [M][K]
   const void* w;            // [N][K] biased int8 or fp16
   const _Float16* scale;    // [N] or nullptr
@@ -52,12 +122,9 @@ size_t gemm_ws_bytes(int M, int N, int K);
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
 
 size_t verify_argmax_ws(int M, int V);
-}  // namespace dspark
 
-struct dspark_state;
-namespace dspark {
 int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32_t* seen, const dspark_state* st,
-                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s);
+                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev = nullptr);
 int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, uint32_t* seen,
                          hipStream_t s);
 

@@ -1,0 +1,743 @@
+// The DSpark engine: model + request buffers in device memory, one round as a fixed launch sequence recorded into a
+// HIP graph, and the draftLaunch protocol over it.
+//
+// Round (reference dspark_kernel sections, dspark.hip:2438-2919):
+//   begin      clear the round's argmax keys, mark the anchor seen
+//   context    last round's committed positions: tap norms -> fc (all taps in one K = taps*H GEMM) -> hidden norm
+//              -> ckv GEMM -> per drafter layer k norm + RoPE, K/V into the drafter ring        (sec 0, 2487-2518)
+//   drafter    embed [anchor, mask x (B-1)] -> layers (norm, q|k|v, RoPE + ring write, block attention over the
+//              ring, out, norm, gated FFN) -> final norm -> cropped head into `base`            (sec 1)
+//   drafts     Markov/confidence steps (markov_kernel x (B-1), finalize)                        (2633-2664)
+//   verify     embed tokens -> target layers (sandwich norms, mix GEMM, gated conv | q/k norm + RoPE + K/V append +
+//              verify attention + gated combine, out GEMM, gated FFN) -> final norm -> LM head -> penalised argmax
+//   commit     acceptance + books; K/V of the accepted positions are already in the pages          (2848-2913)
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "dspark.h"
+#include "dspark_internal.h"
+
+using namespace dspark;
+
+namespace {
+
+struct Tensor {
+  void* ptr;
+  size_t bytes;
+};
+
+struct LayerW {
+  int kind = 0;  // 0 conv, 1 full attention, 2 sliding attention, 3 drafter attention
+  _Float16 *op_norm = nullptr, *ffn_norm = nullptr, *post_op_norm = nullptr, *post_ffn_norm = nullptr;
+  uint8_t* mix_w = nullptr;
+  _Float16* mix_s = nullptr;
+  int mix_rows = 0;
+  uint8_t *out_w = nullptr, *w13_w = nullptr, *w2_w = nullptr;
+  _Float16 *out_s = nullptr, *w13_s = nullptr, *w2_s = nullptr;
+  int ffn = 0;
+  _Float16 *conv_w = nullptr, *conv_ring = nullptr;
+  _Float16 *q_norm = nullptr, *k_norm = nullptr;
+  _Float16 *kv_k = nullptr, *kv_v = nullptr;
+  int64_t kv_pages = 0;
+  const int32_t* bt = nullptr;  // drafter ring table (target layers: identity)
+  int tap_slot = -1;
+};
+
+int align16(int x) { return (x + 15) / 16 * 16; }
+
+constexpr int ROUND_PLAN_BUCKET = 4096;
+
+}  // namespace
+
+struct dspark_engine {
+  dspark_model_desc d;
+  int max_context = 0, B = 0;
+  std::vector<std::string> names;
+  std::map<std::string, Tensor> tensors;
+  std::vector<LayerW> L, DL;
+  _Float16 *embed = nullptr, *final_norm = nullptr, *draft_norm = nullptr, *tap_norms = nullptr, *hidden_norm = nullptr;
+  uint8_t *head_w = nullptr, *crop_w = nullptr, *fc_w = nullptr, *ckv_w = nullptr;
+  _Float16 *head_s = nullptr, *crop_s = nullptr, *fc_s = nullptr, *ckv_s = nullptr;
+  int32_t* crop_ids = nullptr;
+  int8_t *w2q = nullptr, *w1q = nullptr;
+  float *w2s = nullptr, *w1s = nullptr, *c2 = nullptr;
+  _Float16* rope = nullptr;
+  int32_t* ring_bt = nullptr;
+  int ring_pages = 0;
+  int64_t kv_pages = 0;
+  // request state
+  dspark_state* st = nullptr;
+  uint32_t* seen = nullptr;
+  int32_t* out_tokens = nullptr;
+  float* rep = nullptr;  // [2]: rep, 1/rep
+  // activations
+  float *h[2] = {nullptr, nullptr}, *mix = nullptr, *vout = nullptr, *w2out = nullptr, *ctxv = nullptr, *ckvout = nullptr,
+        *taps = nullptr, *logits = nullptr, *base = nullptr, *gate = nullptr;
+  _Float16 *x16 = nullptr, *q16 = nullptr, *y16 = nullptr, *a16 = nullptr;
+  uint64_t* keys = nullptr;  // [B] verify best, then [B] Markov best
+  void* ws_attn = nullptr;
+  size_t ws_attn_bytes = 0;
+  void* ws_gemm = nullptr;
+  size_t ws_gemm_bytes = 0;
+  void* ws_argmax = nullptr;
+  size_t ws_argmax_bytes = 0;
+  int x_cols = 0, mix_cols = 0, crop_n = 0;
+  int cus = 256;
+  dspark_state host_st;  // launch-time uploads stay alive until the stream has consumed them
+  float host_rep[2] = {1.f, 1.f};
+  // recorded rounds: key (force_m, plan bucket) -> graph
+  std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  std::vector<void*> allocs;
+
+  ~dspark_engine() {
+    for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
+    for (void* p : allocs) (void)hipFree(p);
+  }
+
+  void* alloc(const std::string& name, size_t bytes, int* err) {
+    if (*err) return nullptr;
+    void* p = nullptr;
+    const size_t nb = bytes ? bytes : 16;
+    if (hipMalloc(&p, nb) != hipSuccess || hipMemset(p, 0, nb) != hipSuccess) {
+      *err = DSPARK_ENOSPACE;
+      return nullptr;
+    }
+    allocs.push_back(p);
+    if (!name.empty()) {
+      names.push_back(name);
+      tensors[name] = Tensor{p, nb};
+    }
+    return p;
+  }
+};
+
+namespace {
+
+// ---------------------------------------------------------------- random init (synthetic benchmarks)
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+// kind 0: biased int8 (q + 128), q uniform in [-127, 127]; 1: fp16 uniform [a, b); 2: fp16 N(a, b^2);
+// 3: fp32 uniform [a, b); 4: signed int8 uniform [-127, 127]; 5: fp16 per-row GEMM scale u / sqrt(K) with u uniform
+// in [a, b) (b holds K).
+__global__ void rand_fill_kernel(void* dst, size_t n, int kind, float a, float b, uint64_t seed) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const uint64_t r = mix64(seed ^ mix64(i));
+    const float u = (float)(r >> 40) * (1.f / 16777216.f);
+    switch (kind) {
+      case 0: reinterpret_cast<uint8_t*>(dst)[i] = (uint8_t)((int)(r % 255u) - 127 + 128); break;
+      case 1: reinterpret_cast<_Float16*>(dst)[i] = (_Float16)(a + (b - a) * u); break;
+      case 2: {
+        const float u2 = (float)((r >> 16) & 0xffffff) * (1.f / 16777216.f);
+        const float z = sqrtf(-2.f * logf(fmaxf(u, 1e-7f))) * cosf(6.2831853f * u2);
+        reinterpret_cast<_Float16*>(dst)[i] = (_Float16)(a + b * z);
+        break;
+      }
+      case 3: reinterpret_cast<float*>(dst)[i] = a + (b - a) * u; break;
+      case 4: reinterpret_cast<int8_t*>(dst)[i] = (int8_t)((int)(r % 255u) - 127); break;
+      default: reinterpret_cast<_Float16*>(dst)[i] = (_Float16)((0.75f + 0.5f * u) * a / sqrtf(b)); break;
+    }
+  }
+}
+
+int rand_fill(void* dst, size_t n, int kind, float a, float b, uint64_t seed, hipStream_t s) {
+  if (!n) return 0;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(rand_fill_kernel, dim3(blocks), dim3(256), 0, s, dst, n, kind, a, b, seed);
+  return (int)hipGetLastError();
+}
+
+// crop_ids[r] = (r * 40503 + 7) mod V: distinct for odd multipliers coprime to V (V a multiple of 16 and not of 40503).
+__global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r < n) ids[r] = (int32_t)(((int64_t)r * 40503 + 7) % V);
+}
+
+int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
+         float* y32, _Float16* y16, hipStream_t st) {
+  GemmParams p = {};
+  p.st = e->st;
+  p.x = x;
+  p.w = w;
+  p.scale = s;
+  p.y32 = epilogue == 0 ? y32 : nullptr;
+  p.y16 = y16;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.epilogue = epilogue;
+  p.ksplit = gemm_choose_ksplit(N, K, 512);
+  if (p.ksplit > 1) {
+    if (gemm_ws_bytes(M, N, K) > e->ws_gemm_bytes) return DSPARK_ENOSPACE;
+    p.part = static_cast<float*>(e->ws_gemm);
+  }
+  return gemm_launch(p, true, st);
+}
+
+// Residual + RMS norm of the B block rows.
+int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, const _Float16* post_w,
+            const _Float16* norm_w, int sandwich, float* dst, float* tap, hipStream_t s) {
+  ResNormParams p = {};
+  p.st = e->st;
+  p.h_old = h_old;
+  p.v = v;
+  p.bands = bands;
+  p.v_band_stride = (size_t)e->B * e->d.hidden;
+  p.post_w = post_w;
+  p.norm_w = norm_w;
+  p.sandwich = sandwich;
+  p.eps = e->d.eps;
+  p.dst = dst;
+  p.tap = tap;
+  p.x16 = e->x16;
+  p.x_row = e->d.hidden;
+  p.H = e->d.hidden;
+  return resnorm_launch(p, e->B, 1, s);
+}
+
+int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const float* gate, hipStream_t s) {
+  const dspark_model_desc& d = e->d;
+  AttnParams p = {};
+  p.st = e->st;
+  p.drafter = drafter;
+  p.q = e->q16;
+  p.kp = Lw.kv_k;
+  p.vp = Lw.kv_v;
+  p.bt = Lw.bt;
+  p.k_bytes = p.v_bytes = (uint32_t)(Lw.kv_pages * d.kv_heads * PAGE * d.head_dim * 2);
+  p.out16 = e->y16;
+  p.gate = gate;
+  p.M = e->B;
+  p.QH = d.q_heads;
+  p.KVH = d.kv_heads;
+  p.G = d.q_heads / d.kv_heads;
+  p.a = plan_a;
+  p.causal = drafter ? 0 : 1;
+  if (drafter) {
+    p.window = d.draft_window;
+    p.start = std::max(0, plan_a - d.draft_window);
+  } else if (Lw.kind == 2) {
+    p.window = d.window;
+    p.start = std::max(0, plan_a - d.window + 1);
+  }
+  p.S = 0;
+  attn_plan(p, d.head_dim, e->cus);
+  if (drafter) p.window = d.draft_window;  // attn_range (device) derives start and drops the per-token window
+  const size_t slots = (size_t)p.KVH * p.RG * p.S;
+  const size_t acc_bytes = (slots * p.R * d.head_dim * sizeof(float) + 255) / 256 * 256;
+  if (acc_bytes + slots * p.R * sizeof(f32x2_t) > e->ws_attn_bytes) return DSPARK_ENOSPACE;
+  p.part_acc = static_cast<float*>(e->ws_attn);
+  p.part_ml = reinterpret_cast<f32x2_t*>(static_cast<char*>(e->ws_attn) + acc_bytes);
+  return attn_launch(p, d.head_dim, 3, s);
+}
+
+int qkrope(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode, hipStream_t s) {
+  const dspark_model_desc& d = e->d;
+  QkRopeParams p = {};
+  p.st = e->st;
+  p.mix = mix;
+  p.row = row;
+  p.M = e->B;
+  p.QH = d.q_heads;
+  p.KVH = d.kv_heads;
+  p.D = d.head_dim;
+  p.rot = d.rope_pairs;
+  p.q_norm = Lw.q_norm;
+  p.k_norm = Lw.k_norm;
+  p.rope = e->rope;
+  p.eps = d.eps;
+  p.q16 = with_q ? e->q16 : nullptr;
+  p.gate = (with_q && Lw.kind != 3) ? e->gate : nullptr;
+  p.gate_in_mix = p.gate ? 1 : 0;
+  p.kp = Lw.kv_k;
+  p.vp = Lw.kv_v;
+  p.bt = Lw.bt;
+  p.pos_from_ctx = ctx_mode;
+  p.count_from_ctx = ctx_mode;
+  return qkrope_launch(p, s);
+}
+
+#define CK(x)                \
+  do {                       \
+    int _rc = (x);           \
+    if (_rc) return _rc;     \
+  } while (0)
+
+// The round's launch sequence (see the file header).
+int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
+  const dspark_model_desc& d = e->d;
+  const int B = e->B, H = d.hidden;
+  uint64_t* vbest = e->keys;
+  uint64_t* mbest = e->keys + B;
+  CK(round_begin_launch(e->st, e->keys, 2 * B, e->seen, s));
+  if (force_m > 0) {
+    CK(force_m_launch(e->st, force_m, s));
+  } else {
+    // ---- context projection of the last round's committed positions (skipped rows: t >= ctx_new)
+    {
+      ResNormParams p = {};
+      p.st = e->st;
+      p.h_old = e->taps;
+      p.group_stride = (size_t)B * H;
+      p.norm_w = e->tap_norms;
+      p.norm_w_stride = H;
+      p.eps = d.eps;
+      p.x16 = e->x16;
+      p.x_row = d.n_taps * H;
+      p.x_group_stride = H;
+      p.H = H;
+      CK(resnorm_launch(p, B, d.n_taps, s));
+    }
+    CK(gemm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s));
+    CK(resnorm(e, nullptr, e->ctxv, 1, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
+    const int kvrow = 2 * d.kv_heads * d.head_dim;
+    CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
+    for (int j = 0; j < d.draft_layers; ++j)
+      CK(qkrope(e, e->DL[j], e->ckvout + (size_t)j * kvrow, d.draft_layers * kvrow, false, true, s));
+    // ---- drafter block
+    CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
+    int cur = 0;
+    for (int j = 0; j < d.draft_layers; ++j) {
+      const LayerW& W = e->DL[j];
+      CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, j ? 1 : 0, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
+      cur ^= 1;
+      CK(gemm(e, e->x16, B, H, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s));
+      CK(qkrope(e, W, e->mix, W.mix_rows, true, false, s));
+      CK(attention(e, W, 1, plan_a, nullptr, s));
+      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
+      CK(resnorm(e, e->h[cur], e->vout, 1, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
+      cur ^= 1;
+      CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
+      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
+    }
+    CK(resnorm(e, e->h[cur], e->w2out, 1, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
+    CK(gemm(e, e->x16, B, H, e->crop_w, e->crop_s, e->crop_n, 0, e->base, nullptr, s));
+    MarkovParams mp = {};
+    mp.st = e->st;
+    mp.base = e->base;
+    mp.stride = e->crop_n;
+    mp.N = d.crop_rows;
+    mp.rank = d.markov_rank;
+    mp.block = B;
+    mp.max_drafts = d.max_drafts;
+    mp.w2q = e->w2q;
+    mp.w2s = e->w2s;
+    mp.w1q = e->w1q;
+    mp.w1s = e->w1s;
+    mp.c2 = e->c2;
+    mp.crop_ids = e->crop_ids;
+    mp.best = mbest;
+    mp.conf_bias = d.conf_bias;
+    mp.conf_thr = d.conf_thr;
+    CK(markov_launch(mp, s));
+  }
+  // ---- verify
+  CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
+  int cur = 0;
+  for (int i = 0; i < d.n_layers; ++i) {
+    const LayerW& W = e->L[i];
+    const LayerW* P = i ? &e->L[i - 1] : nullptr;
+    float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
+    CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, i ? 1 : 0, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
+               e->h[cur ^ 1], tap, s));
+    cur ^= 1;
+    CK(gemm(e, e->x16, B, H, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s));
+    if (W.kind == 0) {
+      CK(conv_launch(e->mix, W.conv_w, W.conv_ring, e->st, B, H, d.conv_kernel, e->y16, s));
+    } else {
+      CK(qkrope(e, W, e->mix, W.mix_rows, true, false, s));
+      CK(attention(e, W, 0, plan_a, e->gate, s));
+    }
+    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
+    CK(resnorm(e, e->h[cur], e->vout, 1, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
+    cur ^= 1;
+    CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
+    CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
+  }
+  {
+    const LayerW& P = e->L[d.n_layers - 1];
+    float* tap = P.tap_slot >= 0 ? e->taps + (size_t)P.tap_slot * B * H : nullptr;
+    CK(resnorm(e, e->h[cur], e->w2out, 1, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
+  }
+  CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
+  CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep));
+  CK(accept_commit_launch(e->st, vbest, 0, 0, e->out_tokens, e->seen, s));
+  return 0;
+}
+
+bool desc_ok(const dspark_model_desc* d, int max_context) {
+  if (!d || d->hidden < 256 || d->hidden % 256 || d->hidden > 8192) return false;
+  if (d->ffn < 64 || d->ffn % 64 || d->draft_ffn < 64 || d->draft_ffn % 64) return false;
+  if (d->vocab < 16 || d->vocab % 16) return false;
+  if (d->n_layers < 1 || d->n_layers > DSPARK_MAX_LAYERS) return false;
+  if (d->head_dim != 64 && d->head_dim != 128) return false;
+  if (d->kv_heads < 1 || d->q_heads % d->kv_heads || d->q_heads * d->head_dim != d->hidden) return false;
+  if (d->conv_kernel < 1 || d->conv_kernel > 8) return false;
+  if (d->rope_pairs < 0 || d->rope_pairs > d->head_dim / 2) return false;
+  if (d->draft_layers < 1 || d->block < 2 || d->block > 64 || d->max_drafts < 0 || d->max_drafts > d->block - 1) return false;
+  if (d->crop_rows < 16 || d->crop_rows % 16 || d->markov_rank < 16 || d->markov_rank % 16) return false;
+  if (d->crop_rows > d->vocab) return false;
+  if (d->n_taps < 1 || d->n_taps > DSPARK_MAX_TAPS) return false;
+  for (int i = 0; i < d->n_taps; ++i)
+    if (d->tap_layer[i] < 0 || d->tap_layer[i] >= d->n_layers) return false;
+  if (d->ring_positions % PAGE || d->ring_positions < d->draft_window + d->block + PAGE) return false;
+  if (d->mask_token < 0 || d->mask_token >= d->vocab) return false;
+  if (max_context < d->block || max_context > (1 << 24)) return false;
+  int n_attn = 0;
+  for (int i = 0; i < d->n_layers; ++i) {
+    if (d->layer_kind[i] < 0 || d->layer_kind[i] > 2) return false;
+    n_attn += d->layer_kind[i] != 0;
+  }
+  (void)n_attn;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dspark_engine** out) {
+  if (!out || !desc_ok(desc, max_context)) return DSPARK_EINVAL;
+  dspark_engine* e = new dspark_engine();
+  e->d = *desc;
+  const dspark_model_desc& d = e->d;
+  e->max_context = max_context;
+  e->B = d.block;
+  const int B = e->B, H = d.hidden, D = d.head_dim, QH = d.q_heads, KVH = d.kv_heads;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) e->cus = n;
+  }
+  int err = 0;
+  auto h16 = [&](const std::string& n, size_t count) { return static_cast<_Float16*>(e->alloc(n, count * 2, &err)); };
+  auto u8 = [&](const std::string& n, size_t count) { return static_cast<uint8_t*>(e->alloc(n, count, &err)); };
+  const int64_t positions = (int64_t)max_context + B;
+  e->kv_pages = (positions + PAGE - 1) / PAGE + 1;
+  e->ring_pages = d.ring_positions / PAGE;
+  e->embed = h16("embed", (size_t)d.vocab * H);
+  e->final_norm = h16("final_norm", H);
+  e->head_w = u8("head.w", (size_t)d.vocab * H);
+  e->head_s = h16("head.s", d.vocab);
+  int tap_slot[DSPARK_MAX_LAYERS];
+  for (int i = 0; i < DSPARK_MAX_LAYERS; ++i) tap_slot[i] = -1;
+  for (int i = 0; i < d.n_taps; ++i) tap_slot[d.tap_layer[i]] = i;
+  e->L.resize(d.n_layers);
+  for (int i = 0; i < d.n_layers; ++i) {
+    LayerW& W = e->L[i];
+    const std::string pre = "L" + std::to_string(i) + ".";
+    W.kind = d.layer_kind[i];
+    W.tap_slot = tap_slot[i];
+    W.op_norm = h16(pre + "op_norm", H);
+    W.ffn_norm = h16(pre + "ffn_norm", H);
+    W.post_op_norm = h16(pre + "post_op_norm", H);
+    W.post_ffn_norm = h16(pre + "post_ffn_norm", H);
+    W.mix_rows = W.kind == 0 ? 3 * H : align16(QH * D + 2 * KVH * D + QH);
+    W.mix_w = u8(pre + "mix.w", (size_t)W.mix_rows * H);
+    W.mix_s = h16(pre + "mix.s", W.mix_rows);
+    W.out_w = u8(pre + "out.w", (size_t)H * H);
+    W.out_s = h16(pre + "out.s", H);
+    W.ffn = d.ffn;
+    W.w13_w = u8(pre + "w13.w", (size_t)2 * d.ffn * H);
+    W.w13_s = h16(pre + "w13.s", 2 * d.ffn);
+    W.w2_w = u8(pre + "w2.w", (size_t)H * d.ffn);
+    W.w2_s = h16(pre + "w2.s", H);
+    if (W.kind == 0) {
+      W.conv_w = h16(pre + "conv.w", (size_t)H * d.conv_kernel);
+      W.conv_ring = h16("conv.L" + std::to_string(i), (size_t)CONV_RING * H);
+    } else {
+      W.q_norm = h16(pre + "q_norm", D);
+      W.k_norm = h16(pre + "k_norm", D);
+      W.kv_pages = e->kv_pages;
+      W.kv_k = h16("kv.L" + std::to_string(i) + ".k", (size_t)e->kv_pages * KVH * PAGE * D);
+      W.kv_v = h16("kv.L" + std::to_string(i) + ".v", (size_t)e->kv_pages * KVH * PAGE * D);
+    }
+  }
+  const int64_t bt_entries = (positions + PAGE - 1) / PAGE + 1;
+  e->ring_bt = static_cast<int32_t*>(e->alloc("ring_table", bt_entries * 4, &err));
+  e->DL.resize(d.draft_layers);
+  for (int j = 0; j < d.draft_layers; ++j) {
+    LayerW& W = e->DL[j];
+    const std::string pre = "D" + std::to_string(j) + ".";
+    W.kind = 3;
+    W.op_norm = h16(pre + "op_norm", H);
+    W.ffn_norm = h16(pre + "ffn_norm", H);
+    W.mix_rows = align16(QH * D + 2 * KVH * D);
+    W.mix_w = u8(pre + "mix.w", (size_t)W.mix_rows * H);
+    W.mix_s = h16(pre + "mix.s", W.mix_rows);
+    W.out_w = u8(pre + "out.w", (size_t)H * H);
+    W.out_s = h16(pre + "out.s", H);
+    W.ffn = d.draft_ffn;
+    W.w13_w = u8(pre + "w13.w", (size_t)2 * d.draft_ffn * H);
+    W.w13_s = h16(pre + "w13.s", 2 * d.draft_ffn);
+    W.w2_w = u8(pre + "w2.w", (size_t)H * d.draft_ffn);
+    W.w2_s = h16(pre + "w2.s", H);
+    W.q_norm = h16(pre + "q_norm", D);
+    W.k_norm = h16(pre + "k_norm", D);
+    W.kv_pages = e->ring_pages;
+    W.kv_k = h16("ring.D" + std::to_string(j) + ".k", (size_t)e->ring_pages * KVH * PAGE * D);
+    W.kv_v = h16("ring.D" + std::to_string(j) + ".v", (size_t)e->ring_pages * KVH * PAGE * D);
+    W.bt = e->ring_bt;
+  }
+  e->draft_norm = h16("draft_norm", H);
+  e->crop_n = align16(d.crop_rows + 1);
+  e->crop_w = u8("crop.w", (size_t)e->crop_n * H);
+  e->crop_s = h16("crop.s", e->crop_n);
+  e->crop_ids = static_cast<int32_t*>(e->alloc("crop_ids", (size_t)d.crop_rows * 4, &err));
+  e->w2q = static_cast<int8_t*>(e->alloc("markov.w2q", (size_t)d.crop_rows * d.markov_rank, &err));
+  e->w2s = static_cast<float*>(e->alloc("markov.w2s", (size_t)d.crop_rows * 4, &err));
+  e->w1q = static_cast<int8_t*>(e->alloc("markov.w1q", (size_t)d.vocab * d.markov_rank, &err));
+  e->w1s = static_cast<float*>(e->alloc("markov.w1s", (size_t)d.vocab * 4, &err));
+  e->c2 = static_cast<float*>(e->alloc("conf_c2", (size_t)d.vocab * 4, &err));
+  e->tap_norms = h16("tap_norms", (size_t)d.n_taps * H);
+  e->fc_w = u8("fc.w", (size_t)H * d.n_taps * H);
+  e->fc_s = h16("fc.s", H);
+  e->hidden_norm = h16("hidden_norm", H);
+  const int ckv_rows = d.draft_layers * 2 * KVH * D;
+  e->ckv_w = u8("ckv.w", (size_t)ckv_rows * H);
+  e->ckv_s = h16("ckv.s", ckv_rows);
+  e->rope = h16("rope", (size_t)(positions + 1) * D);
+  // request state and activations
+  e->st = static_cast<dspark_state*>(e->alloc("state", sizeof(dspark_state), &err));
+  e->seen = static_cast<uint32_t*>(e->alloc("seen", (size_t)(d.vocab + 31) / 32 * 4, &err));
+  e->out_tokens = static_cast<int32_t*>(e->alloc("out_tokens", (size_t)(1024 + 2 * B) * 4, &err));
+  e->rep = static_cast<float*>(e->alloc("rep", 16, &err));
+  e->x_cols = std::max(std::max(H, d.n_taps * H), std::max(d.ffn, d.draft_ffn));
+  e->mix_cols = std::max(std::max(3 * H, align16(QH * D + 2 * KVH * D + QH)), ckv_rows);
+  e->h[0] = static_cast<float*>(e->alloc("h0", (size_t)B * H * 4, &err));
+  e->h[1] = static_cast<float*>(e->alloc("h1", (size_t)B * H * 4, &err));
+  e->x16 = h16("x16", (size_t)B * e->x_cols);
+  e->mix = static_cast<float*>(e->alloc("mix", (size_t)B * e->mix_cols * 4, &err));
+  e->q16 = h16("q16", (size_t)B * QH * D);
+  e->gate = static_cast<float*>(e->alloc("gate", (size_t)B * QH * 4, &err));
+  e->y16 = h16("y16", (size_t)B * H);
+  e->vout = static_cast<float*>(e->alloc("vout", (size_t)B * H * 4, &err));
+  e->a16 = h16("a16", (size_t)B * std::max(d.ffn, d.draft_ffn));
+  e->w2out = static_cast<float*>(e->alloc("w2out", (size_t)B * H * 4, &err));
+  e->ctxv = static_cast<float*>(e->alloc("ctx", (size_t)B * H * 4, &err));
+  e->ckvout = static_cast<float*>(e->alloc("ckv_out", (size_t)B * ckv_rows * 4, &err));
+  e->taps = static_cast<float*>(e->alloc("taps", (size_t)d.n_taps * B * H * 4, &err));
+  e->logits = static_cast<float*>(e->alloc("logits", (size_t)B * d.vocab * 4, &err));
+  e->base = static_cast<float*>(e->alloc("base", (size_t)B * e->crop_n * 4, &err));
+  e->keys = static_cast<uint64_t*>(e->alloc("keys", (size_t)2 * B * 8, &err));
+  // workspaces: the largest split-K partials, attention partials (<= 64 splits x all rows), argmax chunks
+  size_t gws = 0;
+  const int Ks[] = {H, d.n_taps * H, d.ffn, d.draft_ffn};
+  const int Ns[] = {H, 3 * H, 2 * d.ffn, 2 * d.draft_ffn, d.vocab, e->crop_n, ckv_rows, align16(QH * D + 2 * KVH * D + QH)};
+  for (int K : Ks)
+    for (int N : Ns) gws = std::max(gws, gemm_ws_bytes(B, N, K));
+  e->ws_gemm_bytes = gws + 256;
+  e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
+  const int G = QH / KVH;
+  const size_t rows_pad = (size_t)(G * B + 16 * 8);
+  e->ws_attn_bytes = (size_t)KVH * 64 * rows_pad * (D * 4 + 8) + 1024;
+  e->ws_attn = e->alloc("ws_attn", e->ws_attn_bytes, &err);
+  e->ws_argmax_bytes = verify_argmax_ws(B, d.vocab);
+  e->ws_argmax = e->alloc("ws_argmax", e->ws_argmax_bytes, &err);
+  if (err) {
+    delete e;
+    return err;
+  }
+  // drafter ring table (logical page -> ring page) and the RoPE table (cos | sin per position, fp32 frequencies
+  // rounded to fp16, as internal/model/engine.go:428-461 builds it)
+  std::vector<int32_t> bt(bt_entries);
+  for (int64_t i = 0; i < bt_entries; ++i) bt[i] = (int32_t)(i % e->ring_pages);
+  std::vector<_Float16> rope((size_t)(positions + 1) * D);
+  std::vector<float> inv(D / 2, 0.f);
+  for (int i = 0; i < d.rope_pairs; ++i) inv[i] = (float)(1.0 / std::pow((double)d.rope_base, (double)(2.f * i / D)));
+  for (int64_t pos = 0; pos <= positions; ++pos)
+    for (int i = 0; i < D / 2; ++i) {
+      const double f = (double)((float)pos * inv[i]);
+      rope[(size_t)pos * D + i] = (_Float16)(float)std::cos(f);
+      rope[(size_t)pos * D + D / 2 + i] = (_Float16)(float)std::sin(f);
+    }
+  const float rep[4] = {1.f, 1.f, 0.f, 0.f};
+  if (hipMemcpy(e->ring_bt, bt.data(), bt.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(e->rope, rope.data(), rope.size() * 2, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(e->rep, rep, sizeof(rep), hipMemcpyHostToDevice) != hipSuccess) {
+    delete e;
+    return DSPARK_ENOSPACE;
+  }
+  *out = e;
+  return 0;
+}
+
+void dspark_engine_destroy(dspark_engine* e) { delete e; }
+
+int dspark_engine_tensor(dspark_engine* e, const char* name, void** ptr, size_t* bytes) {
+  if (!e || !name) return DSPARK_EINVAL;
+  auto it = e->tensors.find(name);
+  if (it == e->tensors.end()) return DSPARK_EINVAL;
+  if (ptr) *ptr = it->second.ptr;
+  if (bytes) *bytes = it->second.bytes;
+  return 0;
+}
+
+int dspark_engine_tensor_count(dspark_engine* e) { return e ? (int)e->names.size() : 0; }
+
+const char* dspark_engine_tensor_name(dspark_engine* e, int32_t i) {
+  if (!e || i < 0 || i >= (int)e->names.size()) return nullptr;
+  return e->names[i].c_str();
+}
+
+int dspark_engine_init_random(dspark_engine* e, uint64_t seed, dspark_stream_t stream) {
+  if (!e) return DSPARK_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dspark_model_desc& d = e->d;
+  const int H = d.hidden;
+  uint64_t k = seed * 1000003ull;
+  int rc = 0;
+  auto fill = [&](const std::string& name, int kind, float a, float b) {
+    if (rc) return;
+    auto it = e->tensors.find(name);
+    if (it == e->tensors.end()) {
+      rc = DSPARK_EINVAL;
+      return;
+    }
+    const size_t n = kind == 0 || kind == 4 ? it->second.bytes : (kind == 3 ? it->second.bytes / 4 : it->second.bytes / 2);
+    rc = rand_fill(it->second.ptr, n, kind, a, b, ++k, s);
+  };
+  // one fp16 scale per output row: |y| ~ |x| for inputs of unit RMS (int8 uniform has std 73.3)
+  auto gemm_w = [&](const std::string& pre, int K) {
+    fill(pre + ".w", 0, 0.f, 0.f);
+    fill(pre + ".s", 5, 1.f / 73.3f, (float)K);
+  };
+  fill("embed", 2, 0.f, 1.f);
+  fill("final_norm", 1, 0.8f, 1.2f);
+  gemm_w("head", H);
+  for (int i = 0; i < d.n_layers; ++i) {
+    const std::string pre = "L" + std::to_string(i) + ".";
+    for (const char* n : {"op_norm", "ffn_norm", "post_op_norm", "post_ffn_norm"}) fill(pre + n, 1, 0.8f, 1.2f);
+    gemm_w(pre + "mix", H);
+    gemm_w(pre + "out", H);
+    gemm_w(pre + "w13", H);
+    gemm_w(pre + "w2", d.ffn);
+    if (d.layer_kind[i] == 0) {
+      fill(pre + "conv.w", 2, 0.f, 1.f / std::sqrt((float)d.conv_kernel));
+    } else {
+      fill(pre + "q_norm", 1, 0.8f, 1.2f);
+      fill(pre + "k_norm", 1, 0.8f, 1.2f);
+    }
+  }
+  for (int j = 0; j < d.draft_layers; ++j) {
+    const std::string pre = "D" + std::to_string(j) + ".";
+    fill(pre + "op_norm", 1, 0.8f, 1.2f);
+    fill(pre + "ffn_norm", 1, 0.8f, 1.2f);
+    gemm_w(pre + "mix", H);
+    gemm_w(pre + "out", H);
+    gemm_w(pre + "w13", H);
+    gemm_w(pre + "w2", d.draft_ffn);
+    fill(pre + "q_norm", 1, 0.8f, 1.2f);
+    fill(pre + "k_norm", 1, 0.8f, 1.2f);
+  }
+  fill("draft_norm", 1, 0.8f, 1.2f);
+  gemm_w("crop", H);
+  fill("markov.w2q", 4, 0.f, 0.f);
+  fill("markov.w2s", 3, 0.5f / (73.3f * 16.f), 1.5f / (73.3f * 16.f));
+  fill("markov.w1q", 4, 0.f, 0.f);
+  fill("markov.w1s", 3, 1.f / 73.3f, 1.f / 73.3f);
+  fill("conf_c2", 3, -0.1f, 0.1f);
+  fill("tap_norms", 1, 0.8f, 1.2f);
+  gemm_w("fc", d.n_taps * H);
+  fill("hidden_norm", 1, 0.8f, 1.2f);
+  gemm_w("ckv", H);
+  if (rc) return rc;
+  hipLaunchKernelGGL(crop_ids_kernel, dim3((d.crop_rows + 255) / 256), dim3(256), 0, s, e->crop_ids, d.crop_rows, d.vocab);
+  return (int)hipGetLastError();
+}
+
+int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream) {
+  if (!e || force_m < 0 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int bucket = plan_a / ROUND_PLAN_BUCKET;
+  const auto key = std::make_pair((int)force_m, bucket);
+  auto it = e->graphs.find(key);
+  if (it == e->graphs.end()) {
+    // Record the round on a private stream (capture needs a non-default stream), then replay it on `stream`.
+    hipStream_t cap;
+    if (hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return DSPARK_ENOSPACE;
+    hipGraph_t g = nullptr;
+    int rc = (int)hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal);
+    if (!rc) {
+      const int plan = bucket * ROUND_PLAN_BUCKET + ROUND_PLAN_BUCKET / 2;
+      rc = enqueue_round(e, force_m, plan, cap);
+      const int rc2 = (int)hipStreamEndCapture(cap, &g);
+      if (!rc) rc = rc2;
+    }
+    hipGraphExec_t ex = nullptr;
+    if (!rc) rc = (int)hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(cap);
+    if (rc) return rc;
+    it = e->graphs.emplace(key, ex).first;
+  }
+  return (int)hipGraphLaunch(it->second, s);
+}
+
+int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t* out_tokens, int32_t max_out,
+                         dspark_launch_result* res, dspark_stream_t stream) {
+  if (!e || !a || !res || a->a < 0 || a->rounds < 1 || a->force_m < 0 || a->force_m > e->B) return DSPARK_EINVAL;
+  if (a->anchor < 0 || a->anchor >= e->d.vocab || a->budget < 1) return DSPARK_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int block_tokens = 32;  // the prefix cache's block (internal/model/engine.go:30)
+  const int stop = std::min((a->a / block_tokens + 1) * block_tokens, e->max_context);
+  const int limit = std::min(stop + e->B, e->max_context);
+  if (a->a + e->B > e->max_context) return DSPARK_EINVAL;
+  dspark_state& st = e->host_st;
+  st = dspark_state{};
+  st.a = a->a;
+  st.anchor = a->anchor;
+  st.rounds_left = a->rounds;
+  st.limit = limit;
+  st.budget = std::min(a->budget, 512);
+  st.eos = a->eos;
+  st.ctx_new = a->ctx_new;
+  st.ctx_pos = a->ctx_pos;
+  st.ctx_lo = a->ctx_lo;
+  st.run = 1;
+  st.force_m = a->force_m;
+  st.skip_rounds = 1;
+  st.stop_at = stop;
+  st.ckpt_slot = -1;
+  std::memcpy(st.tokens, a->tokens, sizeof(st.tokens));
+  st.tokens[0] = a->anchor;
+  const float rep = a->rep == 0.f ? 1.f : a->rep;
+  e->host_rep[0] = rep;
+  e->host_rep[1] = 1.f / rep;
+  if (hipMemcpyAsync(e->st, &st, sizeof(st), hipMemcpyHostToDevice, s) != hipSuccess) return DSPARK_EINVAL;
+  if (hipMemcpyAsync(e->rep, e->host_rep, sizeof(e->host_rep), hipMemcpyHostToDevice, s) != hipSuccess)
+    return DSPARK_EINVAL;
+  for (int r = 0; r < a->rounds; ++r) {
+    const int rc = dspark_engine_round(e, a->force_m, a->a, stream);
+    if (rc) return rc;
+  }
+  if (hipMemcpyAsync(&res->state, e->st, sizeof(dspark_state), hipMemcpyDeviceToHost, s) != hipSuccess)
+    return DSPARK_EINVAL;
+  if (hipStreamSynchronize(s) != hipSuccess) return DSPARK_EINVAL;
+  const int n = res->state.count;
+  const int max_n = std::min(limit - a->a, st.budget);
+  if (n < 1 || n > max_n) return DSPARK_EINVAL;  // the reference's "speculative decode: %d tokens" check
+  if (out_tokens) {
+    if (n > max_out) return DSPARK_ENOSPACE;
+    if (hipMemcpy(out_tokens, e->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess) return DSPARK_EINVAL;
+  }
+  res->count = n;
+  res->rounds = res->state.rounds_done;
+  res->accepted = res->state.accepted;
+  res->verified = res->state.verified;
+  res->boundary = stop;
+  return 0;
+}
+
+}  // extern "C"

@@ -53,8 +53,11 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
 }
 
 // TB token blocks of 16. I8: weights biased int8, else fp16. Grid: strips * ksplit.
+__device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st && p.st->run == 0; }
+
 template <int TB, bool I8>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+  if (gemm_stopped(p)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int strip = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
@@ -136,6 +139,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
 
 // Split-K reduce in index order + epilogue: one thread per 4 rows of one token.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+  if (gemm_stopped(p)) return;
   const int idx = blockIdx.x * 256 + threadIdx.x;
   const int groups = p.N / 4;
   if (idx >= p.M * groups) return;
@@ -146,7 +150,9 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
   gemm_store(p, t, r, 0, v);
 }
 
-__global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int strips, uint64_t* best) {
+__global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int strips, uint64_t* best,
+                                                      const dspark_state* st) {
+  if (st && st->run == 0) return;
   const int t = blockIdx.x;
   uint64_t b = 0;
   for (int c = threadIdx.x; c < strips; c += 64) {
@@ -190,7 +196,8 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
     const int threads = p.M * (p.N / 4);
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, p);
   }
-  if (p.best_part) hipLaunchKernelGGL(fold_strip_keys, dim3(p.M), dim3(64), 0, s, p.best_part, p.N / 16, p.best);
+  if (p.best_part && p.best)
+    hipLaunchKernelGGL(fold_strip_keys, dim3(p.M), dim3(64), 0, s, p.best_part, p.N / 16, p.best, p.st);
   return (int)hipGetLastError();
 }
 

@@ -18,7 +18,12 @@ constexpr int ARGMAX_CHUNK = 4096;  // logits per block
 template <bool F16>
 __global__ __launch_bounds__(256) void verify_argmax_partial(const void* logits, int M, int V, const uint32_t* seen,
                                                              const dspark_state* st, float rep, float inv_rep,
-                                                             uint64_t* part, int nchunks) {
+                                                             const float* rep_dev, uint64_t* part, int nchunks) {
+  if (st->run == 0) return;
+  if (rep_dev) {  // {rep, 1/rep} in device memory (the reference's g.rep / g.inv_rep, dspark.go:575-578)
+    rep = rep_dev[0];
+    inv_rep = rep_dev[1];
+  }
   const int t = blockIdx.y, chunk = blockIdx.x;
   // Drafts 1..t that were not seen before this round count as seen for this position (dspark.hip:2226-2232).
   __shared__ int dt[DSPARK_MT_MAX];
@@ -62,7 +67,8 @@ __global__ __launch_bounds__(256) void verify_argmax_partial(const void* logits,
   }
 }
 
-__global__ __launch_bounds__(64) void fold_keys(const uint64_t* part, int nchunks, uint64_t* best) {
+__global__ __launch_bounds__(64) void fold_keys(const uint64_t* part, int nchunks, uint64_t* best, const dspark_state* st) {
+  if (st->run == 0) return;
   const int t = blockIdx.x;
   uint64_t b = 0;
   for (int c = threadIdx.x; c < nchunks; c += 64) {
@@ -77,7 +83,8 @@ __device__ __forceinline__ int key_token(uint64_t k) { return (int)(0xffffffffu 
 
 __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, const uint64_t* best, int m, int skip_now,
                                                            int32_t* out_tokens, uint32_t* seen) {
-  if (threadIdx.x != 0) return;
+  if (threadIdx.x != 0 || st->run == 0) return;
+  if (m <= 0) m = st->M;  // rounds that drafted on the device: the verified count is in the State
   int acc = 0;
   for (int t = 0; t < m - 1; ++t) {
     if (key_token(best[t]) != st->tokens[t + 1]) break;
@@ -127,16 +134,16 @@ size_t verify_argmax_ws(int M, int V) {
 }
 
 int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32_t* seen, const dspark_state* st,
-                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s) {
+                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev) {
   const int nchunks = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
   uint64_t* part = reinterpret_cast<uint64_t*>(ws);
   if (f16)
     hipLaunchKernelGGL(verify_argmax_partial<true>, dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st, rep,
-                       inv_rep, part, nchunks);
+                       inv_rep, rep_dev, part, nchunks);
   else
     hipLaunchKernelGGL(verify_argmax_partial<false>, dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st, rep,
-                       inv_rep, part, nchunks);
-  hipLaunchKernelGGL(fold_keys, dim3(M), dim3(64), 0, s, part, nchunks, best);
+                       inv_rep, rep_dev, part, nchunks);
+  hipLaunchKernelGGL(fold_keys, dim3(M), dim3(64), 0, s, part, nchunks, best, st);
   return (int)hipGetLastError();
 }
 

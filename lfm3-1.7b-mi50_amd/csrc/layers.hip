@@ -1,0 +1,302 @@
+// Elementwise and small kernels of the DSpark round: embedding, residual + RMS norms, gated short conv, q/k norm +
+// RoPE + K/V page write, the drafter's Markov/confidence steps and the round's bookkeeping. Every kernel reads the
+// positions it needs (a, ctx_pos, ...) from the device State and returns at once when State.run is 0, so a whole
+// round is a fixed launch sequence that can be replayed without the host reading anything back.
+// Reference: norm_compute (dspark.hip:722-843), conv_wave (2191-2214), query_fresh + norm_rope (999-1061, 946-951),
+// embed (2463-2486), markov_phase + draft loop (2322-2366, 2633-2664), context ring write (2487-2518).
+#include "common.h"
+#include "dspark.h"
+#include "dspark_internal.h"
+
+namespace dspark {
+
+__device__ __forceinline__ bool stopped(const dspark_state* st) { return st && ldg(&st->run) == 0; }
+
+// ---------------------------------------------------------------- embedding
+// h[t][:] = embed[token(t)][:] (fp16 -> fp32). mode 0: token(t) = st->tokens[t]; mode 1 (drafter block):
+// t == 0 ? st->anchor : mask_token. Tokens outside the vocabulary read row 0.
+__global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const dspark_state* st, int mode, int mask_token,
+                                                    int M, int H, int V, float* h) {
+  if (stopped(st)) return;
+  const int t = blockIdx.x;
+  int tok = mode == 0 ? st->tokens[t] : (t == 0 ? st->anchor : mask_token);
+  if (tok < 0 || tok >= V) tok = 0;
+  for (int i = threadIdx.x; i < H; i += 256) h[(size_t)t * H + i] = (float)embed[(size_t)tok * H + i];
+}
+
+// ---------------------------------------------------------------- residual + RMS norm (norm_compute)
+// v = sum of `bands` inputs; a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
+// h_new = h_old + a * v * post_w; x = fp16(h_new * rsqrt(mean(h_new^2) + eps) * norm_w).
+// One block per (row, group): blockIdx.y selects a group with its own inputs (the drafter's tap norms).
+__global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
+  if (stopped(p.st)) return;
+  const int t = blockIdx.x, gi = blockIdx.y;
+  const int H = p.H;
+  const float* hold = p.h_old ? p.h_old + (size_t)gi * p.group_stride + (size_t)t * H : nullptr;
+  const _Float16* nw = p.norm_w + (size_t)gi * p.norm_w_stride;
+  constexpr int MAXE = 32;  // H <= 8192
+  float hv[MAXE], vv[MAXE];
+  const int ne = H / 256;
+  float s_vv = 0.f;
+  for (int k = 0; k < ne; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    hv[k] = hold ? hold[i] : 0.f;
+    float v = 0.f;
+    for (int b = 0; b < p.bands; ++b) v += p.v[(size_t)b * p.v_band_stride + (size_t)t * H + i];
+    vv[k] = v;
+    s_vv += v * v;
+  }
+  __shared__ float red[8];
+  auto block_sum = [&](float x) -> float {
+    x = wave_sum(x);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+  };
+  float a = 0.f;
+  if (p.bands > 0) a = p.sandwich ? rsqrtf(block_sum(s_vv) / H + p.eps) : 1.f;
+  float s_hh = 0.f;
+  for (int k = 0; k < ne; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const float pw = p.post_w ? (float)p.post_w[i] : 1.f;
+    hv[k] = fmaf(vv[k] * a, pw, hv[k]);
+    s_hh += hv[k] * hv[k];
+  }
+  const float inv = rsqrtf(block_sum(s_hh) / H + p.eps);
+  for (int k = 0; k < ne; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const size_t o = (size_t)gi * p.group_stride + (size_t)t * H + i;
+    if (p.dst) p.dst[o] = hv[k];
+    if (p.tap) p.tap[(size_t)t * H + i] = hv[k];
+    p.x16[(size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i] = (_Float16)(hv[k] * inv * (float)nw[i]);
+  }
+}
+
+// ---------------------------------------------------------------- gated short conv (conv_wave)
+// mix rows per channel c: [B, C, X] at 3c, 3c+1, 3c+2. bx = fp16(B*X); conv = w[K-1]*bx + sum_{k<K-1} w[k]*hist[pos-K+1+k];
+// y = fp16(C*conv); ring[pos] = bx. The history is position-indexed (ring of CONV_RING positions), so a rejected
+// token's entry is simply overwritten by a later round.
+__global__ __launch_bounds__(256) void conv_kernel(const float* mix, const _Float16* conv_w, _Float16* ring, const dspark_state* st,
+                                                   int M, int H, int K, _Float16* y) {
+  if (stopped(st)) return;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  const int a = st->a;
+  float w[8], hist[8];
+  for (int k = 0; k < K; ++k) w[k] = (float)conv_w[(size_t)c * K + k];
+  for (int k = 0; k < K - 1; ++k) hist[k] = (float)ring[(size_t)((a - (K - 1) + k) & (CONV_RING - 1)) * H + c];
+  for (int t = 0; t < M; ++t) {
+    const float* m = mix + (size_t)t * 3 * H + 3 * c;
+    const float B = m[0], C = m[1], X = m[2];
+    const _Float16 bxh = (_Float16)(B * X);
+    const float bx = (float)bxh;
+    float conv = w[K - 1] * bx;
+    for (int k = 0; k < K - 1; ++k) conv = fmaf(w[k], hist[k], conv);
+    for (int k = 0; k + 1 < K - 1; ++k) hist[k] = hist[k + 1];
+    if (K > 1) hist[K - 2] = bx;
+    ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = bxh;
+    y[(size_t)t * H + c] = (_Float16)(C * conv);
+  }
+}
+
+// ---------------------------------------------------------------- q/k norm + RoPE + K/V page write (query_fresh)
+// One wave per (token, head) over heads [0, QH) for q and [QH, QH + KVH) for k (v rides with k). Row layout of `mix`
+// per token: q [QH*D] | k [KVH*D] | v [KVH*D] | gate [QH] (gate optional), `row` floats apart. Position of token t:
+// base + t with base = st->a (verify, drafter block) or st->ctx_pos (context projection); tokens t >= count
+// (count = M, or st->ctx_new) are skipped.
+__global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) {
+  if (stopped(p.st)) return;
+  const int lane = threadIdx.x & 63;
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int heads = p.QH + p.KVH;
+  if (task >= p.M * heads) return;
+  const int t = task / heads, hh = task % heads;
+  const int count = p.count_from_ctx ? p.st->ctx_new : p.M;
+  if (t >= count) return;
+  const int pos = (p.pos_from_ctx ? p.st->ctx_pos : p.st->a) + t;
+  const int D = p.D, half = D / 2;
+  const float* row = p.mix + (size_t)t * p.row;
+  const bool isq = hh < p.QH;
+  if (isq && !p.q16) return;
+  const float* src = isq ? row + (size_t)hh * D : row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)(hh - p.QH) * D;
+  const _Float16* nw = isq ? p.q_norm : p.k_norm;
+  // lane l holds dims l and l + 32 (D = 64) or l, l+32, l+64, l+96 (D = 128): pairs (i, i + D/2) share a lane
+  constexpr int MAXE = 4;
+  const int ne = D / 32;  // 2 or 4
+  float v[MAXE];
+  float ss = 0.f;
+  for (int e = 0; e < ne; ++e) {
+    const int i = (lane & 31) + 32 * e;
+    v[e] = src[i];
+    ss += v[e] * v[e];
+  }
+  // lanes 32..63 duplicate lanes 0..31; sum over the first 32 lanes
+  ss = (lane < 32) ? ss : 0.f;
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / D + p.eps);
+  for (int e = 0; e < ne; ++e) v[e] = v[e] * inv * (float)nw[(lane & 31) + 32 * e];
+  // RoPE: pair (i, i + half) for i < rot, cos/sin from the table row of `pos` (cos | sin, D halves)
+  const _Float16* rt = p.rope + (size_t)pos * D;
+  float r[MAXE];
+  for (int e = 0; e < ne; ++e) r[e] = v[e];
+  for (int e = 0; e < ne / 2; ++e) {
+    const int i = (lane & 31) + 32 * e;  // i < half
+    if (i < p.rot) {
+      const float c = (float)rt[i], s = (float)rt[half + i];
+      const float x0 = v[e], x1 = v[e + ne / 2];
+      r[e] = x0 * c - x1 * s;
+      r[e + ne / 2] = x1 * c + x0 * s;
+    }
+  }
+  if (lane >= 32) return;
+  if (isq) {
+    _Float16* q = p.q16 + ((size_t)t * p.QH + hh) * D;
+    for (int e = 0; e < ne; ++e) q[(lane & 31) + 32 * e] = (_Float16)r[e];
+    if (p.gate && p.gate_in_mix) {
+      if (lane == 0) p.gate[(size_t)t * p.QH + hh] = row[(size_t)(p.QH + 2 * p.KVH) * D + hh];
+    }
+    return;
+  }
+  // K (normed, rotated) and V (as is) into the pages at `pos`
+  const int kvh = hh - p.QH;
+  const float* vsrc = row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)p.KVH * D + (size_t)kvh * D;
+  const int lp = pos / PAGE, slot = pos % PAGE;
+  const int phys = p.bt ? p.bt[lp] : lp;
+  _Float16* kb = p.kp + ((size_t)phys * p.KVH + kvh) * (PAGE * D);
+  _Float16* vb = p.vp + ((size_t)phys * p.KVH + kvh) * (D * PAGE);
+  const int b = (slot >> 2) & 1, nrow = 4 * (slot >> 3) + (slot & 3);
+  for (int e = 0; e < ne; ++e) {
+    const int d = (lane & 31) + 32 * e;
+    const int s = d / 32, g = (d % 32) / 8, j = d % 8;
+    kb[((size_t)(b * (D / 32) + s) * 64 + nrow + 16 * g) * 8 + j] = (_Float16)r[e];
+    vb[(size_t)d * PAGE + slot] = (_Float16)vsrc[d];
+  }
+}
+
+// ---------------------------------------------------------------- drafter: Markov + confidence (markov_phase)
+// Step j (0-based) proposes draft j+1 from prev = (j == 0 ? anchor : the token of step j-1's argmax key):
+//   cap = min(max_drafts, block - 1, min(limit - a, budget - count) - 1); steps j >= cap do nothing;
+//   conf = base[j][N] + c2[prev] + conf_bias; conf < thr stops drafting (st->M = j + 1);
+//   z[r] = base[j][r] + (sum_k w2q[r][k] * w1q[prev][k]) * w2s[r] * w1s[prev]; best[j] = max key(z[r], r);
+//   st->tokens[j] = prev (for j >= 1). A stop recorded by an earlier step turns the later ones into no-ops.
+// Launched as block - 1 steps, then markov_finalize writes the last token and st->M.
+__global__ __launch_bounds__(256) void markov_kernel(MarkovParams p, int j) {
+  dspark_state* st = p.st;
+  if (stopped(st)) return;
+  if (ldg(&st->M) != 0) return;  // drafting already stopped (M is set by the stop or the finalize)
+  const int a = st->a;
+  const int cap = min(min(p.max_drafts, p.block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  if (j >= cap) return;
+  int prev;
+  if (j == 0) {
+    prev = st->anchor;
+  } else {
+    const uint64_t key = __hip_atomic_load(p.best + (j - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = p.crop_ids[0xffffffffu - (uint32_t)key];
+  }
+  const float conf = p.base[(size_t)j * p.stride + p.N] + p.c2[prev] + p.conf_bias;
+  if (!(conf >= p.conf_thr)) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      if (j >= 1) st->tokens[j] = prev;
+      st->M = j + 1;
+    }
+    return;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0 && j >= 1) st->tokens[j] = prev;
+  // rows: one per thread, R rows per block; w2q stored row-major [N][rank]
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  uint64_t best = 0;
+  if (r < p.N) {
+    const int8_t* w2 = p.w2q + (size_t)r * p.rank;
+    const int8_t* w1 = p.w1q + (size_t)prev * p.rank;
+    int acc = 0;
+    for (int k = 0; k < p.rank; k += 16) {
+      const u32x4 a4 = ldg(reinterpret_cast<const u32x4*>(w2 + k));
+      const u32x4 b4 = ldg(reinterpret_cast<const u32x4*>(w1 + k));
+      acc = __builtin_amdgcn_sdot4(a4[0], b4[0], acc, false);
+      acc = __builtin_amdgcn_sdot4(a4[1], b4[1], acc, false);
+      acc = __builtin_amdgcn_sdot4(a4[2], b4[2], acc, false);
+      acc = __builtin_amdgcn_sdot4(a4[3], b4[3], acc, false);
+    }
+    const float z = fmaf((float)acc, p.w2s[r] * p.w1s[prev], p.base[(size_t)j * p.stride + r]);
+    best = argmax_key(z, (uint32_t)r);
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0 && best)
+    __hip_atomic_fetch_max(p.best + j, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After the steps: if drafting ran to its cap, the last draft comes from the last step's key and M = 1 + drafts.
+__global__ void markov_finalize(MarkovParams p) {
+  dspark_state* st = p.st;
+  if (stopped(st) || threadIdx.x != 0) return;
+  st->tokens[0] = st->anchor;
+  if (st->M != 0) return;  // stopped by confidence: tokens and M already written
+  const int a = st->a;
+  const int cap = min(min(p.max_drafts, p.block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  const int drafts = max(cap, 0);
+  if (drafts >= 1) {
+    const uint64_t key = p.best[drafts - 1];
+    st->tokens[drafts] = p.crop_ids[0xffffffffu - (uint32_t)key];
+  }
+  st->M = drafts + 1;
+}
+
+// ---------------------------------------------------------------- round start
+// Clears the per-round scratch the kernels fold into (argmax keys) and the draft count, marks the anchor seen
+// (dspark.hip:2432-2435).
+__global__ void round_begin_kernel(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen) {
+  if (stopped(st)) return;
+  for (int i = threadIdx.x; i < nkeys; i += blockDim.x) keys[i] = 0;
+  if (threadIdx.x == 0) {
+    st->M = 0;
+    const int t = st->anchor;
+    if (seen && t >= 0) seen[t >> 5] |= 1u << (t & 31);
+  }
+}
+
+// Verify-only rounds (force_m: verify the tokens already in the State, no drafter; dspark.hip:147, 2442-2451).
+__global__ void force_m_kernel(dspark_state* st, int m) {
+  if (stopped(st) || threadIdx.x != 0) return;
+  st->tokens[0] = st->anchor;
+  st->M = m;
+}
+
+// ---------------------------------------------------------------- host launchers
+int embed_launch(const void* embed, const dspark_state* st, int mode, int mask_token, int M, int H, int V, float* h,
+                 hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, (const _Float16*)embed, st, mode, mask_token, M, H, V, h);
+  return (int)hipGetLastError();
+}
+int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) {
+  hipLaunchKernelGGL(resnorm_kernel, dim3(rows, groups), dim3(256), 0, s, p);
+  return (int)hipGetLastError();
+}
+int conv_launch(const float* mix, const void* conv_w, void* ring, const dspark_state* st, int M, int H, int K, void* y,
+                hipStream_t s) {
+  hipLaunchKernelGGL(conv_kernel, dim3((H + 255) / 256), dim3(256), 0, s, mix, (const _Float16*)conv_w, (_Float16*)ring, st,
+                     M, H, K, (_Float16*)y);
+  return (int)hipGetLastError();
+}
+int qkrope_launch(const QkRopeParams& p, hipStream_t s) {
+  const int tasks = p.M * (p.QH + p.KVH);
+  hipLaunchKernelGGL(qkrope_kernel, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
+  return (int)hipGetLastError();
+}
+int markov_launch(const MarkovParams& p, hipStream_t s) {
+  const int blocks = (p.N + 255) / 256;
+  for (int j = 0; j < p.block - 1; ++j) hipLaunchKernelGGL(markov_kernel, dim3(blocks), dim3(256), 0, s, p, j);
+  hipLaunchKernelGGL(markov_finalize, dim3(1), dim3(64), 0, s, p);
+  return (int)hipGetLastError();
+}
+int round_begin_launch(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, hipStream_t s) {
+  hipLaunchKernelGGL(round_begin_kernel, dim3(1), dim3(256), 0, s, st, keys, nkeys, seen);
+  return (int)hipGetLastError();
+}
+int force_m_launch(dspark_state* st, int m, hipStream_t s) {
+  hipLaunchKernelGGL(force_m_kernel, dim3(1), dim3(64), 0, s, st, m);
+  return (int)hipGetLastError();
+}
+
+}  // namespace dspark

@@ -297,3 +297,167 @@ def head_argmax(x, w, y_f32=None, best=None, workspace=None, stream=None):
                                       stream_handle(stream))
     check(rc, "dspark_head_argmax_f16")
     return best
+
+
+# ---------------------------------------------------------------- the full step (engine)
+MAX_LAYERS = 64
+MAX_TAPS = 8
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int32), ("ffn", ctypes.c_int32), ("vocab", ctypes.c_int32),
+                ("n_layers", ctypes.c_int32), ("layer_kind", ctypes.c_int32 * MAX_LAYERS),
+                ("q_heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("conv_kernel", ctypes.c_int32), ("window", ctypes.c_int32), ("rope_base", ctypes.c_float),
+                ("rope_pairs", ctypes.c_int32), ("draft_layers", ctypes.c_int32), ("draft_ffn", ctypes.c_int32),
+                ("block", ctypes.c_int32), ("max_drafts", ctypes.c_int32), ("crop_rows", ctypes.c_int32),
+                ("markov_rank", ctypes.c_int32), ("n_taps", ctypes.c_int32), ("tap_layer", ctypes.c_int32 * MAX_TAPS),
+                ("draft_window", ctypes.c_int32), ("ring_positions", ctypes.c_int32), ("mask_token", ctypes.c_int32),
+                ("conf_bias", ctypes.c_float), ("conf_thr", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+class LaunchArgs(ctypes.Structure):
+    _fields_ = [("a", ctypes.c_int32), ("anchor", ctypes.c_int32), ("budget", ctypes.c_int32), ("eos", ctypes.c_int32),
+                ("rep", ctypes.c_float), ("rounds", ctypes.c_int32), ("ctx_new", ctypes.c_int32),
+                ("ctx_pos", ctypes.c_int32), ("ctx_lo", ctypes.c_int32), ("force_m", ctypes.c_int32),
+                ("tokens", ctypes.c_int32 * MT_MAX)]
+
+
+class LaunchResult(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_int32), ("rounds", ctypes.c_int32), ("accepted", ctypes.c_int32),
+                ("verified", ctypes.c_int32), ("boundary", ctypes.c_int32), ("state", State)]
+
+
+_SIGS.update({
+    "dspark_engine_create": (ctypes.c_int, [ctypes.POINTER(ModelDesc), ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p)]),
+    "dspark_engine_destroy": (None, [ctypes.c_void_p]),
+    "dspark_engine_init_random": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]),
+    "dspark_engine_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                            ctypes.POINTER(ctypes.c_size_t)]),
+    "dspark_engine_tensor_count": (ctypes.c_int, [ctypes.c_void_p]),
+    "dspark_engine_tensor_name": (ctypes.c_char_p, [ctypes.c_void_p, ctypes.c_int32]),
+    "dspark_engine_round": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_engine_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchArgs), ctypes.c_void_p, ctypes.c_int32,
+                                            ctypes.POINTER(LaunchResult), ctypes.c_void_p]),
+})
+
+
+def model_desc(**kw):
+    d = ModelDesc()
+    for k, v in kw.items():
+        if k in ("layer_kind", "tap_layer"):
+            arr = getattr(d, k)
+            for i, x in enumerate(v):
+                arr[i] = int(x)
+        else:
+            setattr(d, k, v)
+    return d
+
+
+def c4_desc(block=16, vocab=65536):
+    """16-layer LFM-style target (10 gated short-conv k=3 + 6 GQA 32/8/64), hidden 2048, FFN 8192,
+    vocab 65536, int8 weights; 4-layer drafter proposing 16-token blocks."""
+    kinds = [0, 0, 1, 0, 0, 1, 0, 0, 1, 0, 1, 0, 1, 0, 1, 0]
+    return model_desc(hidden=2048, ffn=8192, vocab=vocab, n_layers=16, layer_kind=kinds, q_heads=32, kv_heads=8,
+                      head_dim=64, conv_kernel=3, window=0, rope_base=1e6, rope_pairs=32, draft_layers=4,
+                      draft_ffn=8192, block=block, max_drafts=block - 1, crop_rows=16384, markov_rank=256, n_taps=5,
+                      tap_layer=[1, 4, 8, 11, 15], draft_window=2048, ring_positions=4096, mask_token=vocab - 1,
+                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
+
+
+class Engine:
+    """One model + one request's device buffers (dspark_engine_* in include/dspark.h)."""
+
+    def __init__(self, desc, max_context):
+        self.desc = desc
+        self.max_context = max_context
+        h = ctypes.c_void_p()
+        check(lib().dspark_engine_create(ctypes.byref(desc), max_context, ctypes.byref(h)), "dspark_engine_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().dspark_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor(self, name):
+        p = ctypes.c_void_p()
+        n = ctypes.c_size_t()
+        check(lib().dspark_engine_tensor(self.h, name.encode(), ctypes.byref(p), ctypes.byref(n)), f"tensor {name}")
+        return p.value, n.value
+
+    def names(self):
+        n = lib().dspark_engine_tensor_count(self.h)
+        return [lib().dspark_engine_tensor_name(self.h, i).decode() for i in range(n)]
+
+    def init_random(self, seed, stream=None):
+        check(lib().dspark_engine_init_random(self.h, seed, stream_handle(stream)), "dspark_engine_init_random")
+
+    def round(self, force_m=0, plan_a=0, stream=None):
+        check(lib().dspark_engine_round(self.h, force_m, plan_a, stream_handle(stream)), "dspark_engine_round")
+
+    def launch(self, a, anchor, budget=512, eos=-1, rep=1.0, rounds=32, ctx_new=0, ctx_pos=0, ctx_lo=0, force_m=0,
+               tokens=(), max_out=1024, stream=None):
+        args = LaunchArgs()
+        args.a, args.anchor, args.budget, args.eos, args.rep, args.rounds = a, anchor, budget, eos, rep, rounds
+        args.ctx_new, args.ctx_pos, args.ctx_lo, args.force_m = ctx_new, ctx_pos, ctx_lo, force_m
+        for i, t in enumerate(tokens):
+            args.tokens[i] = int(t)
+        out = (ctypes.c_int32 * max_out)()
+        res = LaunchResult()
+        check(lib().dspark_engine_launch(self.h, ctypes.byref(args), out, max_out, ctypes.byref(res),
+                                         stream_handle(stream)), "dspark_engine_launch")
+        return list(out[:res.count]), res
+
+    # host <-> device copies of named tensors (plumbing for tests, loaders and benchmarks)
+    def upload(self, name, array):
+        import numpy as np
+        ptr_, nbytes = self.tensor(name)
+        a = np.ascontiguousarray(array)
+        assert a.nbytes <= nbytes, (name, a.nbytes, nbytes)
+        _hip().hipMemcpy(ctypes.c_void_p(ptr_), a.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(a.nbytes), 1)
+
+    def download(self, name, dtype, shape=None):
+        import numpy as np
+        ptr_, nbytes = self.tensor(name)
+        out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype=dtype)
+        _hip().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr_), ctypes.c_size_t(out.nbytes), 2)
+        if shape is not None:
+            out = out[:int(np.prod(shape))].reshape(shape)
+        return out
+
+    def state(self):
+        import numpy as np
+        raw = self.download("state", np.int32)
+        st = State()
+        ctypes.memmove(ctypes.byref(st), raw.tobytes(), ctypes.sizeof(State))
+        return st
+
+    def set_state(self, **fields):
+        import numpy as np
+        st = State()
+        for k, v in fields.items():
+            if k == "tokens":
+                for i, t in enumerate(v):
+                    st.tokens[i] = int(t)
+            else:
+                setattr(st, k, int(v))
+        self.upload("state", np.frombuffer(bytes(st), dtype=np.int32))
+
+
+_hip_lib = None
+
+
+def _hip():
+    global _hip_lib
+    if _hip_lib is None:
+        _hip_lib = ctypes.CDLL("libamdhip64.so")
+        _hip_lib.hipMemcpy.restype = ctypes.c_int
+        _hip_lib.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return _hip_lib

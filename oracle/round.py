@@ -1,0 +1,269 @@
+"""CPU restatement of one DSpark round -- TEST INFRASTRUCTURE ONLY (tests/ and bench.py's cpu_baseline leg).
+
+Composes the pinned pieces of liborc.so (fp16 RNE, fp64 verify attention, penalised argmax keys, acceptance/commit)
+with numpy statements of the layer arithmetic, following the reference's dspark_kernel section by section:
+  context projection   dspark.hip:2487-2518, 2682-2705 (tap norms -> fc -> hidden norm -> ckv -> k norm + RoPE)
+  drafter block        dspark.hip:2463-2486, 2706-2780 (kind 3: no sandwich norms, no gate, bidirectional block)
+  cropped head         dspark.hip:2564-2587
+  Markov/confidence    dspark.hip:2322-2366, 2633-2664
+  verify               dspark.hip:2519-2846 (sandwich norms 722-843, conv_wave 2191-2214, query_fresh 999-1061,
+                       gated combine 2132-2185, LM head + argmax 2219-2318)
+  commit               dspark.hip:2848-2913
+Rounding points are the ones the GPU path uses: GEMM inputs, attention Q/K/V and conv/attention/FFN outputs are
+fp16; residuals, GEMM outputs and scores are wider (fp64 here).
+"""
+import numpy as np
+
+from . import oracle as orc
+
+
+def f16(x):
+    return np.asarray(x, dtype=np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+def h2f(u16):
+    return np.asarray(u16, dtype=np.uint16).view(np.float16).astype(np.float64)
+
+
+class Weights:
+    """Host copies of an engine's tensors (names as include/dspark.h's engine documents)."""
+
+    def __init__(self, desc, tensors):
+        self.d = desc
+        self.t = tensors
+
+    def f16(self, name, shape=None):
+        a = h2f(self.t[name])
+        return a.reshape(shape) if shape else a
+
+    def gemm_w(self, name, rows, cols):
+        w = (self.t[name + ".w"][:rows * cols].astype(np.int16) - 128).reshape(rows, cols).astype(np.float64)
+        s = h2f(self.t[name + ".s"][:rows])
+        return w, s
+
+
+def gemm(x16, w, s):
+    """y = (x @ q^T) * scale (per output row), fp64; x already fp16-valued."""
+    return (x16 @ w.T) * s[None, :]
+
+
+def resnorm(h_old, v, post_w, norm_w, sandwich, eps):
+    """norm_compute (dspark.hip:722-843) for a block of rows: returns (h_new, x fp16-valued)."""
+    H = norm_w.shape[0]
+    h = np.zeros_like(v if v is not None else h_old) if h_old is None else h_old.copy()
+    if v is not None:
+        a = 1.0 / np.sqrt((v * v).sum(1, keepdims=True) / H + eps) if sandwich else 1.0
+        pw = post_w if post_w is not None else 1.0
+        h = h + (v * a) * pw
+    inv = 1.0 / np.sqrt((h * h).sum(1, keepdims=True) / H + eps)
+    return h, f16(h * inv * norm_w[None, :])
+
+
+def rope_rows(x, pos, table, rot):
+    """x [D] (one head), rotated by the table row of `pos` (cos | sin, fp16 values), pairs (i, i + D/2), i < rot."""
+    D = x.shape[0]
+    half = D // 2
+    c = table[pos, :half]
+    s = table[pos, half:]
+    y = x.copy()
+    i = np.arange(rot)
+    y[i] = x[i] * c[i] - x[i + half] * s[i]
+    y[i + half] = x[i + half] * c[i] + x[i] * s[i]
+    return y
+
+
+def norm_head(x, w, eps):
+    D = x.shape[0]
+    return x / np.sqrt((x * x).sum() / D + eps) * w
+
+
+class Caches:
+    """Logical K/V per attention layer ([positions][KVH][D] fp16 values), conv rings, drafter rings, taps."""
+
+    def __init__(self):
+        self.kv = {}      # target layer -> (K, V) arrays [T][KVH][D] (fp64 holding fp16 values)
+        self.ring = {}    # drafter layer -> (K, V) arrays indexed by absolute position
+        self.conv = {}    # target layer -> {position: bx [H]}
+        self.taps = None  # [n_taps][B][H]
+
+
+def attn_fp16(q16, K, V, a, M, start, window, causal):
+    """fp64 verify attention via liborc (q [M][QH][D], K/V [T][KVH][D], all fp16-valued)."""
+    to16 = lambda x: np.ascontiguousarray(np.asarray(x, np.float64).astype(np.float16).view(np.uint16))
+    T = a + M
+    return orc.verify_attention(to16(q16), to16(K[:T]), to16(V[:T]), a, start, window, causal)
+
+
+def context_projection(W, C, st, rope):
+    d = W.d
+    H, B = d.hidden, d.block
+    n_new, pos0 = st["ctx_new"], st["ctx_pos"]
+    if n_new <= 0:
+        return
+    tn = W.f16("tap_norms", (d.n_taps, H))
+    xs = [resnorm(C.taps[b][:B], None, None, tn[b], 0, d.eps)[1] for b in range(d.n_taps)]
+    x = np.concatenate(xs, axis=1)                         # [B][taps*H]
+    fw, fs = W.gemm_w("fc", H, d.n_taps * H)
+    c = gemm(x, fw, fs)
+    _, x2 = resnorm(None, c, None, W.f16("hidden_norm"), 0, d.eps)
+    KVH, D = d.kv_heads, d.head_dim
+    rows = d.draft_layers * 2 * KVH * D
+    cw, cs = W.gemm_w("ckv", rows, H)
+    kv = gemm(x2, cw, cs)
+    for j in range(d.draft_layers):
+        kn = W.f16(f"D{j}.k_norm")
+        K, V = C.ring[j]
+        for t in range(n_new):
+            pos = pos0 + t
+            row = kv[t, j * 2 * KVH * D:(j + 1) * 2 * KVH * D]
+            for h in range(KVH):
+                k = norm_head(row[h * D:(h + 1) * D], kn, d.eps)
+                K[pos, h] = f16(rope_rows(k, pos, rope, d.rope_pairs))
+                V[pos, h] = f16(row[KVH * D + h * D:KVH * D + (h + 1) * D])
+
+
+def drafter_block(W, C, st, rope):
+    """Returns base [B][crop_rows + 1] (fp64): the cropped head over the drafter block."""
+    d = W.d
+    H, B, QH, KVH, D = d.hidden, d.block, d.q_heads, d.kv_heads, d.head_dim
+    emb = W.f16("embed", (d.vocab, H))
+    toks = [st["anchor"]] + [d.mask_token] * (B - 1)
+    h = emb[toks]
+    a = st["a"]
+    v_prev = None
+    for j in range(d.draft_layers):
+        pre = f"D{j}."
+        h, x = resnorm(h, v_prev, None, W.f16(pre + "op_norm"), 0, d.eps)
+        rows = QH * D + 2 * KVH * D
+        mw, ms = W.gemm_w(pre + "mix", rows, H)
+        mix = gemm(x, mw, ms)
+        qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
+        K, V = C.ring[j]
+        q16 = np.zeros((B, QH, D))
+        for t in range(B):
+            pos = a + t
+            for qh in range(QH):
+                q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, rope, d.rope_pairs))
+            for hh in range(KVH):
+                o = QH * D + hh * D
+                K[pos, hh] = f16(rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs))
+                o = QH * D + KVH * D + hh * D
+                V[pos, hh] = f16(mix[t, o:o + D])
+        start = max(st["ctx_lo"], a - d.draft_window)
+        o = attn_fp16(q16, K, V, a, B, start, 0, False)
+        y = f16(o.reshape(B, QH * D))
+        ow, os_ = W.gemm_w(pre + "out", H, H)
+        vout = gemm(y, ow, os_)
+        h, x = resnorm(h, vout, None, W.f16(pre + "ffn_norm"), 0, d.eps)
+        ww, ws = W.gemm_w(pre + "w13", 2 * d.draft_ffn, H)
+        gu = gemm(x, ww, ws)
+        g, u = gu[:, 0::2], gu[:, 1::2]
+        act = f16(g / (1.0 + np.exp(-g)) * u)
+        w2, s2 = W.gemm_w(pre + "w2", H, d.draft_ffn)
+        v_prev = gemm(act, w2, s2)
+    h, x = resnorm(h, v_prev, None, W.f16("draft_norm"), 0, d.eps)
+    cw, cs = W.gemm_w("crop", d.crop_rows + 1, H)
+    return gemm(x, cw, cs)
+
+
+def markov(W, st, base):
+    """Draft tokens and the verified count M (dspark.hip:2633-2664); returns (tokens list, M, per-step z rows)."""
+    d = W.d
+    N, R = d.crop_rows, d.markov_rank
+    w2q = W.t["markov.w2q"][:N * R].view(np.int8).reshape(N, R).astype(np.int64)
+    w2s = W.t["markov.w2s"][:N].astype(np.float32)
+    w1q = W.t["markov.w1q"].view(np.int8).reshape(d.vocab, R).astype(np.int64)
+    w1s = W.t["markov.w1s"].astype(np.float32)
+    c2 = W.t["conf_c2"].astype(np.float32)
+    crop_ids = W.t["crop_ids"][:N].astype(np.int64)
+    a = st["a"]
+    cap = min(min(d.max_drafts, d.block - 1), min(st["limit"] - a, st["budget"] - st["count"]) - 1)
+    prev = st["anchor"]
+    toks = [prev]
+    zs = []
+    for j in range(max(cap, 0)):
+        conf = np.float32(base[j, N]) + c2[prev] + np.float32(d.conf_bias)
+        if not conf >= np.float32(d.conf_thr):
+            break
+        dots = (w2q @ w1q[prev]).astype(np.float64)   # exact integers
+        # fmaf(dot, w2s * w1s, base): one rounding of the exact product plus base
+        z = (dots * (w2s * w1s[prev]).astype(np.float64) + base[j, :N].astype(np.float32).astype(np.float64)).astype(np.float32)
+        zs.append(z)
+        r = int(orc.row_argmax(z[None, :].astype(np.float32))[0])
+        prev = int(crop_ids[r])
+        toks.append(prev)
+    return toks, len(toks), zs
+
+
+def verify(W, C, st, tokens, rope):
+    """Logits [B][V] (fp64) of the verify pass over the B block tokens; updates K/V caches, conv rings and taps."""
+    d = W.d
+    H, B, QH, KVH, D, I = d.hidden, d.block, d.q_heads, d.kv_heads, d.head_dim, d.ffn
+    emb = W.f16("embed", (d.vocab, H))
+    toks = [t if 0 <= t < d.vocab else 0 for t in tokens[:B]]
+    h = emb[toks]
+    a = st["a"]
+    v_prev = None
+    taps = np.zeros((d.n_taps, B, H))
+    tap_of = {l: i for i, l in enumerate(d.tap_layer[:d.n_taps])}
+    for i in range(d.n_layers):
+        pre = f"L{i}."
+        post = W.f16(f"L{i - 1}.post_ffn_norm") if i else None
+        h, x = resnorm(h, v_prev, post, W.f16(pre + "op_norm"), 1, d.eps)
+        if i and (i - 1) in tap_of:
+            taps[tap_of[i - 1]] = h
+        kind = d.layer_kind[i]
+        if kind == 0:
+            mw, ms = W.gemm_w(pre + "mix", 3 * H, H)
+            mix = gemm(x, mw, ms)
+            cw = W.f16(pre + "conv.w", (H, d.conv_kernel))
+            ring = C.conv[i]
+            Kc = d.conv_kernel
+            y = np.zeros((B, H))
+            for t in range(B):
+                Bv, Cv, Xv = mix[t, 0::3], mix[t, 1::3], mix[t, 2::3]
+                bx = f16(Bv * Xv)
+                conv = cw[:, Kc - 1] * bx
+                for k in range(Kc - 1):
+                    conv = conv + cw[:, k] * ring[a + t - (Kc - 1) + k]
+                ring[a + t] = bx
+                y[t] = f16(Cv * conv)
+        else:
+            rows = QH * D + 2 * KVH * D + QH
+            rows16 = (rows + 15) // 16 * 16
+            mw, ms = W.gemm_w(pre + "mix", rows16, H)
+            mix = gemm(x, mw, ms)
+            qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
+            K, V = C.kv[i]
+            q16 = np.zeros((B, QH, D))
+            for t in range(B):
+                pos = a + t
+                for qh in range(QH):
+                    q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, rope,
+                                               d.rope_pairs))
+                for hh in range(KVH):
+                    o = QH * D + hh * D
+                    K[pos, hh] = f16(rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs))
+                    o = QH * D + KVH * D + hh * D
+                    V[pos, hh] = f16(mix[t, o:o + D])
+            window = d.window if kind == 2 else 0
+            start = max(0, a - window + 1) if window else 0
+            o = attn_fp16(q16, K, V, a, B, start, window, True)
+            gate = mix[:, (QH + 2 * KVH) * D:(QH + 2 * KVH) * D + QH].astype(np.float32).astype(np.float64)
+            y = f16((o * (1.0 / (1.0 + np.exp(-gate)))[:, :, None]).reshape(B, QH * D))
+        ow, os_ = W.gemm_w(pre + "out", H, H)
+        vout = gemm(y, ow, os_)
+        h, x = resnorm(h, vout, W.f16(pre + "post_op_norm"), W.f16(pre + "ffn_norm"), 1, d.eps)
+        ww, ws = W.gemm_w(pre + "w13", 2 * I, H)
+        gu = gemm(x, ww, ws)
+        g, u = gu[:, 0::2], gu[:, 1::2]
+        act = f16(g / (1.0 + np.exp(-g)) * u)
+        w2, s2 = W.gemm_w(pre + "w2", H, I)
+        v_prev = gemm(act, w2, s2)
+    last = d.n_layers - 1
+    h, x = resnorm(h, v_prev, W.f16(f"L{last}.post_ffn_norm"), W.f16("final_norm"), 1, d.eps)
+    if last in tap_of:
+        taps[tap_of[last]] = h
+    C.taps = taps
+    hw, hs = W.gemm_w("head", d.vocab, H)
+    return gemm(x, hw, hs)

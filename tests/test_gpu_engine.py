@@ -1,0 +1,203 @@
+"""GPU parity of one full DSpark round (context projection, drafter, Markov drafts, verify, argmax, commit) through
+the engine's C ABI, against the oracle's restatement (oracle/round.py) on a small geometry with seeded weights.
+
+Bars: drafts, verify argmax keys, acceptance and every State field bit-exact (a draft/argmax may differ only where
+the oracle's own top two values are a near tie); ring K/V, cropped-head outputs and logits within tolerances stated
+below (fp16 activations through several layers: the GPU and the oracle round at the same points, so differences are
+accumulation order and fp16 last-bit flips)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import load_host
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=256, ffn=512, vocab=2048, n_layers=4, layer_kind=[0, 1, 0, 2], q_heads=4, kv_heads=2, head_dim=64,
+             conv_kernel=3, window=40, rope_base=1e4, rope_pairs=32, draft_layers=2, draft_ffn=512, block=8,
+             max_drafts=7, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[1, 3], draft_window=100,
+             ring_positions=256, mask_token=2047, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch
+
+
+def make_weights(eng, desc, seed):
+    rng = np.random.default_rng(seed)
+    host = {}
+    names = eng.names()
+    sizes = {n: eng.tensor(n)[1] for n in names}
+    weight_names = [n for n in names if not n.startswith(("kv.", "ring.", "conv.", "state", "seen", "out_tokens", "rep",
+                                                           "h0", "h1", "x16", "mix", "q16", "gate", "y16", "vout", "a16",
+                                                           "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys",
+                                                           "ws_", "rope", "ring_table"))]
+    for n in weight_names:
+        nb = sizes[n]
+        if n.endswith(".w") and not n.endswith("conv.w"):
+            a = rng.integers(1, 256, nb, dtype=np.uint8)
+        elif n.endswith(".s"):
+            rows = nb // 2
+            K = sizes[n[:-2] + ".w"] // rows
+            a = (rng.uniform(0.75, 1.25, rows) / (73.3 * np.sqrt(K))).astype(np.float16).view(np.uint16)
+        elif n == "embed":
+            a = rng.standard_normal(nb // 2).astype(np.float16).view(np.uint16)
+        elif n.endswith("conv.w"):
+            a = (rng.standard_normal(nb // 2) / np.sqrt(desc.conv_kernel)).astype(np.float16).view(np.uint16)
+        elif n in ("markov.w2q", "markov.w1q"):
+            a = rng.integers(-127, 128, nb, dtype=np.int8).view(np.uint8)
+        elif n == "markov.w2s":
+            a = rng.uniform(0.5, 1.5, nb // 4).astype(np.float32) / np.float32(73.3 * 8)
+        elif n == "markov.w1s":
+            a = np.full(nb // 4, 1 / 73.3, np.float32)
+        elif n == "conf_c2":
+            a = rng.uniform(-0.1, 0.1, nb // 4).astype(np.float32)
+        elif n == "crop_ids":
+            a = rng.permutation(desc.vocab)[:nb // 4].astype(np.int32)
+        else:  # norms
+            a = rng.uniform(0.8, 1.2, nb // 2).astype(np.float16).view(np.uint16)
+        eng.upload(n, a)
+        host[n] = a
+    return host
+
+
+def setup_caches(eng, host_mod, desc, a, ctx_lo, seed):
+    """Random K/V for cache positions < a (target) and [ctx_lo, a) (drafter ring), conv history, taps."""
+    from oracle.round import Caches
+    rng = np.random.default_rng(seed)
+    B, H, KVH, D = desc.block, desc.hidden, desc.kv_heads, desc.head_dim
+    T = eng.max_context + B
+    C = Caches()
+    lib = host_mod.lib()
+    import torch
+
+    def write(kname, vname, K, V, pos0, n, bt_name=None):
+        kd = torch.from_numpy(np.ascontiguousarray(K[pos0:pos0 + n]).astype(np.float16)).cuda()
+        vd = torch.from_numpy(np.ascontiguousarray(V[pos0:pos0 + n]).astype(np.float16)).cuda()
+        bt = ctypes.c_void_p(eng.tensor(bt_name)[0]) if bt_name else None
+        rc = lib.dspark_kv_write(ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()), KVH * D,
+                                 ctypes.c_void_p(eng.tensor(kname)[0]), ctypes.c_void_p(eng.tensor(vname)[0]), bt,
+                                 KVH, D, pos0, n, None)
+        host_mod.check(rc, "kv_write")
+        torch.cuda.synchronize()
+
+    for i in range(desc.n_layers):
+        if desc.layer_kind[i] == 0:
+            ring = rng.standard_normal((128, H)).astype(np.float16)
+            eng.upload(f"conv.L{i}", ring.view(np.uint16))
+            C.conv[i] = {pos: ring[pos % 128].astype(np.float64) for pos in range(a - desc.conv_kernel + 1, a)}
+        else:
+            K = np.zeros((T, KVH, D))
+            V = np.zeros((T, KVH, D))
+            K[:a] = rng.standard_normal((a, KVH, D)).astype(np.float16)
+            V[:a] = rng.standard_normal((a, KVH, D)).astype(np.float16)
+            write(f"kv.L{i}.k", f"kv.L{i}.v", K, V, 0, a)
+            C.kv[i] = (K, V)
+    for j in range(desc.draft_layers):
+        K = np.zeros((T, KVH, D))
+        V = np.zeros((T, KVH, D))
+        K[ctx_lo:a] = rng.standard_normal((a - ctx_lo, KVH, D)).astype(np.float16)
+        V[ctx_lo:a] = rng.standard_normal((a - ctx_lo, KVH, D)).astype(np.float16)
+        write(f"ring.D{j}.k", f"ring.D{j}.v", K, V, ctx_lo, a - ctx_lo, "ring_table")
+        C.ring[j] = (K, V)
+    taps = rng.standard_normal((desc.n_taps, B, H)).astype(np.float32)
+    eng.upload("taps", taps)
+    C.taps = taps.astype(np.float64)
+    return C
+
+
+def near_tie_ok(values, got, want, rel=1e-3):
+    """got != want only if values[got] and values[want] are within rel of the row's scale."""
+    if got == want:
+        return True
+    scale = np.max(np.abs(values))
+    return abs(values[got] - values[want]) <= rel * scale
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_engine_round_matches_oracle(dev, orc, seed):
+    torch = dev
+    host = load_host()
+    from oracle import round as rnd
+    desc = host.model_desc(**SMALL)
+    eng = host.Engine(desc, 512)
+    weights = make_weights(eng, desc, seed)
+    a, ctx_lo, ctx_new = 300, 150, 3
+    C = setup_caches(eng, host, desc, a, ctx_lo, seed + 100)
+    anchor = 17
+    st0 = dict(a=a, anchor=anchor, count=0, rounds_left=1, limit=a + 40, budget=512, eos=-1, ctx_new=ctx_new,
+               ctx_pos=a - ctx_new, ctx_lo=ctx_lo, run=1, skip_rounds=1, stop_at=a + 64, ckpt_slot=-1,
+               tokens=[anchor])
+    eng.set_state(**st0)
+    torch.cuda.synchronize()
+    print(f"case engine round seed={seed}", flush=True)
+    eng.round(0, a)
+    torch.cuda.synchronize()
+    B, V, N = desc.block, desc.vocab, desc.crop_rows
+    st = eng.state()
+    base_gpu = eng.download("base", np.float32)[:B * ((N + 1 + 15) // 16 * 16)].reshape(B, -1)
+    logits_gpu = eng.download("logits", np.float32, (B, V))
+    keys_gpu = eng.download("keys", np.uint64, (2 * B,))[:B]
+    rope = rnd.h2f(eng.download("rope", np.uint16)).reshape(-1, desc.head_dim)
+    W = rnd.Weights(desc, weights)
+
+    # context projection -> drafter ring rows of positions ctx_pos .. ctx_pos + ctx_new - 1
+    rnd.context_projection(W, C, st0, rope)
+    kr, vr = host.kv_from_pages(torch.from_numpy(eng.download("ring.D1.k", np.uint16)).view(torch.float16).reshape(
+        -1, desc.kv_heads, 32, desc.head_dim), torch.from_numpy(eng.download("ring.D1.v", np.uint16)).view(
+        torch.float16).reshape(-1, desc.kv_heads, desc.head_dim, 32), range(a - ctx_new, a),
+        torch.from_numpy(eng.download("ring_table", np.int32)))
+    want_k = C.ring[1][0][a - ctx_new:a]
+    assert np.max(np.abs(kr.astype(np.float64) - want_k)) <= 2e-2 * max(1.0, np.max(np.abs(want_k)))
+
+    # drafter block -> cropped head outputs
+    base = rnd.drafter_block(W, C, st0, rope)
+    scale = np.max(np.abs(base[:, :N + 1]))
+    err = np.max(np.abs(base_gpu[:, :N + 1] - base[:, :N + 1]))
+    print(f"base max-abs {err:.3e} (scale {scale:.2f})", flush=True)
+    assert err <= 2e-2 * scale
+
+    # Markov drafts from the GPU's own base: exact up to near ties
+    toks, M, zs = rnd.markov(W, dict(st0), base_gpu.astype(np.float64))
+    gpu_toks = [anchor] + list(st.tokens)[1:st.M]  # commit replaced tokens[0] by the bonus token
+    assert st.M >= 1
+    for j in range(1, min(len(toks), len(gpu_toks))):
+        if toks[j] != gpu_toks[j]:
+            crop = list(weights["crop_ids"])
+            assert near_tie_ok(zs[j - 1], crop.index(gpu_toks[j]), crop.index(toks[j])), (j, toks, gpu_toks)
+            break
+    else:
+        assert M == st.M and toks == gpu_toks
+
+    # verify over the tokens the GPU verified
+    verified = gpu_toks + list(st.tokens)[st.M:B]  # positions past M hold what the State held (verified, unused)
+    logits = rnd.verify(W, C, dict(st0, tokens=verified), verified[:B], rope)
+    lscale = np.max(np.abs(logits))
+    lerr = np.max(np.abs(logits_gpu - logits))
+    print(f"logits max-abs {lerr:.3e} (scale {lscale:.2f})", flush=True)
+    assert lerr <= 2e-2 * lscale
+    # argmax keys on the GPU's logits are bit-exact with the oracle's key rule
+    seen = eng.download("seen", np.uint32)
+    want_keys = orc.verify_argmax(logits_gpu.astype(np.float32), seen, np.array(verified[:B], np.int32))
+    assert np.array_equal(keys_gpu, want_keys)
+    # and agree with the oracle's own logits up to near ties
+    ok = orc.keys_to_tokens(orc.verify_argmax(logits.astype(np.float32), seen, np.array(verified[:B], np.int32)))
+    for t in range(st.M):
+        g = int(orc.keys_to_tokens(keys_gpu[t:t + 1])[0])
+        assert near_tie_ok(logits[t], g, int(ok[t])), (t, g, ok[t])
+    # commit books: the oracle's accept_commit on the same keys
+    ost = orc.new_state(**dict(st0, tokens=verified[:st.M]))
+    out = np.zeros(1024, np.int32)
+    acc = orc.accept_commit(ost, orc.keys_to_tokens(keys_gpu), st.M, out, np.zeros_like(seen))
+    for f in host.STATE_FIELDS:
+        if f in ("M",):
+            continue
+        assert getattr(st, f) == getattr(ost, f), f
+    assert st.a == a + acc + 1
+    got_out = eng.download("out_tokens", np.int32)[:st.count]
+    assert got_out.tolist() == out[:st.count].tolist()
+    eng.close()
