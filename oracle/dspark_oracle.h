@@ -17,7 +17,7 @@
  *   int8 GEMM / crop head ... numpy fp64 matmul; quantization KATs internal/weights/quant_test.go:9-55
  *   Markov lane transpose ... reference KAT cmd/pack/main_test.go:8-28
  *   target/drafter layers ... composed of the pinned pieces above + numpy restatements of RMS norm, RoPE,
- *                             short conv (tests/test_oracle_layers.py)
+ *                             short conv (tests/test_oracle.py::test_rms_norm_rope_conv)
  */
 #ifndef DSPARK_ORACLE_H
 #define DSPARK_ORACLE_H
