@@ -3,12 +3,12 @@
 
 Default workload ("C2"): verify attention alone, 6 GQA layers (32 query / 8 KV heads,
 head_dim 64), fp16 K/V cache at context 32768, 16 verify tokens per step, causal inside the drafted block. A step
-runs each layer's verify attention (split pass + combine) over pages that already hold the 16 tokens' own K/V.
+runs each layer's verify attention (one kernel: key splits + fused merge) over pages that already hold the 16 tokens' own K/V.
 Inputs are synthetic N(0,1) fp16 resident in HBM; two full KV sets (2 x 6 x 64 MiB) alternate between steps so the
 256 MB Infinity Cache cannot serve a step from the previous one.
 
-Prints one JSON line (the driver's contract) with a `roofline` object for the dominant kernel (the split pass,
-`verify_attn_kernel`) timed with HIP events on the library's stream, and a `cpu_baseline` object (the C oracle's
+Prints one JSON line (the driver's contract) with a `roofline` object for the dominant kernel (`verify_attn_kernel`,
+the only kernel of the step) timed with HIP events on the library's stream, and a `cpu_baseline` object (the C oracle's
 fp32 multi-threaded restatement timed on a bounded sample of the same workload).
 """
 import argparse
@@ -100,7 +100,7 @@ def bench_c2(args, host, torch):
     out = [torch.empty((M, QH, D), dtype=torch.float16, device=dev) for _ in range(L)]
     argv = [[host.attn_args(q[l], kv[s][l][0], kv[s][l][1], ctx, out=out[l]) for l in range(L)] for s in range(SETS)]
     need = lib.dspark_verify_attention_workspace(ctypes.byref(argv[0][0]))
-    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
     for s in range(SETS):
         for l in range(L):
             argv[s][l].workspace, argv[s][l].workspace_bytes = ws.data_ptr(), ws.numel()
@@ -134,32 +134,37 @@ def bench_c2(args, host, torch):
     layer_bytes = ctx * KVH * D * 2 * 2
     step_bytes = L * layer_bytes
 
-    # Dominant kernel (the split pass): the same launches back to back, HIP events around the whole run on the
-    # library's stream, average = elapsed / launches (launch gaps included, so this errs low).
+    # Dominant kernel: a step is L launches of verify_attn_kernel (key splits with the fused merge) and nothing else,
+    # so its average launch duration is the timed region's HIP-event time (recorded on the library's stream) over
+    # the launches; the gaps between launches are included, so this errs low.
     n_launch = args.steps * L
-    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    b0.record(stream)
-    for i in range(args.steps):
-        for l in range(L):
-            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
-    b1.record(stream)
-    torch.cuda.synchronize()
-    split_avg = b0.elapsed_time(b1) / n_launch
-    # Per-launch brackets (event overhead included, so these err high), split and combine separately.
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_launch)]
+    kern_avg = total_ms / n_launch
+    # Per-launch brackets (event overhead included, so these err high).
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n_launch)]
     j = 0
     for i in range(args.steps):
         for l in range(L):
             ev[j][0].record(stream)
-            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
+            host.check(lib.dspark_verify_attention(ctypes.byref(argv[i % SETS][l]), sh), "verify_attention")
             ev[j][1].record(stream)
-            host.check(lib.dspark_verify_attention_combine(ctypes.byref(argv[i % SETS][l]), sh), "combine")
-            ev[j][2].record(stream)
             j += 1
     torch.cuda.synchronize()
-    split_br = sorted(e[0].elapsed_time(e[1]) for e in ev)
-    comb_br = sorted(e[1].elapsed_time(e[2]) for e in ev)
-    achieved = layer_bytes / (split_avg * 1e-3) / 1e9
+    fused_br = sorted(e[0].elapsed_time(e[1]) for e in ev)
+    # For comparison: the same work as two launches (split pass, then the stand-alone merge).
+    t0, t1, t2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    t0.record(stream)
+    for i in range(args.steps):
+        for l in range(L):
+            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
+    t1.record(stream)
+    for i in range(args.steps):
+        for l in range(L):
+            host.check(lib.dspark_verify_attention_combine(ctypes.byref(argv[i % SETS][l]), sh), "combine")
+    t2.record(stream)
+    torch.cuda.synchronize()
+    split_only = t0.elapsed_time(t1) / n_launch
+    combine_only = t1.elapsed_time(t2) / n_launch
+    achieved = layer_bytes / (kern_avg * 1e-3) / 1e9
     traffic = read_traffic()
     res = {
         "metric": METRIC,
@@ -175,16 +180,17 @@ def bench_c2(args, host, torch):
         "dtype": "fp16",
         "data": "synthetic N(0,1) fp16 K/V/Q resident in HBM, 2 rotating KV sets",
         "config": {"workload": "C2 verify attention (BASELINE configs[1]): 6 GQA layers, 32 q / 8 kv heads, head_dim 64, "
-                               "fp16 paged K/V at context 32768, 16 verify tokens causal in block; per layer: split pass + "
-                               "combine (the block's K/V appended once at setup)",
+                               "fp16 paged K/V at context 32768, 16 verify tokens causal in block; per layer one launch "
+                               "(key splits + fused merge; the block's K/V appended once at setup)",
                    "layers": L, "ctx": ctx, "verify_tokens": M, "q_heads": QH, "kv_heads": KVH, "head_dim": D,
                    "algorithmic_bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "verify_attn_kernel", "algorithmic_bytes_per_launch": layer_bytes,
-                     "avg_launch_us": round(split_avg * 1e3, 2),
-                     "bracketed_median_us": round(split_br[len(split_br) // 2] * 1e3, 2),
-                     "combine_bracketed_median_us": round(comb_br[len(comb_br) // 2] * 1e3, 2)},
+                     "avg_launch_us": round(kern_avg * 1e3, 2),
+                     "bracketed_median_us": round(fused_br[len(fused_br) // 2] * 1e3, 2),
+                     "two_launch_split_us": round(split_only * 1e3, 2),
+                     "two_launch_combine_us": round(combine_only * 1e3, 2)},
     }
     return res
 

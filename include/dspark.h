@@ -71,7 +71,10 @@ typedef struct dspark_attn_args {
   void* out;                   /* fp16 [M][QH][D] or NULL */
   float* out_f32;              /* fp32 [M][QH][D] or NULL */
   const float* gate;           /* fp32 [M][QH] pre-sigmoid gate or NULL (target layers gate the output) */
-  void* workspace;             /* split partials; size from dspark_verify_attention_workspace */
+  void* workspace;             /* split partials + split-arrival counters; size from dspark_verify_attention_workspace.
+                                  Zero-fill it before its first use: each dspark_verify_attention call leaves its
+                                  counters at zero again, so one workspace serves any number of stream-ordered calls
+                                  (calls that overlap on different streams need separate workspaces). */
   size_t workspace_bytes;
   int32_t M, QH, KVH, D;       /* D in {64, 128}; QH % KVH == 0; 1 <= M <= DSPARK_MT_MAX */
   int32_t a, start, window, causal;
@@ -80,9 +83,11 @@ typedef struct dspark_attn_args {
 
 size_t dspark_verify_attention_workspace(const dspark_attn_args* args);
 int dspark_verify_attention(const dspark_attn_args* args, dspark_stream_t stream);
-/* The two phases of dspark_verify_attention, for callers that schedule them apart (the reference separates them by a
- * grid barrier: attention phase, then combine_phase, dspark.hip:2519-2556): the key-split pass writes partials into
- * the workspace; the combine merges them (same args, same workspace, same stream order). */
+/* dspark_verify_attention runs one kernel: key-range splits write partials and the last split of each (KV head, row
+ * group) to finish merges them in split order. The two phases below do the same work as two launches, for callers
+ * that schedule them apart (the reference separates them by a grid barrier: attention phase, then combine_phase,
+ * dspark.hip:2519-2556): the key-split pass writes partials into the workspace; the combine merges them (same args,
+ * same workspace, same stream order). Both paths give bit-identical outputs. */
 int dspark_verify_attention_splits(const dspark_attn_args* args, dspark_stream_t stream);
 int dspark_verify_attention_combine(const dspark_attn_args* args, dspark_stream_t stream);
 

@@ -1,24 +1,25 @@
-// Verify attention for gfx950: one pass over each KV head's pages for all verified tokens and all query heads of the
+// Verify attention for gfx950: each KV head's pages are read once for all verified tokens and all query heads of the
 // GQA group, on the matrix cores.
 //
-// Work split. A workgroup owns one (KV head, row group, key split); its four waves take the split's 32-key pages in
-// turn, so every K/V byte travels from HBM into exactly one wave's registers and no LDS staging is needed. A wave
-// holds all QB*16 query rows (token t, group member j -> row t*G + j) of its row group:
-//   S^T[keys][rows] = K[keys][D] * Q^T[D][rows]           (A = K rows, 16-byte loads straight from a K page)
-//   O^T[D][rows]   += V^T[D][keys] * P^T[keys][rows]      (A = V^T rows, 16-byte loads from a transposed V page)
+// Tile math (both kernels). In the 16x16x32 MFMA layout a lane holds one query row (lane % 16):
+//   S^T[keys][rows] = K[keys][D] * Q^T[D][rows]           (A = K rows from a page, B = Q)
+//   O^T[D][rows]   += V^T[D][keys] * P^T[keys][rows]      (A = V^T rows from a transposed page)
 //   l[rows]        += ones[16][keys] * P^T[keys][rows]    (the softmax row sum rides the matrix cores too)
-// In the 16x16x32 layout a lane holds one query row (lane % 16) in both S^T and O^T, so the online-softmax state of
-// a row is lane-local apart from the 4-lane max exchange when the running max moves. The running max moves lazily:
-// only when a score exceeds it by more than TAU (P stays <= 2^TAU, exact in fp16), so the common tile costs one
-// max3 tree, one compare and a ballot per 8 scores.
-//
+// so the online-softmax state of a row is lane-local apart from the 4-lane max exchange when the running max moves.
+// The running max moves lazily: only when a score exceeds it by more than TAU (P stays <= 2^TAU, exact in fp16).
 // The K rows of key block b of a page are permuted (row m <- key 8*(m/4) + 4*b + m%4) so that the P^T values a lane
-// ends up with are keys 8*(lane/16)..+7 of the page -- exactly the contiguous 16 bytes its V^T load holds. K pages are
-// stored in that operand order, so both K and V loads read whole contiguous kilobytes.
+// ends up with are keys 8*(lane/16)..+7 of the page -- exactly the 16 bytes its V^T operand holds. K pages are stored
+// in that operand order, so K and V reads are whole contiguous kilobytes.
 //
-// Splits write unnormalised partials (acc, max, sum); attn_combine merges them in a fixed order (deterministic, no
-// float atomics), applies the optional sigmoid gate and stores fp16/fp32. Reference: dspark.hip:1070-1412
-// (attention_pass), 1488-2120 (attention_v2/v3), 2132-2185 (combine_phase); masks 975-978, 1308-1312, 2006-2012.
+// Work split. verify_attn_lds_kernel: a workgroup per (KV head, key split) holds every query row of the head, one
+// wave per 16-row block and page lane, and streams the split's pages through an LDS ring (each page read from HBM
+// once). verify_attn_kernel (shapes the LDS kernel does not cover): a workgroup per (KV head, row group, key split),
+// its four waves take pages in turn into registers.
+//
+// Splits write unnormalised partials (acc, max, sum); attn_combine_kernel merges them in a fixed order
+// (deterministic, no float atomics), applies the optional sigmoid gate and stores fp16/fp32. Reference:
+// dspark.hip:1070-1412 (attention_pass), 1488-2120 (attention_v2/v3), 2132-2185 (combine_phase); masks 975-978,
+// 1308-1312, 2006-2012.
 #include "common.h"
 #include "dspark.h"
 #include "dspark_internal.h"
@@ -37,8 +38,13 @@ struct Tile {
 // K pages are stored in matrix-core operand order: for key block b and k-step s, 64 lanes x 16 bytes, lane (n, g)
 // holding K[key(n, b)][32 s + 8 g .. + 8] with key(n, b) = 8 (n / 4) + 4 b + n % 4. Every K load instruction then reads
 // 1 KB of contiguous memory. V pages are stored transposed ([d][32 keys]): V load c reads rows 16 c .. 16 c + 15, also
-// 1 KB contiguous. Page loads are non-temporal (the cache policy of a one-pass stream).
-constexpr int NT = 2;  // buffer-load cache-policy bits: nt
+// 1 KB contiguous. Page loads use the default cache policy: when row groups of one split read the same pages (their
+// workgroups sit on one XCD), the second reader hits L2. (Non-temporal loads measured 14.2 us against 11.0 us for a
+// 64 MiB two-reader page stream on MI355X: the second reader missed L2.)
+#ifndef DSPARK_ATTN_CPOL
+#define DSPARK_ATTN_CPOL 0
+#endif
+constexpr int CPOL = DSPARK_ATTN_CPOL;  // buffer-load cache-policy bits
 
 template <int D>
 __device__ __forceinline__ void load_tile(const AttnParams& p, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int h,
@@ -47,17 +53,20 @@ __device__ __forceinline__ void load_tile(const AttnParams& p, __amdgpu_buffer_r
   // traffic, and no branch for the load counter to merge around.
   uint32_t base = 0x80000000u;  // beyond any pool (pools are < 2 GiB)
   if (valid) {
-    const int phys = p.bt ? p.bt[lpage] : lpage;
+    // The page is wave-uniform: a scalar load of the table entry waits on lgkmcnt only. (A vector load here makes
+    // the compiler wait for vmcnt(0) -- every page still in flight -- before the next page's loads are issued.)
+    const int lp = __builtin_amdgcn_readfirstlane(lpage);
+    const int phys = p.bt ? p.bt[lp] : lp;
     base = (uint32_t)(phys * p.KVH + h) * (uint32_t)(PAGE * D * 2);
   }
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int s = 0; s < D / 32; ++s)
-      tl.k[b][s] = as_half8(__builtin_amdgcn_raw_buffer_load_b128(rk, base + lane16 + (uint32_t)((b * (D / 32) + s) * 1024), 0, NT));
+      tl.k[b][s] = as_half8(__builtin_amdgcn_raw_buffer_load_b128(rk, base + lane16 + (uint32_t)((b * (D / 32) + s) * 1024), 0, CPOL));
 #pragma unroll
   for (int c = 0; c < D / 16; ++c)
-    tl.v[c] = as_half8(__builtin_amdgcn_raw_buffer_load_b128(rv, base + voff + (uint32_t)(c * 16 * PAGE * 2), 0, NT));
+    tl.v[c] = as_half8(__builtin_amdgcn_raw_buffer_load_b128(rv, base + voff + (uint32_t)(c * 16 * PAGE * 2), 0, CPOL));
 }
 
 // Q operands: registers, or (QLDS, for many row blocks) an LDS copy in operand order [QB][D/32][64 lanes].
@@ -71,29 +80,45 @@ struct QOps {
   }
 };
 
-// One page for every row block. Q operands carry log2(e)/sqrt(D), and the score MFMA starts from C = -m (the row's
-// running max, log2 units), so its output is already s*log2(e)/sqrt(D) - m: the softmax costs one exp2 per score,
-// a max3 tree, one compare against TAU and a ballot (no rescale in the common tile).
+// Online-softmax state of the rows a wave holds (in the 16x16 MFMA layout a lane owns one row of each 16-row block).
+// Q operands carry log2(e)/sqrt(D) and the score MFMA starts from C = c = -m (the row's running max, log2 units), so
+// its output is already s*log2(e)/sqrt(D) - m: a page costs one exp2 per score, a max3 tree, one compare against TAU
+// and a ballot. The running max moves lazily, only when a score passes it by more than TAU (P stays <= 2^TAU, exact
+// in fp16), so the common page has no rescale.
+template <int D, int QB>
+struct RowState {
+  f32x4 o[QB][D / 16];  // O^T accumulators
+  f32x4 ls[QB];         // row sums (the same value in the 4 lanes of a row)
+  float m[QB];          // running max; M_INIT before the row's first visible key
+  f32x4 c[QB];          // score accumulator start: -m (0 while m is M_INIT)
+};
+
+// Scores of one page for every row block: s[qb][b] = K_b Q^T + c.
 template <int D, int QB, bool QLDS>
-__device__ __forceinline__ void tile_step(const AttnParams& p, const Tile<D>& tl, int lpage, const QOps<D, QB, QLDS>& qf,
-                                          int row0, float (&mrun)[QB], f32x4 (&o)[QB][D / 16], f32x4 (&ls)[QB], int g,
-                                          int lane) {
-  const int base = lpage * PAGE;
-  const bool edge = base < p.full_lo || base + PAGE - 1 > p.full_hi;
-  const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+__device__ __forceinline__ void page_scores(const Tile<D>& tl, const QOps<D, QB, QLDS>& qf, const f32x4 (&c)[QB],
+                                            f32x4 (&s)[QB][2], int lane) {
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    // A row that has not seen a key yet (mrun == M_INIT) starts from C = 0 and adopts its first page's maximum.
-    const bool fresh = mrun[qb] == M_INIT;
-    const float nm = fresh ? 0.f : -mrun[qb];
-    f32x4 s0 = {nm, nm, nm, nm}, s1 = s0;
+    f32x4 s0 = c[qb], s1 = c[qb];
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) {
-      const half8 qs = qf.get(qb, s, lane);
-      s0 = mfma16x16x32(tl.k[0][s], qs, s0);
-      s1 = mfma16x16x32(tl.k[1][s], qs, s1);
+    for (int ks = 0; ks < D / 32; ++ks) {
+      const half8 qs = qf.get(qb, ks, lane);
+      s0 = mfma16x16x32(tl.k[0][ks], qs, s0);
+      s1 = mfma16x16x32(tl.k[1][ks], qs, s1);
     }
-    if (edge) {
+    s[qb][0] = s0;
+    s[qb][1] = s1;
+  }
+}
+
+// Masks (pages at the edges of the visible range only) and the lazy running-max update of one page.
+template <int D, int QB>
+__device__ __forceinline__ void page_prep(const AttnParams& p, int lpage, int row0, RowState<D, QB>& rs,
+                                          f32x4 (&s)[QB][2], int g, int lane) {
+  const int base = lpage * PAGE;
+  if (base < p.full_lo || base + PAGE - 1 > p.full_hi) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
       // Visible keys of the lane's row (token t = row / G; padding rows act as the last token).
       const int t = min((row0 + 16 * qb + (lane & 15)) / p.G, p.M - 1);
       const int lo = max(p.start, p.window > 0 ? p.a + t - p.window + 1 : 0);
@@ -101,38 +126,56 @@ __device__ __forceinline__ void tile_step(const AttnParams& p, const Tile<D>& tl
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int k0 = base + 8 * g + i, k1 = k0 + 4;
-        s0[i] = (k0 >= lo && k0 <= hi) ? s0[i] : -INFINITY;
-        s1[i] = (k1 >= lo && k1 <= hi) ? s1[i] : -INFINITY;
+        s[qb][0][i] = (k0 >= lo && k0 <= hi) ? s[qb][0][i] : -INFINITY;
+        s[qb][1][i] = (k1 >= lo && k1 <= hi) ? s[qb][1][i] : -INFINITY;
       }
     }
-    const float tmax = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-    if (__builtin_amdgcn_ballot_w64(fresh ? tmax > -INFINITY : tmax > TAU) != 0) {
-      // Some row passed its running max by more than TAU (or saw its first key): move that row's max up to its page
-      // maximum. fresh and rm are the same on the four lanes of a row.
-      float rm = fmaxf(tmax, __shfl_xor(tmax, 16));
+  }
+  float tmax[QB];
+  bool need = false;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const f32x4 a = s[qb][0], b = s[qb][1];
+    tmax[qb] = fmaxf(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])), fmaxf(fmaxf(b[0], b[1]), fmaxf(b[2], b[3])));
+    need = need || (rs.m[qb] == M_INIT ? tmax[qb] > -INFINITY : tmax[qb] > TAU);
+  }
+  if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    // Some row passed its running max by more than TAU (or saw its first key): move that row's max up to its page
+    // maximum. m and the row maximum are the same on the four lanes of a row.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const bool fresh = rs.m[qb] == M_INIT;
+      float rm = fmaxf(tmax[qb], __shfl_xor(tmax[qb], 16));
       rm = fmaxf(rm, __shfl_xor(rm, 32));
       if (fresh ? rm > -INFINITY : rm > TAU) {
         const float alpha = fresh ? 0.f : fast_exp2(-rm);
 #pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc) o[qb][cc] *= alpha;
-        ls[qb] *= alpha;
-        mrun[qb] = fresh ? rm : mrun[qb] + rm;
-        s0 -= rm;
-        s1 -= rm;
+        for (int cc = 0; cc < D / 16; ++cc) rs.o[qb][cc] *= alpha;
+        rs.ls[qb] *= alpha;
+        rs.m[qb] = fresh ? rm : rs.m[qb] + rm;
+        rs.c[qb] = f32x4{-rs.m[qb], -rs.m[qb], -rs.m[qb], -rs.m[qb]};
+        s[qb][0] -= rm;
+        s[qb][1] -= rm;
       }
     }
+  }
+}
+
+// P = exp2(scores) in fp16, then O^T += V^T P^T and the row sums ride the matrix cores too (ones x P^T).
+template <int D, int QB>
+__device__ __forceinline__ void page_accumulate(const Tile<D>& tl, RowState<D, QB>& rs, const f32x4 (&s)[QB][2]) {
+  const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
     half8 pp;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pp[i] = (_Float16)fast_exp2(s0[i]);
-      pp[4 + i] = (_Float16)fast_exp2(s1[i]);
+      pp[i] = (_Float16)fast_exp2(s[qb][0][i]);
+      pp[4 + i] = (_Float16)fast_exp2(s[qb][1][i]);
     }
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) o[qb][cc] = mfma16x16x32(tl.v[cc], pp, o[qb][cc]);
-    ls[qb] = mfma16x16x32(ones, pp, ls[qb]);
-    // With many blocks, keep one block's scores live at a time (the scheduler would otherwise hoist every block's
-    // score products ahead of the softmax and run out of registers).
-    if constexpr (QLDS) __builtin_amdgcn_sched_barrier(0);
+    for (int cc = 0; cc < D / 16; ++cc) rs.o[qb][cc] = mfma16x16x32(tl.v[cc], pp, rs.o[qb][cc]);
+    rs.ls[qb] = mfma16x16x32(ones, pp, rs.ls[qb]);
   }
 }
 
@@ -203,19 +246,21 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
       for (int s = 0; s < D / 32; ++s) qf.r[qb][s] = q_operand(qb, s, lane);
   }
 
-  f32x4 o[QB][D / 16];
-  f32x4 ls[QB];
-  float mrun[QB];  // running max of the lane's row (log2 units); the score MFMA starts from -mrun
+  RowState<D, QB> rs;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) o[qb][cc] = f32x4{0, 0, 0, 0};
-    ls[qb] = f32x4{0, 0, 0, 0};
-    mrun[qb] = M_INIT;
+    for (int cc = 0; cc < D / 16; ++cc) rs.o[qb][cc] = f32x4{0, 0, 0, 0};
+    rs.ls[qb] = f32x4{0, 0, 0, 0};
+    rs.m[qb] = M_INIT;
+    rs.c[qb] = f32x4{0, 0, 0, 0};
   }
 
-  // PF pages in flight per wave while one is computed: a ring of PF + 1 register tiles, unrolled so every index is
-  // static. A wave's pages are pb + wave, pb + wave + 4, ...
+  // A wave's pages are pb + wave, pb + wave + 4, ...; a ring of PF + 1 register tiles keeps the next PF pages in
+  // flight, unrolled so every index is static. Software pipeline: in the iteration of page j the score products of
+  // page j + 1 are issued next to the exp2 / PV work of page j (independent, so the matrix cores and the VALU
+  // overlap); the rare running-max update of page j comes first, so page j + 1's scores already use the new max.
+  // Pages past the split load as zeros (out-of-range buffer loads) and their scores are never used.
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)p.kp, (short)0, (int)p.k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)p.vp, (short)0, (int)p.v_bytes, 0x00020000);
   const uint32_t koff = (uint32_t)lane * 16u, voff = (uint32_t)((n * PAGE + 8 * g) * 2);
@@ -225,12 +270,24 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
   Tile<D> buf[NBUF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) load_tile<D>(p, rk, rv, h, pb + wave + 4 * i, pb + wave + 4 * i < pe, buf[i], koff, voff);
+  f32x4 sc[QB][2];
+  page_scores<D, QB, QLDS>(buf[0], qf, rs.c, sc, lane);
   int pg = pb + wave;
   while (pg < pe) {
 #pragma unroll
     for (int j = 0; j < NBUF; ++j) {
       load_tile<D>(p, rk, rv, h, pg + 4 * PF, pg + 4 * PF < pe, buf[(j + PF) % NBUF], koff, voff);
-      if (pg < pe) tile_step<D, QB, QLDS>(p, buf[j], pg, qf, rg * R, mrun, o, ls, g, lane);
+      if (pg < pe) {
+        page_prep<D, QB>(p, pg, rg * R, rs, sc, g, lane);
+        f32x4 sn[QB][2];
+        page_scores<D, QB, QLDS>(buf[(j + 1) % NBUF], qf, rs.c, sn, lane);
+        page_accumulate<D, QB>(buf[j], rs, sc);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          sc[qb][0] = sn[qb][0];
+          sc[qb][1] = sn[qb][1];
+        }
+      }
       pg += 4;
     }
   }
@@ -242,8 +299,8 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)
     if (g == 0) {
-      sm_m[wave][16 * qb + n] = mrun[qb];
-      sm_l[wave][16 * qb + n] = ls[qb][0];
+      sm_m[wave][16 * qb + n] = rs.m[qb];
+      sm_l[wave][16 * qb + n] = rs.ls[qb][0];
     }
   __syncthreads();
   float fw[QB];
@@ -251,13 +308,13 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
   for (int qb = 0; qb < QB; ++qb) {
     const int r = 16 * qb + n;
     const float mx = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
-    fw[qb] = fast_exp2(mrun[qb] - mx);
+    fw[qb] = fast_exp2(rs.m[qb] - mx);
   }
   if (wave & 1) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int cc = 0; cc < D / 16; ++cc) sm_o[wave >> 1][16 * qb + n][4 * cc + g] = o[qb][cc] * fw[qb];
+      for (int cc = 0; cc < D / 16; ++cc) sm_o[wave >> 1][16 * qb + n][4 * cc + g] = rs.o[qb][cc] * fw[qb];
   }
   __syncthreads();
   if (!(wave & 1)) {
@@ -266,7 +323,7 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
         f32x4& dst = sm_o[wave >> 1][16 * qb + n][4 * cc + g];
-        dst = dst + o[qb][cc] * fw[qb];
+        dst = dst + rs.o[qb][cc] * fw[qb];
       }
   }
   __syncthreads();
@@ -284,53 +341,262 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
   }
 }
 
-// One wave per output row (KV head h, row r = t*G + j); lanes over D. Splits merge in index order.
+// ---------------------------------------------------------------- LDS-staged verify attention
+// A workgroup owns one (KV head, key split) and every query row of the head: NW = NRB x PL waves, wave w holds row
+// block rb = w % NRB (16 rows: token t, group member j -> row t*G + j) for page lane pl = w / NRB. Step k of the split
+// covers pages pb + k*PL + pl (pl < PL). The workgroup brings a step's PL pages from HBM into one slot of a 3-slot LDS
+// ring with direct-to-LDS buffer loads -- every page byte crosses HBM once -- and each wave reads its page lane's page
+// from LDS for its rows. Two steps are in flight while one is computed:
+//   step k:  s_waitcnt (this wave's loads of step k done) ; s_barrier (everyone's) ; issue step k + 2 into the slot of
+//            step k - 1 (free: every wave finished step k - 1 before the barrier) ; compute step k.
+// The ring slots are separate LDS arrays selected by static index (the loop is unrolled by 3), which lets the compiler
+// see that reads of slot k never alias the loads in flight into slots k + 1 and k + 2, so it keeps the counted wait
+// above instead of draining every load before each read.
+// LDS page layout: 1 KB chunks in lane order -- K chunk (b, s) holds lane l's 16-byte operand at l*16 (the global
+// layout), V^T chunk c holds lane (n, g)'s keys 8g..8g+7 of row 16c + n at (n + 16g)*16 (permuted by the loads'
+// source offsets), so every ds_read_b128 of the compute is a conflict-free lane-order read.
+// At the end the PL page lanes of each row block merge in order pl = 0, 1, ... through LDS and page lane 0 writes the
+// workgroup's partial (all rows of the head).
+constexpr int RING = 3;
+// Each page has exactly one reader here, so its loads are non-temporal (15.4 against 16.4 us per C2 layer measured).
+#ifndef DSPARK_ATTN_LDS_CPOL
+#define DSPARK_ATTN_LDS_CPOL 2
+#endif
+constexpr int LDS_CPOL = DSPARK_ATTN_LDS_CPOL;
+constexpr int LDS_BT_MAX = 2048;  // pages per split the LDS kernel accepts
+
+__device__ __forceinline__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
+#define DSPARK_LDSP(x) ((__attribute__((address_space(3))) void*)(x))
+
+template <int D, int PL, int LPW>
+__global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
+  constexpr int PAGEB = 4 * PAGE * D;  // K + V bytes of one (page, KV head)
+  constexpr int CPG = PAGEB / 1024;    // 1 KB chunks per page: K chunks first, then V^T chunks
+  __shared__ __attribute__((aligned(16))) char ring0[PL * PAGEB], ring1[PL * PAGEB], ring2[PL * PAGEB];
+  __shared__ __attribute__((aligned(16))) char trash[1024];  // destination of the padding loads
+  __shared__ int32_t sm_bt[LDS_BT_MAX];                       // the split's block-table entries
+  if (p.st) {
+    if (p.st->run == 0) return;
+    attn_range(p);
+  }
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int NRB = p.nrb, NW = NRB * PL;
+  const int rb = wave % NRB, pl = wave / NRB;
+  const int h = blockIdx.x / p.S, split = blockIdx.x % p.S;
+  const int R = NRB * 16;
+
+  // Q operands of the wave's 16 rows, scaled to log2 units
+  QOps<D, 1, false> qf;
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    const int r = rb * 16 + n;
+    u32x4 u = {0, 0, 0, 0};
+    if (r < p.G * p.M) {
+      const int t = r / p.G, qh = h * p.G + r % p.G;
+      u = ldg(reinterpret_cast<const u32x4*>(p.q + ((size_t)t * p.QH + qh) * D + 32 * s + 8 * g));
+    }
+    half8 q = as_half8(u);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
+    qf.r[0][s] = q;
+  }
+  RowState<D, 1> rs;
+#pragma unroll
+  for (int cc = 0; cc < D / 16; ++cc) rs.o[0][cc] = f32x4{0, 0, 0, 0};
+  rs.ls[0] = f32x4{0, 0, 0, 0};
+  rs.m[0] = M_INIT;
+  rs.c[0] = f32x4{0, 0, 0, 0};
+
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)p.kp, (short)0, (int)p.k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)p.vp, (short)0, (int)p.v_bytes, 0x00020000);
+  // split bounds are workgroup-uniform: keep them scalar so every step condition is a scalar branch
+  const int pb = __builtin_amdgcn_readfirstlane(p.page0 + split * p.pps);
+  const int pe = __builtin_amdgcn_readfirstlane(min(pb + p.pps, p.page0 + p.npages));
+  const int nsteps = pe > pb ? (pe - pb + PL - 1) / PL : 0;
+  p.full_lo = __builtin_amdgcn_readfirstlane(p.full_lo);
+  p.full_hi = __builtin_amdgcn_readfirstlane(p.full_hi);
+  const uint32_t koff = (uint32_t)lane * 16u, voff = (uint32_t)(n * 64 + g * 16);
+  // Block-table entries of the split into LDS before any page load: a table read inside the step loop would be a
+  // vector load (the direct-to-LDS loads count as possible clobbers), and its wait would drain the pages in flight.
+  const bool paged = p.bt != nullptr;
+  if (paged) {
+    for (int i = threadIdx.x; i < pe - pb; i += blockDim.x) sm_bt[i] = ldg(p.bt + pb + i);
+    __syncthreads();
+  }
+
+  // Step `k`'s chunks into `slot`: chunk c of [0, PL*CPG) goes to wave c % NW; every wave issues exactly LPW loads
+  // (chunks past the step, or of pages past the split, become out-of-range loads into `trash`), so the counted waits
+  // are compile-time constants.
+  auto issue = [&](int k, char* slot) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int c = wave + i * NW;
+      const int pp = c / CPG, cc = c % CPG;
+      const int page = pb + k * PL + pp;
+      const bool isv = cc >= CPG / 2;
+      char* dst = trash;
+      uint32_t off = 0x80000000u;
+      if (c < PL * CPG && page < pe) {
+        const int phys = paged ? __builtin_amdgcn_readfirstlane(sm_bt[page - pb]) : page;
+        const uint32_t base = (uint32_t)(phys * p.KVH + h) * (uint32_t)(PAGEB / 2);
+        off = isv ? base + (uint32_t)(cc - CPG / 2) * 1024u + voff : base + (uint32_t)cc * 1024u + koff;
+        dst = slot + pp * PAGEB + cc * 1024;
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk, DSPARK_LDSP(dst), 16, off, 0, 0, LDS_CPOL);
+    }
+  };
+  auto step = [&](int k, const char* cur, char* nxt) {
+    if (k + 1 < nsteps)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));  // step k + 1 may still be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_barrier();
+    if (k + 2 < nsteps) issue(k + 2, nxt);
+    const int page = pb + k * PL + pl;
+    if (page < pe) {
+      const char* src = cur + pl * PAGEB;
+      Tile<D> tl;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        tl.k[c / (D / 32)][c % (D / 32)] = *reinterpret_cast<const half8*>(src + c * 1024 + lane * 16);
+        tl.v[c] = *reinterpret_cast<const half8*>(src + (D / 16 + c) * 1024 + lane * 16);
+      }
+      f32x4 sc[1][2];
+      page_scores<D, 1, false>(tl, qf, rs.c, sc, lane);
+      page_prep<D, 1>(p, page, rb * 16, rs, sc, g, lane);
+      page_accumulate<D, 1>(tl, rs, sc);
+    }
+  };
+  // Q (and the table) loads complete before the first page load is issued: a wait for them placed after the page
+  // loads would wait for the pages too (the load counter is in order).
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if (nsteps > 0) issue(0, ring0);
+  if (nsteps > 1) issue(1, ring1);
+  for (int k = 0; k < nsteps; k += RING) {
+    step(k, ring0, ring2);
+    if (k + 1 < nsteps) step(k + 1, ring1, ring0);
+    if (k + 2 < nsteps) step(k + 2, ring2, ring1);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // Page lanes of each row block merge in order through LDS: row block rb's state goes to ring slot rb % 3 at
+  // (rb / 3) * 16 rows of (D + 6) floats: o [16][D + 4], then m [16] and l [16].
+  if constexpr (PL > 1) {
+    constexpr int ROWF = D + 4;
+    char* const slots[RING] = {ring0, ring1, ring2};
+    for (int r = 1; r < PL; ++r) {
+      __syncthreads();
+      float* area = nullptr;
+#pragma unroll
+      for (int i = 0; i < RING; ++i)
+        if (rb % RING == i) area = reinterpret_cast<float*>(slots[i]) + (rb / RING) * 16 * (ROWF + 2);
+      if (pl == r) {
+#pragma unroll
+        for (int cc = 0; cc < D / 16; ++cc) *reinterpret_cast<f32x4*>(area + n * ROWF + 16 * cc + 4 * g) = rs.o[0][cc];
+        if (g == 0) {
+          area[16 * ROWF + n] = rs.m[0];
+          area[16 * ROWF + 16 + n] = rs.ls[0][0];
+        }
+      }
+      __syncthreads();
+      if (pl == 0) {
+        const float mb = area[16 * ROWF + n], lb = area[16 * ROWF + 16 + n];
+        const float mx = fmaxf(rs.m[0], mb);
+        const float fa = fast_exp2(rs.m[0] - mx), fb = fast_exp2(mb - mx);
+#pragma unroll
+        for (int cc = 0; cc < D / 16; ++cc)
+          rs.o[0][cc] = rs.o[0][cc] * fa + *reinterpret_cast<const f32x4*>(area + n * ROWF + 16 * cc + 4 * g) * fb;
+        rs.ls[0] = rs.ls[0] * fa + f32x4{lb, lb, lb, lb} * fb;
+        rs.m[0] = mx;
+      }
+    }
+  }
+  if (pl != 0) return;
+  const size_t slot = (size_t)h * p.S + split;
+  float* dst = p.part_acc + (slot * R + rb * 16 + n) * D;
+#pragma unroll
+  for (int cc = 0; cc < D / 16; ++cc) *reinterpret_cast<f32x4*>(dst + 16 * cc + 4 * g) = rs.o[0][cc];
+  if (g == 0) {
+    const float L = rs.ls[0][0];
+    p.part_ml[slot * R + rb * 16 + n] = f32x2{L > 0.f ? rs.m[0] : -INFINITY, L};
+  }
+}
+#undef DSPARK_LDSP
+
+// ---------------------------------------------------------------- merge of the split partials
+// Four lanes per output quad (row r, dims 4 c4 .. + 3): lane j takes splits j, j + 4, ... with all its loads in flight
+// and merges them as an online log-sum-exp (m = max, l = sum f_s l_s, acc = sum f_s acc_s, f_s = exp2(m_s - m)); the
+// four lanes then merge in the fixed order ((0 + 1) + 2) + 3, so outputs are bit-identical run to run. o = acc / l (0
+// when nothing was visible), times the optional sigmoid gate, stored fp16 and/or fp32. blockIdx.y = KV head x row
+// group. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
+constexpr int COMBINE_LANES = 4, COMBINE_MAX_PER_LANE = 16;  // S <= 64
+
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
   if (p.st && p.st->run == 0) return;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rows = p.G * p.M;
-  const int task = blockIdx.x * 4 + wave;
-  if (task >= p.KVH * rows) return;
-  const int h = task / rows, r = task % rows;
-  const int R = p.R, rg = r / R, rr = r % R;
-  const int t = r / p.G, qh = h * p.G + r % p.G;
-  const size_t slot0 = ((size_t)h * p.RG + rg) * p.S;
-  float ms = -INFINITY, lsv = 0.f;
-  if (lane < p.S) {
-    const f32x2 ml = p.part_ml[(slot0 + lane) * R + rr];
-    ms = ml[0];
-    lsv = ml[1];
+  const int hr = blockIdx.y, h = hr / p.RG, rg = hr % p.RG;
+  const int R = p.R;
+  const int e = blockIdx.x * (256 / COMBINE_LANES) + (int)(threadIdx.x / COMBINE_LANES);
+  const int j = threadIdx.x % COMBINE_LANES;
+  const bool live = e < R * D / 4;
+  const int r = live ? e / (D / 4) : 0, c4 = e % (D / 4);
+  const size_t slot0 = (size_t)hr * p.S;
+  f32x2 ml[COMBINE_MAX_PER_LANE];
+  f32x4 av[COMBINE_MAX_PER_LANE];
+#pragma unroll
+  for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
+    const int sp = j + COMBINE_LANES * i;
+    const bool ok = live && sp < p.S;
+    ml[i] = ok ? ldg(p.part_ml + (slot0 + sp) * R + r) : f32x2{-INFINITY, 0.f};
+    av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + ((slot0 + sp) * R + r) * D) + c4) : f32x4{0, 0, 0, 0};
   }
-  const float mx = wave_max(ms);
-  const float f = (ms == -INFINITY) ? 0.f : fast_exp2(ms - mx);
-  const float L = wave_sum(f * lsv);
-  constexpr int DL = D / 64;
-  float acc[DL];
+  float m = -INFINITY, l = 0.f;
+  f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-  for (int k = 0; k < DL; ++k) acc[k] = 0.f;
-  const float* src = p.part_acc + (slot0 * R + rr) * D + lane;
-  const size_t sstride = (size_t)R * D;
-  float v[64][DL];
+  for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) m = fmaxf(m, ml[i][0]);
+  if (m > -INFINITY) {
 #pragma unroll
-  for (int j = 0; j < 64; ++j)
-#pragma unroll
-    for (int k = 0; k < DL; ++k) v[j][k] = (j < p.S) ? ldg(src + j * sstride + 64 * k) : 0.f;
-#pragma unroll
-  for (int j = 0; j < 64; ++j) {
-    const float fj = __shfl(f, j);
-#pragma unroll
-    for (int k = 0; k < DL; ++k) acc[k] = fmaf(fj, v[j][k], acc[k]);
+    for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
+      const float f = ml[i][0] == -INFINITY ? 0.f : fast_exp2(ml[i][0] - m);
+      l = fmaf(f, ml[i][1], l);
+      acc += f * av[i];
+    }
   }
-  float scale = L > 0.f ? 1.f / L : 0.f;
+  // lanes 1..3 hand their own (unmerged) states to lane 0 of the quad
+  const int base_lane = (int)(threadIdx.x & 63) & ~(COMBINE_LANES - 1);
+  const float m_own = m, l_own = l;
+  const f32x4 a_own = acc;
+#pragma unroll
+  for (int k = 1; k < COMBINE_LANES; ++k) {
+    const float mk = __shfl(m_own, base_lane + k), lk = __shfl(l_own, base_lane + k);
+    f32x4 ak;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ak[i] = __shfl(a_own[i], base_lane + k);
+    const float mx = fmaxf(m, mk);
+    if (mx > -INFINITY) {
+      const float fa = m == -INFINITY ? 0.f : fast_exp2(m - mx), fb = mk == -INFINITY ? 0.f : fast_exp2(mk - mx);
+      l = l * fa + lk * fb;
+      acc = acc * fa + ak * fb;
+      m = mx;
+    }
+  }
+  if (j != 0 || !live) return;
+  const int row = rg * R + r;
+  if (row >= p.G * p.M) return;
+  float scale = l > 0.f ? 1.f / l : 0.f;
+  const int t = row / p.G, qh = h * p.G + row % p.G;
   if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * p.QH + qh)));
+  acc *= scale;
+  const size_t idx = ((size_t)t * p.QH + qh) * D + 4 * c4;
+  if (p.out16) {
+    half4 hv;
 #pragma unroll
-  for (int k = 0; k < DL; ++k) {
-    const float val = acc[k] * scale;
-    const size_t idx = ((size_t)t * p.QH + qh) * D + lane + 64 * k;
-    if (p.out16) p.out16[idx] = (_Float16)val;
-    if (p.out32) p.out32[idx] = val;
+    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)acc[i];
+    *reinterpret_cast<half4*>(p.out16 + idx) = hv;
   }
+  if (p.out32) *reinterpret_cast<f32x4*>(p.out32 + idx) = acc;
 }
 
 // K/V rows of positions pos0..pos0+n-1 into the pages: one thread per (token, head, 8 dims).
@@ -361,28 +627,63 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const _Float16* k, const 
 }
 
 // ---------------------------------------------------------------- host launchers
-// Two launch shapes. OCC = 1: one 4-wave workgroup per CU, a wave may hold up to 512 VGPR + AGPR -- every query row of
-// its KV head (up to 7 blocks of 16 rows at D = 64, 2 at D = 128) and a ring of PF pages in flight; no page is read
-// twice, which long contexts need. OCC = 2: two workgroups per CU, 256 registers per wave, so at most 2 blocks per
-// wave and row groups of one split share pages through the XCD's L2; twice the waves hide the launch's ramp and
-// drain better, which short splits (few pages per wave) need.
+// Two kernels. The LDS-ring kernel (verify_attn_lds_kernel) reads every page from HBM once for all query rows of its
+// KV head; it covers up to 16 row blocks (256 rows: M <= 64 at 4 query heads per KV head). The register kernel
+// (verify_attn_kernel) covers the rest: a wave holds QB row blocks and takes pages in turn, row groups of one split
+// share pages through the XCD's L2. OCC = 1: one 4-wave workgroup per CU (up to 6 blocks per wave at D = 64);
+// OCC = 2: two workgroups per CU, at most 2 blocks per wave.
 #ifndef DSPARK_ATTN_PF
 #define DSPARK_ATTN_PF 2
 #endif
 #ifndef DSPARK_ATTN_OCC2_MAX_PAGES
 #define DSPARK_ATTN_OCC2_MAX_PAGES 12  // pages per wave (at one workgroup per CU) below which OCC = 2 is used
 #endif
-// The largest blocks per wave at OCC = 1. Up to 9 blocks fit with the Q operands in LDS (QLDS), but with one page in
-// flight such a wave is latency-bound: two row groups of <= 6 blocks are faster on MI355X (measured at M = 33).
-constexpr int QB_MAX_64 = 6, QB_MAX_128 = 2;
-constexpr int QB_MAX_OCC2 = 2;
+#ifndef DSPARK_ATTN_PF2
+#define DSPARK_ATTN_PF2 2  // pages in flight per wave at OCC = 2
+#endif
+#ifndef DSPARK_ATTN_QB_MAX_64
+#define DSPARK_ATTN_QB_MAX_64 6
+#endif
+#ifndef DSPARK_ATTN_QB_MAX_OCC2
+#define DSPARK_ATTN_QB_MAX_OCC2 2
+#endif
+#ifndef DSPARK_ATTN_LDS
+#define DSPARK_ATTN_LDS 1  // 0: register kernel only
+#endif
+constexpr int QB_MAX_64 = DSPARK_ATTN_QB_MAX_64, QB_MAX_128 = 2;
+constexpr int QB_MAX_OCC2 = DSPARK_ATTN_QB_MAX_OCC2;
 
 template <int D, int QB, int OCC>
 static void launch_attn(const AttnParams& p, hipStream_t s) {
   constexpr bool QLDS = QB > 6;
-  constexpr int PF = QLDS ? 1 : (OCC == 2 ? 2 : ((QB * D <= 4 * 64) ? DSPARK_ATTN_PF : 2));
+  constexpr int PF = QLDS ? 1 : (OCC == 2 ? DSPARK_ATTN_PF2 : ((QB * D <= 4 * 64) ? DSPARK_ATTN_PF : 2));
   const int units = p.KVH * p.S;
   hipLaunchKernelGGL((verify_attn_kernel<D, QB, PF, OCC, QLDS>), dim3((units + 7) / 8 * 8 * p.RG), dim3(256), 0, s, p);
+}
+
+template <int D, int PL, int LPW>
+static void launch_lds(const AttnParams& p, hipStream_t s) {
+  hipLaunchKernelGGL((verify_attn_lds_kernel<D, PL, LPW>), dim3(p.KVH * p.S), dim3(p.nrb * PL * 64), 0, s, p);
+}
+
+// LDS-ring shape for nblk row blocks: page lanes PL (NRB * PL <= 16 waves; the page-lane merge fits the ring) and the
+// loads per wave per step LPW = ceil(chunks per page / NRB). Returns false when the register kernel is needed.
+static bool lds_shape(int D, int nblk, int* pl, int* lpw) {
+  if (!DSPARK_ATTN_LDS || nblk < 1 || nblk > 16) return false;
+  const int cpg = D / 8;
+  const int pl_max = D == 64 ? 4 : 2;
+  int PL = 1;
+  for (int c = pl_max; c >= 1; c /= 2) {
+    const size_t slot = (size_t)c * 4 * PAGE * D;
+    const size_t merge = (size_t)((nblk - 1) / RING + 1) * 16 * (D + 6) * 4;
+    if (nblk * c <= 16 && (c == 1 || merge <= slot)) {
+      PL = c;
+      break;
+    }
+  }
+  *pl = PL;
+  *lpw = (cpg + nblk - 1) / nblk;
+  return true;
 }
 
 void attn_plan(AttnParams& p, int D, int cus) {
@@ -395,7 +696,36 @@ void attn_plan(AttnParams& p, int D, int cus) {
   p.full_hi = p.causal ? p.a : hi_last;
   p.page0 = lo0 / PAGE;
   p.npages = hi_last / PAGE - p.page0 + 1;
-  // Launch shape: one workgroup per CU unless the pages per wave are few and the rows fit OCC = 2.
+  p.c = (float)(1.4426950408889634 / std::sqrt((double)D));
+  const int S_req = p.S;
+  auto finish = [&](int S) {
+    S = std::max(1, std::min(S, std::min(64, p.npages)));
+    p.pps = (p.npages + S - 1) / S;
+    p.S = (p.npages + p.pps - 1) / p.pps;
+  };
+  int pl = 0, lpw = 0;
+  // LDS-ring kernel: one workgroup per (KV head, split) holding all rows; enough workgroups for every CU (two per
+  // CU for small ones); splits no longer than its LDS block table.
+  if (lds_shape(D, nblk, &pl, &lpw) && (p.npages + 63) / 64 <= LDS_BT_MAX) {
+    p.lds = 1;
+    p.nrb = nblk;
+    p.pl = pl;
+    p.lpw = lpw;
+    p.RG = 1;
+    p.QB = 1;
+    p.R = 16 * nblk;
+    p.OCC = nblk * pl <= 8 ? 2 : 1;
+    int S = S_req;
+    if (S <= 0) {
+      S = (cus * p.OCC + p.KVH - 1) / p.KVH;
+      S = std::min(S, (p.npages + pl - 1) / pl);  // at least one step per split
+    }
+    S = std::max(S, (p.npages + LDS_BT_MAX - 1) / LDS_BT_MAX);
+    finish(S);
+    return;
+  }
+  // Register kernel: one workgroup per CU unless the pages per wave are few and the rows fit OCC = 2.
+  p.lds = 0;
   const int qb_max1 = D == 64 ? QB_MAX_64 : QB_MAX_128;
   const int rg1 = (nblk + qb_max1 - 1) / qb_max1;
   const double pages_per_wave = (double)p.npages * p.KVH * rg1 / (4.0 * cus);
@@ -404,26 +734,53 @@ void attn_plan(AttnParams& p, int D, int cus) {
   p.RG = (nblk + qb_max - 1) / qb_max;
   p.QB = (nblk + p.RG - 1) / p.RG;
   p.R = 16 * p.QB;
-  int S = p.S;
+  int S = S_req;
   if (S <= 0) {
     const int groups = p.KVH * p.RG;
-    const int target_wgs = cus * p.OCC;
-    S = (target_wgs + groups - 1) / groups;
+    S = (cus * p.OCC + groups - 1) / groups;
     S = std::min(S, (p.npages + 3) / 4);  // at least one page per wave
   }
-  S = std::max(1, std::min(S, std::min(64, p.npages)));
-  p.pps = (p.npages + S - 1) / S;
-  p.S = (p.npages + p.pps - 1) / p.pps;
-  p.c = (float)(1.4426950408889634 / std::sqrt((double)D));
+  finish(S);
 }
+
+// Workspace: partial accumulators [KVH][RG][S][R][D] f32, then (max, sum) pairs [KVH][RG][S][R].
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 size_t attn_workspace_bytes(const AttnParams& p, int D) {
   const size_t slots = (size_t)p.KVH * p.RG * p.S;
-  return slots * p.R * D * sizeof(float) + slots * p.R * sizeof(f32x2) + 256;
+  return round256(slots * p.R * D * sizeof(float)) + round256(slots * p.R * sizeof(f32x2));
 }
 
-int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
-  if (!(phases & 1)) {
+void attn_bind_workspace(AttnParams& p, int D, void* ws) {
+  const size_t slots = (size_t)p.KVH * p.RG * p.S;
+  char* b = static_cast<char*>(ws);
+  p.part_acc = reinterpret_cast<float*>(b);
+  p.part_ml = reinterpret_cast<f32x2_t*>(b + round256(slots * p.R * D * sizeof(float)));
+}
+
+static int launch_split(const AttnParams& p, int D, hipStream_t s) {
+  if (p.lds) {
+    // instantiated shapes (see lds_shape): D = 64: PL 4 (LPW 8, 4, 3, 2), 2 (LPW 2, 1), 1 (LPW 1);
+    // D = 128: PL 2 (LPW 16, 8, 6, 4, 3, 2), 1 (LPW 2, 1)
+    const int key = D * 1000 + p.pl * 100 + p.lpw;
+    switch (key) {
+      case 64408: launch_lds<64, 4, 8>(p, s); break;
+      case 64404: launch_lds<64, 4, 4>(p, s); break;
+      case 64403: launch_lds<64, 4, 3>(p, s); break;
+      case 64402: launch_lds<64, 4, 2>(p, s); break;
+      case 64202: launch_lds<64, 2, 2>(p, s); break;
+      case 64201: launch_lds<64, 2, 1>(p, s); break;
+      case 64101: launch_lds<64, 1, 1>(p, s); break;
+      case 128216: launch_lds<128, 2, 16>(p, s); break;
+      case 128208: launch_lds<128, 2, 8>(p, s); break;
+      case 128206: launch_lds<128, 2, 6>(p, s); break;
+      case 128204: launch_lds<128, 2, 4>(p, s); break;
+      case 128203: launch_lds<128, 2, 3>(p, s); break;
+      case 128202: launch_lds<128, 2, 2>(p, s); break;
+      case 128102: launch_lds<128, 1, 2>(p, s); break;
+      case 128101: launch_lds<128, 1, 1>(p, s); break;
+      default: return DSPARK_EUNSUPPORTED;
+    }
   } else if (D == 64 && p.OCC == 2) {
     if (p.QB == 1) launch_attn<64, 1, 2>(p, s);
     else launch_attn<64, 2, 2>(p, s);
@@ -440,12 +797,21 @@ int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
     if (p.QB == 1) launch_attn<128, 1, 1>(p, s);
     else launch_attn<128, 2, 1>(p, s);
   }
-  const int tasks = p.KVH * p.G * p.M;
-  if (!(phases & 2)) {
-  } else if (D == 64)
-    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
+  return 0;
+}
+
+int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
+  if (phases & 1) {
+    const int rc = launch_split(p, D, s);
+    if (rc) return rc;
+  }
+  if (phases & 2) {
+    const dim3 grid((p.R * D / 4 + 63) / 64, p.KVH * p.RG);
+    if (D == 64)
+      hipLaunchKernelGGL(attn_combine_kernel<64>, grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(attn_combine_kernel<128>, grid, dim3(256), 0, s, p);
+  }
   return (int)hipGetLastError();
 }
 

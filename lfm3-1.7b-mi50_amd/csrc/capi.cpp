@@ -88,12 +88,7 @@ static int verify_attention_phases(const dspark_attn_args* a, int phases, dspark
   AttnParams p = attn_params(a);
   const size_t need = attn_workspace_bytes(p, a->D);
   if (!a->workspace || a->workspace_bytes < need) return DSPARK_ENOSPACE;
-  const size_t slots = (size_t)p.KVH * p.RG * p.S;
-  p.part_acc = static_cast<float*>(a->workspace);
-  // partial (max, sum) pairs after the accumulators, 256-byte aligned
-  const size_t acc_bytes = (slots * p.R * a->D * sizeof(float) + 255) / 256 * 256;
-  p.part_ml = reinterpret_cast<f32x2_t*>(static_cast<char*>(a->workspace) + acc_bytes);
-  if (acc_bytes + slots * p.R * sizeof(f32x2_t) > a->workspace_bytes) return DSPARK_ENOSPACE;
+  attn_bind_workspace(p, a->D, a->workspace);
   return attn_launch(p, a->D, phases, S(stream));
 }
 

@@ -31,6 +31,7 @@ struct AttnParams {
   int a, start, window, causal;
   int page0, npages, pps, S;  // logical page range and its split
   int RG, QB, R, OCC;         // row groups, 16-row blocks per wave, rows per group, workgroups per CU
+  int lds, nrb, pl, lpw;      // LDS-ring kernel: row blocks, page lanes, loads per wave per step
   int full_lo, full_hi;       // pages inside [full_lo, full_hi] need no mask
   float c;                    // log2(e) / sqrt(D)
 };
@@ -100,7 +101,10 @@ int markov_launch(const MarkovParams& p, hipStream_t s);
 int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, hipStream_t s);
 int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);
 size_t attn_workspace_bytes(const AttnParams& p, int D);
-int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);  // phases: 1 split pass, 2 combine, 3 both
+// Carves counters and partials out of a workspace of attn_workspace_bytes (256-byte aligned pieces).
+void attn_bind_workspace(AttnParams& p, int D, void* ws);
+// phases: 1 split pass (partials into the workspace), 2 merge of those partials, 3 both
+int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);
 int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt, int KVH,
                     int D, int pos0, int n, hipStream_t s);
 

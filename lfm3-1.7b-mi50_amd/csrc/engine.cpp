@@ -234,11 +234,8 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   p.S = 0;
   attn_plan(p, d.head_dim, e->cus);
   if (drafter) p.window = d.draft_window;  // attn_range (device) derives start and drops the per-token window
-  const size_t slots = (size_t)p.KVH * p.RG * p.S;
-  const size_t acc_bytes = (slots * p.R * d.head_dim * sizeof(float) + 255) / 256 * 256;
-  if (acc_bytes + slots * p.R * sizeof(f32x2_t) > e->ws_attn_bytes) return DSPARK_ENOSPACE;
-  p.part_acc = static_cast<float*>(e->ws_attn);
-  p.part_ml = reinterpret_cast<f32x2_t*>(static_cast<char*>(e->ws_attn) + acc_bytes);
+  if (attn_workspace_bytes(p, d.head_dim) > e->ws_attn_bytes) return DSPARK_ENOSPACE;
+  attn_bind_workspace(p, d.head_dim, e->ws_attn);
   return attn_launch(p, d.head_dim, 3, s);
 }
 
@@ -541,7 +538,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
   const int G = QH / KVH;
   const size_t rows_pad = (size_t)(G * B + 16 * 8);
-  e->ws_attn_bytes = (size_t)KVH * 64 * rows_pad * (D * 4 + 8) + 1024;
+  e->ws_attn_bytes = (size_t)KVH * 64 * rows_pad * (D * 4 + 8) + (size_t)KVH * 64 * 4 + 4096;
   e->ws_attn = e->alloc("ws_attn", e->ws_attn_bytes, &err);
   e->ws_argmax_bytes = verify_argmax_ws(B, d.vocab);
   e->ws_argmax = e->alloc("ws_argmax", e->ws_argmax_bytes, &err);

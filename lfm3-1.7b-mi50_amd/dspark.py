@@ -119,7 +119,8 @@ class Workspace:
         torch = _torch()
         nbytes = max(int(nbytes), 256)
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            # zero-filled: verify attention keeps split-arrival counters here (zero between calls)
+            self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         return self.buf
 
 

@@ -4,6 +4,8 @@ Bar: max-abs error <= 2e-3 against the oracle on the same seeded fp16 inputs (BA
 run-to-run bit identity. Shapes cover the configs' geometry (32/8/64), the reference geometry (16/4/128), causal and
 bidirectional blocks, sliding windows, a paged block table, empty and ragged contexts.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -83,6 +85,46 @@ def test_verify_attention_matches_oracle(dev, orc, M, QH, KVH, D, a, start, wind
 def test_verify_attention_split_counts(dev, orc, splits):
     host = load_host()
     run_case(dev, orc, host, 16, 32, 8, 64, 3000, splits=splits, seed=300)
+
+
+@pytest.mark.parametrize("M,D,a,splits", [(16, 64, 5000, 0), (33, 64, 2048, 0), (9, 128, 1500, 0), (16, 64, 3000, 64)])
+def test_one_call_matches_two_phases(dev, orc, M, D, a, splits):
+    """dspark_verify_attention gives the same bits as its two phases called apart (split pass, then merge), call after
+    call on one workspace, with the sigmoid gate."""
+    torch = dev
+    host = load_host()
+    lib = host.lib()
+    QH, KVH = (32, 8) if D == 64 else (16, 4)
+    print(f"case one-call M={M} D={D} a={a} splits={splits}", flush=True)
+    T = a + M
+    q = orc.normal_f16(700 + M, (M, QH, D))
+    k = orc.normal_f16(701 + M, (T, KVH, D))
+    v = orc.normal_f16(702 + M, (T, KVH, D))
+    kp, vp = host.kv_to_pages(f16(torch, k), f16(torch, v))
+    ws = host.Workspace()
+    gate = torch.from_numpy(np.random.default_rng(M).standard_normal((M, QH)).astype(np.float32)).cuda()
+    ref = torch.empty((M, QH, D), dtype=torch.float32, device="cuda")
+    qd = f16(torch, q)  # attn_args keeps raw pointers: the tensors must stay alive while args is used
+    args = host.attn_args(qd, kp, vp, a, out_f32=ref, gate=gate, splits=splits)
+    need = lib.dspark_verify_attention_workspace(ctypes.byref(args))
+    buf = ws.get(need)
+    args.workspace, args.workspace_bytes = buf.data_ptr(), buf.numel()
+    sh = host.stream_handle()
+    host.check(lib.dspark_verify_attention_splits(ctypes.byref(args), sh), "splits")
+    host.check(lib.dspark_verify_attention_combine(ctypes.byref(args), sh), "combine")
+    torch.cuda.synchronize()
+    want = orc.verify_attention(q, k, v, a) * (1.0 / (1.0 + np.exp(-gate.cpu().numpy().astype(np.float64))))[:, :, None]
+    assert np.max(np.abs(ref.cpu().numpy() - want)) <= TOL
+    for rep in range(3):
+        out = torch.full((M, QH, D), float("nan"), dtype=torch.float32, device="cuda")
+        args.out_f32 = out.data_ptr()
+        host.check(lib.dspark_verify_attention(ctypes.byref(args), sh), "verify_attention")
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.max(np.abs(got - want)) <= TOL, f"call {rep}: max-abs {np.max(np.abs(got - want))} vs the oracle"
+        diff = np.abs(got - ref.cpu().numpy())
+        assert torch.equal(out, ref), f"call {rep}: max diff {diff.max()} at {np.unravel_index(diff.argmax(), diff.shape)}, " \
+                                      f"{int((diff > 0).sum())} of {diff.size} differ"
 
 
 def test_verify_attention_c2_full_context(dev, orc):
