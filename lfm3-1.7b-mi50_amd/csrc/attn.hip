@@ -344,20 +344,25 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
 // ---------------------------------------------------------------- LDS-staged verify attention
 // A workgroup owns one (KV head, key split) and every query row of the head: NW = NRB x PL waves, wave w holds row
 // block rb = w % NRB (16 rows: token t, group member j -> row t*G + j) for page lane pl = w / NRB. Step k of the split
-// covers pages pb + k*PL + pl (pl < PL). The workgroup brings a step's PL pages from HBM into one slot of a 3-slot LDS
-// ring with direct-to-LDS buffer loads -- every page byte crosses HBM once -- and each wave reads its page lane's page
-// from LDS for its rows. Two steps are in flight while one is computed:
-//   step k:  s_waitcnt (this wave's loads of step k done) ; s_barrier (everyone's) ; issue step k + 2 into the slot of
-//            step k - 1 (free: every wave finished step k - 1 before the barrier) ; compute step k.
-// The ring slots are separate LDS arrays selected by static index (the loop is unrolled by 3), which lets the compiler
-// see that reads of slot k never alias the loads in flight into slots k + 1 and k + 2, so it keeps the counted wait
-// above instead of draining every load before each read.
+// covers pages pb + k*PL + pl (pl < PL). The workgroup brings a step's PL pages from HBM into one slot of a RING-slot
+// LDS ring with direct-to-LDS buffer loads -- every page byte crosses HBM once -- and each wave reads its page lane's page
+// from LDS for its rows. RING - 1 steps are in flight while one is computed:
+//   step k:  s_waitcnt (this wave's loads of step k done) ; s_barrier (everyone's) ; issue step k + RING - 1 into the
+//            slot of step k - 1 (free: every wave finished step k - 1 before the barrier) ; compute step k.
+// The ring slots are separate LDS arrays selected by static index (the loop is unrolled by RING), which lets the
+// compiler see that reads of slot k never alias the loads in flight into the other slots, so it keeps the counted
+// wait above instead of draining every load before each read. (3 slots measured 16.2 against 16.5 us for 4 slots per
+// C2 layer on MI355X.)
 // LDS page layout: 1 KB chunks in lane order -- K chunk (b, s) holds lane l's 16-byte operand at l*16 (the global
 // layout), V^T chunk c holds lane (n, g)'s keys 8g..8g+7 of row 16c + n at (n + 16g)*16 (permuted by the loads'
 // source offsets), so every ds_read_b128 of the compute is a conflict-free lane-order read.
 // At the end the PL page lanes of each row block merge in order pl = 0, 1, ... through LDS and page lane 0 writes the
 // workgroup's partial (all rows of the head).
-constexpr int RING = 3;
+#ifndef DSPARK_ATTN_RING
+#define DSPARK_ATTN_RING 3
+#endif
+constexpr int RING = DSPARK_ATTN_RING;  // LDS ring slots (3 or 4): RING - 1 steps in flight
+static_assert(RING == 3 || RING == 4, "ring of 3 or 4 slots");
 // Each page has exactly one reader here, so its loads are non-temporal (15.4 against 16.4 us per C2 layer measured).
 #ifndef DSPARK_ATTN_LDS_CPOL
 #define DSPARK_ATTN_LDS_CPOL 2
@@ -374,6 +379,7 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   constexpr int PAGEB = 4 * PAGE * D;  // K + V bytes of one (page, KV head)
   constexpr int CPG = PAGEB / 1024;    // 1 KB chunks per page: K chunks first, then V^T chunks
   __shared__ __attribute__((aligned(16))) char ring0[PL * PAGEB], ring1[PL * PAGEB], ring2[PL * PAGEB];
+  __shared__ __attribute__((aligned(16))) char ring3[RING > 3 ? PL * PAGEB : 16];
   __shared__ __attribute__((aligned(16))) char trash[1024];  // destination of the padding loads
   __shared__ int32_t sm_bt[LDS_BT_MAX];                       // the split's block-table entries
   if (p.st) {
@@ -448,12 +454,16 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
     }
   };
   auto step = [&](int k, const char* cur, char* nxt) {
-    if (k + 1 < nsteps)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));  // step k + 1 may still be in flight
+    // steps issued after step k that may still be in flight
+    const int ahead = min(RING - 2, nsteps - 1 - k);
+    if (RING > 3 && ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPW));
+    else if (ahead >= 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
-    if (k + 2 < nsteps) issue(k + 2, nxt);
+    if (k + RING - 1 < nsteps) issue(k + RING - 1, nxt);
     const int page = pb + k * PL + pl;
     if (page < pe) {
       const char* src = cur + pl * PAGEB;
@@ -472,20 +482,21 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   // Q (and the table) loads complete before the first page load is issued: a wait for them placed after the page
   // loads would wait for the pages too (the load counter is in order).
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  if (nsteps > 0) issue(0, ring0);
-  if (nsteps > 1) issue(1, ring1);
+  char* const slots[4] = {ring0, ring1, ring2, ring3};
+#pragma unroll
+  for (int u = 0; u < RING - 1; ++u)
+    if (u < nsteps) issue(u, slots[u]);
   for (int k = 0; k < nsteps; k += RING) {
-    step(k, ring0, ring2);
-    if (k + 1 < nsteps) step(k + 1, ring1, ring0);
-    if (k + 2 < nsteps) step(k + 2, ring2, ring1);
+#pragma unroll
+    for (int u = 0; u < RING; ++u)
+      if (k + u < nsteps) step(k + u, slots[u], slots[(u + RING - 1) % RING]);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // Page lanes of each row block merge in order through LDS: row block rb's state goes to ring slot rb % 3 at
-  // (rb / 3) * 16 rows of (D + 6) floats: o [16][D + 4], then m [16] and l [16].
+  // Page lanes of each row block merge in order through LDS: row block rb's state goes to ring slot rb % RING at
+  // (rb / RING) * 16 rows of (D + 6) floats: o [16][D + 4], then m [16] and l [16].
   if constexpr (PL > 1) {
     constexpr int ROWF = D + 4;
-    char* const slots[RING] = {ring0, ring1, ring2};
     for (int r = 1; r < PL; ++r) {
       __syncthreads();
       float* area = nullptr;
@@ -531,7 +542,10 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
 // four lanes then merge in the fixed order ((0 + 1) + 2) + 3, so outputs are bit-identical run to run. o = acc / l (0
 // when nothing was visible), times the optional sigmoid gate, stored fp16 and/or fp32. blockIdx.y = KV head x row
 // group. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
-constexpr int COMBINE_LANES = 4, COMBINE_MAX_PER_LANE = 16;  // S <= 64
+#ifndef DSPARK_ATTN_COMBINE_LANES
+#define DSPARK_ATTN_COMBINE_LANES 4
+#endif
+constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 64 / COMBINE_LANES;  // S <= 64
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
@@ -806,7 +820,8 @@ int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
     if (rc) return rc;
   }
   if (phases & 2) {
-    const dim3 grid((p.R * D / 4 + 63) / 64, p.KVH * p.RG);
+    constexpr int QPB = 256 / COMBINE_LANES;  // output quads per block
+    const dim3 grid((p.R * D / 4 + QPB - 1) / QPB, p.KVH * p.RG);
     if (D == 64)
       hipLaunchKernelGGL(attn_combine_kernel<64>, grid, dim3(256), 0, s, p);
     else
