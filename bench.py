@@ -194,6 +194,240 @@ def bench_c2(args, host, torch):
     return res
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+MI50_TOK_S = {1024: 1174.0, 32768: 687.9, 131072: 423.7}  # README.md:233, 235, 237 (cold, median of 3)
+MI50_TAU = {1024: 3.47, 32768: 3.30, 131072: 2.27}         # benchmarks/verify_attention.txt:54-58
+
+
+def bench_c3(args, host, torch):
+    """int8-weight FFN 2048 -> 8192 (SiLU) -> 2048 for M = 16 tokens with one fp16 scale per output
+    row, then the 2048 x 16384 fp16 cropped-head projection with its row argmax. Three weight sets rotate (3 x 100.7 MB
+    > the 256 MB Infinity Cache)."""
+    M, H, I, N = 16, 2048, 8192, 16384
+    SETS = 3
+    dev = "cuda"
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device=dev)
+    g.manual_seed(20261201 + 2)
+
+    def u8(*shape):
+        return torch.randint(1, 256, shape, generator=g, device=dev, dtype=torch.uint8)  # biased int8 in [-127, 127]
+
+    def scales(rows, K):
+        return (torch.rand(rows, generator=g, device=dev) * 0.5 + 0.75).div(73.3 * K ** 0.5).to(torch.float16)
+
+    sets = [dict(up=u8(I, H), up_s=scales(I, H), dn=u8(H, I), dn_s=scales(H, I),
+                 crop=(torch.randn((N, H), generator=g, device=dev) / H ** 0.5).to(torch.float16)) for _ in range(SETS)]
+    x = torch.randn((M, H), generator=g, device=dev).to(torch.float16)
+    hmid = torch.empty((M, I), dtype=torch.float16, device=dev)
+    y16 = torch.empty((M, H), dtype=torch.float16, device=dev)
+    best = torch.empty(M, dtype=torch.int64, device=dev)
+    ws = host.Workspace(dev)
+
+    def up(s):
+        host.gemm_i8(x, s["up"], s["up_s"], epilogue=2, y_f16=hmid, workspace=ws)
+
+    def down(s):
+        host.gemm_i8(hmid, s["dn"], s["dn_s"], epilogue=0, y_f16=y16, workspace=ws)
+
+    def crop(s):
+        host.head_argmax(y16, s["crop"], best=best, workspace=ws)
+
+    def timed(fn, n):
+        for i in range(args.warmup):
+            fn(sets[i % SETS])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            fn(sets[i % SETS])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    t_up, t_dn, t_crop = timed(up, args.steps), timed(down, args.steps), timed(crop, args.steps)
+    t_step = timed(lambda s: (up(s), down(s), crop(s)), args.steps)
+    bytes_up = I * H + 2 * I
+    bytes_dn = H * I + 2 * H
+    bytes_crop = 2 * N * H
+    flops_ffn = 2 * M * H * I * 2
+    flops_crop = 2 * M * H * N
+    total_bytes = bytes_up + bytes_dn + bytes_crop
+    gbs = total_bytes / (t_step * 1e-3) / 1e9
+
+    def k(name, ms, nbytes, flops):
+        return {"kernel": name, "us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+                "mfma_util": round(flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+
+    return {
+        "metric": "C3 int8 FFN + crop head: weight GB/s and MFMA utilisation", "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t_step, 5),
+        "higher_is_better": True, "dtype": "int8 weights, fp16 MFMA, fp32 accumulation",
+        "data": "synthetic: int8 uniform [-127, 127] weights, fp16 N(0,1) activations, 3 rotating weight sets",
+        "config": {"workload": "C3 (BASELINE configs[2]): M=16, FFN 2048->8192 (SiLU epilogue)->2048 int8 with per-row "
+                               "fp16 scales, then 2048x16384 fp16 crop head + row argmax",
+                   "algorithmic_bytes_per_step": total_bytes, "flops_per_step": flops_ffn + flops_crop},
+        "kernels": [k("up 8192x2048 int8 (gemm_kernel)", t_up, bytes_up, flops_ffn / 2),
+                    k("down 2048x8192 int8 (gemm_kernel + split-K reduce)", t_dn, bytes_dn, flops_ffn / 2),
+                    k("crop 16384x2048 fp16 + argmax (gemm_kernel<fp16> + fold)", t_crop, bytes_crop, flops_crop)],
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "mfma_util": round((flops_ffn + flops_crop) / (t_step * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)},
+    }
+
+
+def engine_setup(host, torch, ctx, block, seed):
+    """C4 model (random init, block `block`) with every cache filled for positions < ctx: target K/V pages, the
+    drafter ring, conv histories and taps hold N(0,1) fp16 / fp32 values."""
+    desc = host.c4_desc(block=block)
+    eng = host.Engine(desc, ctx + 4096)
+    eng.init_random(seed)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    for name in eng.names():
+        if name.startswith(("kv.", "ring.D", "conv.")):
+            ptr_, nbytes = eng.tensor(name)
+            chunk = 64 << 20
+            for off in range(0, nbytes, chunk):
+                n = min(chunk, nbytes - off) // 2
+                t = torch.randn(n, generator=g, device="cuda").to(torch.float16)
+                host._hip().hipMemcpy(ctypes.c_void_p(ptr_ + off), ctypes.c_void_p(t.data_ptr()),
+                                      ctypes.c_size_t(2 * n), 3)
+        elif name == "taps":
+            ptr_, nbytes = eng.tensor(name)
+            t = torch.randn(nbytes // 4, generator=g, device="cuda")
+            host._hip().hipMemcpy(ctypes.c_void_p(ptr_), ctypes.c_void_p(t.data_ptr()), ctypes.c_size_t(nbytes), 3)
+    torch.cuda.synchronize()
+    return desc, eng
+
+
+def engine_state(eng, a, anchor, big=1 << 30):
+    eng.set_state(a=a, anchor=anchor, count=0, rounds_left=big, limit=eng.max_context, budget=big, eos=-1,
+                  ctx_new=1, ctx_pos=a - 1, ctx_lo=max(0, a - 2048), run=1, skip_rounds=1, stop_at=eng.max_context,
+                  ckpt_slot=-1, tokens=[anchor])
+
+
+def greedy_chain(eng, host, torch, a0, anchor, n):
+    """The target's greedy continuation of positions a0 + 1 .. a0 + n: one-token verify rounds (force_m = 1).
+
+    The short-conv history is a ring of the last CONV_RING positions, so a chain longer than that overwrites the
+    history of positions before a0; the rings are saved before the chain and restored after it, so that rounds
+    restarted at a0 see the same history the chain started from (the KV pages are position-indexed and need no
+    restore: a round rewrites the rows it verifies before it reads them)."""
+    import numpy as np
+    torch.cuda.synchronize()
+    saved = {nm: eng.download(nm, np.uint16) for nm in eng.names() if nm.startswith("conv.L")}
+    engine_state(eng, a0, anchor)
+    for _ in range(n):
+        eng.round(1, a0)
+    torch.cuda.synchronize()
+    st = eng.state()
+    assert st.count == n, (st.count, n)
+    chain = eng.download("out_tokens", np.int32)[:n].copy()
+    for nm, buf in saved.items():
+        eng.upload(nm, buf)
+    return chain
+
+
+def run_rounds(eng, torch, mode, a0, anchor, warmup, rounds, hist=False):
+    """Timed rounds from position a0; returns (ms per round, committed tokens per round, per-round accepted)."""
+    stream = torch.cuda.current_stream()
+    engine_state(eng, a0, anchor)
+    for _ in range(warmup):
+        eng.round(mode, a0)
+    torch.cuda.synchronize()
+    st0 = eng.state()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(rounds):
+        eng.round(mode, a0)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    st1 = eng.state()
+    ms = e0.elapsed_time(e1) / rounds
+    committed = (st1.count - st0.count) / rounds
+    accs = []
+    if hist:  # untimed: one round at a time, the State read after each
+        for _ in range(rounds):
+            before = eng.state().accepted
+            eng.round(mode, a0)
+            torch.cuda.synchronize()
+            accs.append(eng.state().accepted - before)
+    return ms, committed, accs, st1
+
+
+def plant_drafts(eng, chain, a0, p, seed, vocab):
+    """plant[a0 + i] = chain token of that position with probability p, else a different token."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    ok = rng.random(len(chain)) < p
+    planted = np.where(ok, chain, (chain + 1 + rng.integers(0, vocab - 1, len(chain))) % vocab).astype(np.int32)
+    planted = np.where(ok, chain, np.where(planted == chain, (chain + 1) % vocab, planted)).astype(np.int32)
+    buf = eng.download("plant", np.int32)
+    buf[a0 + 1:a0 + 1 + len(chain)] = planted
+    eng.upload("plant", buf)
+
+
+def p_for_tau(tau, drafts):
+    """Per-position planting probability whose expected committed tokens per round is tau (truncated geometric)."""
+    lo, hi = 0.0, 1.0
+    for _ in range(60):
+        p = (lo + hi) / 2
+        e = sum(p ** k for k in range(1, drafts + 1)) + 1
+        lo, hi = (p, hi) if e < tau else (lo, p)
+    return (lo + hi) / 2
+
+
+def bench_engine(args, host, torch, workload):
+    """C4 / C5 / tiers: the full DSpark round (context projection, drafter, Markov drafts, verify, greedy argmax,
+    acceptance + commit) as HIP-graph replays on a random-init C4 model."""
+    out = []
+    if workload == "c4":
+        cases = [(32768, 16, None)]
+    elif workload == "c5":
+        cases = [(131072, 33, 0.0), (131072, 33, 0.5), (131072, 33, 1.0)]
+    else:  # tiers: the reference's verify block (MT = 9) at the MI50's measured committed tokens per round
+        cases = [(c, 9, ("tau", MI50_TAU[c])) for c in (1024, 32768, 131072)]
+    rounds, warm = args.steps, args.warmup
+    cache = {}
+    for ctx, block, plant in cases:
+        if (ctx, block) not in cache:
+            for k in list(cache):
+                cache.pop(k)[1].close()
+            cache[(ctx, block)] = engine_setup(host, torch, ctx, block, 20261201 + ctx + block)
+        desc, eng = cache[(ctx, block)]
+        a0, anchor = ctx, 17
+        print(f"case {workload} ctx={ctx} block={block} plant={plant}", file=sys.stderr, flush=True)
+        rec = {"ctx": ctx, "block": block}
+        if plant is None:
+            ms, committed, accs, st = run_rounds(eng, torch, 0, a0, anchor, warm, rounds, hist=True)
+            import collections
+            rec["accepted_histogram"] = dict(sorted(collections.Counter(accs).items()))
+        else:
+            p = plant if not isinstance(plant, tuple) else p_for_tau(plant[1], block - 1)
+            need = (warm + rounds + 1) * block + 2
+            chain = greedy_chain(eng, host, torch, a0, anchor, need)
+            plant_drafts(eng, chain, a0, p, 7, desc.vocab)
+            ms, committed, accs, st = run_rounds(eng, torch, -1, a0, anchor, warm, rounds)
+            rec["planted_p"] = round(p, 4)
+            rec["planted_tau_expected"] = round(1 + sum(p ** k for k in range(1, block)), 3)
+        rec.update({"ms_per_round": round(ms, 4), "tokens_per_round": round(committed, 3),
+                    "tok_s": round(committed / (ms * 1e-3), 1)})
+        if isinstance(plant, tuple):
+            rec["mi50_tok_s"] = MI50_TOK_S[ctx]
+            rec["vs_mi50"] = round(rec["tok_s"] / MI50_TOK_S[ctx], 3)
+        out.append(rec)
+        print(json.dumps(rec), file=sys.stderr, flush=True)
+    for k in list(cache):
+        cache.pop(k)[1].close()
+    return {"metric": "greedy decode tok/s (DSpark rounds, random-init C4 model)", "workload": workload,
+            "rounds": rounds, "warmup": warm, "cases": out,
+            "data": "random-init weights (int8 uniform, per-row fp16 scales), N(0,1) fp16 KV caches; planted drafts "
+                    "replay the target's own greedy chain (one-token verify rounds) with per-position probability p"}
+
+
 def bench_copy(args, torch):
     """Plain device copy of a known size: the calibration point for rocprofv3 FETCH_SIZE / WRITE_SIZE."""
     nbytes = 512 << 20
@@ -217,7 +451,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="c2", choices=["c2", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "copy"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -231,6 +465,12 @@ def main():
         print(json.dumps(bench_copy(args, torch)), flush=True)
         return
     host = load_host()
+    if args.workload == "c3":
+        print(json.dumps(bench_c3(args, host, torch)), flush=True)
+        return
+    if args.workload in ("c4", "c5", "tiers"):
+        print(json.dumps(bench_engine(args, host, torch, args.workload)), flush=True)
+        return
     res = bench_c2(args, host, torch)
     if not args.no_cpu:
         sys.path.insert(0, ROOT)

@@ -189,7 +189,9 @@ int dspark_engine_tensor(dspark_engine* e, const char* name, void** ptr, size_t*
 int dspark_engine_tensor_count(dspark_engine* e);
 const char* dspark_engine_tensor_name(dspark_engine* e, int32_t i);
 /* Enqueue one round on `stream`. force_m > 0 skips the drafter and verifies tokens[0..force_m) of the State as they
- * are (the reference's force_m debug mode, dspark.hip:147, 2442-2451). The first call for a (force_m, plan) records
+ * are (the reference's force_m debug mode, dspark.hip:147, 2442-2451). force_m = -1 runs the drafter, then replaces
+ * its drafts by the engine tensor "plant" (int32 by position: draft j of a round at anchor position a is plant[a + j])
+ * -- benchmarks of a set acceptance rate on random-init models; this mode has no counterpart in the reference. The first call for a (force_m, plan) records
  * the round as a HIP graph; later calls replay it. `plan_a` is the position the attention plan is tuned for (any
  * run-time a is correct; the plan is re-recorded when plan_a moves to another 4096-position bucket). */
 int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream);
@@ -205,7 +207,8 @@ typedef struct dspark_launch_args {
   float rep;               /* repetition penalty (1 = none) */
   int32_t rounds;          /* rounds per launch (the reference uses 32) */
   int32_t ctx_new, ctx_pos, ctx_lo;  /* drafter context bookkeeping carried between launches */
-  int32_t force_m;         /* > 0: verify-only rounds of the State's tokens (the tokens array below) */
+  int32_t force_m;         /* > 0: verify-only rounds of the State's tokens (the tokens array below); -1: planted
+                              drafts (see dspark_engine_round) */
   int32_t tokens[DSPARK_MT_MAX];
 } dspark_launch_args;
 

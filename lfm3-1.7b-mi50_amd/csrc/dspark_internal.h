@@ -98,8 +98,10 @@ int conv_launch(const float* mix, const void* conv_w, void* ring, const struct :
                 void* y, hipStream_t s);
 int qkrope_launch(const QkRopeParams& p, hipStream_t s);
 int markov_launch(const MarkovParams& p, hipStream_t s);
-int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, hipStream_t s);
+int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos,
+                       int vocab, int out_cap, hipStream_t s);
 int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);
+int plant_launch(struct ::dspark_state* st, const int32_t* plant, int block, int max_drafts, hipStream_t s);
 size_t attn_workspace_bytes(const AttnParams& p, int D);
 // Carves counters and partials out of a workspace of attn_workspace_bytes (256-byte aligned pieces).
 void attn_bind_workspace(AttnParams& p, int D, void* ws);

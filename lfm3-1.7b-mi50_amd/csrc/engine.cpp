@@ -76,6 +76,7 @@ struct dspark_engine {
   dspark_state* st = nullptr;
   uint32_t* seen = nullptr;
   int32_t* out_tokens = nullptr;
+  int32_t* plant = nullptr;  // planted drafts by position (force_m = -1 rounds)
   float* rep = nullptr;  // [2]: rep, 1/rep
   // activations
   float *h[2] = {nullptr, nullptr}, *mix = nullptr, *vout = nullptr, *w2out = nullptr, *ctxv = nullptr, *ckvout = nullptr,
@@ -277,7 +278,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   const int B = e->B, H = d.hidden;
   uint64_t* vbest = e->keys;
   uint64_t* mbest = e->keys + B;
-  CK(round_begin_launch(e->st, e->keys, 2 * B, e->seen, s));
+  CK(round_begin_launch(e->st, e->keys, 2 * B, e->seen, B, e->max_context + B, d.vocab, e->max_context + 2 * B, s));
   if (force_m > 0) {
     CK(force_m_launch(e->st, force_m, s));
   } else {
@@ -338,6 +339,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     mp.conf_bias = d.conf_bias;
     mp.conf_thr = d.conf_thr;
     CK(markov_launch(mp, s));
+    if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, s));
   }
   // ---- verify
   CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
@@ -508,7 +510,10 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   // request state and activations
   e->st = static_cast<dspark_state*>(e->alloc("state", sizeof(dspark_state), &err));
   e->seen = static_cast<uint32_t*>(e->alloc("seen", (size_t)(d.vocab + 31) / 32 * 4, &err));
-  e->out_tokens = static_cast<int32_t*>(e->alloc("out_tokens", (size_t)(1024 + 2 * B) * 4, &err));
+  // tokens emitted since the State was set: a round commits at most M <= limit - a tokens and limit <= max_context,
+  // so the count stays below max_context
+  e->out_tokens = static_cast<int32_t*>(e->alloc("out_tokens", (size_t)(max_context + 2 * B) * 4, &err));
+  e->plant = static_cast<int32_t*>(e->alloc("plant", (size_t)(positions + B + 1) * 4, &err));
   e->rep = static_cast<float*>(e->alloc("rep", 16, &err));
   e->x_cols = std::max(std::max(H, d.n_taps * H), std::max(d.ffn, d.draft_ffn));
   e->mix_cols = std::max(std::max(3 * H, align16(QH * D + 2 * KVH * D + QH)), ckv_rows);
@@ -655,7 +660,7 @@ int dspark_engine_init_random(dspark_engine* e, uint64_t seed, dspark_stream_t s
 }
 
 int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream) {
-  if (!e || force_m < 0 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
+  if (!e || force_m < -1 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int bucket = plan_a / ROUND_PLAN_BUCKET;
   const auto key = std::make_pair((int)force_m, bucket);
@@ -684,7 +689,7 @@ int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspar
 
 int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t* out_tokens, int32_t max_out,
                          dspark_launch_result* res, dspark_stream_t stream) {
-  if (!e || !a || !res || a->a < 0 || a->rounds < 1 || a->force_m < 0 || a->force_m > e->B) return DSPARK_EINVAL;
+  if (!e || !a || !res || a->a < 0 || a->rounds < 1 || a->force_m < -1 || a->force_m > e->B) return DSPARK_EINVAL;
   if (a->anchor < 0 || a->anchor >= e->d.vocab || a->budget < 1) return DSPARK_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int block_tokens = 32;  // the prefix cache's block (internal/model/engine.go:30)

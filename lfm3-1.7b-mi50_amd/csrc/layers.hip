@@ -245,9 +245,17 @@ __global__ void markov_finalize(MarkovParams p) {
 
 // ---------------------------------------------------------------- round start
 // Clears the per-round scratch the kernels fold into (argmax keys) and the draft count, marks the anchor seen
-// (dspark.hip:2432-2435).
-__global__ void round_begin_kernel(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen) {
+// (dspark.hip:2432-2435). A State the buffers cannot hold -- anchor position a with a + block > max_pos, an anchor
+// outside the vocabulary, or an emitted count with no room for a block more in out_tokens -- stops the run instead
+// (every later kernel of the round returns on run == 0).
+__global__ void round_begin_kernel(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos,
+                                   int vocab, int out_cap) {
   if (stopped(st)) return;
+  const int a = st->a, anchor = st->anchor, count = st->count;
+  if (a < 0 || a + block > max_pos || anchor < 0 || anchor >= vocab || count < 0 || count + block > out_cap) {
+    if (threadIdx.x == 0) st->run = 0;
+    return;
+  }
   for (int i = threadIdx.x; i < nkeys; i += blockDim.x) keys[i] = 0;
   if (threadIdx.x == 0) {
     st->M = 0;
@@ -261,6 +269,19 @@ __global__ void force_m_kernel(dspark_state* st, int m) {
   if (stopped(st) || threadIdx.x != 0) return;
   st->tokens[0] = st->anchor;
   st->M = m;
+}
+
+// Planted drafts (benchmarks of a set acceptance rate on random-init models): after the drafter has run, its drafts
+// are replaced by plant[a + 1 .. a + M - 1], with M = 1 + the drafter's cap on drafts this round (the same cap
+// markov_kernel applies, so limit and budget still bound the round).
+__global__ void plant_kernel(dspark_state* st, const int32_t* plant, int block, int max_drafts) {
+  if (stopped(st) || threadIdx.x != 0) return;
+  const int a = st->a;
+  const int cap = min(min(max_drafts, block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  const int drafts = max(cap, 0);
+  st->tokens[0] = st->anchor;
+  for (int j = 1; j <= drafts; ++j) st->tokens[j] = plant[a + j];
+  st->M = drafts + 1;
 }
 
 // ---------------------------------------------------------------- host launchers
@@ -290,8 +311,13 @@ int markov_launch(const MarkovParams& p, hipStream_t s) {
   hipLaunchKernelGGL(markov_finalize, dim3(1), dim3(64), 0, s, p);
   return (int)hipGetLastError();
 }
-int round_begin_launch(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, hipStream_t s) {
-  hipLaunchKernelGGL(round_begin_kernel, dim3(1), dim3(256), 0, s, st, keys, nkeys, seen);
+int round_begin_launch(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos, int vocab,
+                       int out_cap, hipStream_t s) {
+  hipLaunchKernelGGL(round_begin_kernel, dim3(1), dim3(256), 0, s, st, keys, nkeys, seen, block, max_pos, vocab, out_cap);
+  return (int)hipGetLastError();
+}
+int plant_launch(dspark_state* st, const int32_t* plant, int block, int max_drafts, hipStream_t s) {
+  hipLaunchKernelGGL(plant_kernel, dim3(1), dim3(64), 0, s, st, plant, block, max_drafts);
   return (int)hipGetLastError();
 }
 int force_m_launch(dspark_state* st, int m, hipStream_t s) {
