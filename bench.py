@@ -25,6 +25,7 @@ PKG = os.path.join(ROOT, "lfm3-1.7b-mi50_amd")
 METRIC = "greedy decode tok/s at 1k/32k/128k ctx; verify-attn HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "verify_attn_c2_traffic.txt")
+ROOFLINE_KERNEL = "verify_attn_lds_kernel"
 
 
 def load_host():
@@ -35,7 +36,8 @@ def load_host():
 
 
 def read_traffic():
-    """HBM bytes per launch of verify_attn_kernel from the committed rocprofv3 --pmc summary, if present."""
+    """HBM bytes per launch of the key-split pass from the committed rocprofv3 --pmc summary, if present and taken
+    from the kernel this build launches (the summary's `kernel:` line)."""
     if not os.path.exists(TRAFFIC_FILE):
         return None
     vals = {}
@@ -43,6 +45,8 @@ def read_traffic():
         if ":" in line:
             k, _, v = line.partition(":")
             vals[k.strip()] = v.strip()
+    if not vals.get("kernel", "").startswith(ROOFLINE_KERNEL):
+        return None
     try:
         return int(float(vals["hbm_bytes_per_launch"]))
     except (KeyError, ValueError):

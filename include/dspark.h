@@ -71,10 +71,10 @@ typedef struct dspark_attn_args {
   void* out;                   /* fp16 [M][QH][D] or NULL */
   float* out_f32;              /* fp32 [M][QH][D] or NULL */
   const float* gate;           /* fp32 [M][QH] pre-sigmoid gate or NULL (target layers gate the output) */
-  void* workspace;             /* split partials + split-arrival counters; size from dspark_verify_attention_workspace.
-                                  Zero-fill it before its first use: each dspark_verify_attention call leaves its
-                                  counters at zero again, so one workspace serves any number of stream-ordered calls
-                                  (calls that overlap on different streams need separate workspaces). */
+  void* workspace;             /* per-split partials (o, running max, sum); size from
+                                  dspark_verify_attention_workspace. Needs no clearing: the key-split pass writes every
+                                  partial the merge reads. Stream-ordered calls may share one workspace; calls that
+                                  overlap on different streams need separate workspaces. */
   size_t workspace_bytes;
   int32_t M, QH, KVH, D;       /* D in {64, 128}; QH % KVH == 0; 1 <= M <= DSPARK_MT_MAX */
   int32_t a, start, window, causal;
@@ -83,11 +83,12 @@ typedef struct dspark_attn_args {
 
 size_t dspark_verify_attention_workspace(const dspark_attn_args* args);
 int dspark_verify_attention(const dspark_attn_args* args, dspark_stream_t stream);
-/* dspark_verify_attention runs one kernel: key-range splits write partials and the last split of each (KV head, row
- * group) to finish merges them in split order. The two phases below do the same work as two launches, for callers
- * that schedule them apart (the reference separates them by a grid barrier: attention phase, then combine_phase,
- * dspark.hip:2519-2556): the key-split pass writes partials into the workspace; the combine merges them (same args,
- * same workspace, same stream order). Both paths give bit-identical outputs. */
+/* dspark_verify_attention enqueues two kernels on the stream: the key-split pass (each split of a KV head's key range
+ * writes an unnormalised partial output, its running max and its sum into the workspace) and the merge (partials
+ * combined in split order, normalised, gated, stored). The two phases below are the same kernels called apart, for
+ * callers that schedule them separately (the reference separates them by a grid barrier: attention phase, then
+ * combine_phase, dspark.hip:2519-2556); same args, same workspace, same stream order. Both ways give bit-identical
+ * outputs. */
 int dspark_verify_attention_splits(const dspark_attn_args* args, dspark_stream_t stream);
 int dspark_verify_attention_combine(const dspark_attn_args* args, dspark_stream_t stream);
 

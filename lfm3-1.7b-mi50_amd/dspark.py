@@ -119,7 +119,7 @@ class Workspace:
         torch = _torch()
         nbytes = max(int(nbytes), 256)
         if self.buf is None or self.buf.numel() < nbytes:
-            # zero-filled: verify attention keeps split-arrival counters here (zero between calls)
+            # contents need no clearing (every kernel writes what it later reads); zeros keep a dump readable
             self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         return self.buf
 

@@ -90,7 +90,7 @@ def test_verify_attention_split_counts(dev, orc, splits):
 @pytest.mark.parametrize("M,D,a,splits", [(16, 64, 5000, 0), (33, 64, 2048, 0), (9, 128, 1500, 0), (16, 64, 3000, 64)])
 def test_one_call_matches_two_phases(dev, orc, M, D, a, splits):
     """dspark_verify_attention gives the same bits as its two phases called apart (split pass, then merge), call after
-    call on one workspace, with the sigmoid gate."""
+    call on one workspace that starts out filled with NaN bytes, with the sigmoid gate."""
     torch = dev
     host = load_host()
     lib = host.lib()
@@ -108,6 +108,7 @@ def test_one_call_matches_two_phases(dev, orc, M, D, a, splits):
     args = host.attn_args(qd, kp, vp, a, out_f32=ref, gate=gate, splits=splits)
     need = lib.dspark_verify_attention_workspace(ctypes.byref(args))
     buf = ws.get(need)
+    buf.fill_(0xFF)  # all-NaN partials: the split pass must write every partial the merge reads
     args.workspace, args.workspace_bytes = buf.data_ptr(), buf.numel()
     sh = host.stream_handle()
     host.check(lib.dspark_verify_attention_splits(ctypes.byref(args), sh), "splits")
