@@ -152,7 +152,7 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
-  p.ksplit = gemm_choose_ksplit(N, K, 512);
+  gemm_plan(M, N, K, true, true, &p.ksplit, &p.wpg);
   if (p.ksplit > 1) {
     if (!workspace || workspace_bytes < gemm_ws_bytes(M, N, K)) return DSPARK_ENOSPACE;
     p.part = static_cast<float*>(workspace);
@@ -177,7 +177,7 @@ int dspark_head_argmax_f16(const void* x, int32_t M, int32_t K, const void* w, i
   p.M = M;
   p.N = N;
   p.K = K;
-  p.ksplit = 1;
+  gemm_plan(M, N, K, false, false, &p.ksplit, &p.wpg);
   p.best_part = static_cast<uint64_t*>(workspace);
   p.best = best_keys;
   return gemm_launch(p, false, S(stream));

@@ -46,6 +46,7 @@ struct ResNormParams {
   const float* v;               // bands of [M][H], v_band_stride apart, or nullptr
   int bands;
   size_t v_band_stride;
+  const _Float16* v_scale;      // [H] per-column factor applied to the band sum (split-K partials of a scaled GEMM)
   const _Float16* post_w;       // [H] or nullptr (1)
   const _Float16* norm_w;       // [groups][H]
   size_t norm_w_stride;
@@ -103,7 +104,7 @@ int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uin
 int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);
 int plant_launch(struct ::dspark_state* st, const int32_t* plant, int block, int max_drafts, hipStream_t s);
 size_t attn_workspace_bytes(const AttnParams& p, int D);
-// Carves counters and partials out of a workspace of attn_workspace_bytes (256-byte aligned pieces).
+// Carves the split partials out of a workspace of attn_workspace_bytes (256-byte aligned pieces).
 void attn_bind_workspace(AttnParams& p, int D, void* ws);
 // phases: 1 split pass (partials into the workspace), 2 merge of those partials, 3 both
 int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);
@@ -121,9 +122,11 @@ struct GemmParams {
   uint64_t* best_part;      // row-argmax keys per strip [M][N/16] (head) or nullptr
   uint64_t* best;           // [M]
   int M, N, K, ksplit, epilogue;
+  int defer_reduce;         // split-K: leave the partials for the consumer (a resnorm sums them with the scale)
+  int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
 };
 
-int gemm_choose_ksplit(int N, int K, int target_wgs);
+void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg);
 size_t gemm_ws_bytes(int M, int N, int K);
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
 

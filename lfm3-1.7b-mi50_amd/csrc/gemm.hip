@@ -52,17 +52,34 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
   }
 }
 
-// TB token blocks of 16. I8: weights biased int8, else fp16. Grid: strips * ksplit.
+// TB token blocks of 16. I8: weights biased int8, else fp16.
 __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st && p.st->run == 0; }
 
+// Chunks (64 columns) per batch of weight loads: 16 B per lane per chunk int8, 32 B fp16; two batches in registers.
+template <bool I8>
+constexpr int gemm_cpb() { return I8 ? 8 : 4; }
+constexpr int GEMM_PHASE_UNITS = 32;  // X staged per phase: TB x chunks <= 32 (64 KB of LDS)
+
+// Grid: (ceil(strips / waves per group)) groups x ksplit; each wave owns one 16-row strip and the group's K range.
+// The group stages its X slice into LDS once per phase (64 KB at most), in operand order [tb][chunk][half][lane]
+// (16 B each, so every B-operand read is one contiguous 1 KB row of LDS), and every wave streams its strip's
+// weights in batches of gemm_cpb chunks, the next batch in flight while the current one is multiplied. Loads past
+// the range are clamped to valid addresses and discarded, so the number of loads in flight is the same on every path
+// and the compiler's waits stay counted.
 template <int TB, bool I8>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   if (gemm_stopped(p)) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  extern __shared__ u32x4 xs[];
+  constexpr int CPB = gemm_cpb<I8>(), WV = I8 ? 1 : 2, PH = GEMM_PHASE_UNITS / TB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int strip = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
+  const int grp = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
+  const int strips = p.N / 16;
+  const int strip_raw = grp * nw + wave;
+  const bool live = strip_raw < strips;
+  const int strip = live ? strip_raw : strips - 1;
   const int row0 = strip * 16;
-  const int chunks = p.K / 64;                 // 64 columns per chunk
+  const int chunks = p.K / 64;
   const int cpk = (chunks + p.ksplit - 1) / p.ksplit;
   const int c0 = ks * cpk, c1 = min(chunks, c0 + cpk);
 
@@ -71,40 +88,67 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0, 0, 0, 0};
 
   const uint8_t* wrow = reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K * (I8 ? 1 : 2);
-  for (int c = c0 + wave; c < c1; c += 4) {
-    const int k0 = c * 64;
-    half8 a[2];
-    if (I8) {
-      const u32x4 wv = ldg_nt(reinterpret_cast<const u32x4*>(wrow + k0 + 16 * g));
-      a[0] = i8x8_to_half8(wv[0], wv[1]);
-      a[1] = i8x8_to_half8(wv[2], wv[3]);
-    } else {
-      const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * (k0 + 16 * g));
-      a[0] = as_half8(ldg_nt(wp));
-      a[1] = as_half8(ldg_nt(wp + 1));
-    }
+  // chunks cb .. cb + CPB - 1, clamped to the phase's last chunk ce - 1 (a re-read of a line just fetched)
+  auto load = [&](u32x4 (&w)[CPB][WV], int cb, int ce) {
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int t = 16 * tb + n;
-      half8 b0 = {0, 0, 0, 0, 0, 0, 0, 0}, b1 = b0;
-      if (t < p.M) {
-        const u32x4* xp = reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + k0 + 16 * g);
-        b0 = as_half8(ldg(xp));
-        b1 = as_half8(ldg(xp + 1));
+    for (int i = 0; i < CPB; ++i) {
+      const int c = min(cb + i, ce - 1);
+      if (I8) {
+        w[i][0] = ldg_nt(reinterpret_cast<const u32x4*>(wrow + c * 64 + 16 * g));
+      } else {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * (c * 64 + 16 * g));
+        w[i][0] = ldg_nt(wp);
+        w[i][WV - 1] = ldg_nt(wp + 1);
       }
-      acc[tb] = mfma16x16x32(a[0], b0, acc[tb]);
-      acc[tb] = mfma16x16x32(a[1], b1, acc[tb]);
+    }
+  };
+  // chunk cb + i of the phase starting at chunk ph (pc chunks staged)
+  auto compute = [&](const u32x4 (&w)[CPB][WV], int cb, int ph, int pc) {
+#pragma unroll
+    for (int i = 0; i < CPB; ++i) {
+      const int j = cb + i - ph;
+      if (j < pc) {
+        half8 a[2];
+        if (I8) {
+          a[0] = i8x8_to_half8(w[i][0][0], w[i][0][1]);
+          a[1] = i8x8_to_half8(w[i][0][2], w[i][0][3]);
+        } else {
+          a[0] = as_half8(w[i][0]);
+          a[1] = as_half8(w[i][WV - 1]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          const u32x4* xb = xs + ((size_t)(tb * pc + j) * 2) * 64 + lane;
+          acc[tb] = mfma16x16x32(a[0], as_half8(xb[0]), acc[tb]);
+          acc[tb] = mfma16x16x32(a[1], as_half8(xb[64]), acc[tb]);
+        }
+      }
+    }
+  };
+
+  u32x4 wa[CPB][WV], wb[CPB][WV];
+  for (int ph = c0; ph < c1; ph += PH) {
+    const int pc = min(PH, c1 - ph), pe = ph + pc;
+    load(wa, ph, pe);
+    // stage X[16 TB tokens][chunks ph .. ph + pc) (token rows past M repeat row M - 1: their output columns are
+    // never stored, and a column of the product depends only on its own token)
+    if (ph != c0) __syncthreads();  // every wave is done reading the previous phase
+    const int units = TB * pc * 128;
+#pragma unroll 4
+    for (int u = threadIdx.x; u < units; u += blockDim.x) {
+      const int l = u & 63, h = (u >> 6) & 1, j = (u >> 7) % pc, tb = (u >> 7) / pc;
+      const int t = min(16 * tb + (l & 15), p.M - 1);
+      xs[u] = ldg(reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + (ph + j) * 64 + 16 * (l >> 4) + 8 * h));
+    }
+    __syncthreads();
+    for (int cb = ph; cb < pe; cb += 2 * CPB) {
+      if (cb + CPB < pe) load(wb, cb + CPB, pe);
+      compute(wa, cb, ph, pc);
+      if (cb + 2 * CPB < pe) load(wa, cb + 2 * CPB, pe);
+      if (cb + CPB < pe) compute(wb, cb + CPB, ph, pc);
     }
   }
-
-  // Fixed-order reduction of the four waves.
-  __shared__ f32x4 red[4][TB][64];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) red[wave][tb][lane] = acc[tb];
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb) acc[tb] = ((red[0][tb][lane] + red[1][tb][lane]) + red[2][tb][lane]) + red[3][tb][lane];
+  if (!live) return;
 
   if (p.ksplit > 1) {
     // partial [ks][M][N] fp32, epilogue in the reduce kernel
@@ -163,27 +207,60 @@ __global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int 
   if (threadIdx.x == 0) best[t] = b;
 }
 
+#ifndef DSPARK_GEMM_TARGET_WGS
+#define DSPARK_GEMM_TARGET_WGS 256  // groups x splits to aim for: one workgroup per CU
+#endif
+#ifndef DSPARK_GEMM_MIN_CHUNKS
+#define DSPARK_GEMM_MIN_CHUNKS 4  // a split keeps at least this many 64-column chunks
+#endif
+#ifndef DSPARK_GEMM_MAX_WPG
+#define DSPARK_GEMM_MAX_WPG 8  // widest group (waves = 16-row strips per workgroup)
+#endif
+
+static size_t gemm_lds_bytes(int tb, int K, int ksplit) {
+  const int chunks = K / 64, cpk = (chunks + ksplit - 1) / ksplit;
+  return (size_t)tb * std::min(cpk, GEMM_PHASE_UNITS / tb) * 2048;
+}
+
 template <bool I8>
 static void launch_gemm(const GemmParams& p, hipStream_t s) {
   const int tb = (p.M + 15) / 16;
-  const dim3 grid((p.N / 16) * p.ksplit), block(256);
+  const int strips = p.N / 16;
+  const int groups = (strips + p.wpg - 1) / p.wpg;
+  const dim3 grid(groups * p.ksplit), block(64 * p.wpg);
+  const size_t lds = gemm_lds_bytes(tb, p.K, p.ksplit);
   switch (tb) {
-    case 1: hipLaunchKernelGGL((gemm_kernel<1, I8>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gemm_kernel<2, I8>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_kernel<3, I8>), grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL((gemm_kernel<4, I8>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((gemm_kernel<1, I8>), grid, block, lds, s, p); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<2, I8>), grid, block, lds, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_kernel<3, I8>), grid, block, lds, s, p); break;
+    default: hipLaunchKernelGGL((gemm_kernel<4, I8>), grid, block, lds, s, p); break;
   }
 }
 
-int gemm_choose_ksplit(int N, int K, int target_wgs) {
+// Group width and split-K: the widest group (the most strips sharing one staged X) that, split along K where
+// allowed (each split keeping DSPARK_GEMM_MIN_CHUNKS chunks), still gives DSPARK_GEMM_TARGET_WGS workgroups; failing
+// that, two-strip groups with the deepest split. No split when `split` is false (the fused head argmax needs whole
+// rows).
+void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg) {
+  (void)M;
+  (void)i8;
   const int strips = N / 16, chunks = K / 64;
-  int ks = 1;
-  while (strips * ks < target_wgs && ks * 2 * 4 <= chunks && ks < 16) ks *= 2;
-  return ks;
+  int ks = 1, w = 2;
+  for (w = DSPARK_GEMM_MAX_WPG; w >= 2; w /= 2) {
+    const int groups = (strips + w - 1) / w;
+    ks = 1;
+    if (split)
+      while (groups * ks < DSPARK_GEMM_TARGET_WGS && chunks / (2 * ks) >= DSPARK_GEMM_MIN_CHUNKS && ks < 32) ks *= 2;
+    if (groups * ks >= DSPARK_GEMM_TARGET_WGS) break;
+  }
+  if (w < 2) w = 2;
+  *ksplit = ks;
+  *wpg = std::max(1, std::min(w, strips));
 }
 
 size_t gemm_ws_bytes(int M, int N, int K) {
-  const int ks = gemm_choose_ksplit(N, K, 512);
+  int ks = 1, wpg = 1;
+  gemm_plan(M, N, K, true, true, &ks, &wpg);
   return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
 }
 
@@ -192,7 +269,7 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
     launch_gemm<true>(p, s);
   else
     launch_gemm<false>(p, s);
-  if (p.ksplit > 1) {
+  if (p.ksplit > 1 && !p.defer_reduce) {
     const int threads = p.M * (p.N / 4);
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, p);
   }

@@ -25,36 +25,75 @@ __global__ __launch_bounds__(256) void verify_argmax_partial(const void* logits,
     inv_rep = rep_dev[1];
   }
   const int t = blockIdx.y, chunk = blockIdx.x;
-  // Drafts 1..t that were not seen before this round count as seen for this position (dspark.hip:2226-2232).
+  // Drafts 1..t that were not seen before this round count as seen for this position (dspark.hip:2226-2232). Lane j
+  // of wave 0 looks up draft j; a draft outside the vocabulary matches no logit (and is not looked up in seen).
   __shared__ int dt[DSPARK_MT_MAX];
   __shared__ uint64_t isnew_s;
-  if (threadIdx.x == 0) {
-    uint64_t bits = 0;
-    for (int j = 1; j <= t && j < M; ++j) {
-      dt[j] = st->tokens[j];
-      // a draft outside the vocabulary matches no logit (and is not looked up in seen)
-      if (dt[j] >= 0 && dt[j] < V && ((seen[dt[j] >> 5] >> (dt[j] & 31)) & 1u) == 0) bits |= 1ull << j;
+  if (threadIdx.x < 64) {
+    const int j = threadIdx.x;
+    bool fresh = false;
+    if (j >= 1 && j <= t && j < M) {
+      const int d = st->tokens[j];
+      dt[j] = d;
+      fresh = d >= 0 && d < V && ((seen[d >> 5] >> (d & 31)) & 1u) == 0;
     }
-    isnew_s = bits;
+    const uint64_t bits = __ballot(fresh);
+    if (j == 0) isnew_s = bits;
   }
   __syncthreads();
   const uint64_t isnew = isnew_s;
   uint64_t best = 0;
+  // Four consecutive logits per thread per 1024 (one seen word covers them); every load of the chunk is issued
+  // before the first is used.
+  constexpr int NK = ARGMAX_CHUNK / 1024;
   const int r0 = chunk * ARGMAX_CHUNK, r1 = min(V, r0 + ARGMAX_CHUNK);
-  for (int r = r0 + (int)threadIdx.x; r < r1; r += 256) {
-    float vr;
-    if (F16) {
-      vr = (float)ldg(reinterpret_cast<const _Float16*>(logits) + (size_t)t * V + r);
+  float lv[NK][4];
+  uint32_t sw[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int rb = r0 + 1024 * k + 4 * (int)threadIdx.x;
+    sw[k] = rb < r1 ? ldg(seen + (rb >> 5)) : 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lv[k][i] = 0.f;
+    if ((V & 3) == 0 && rb + 3 < r1) {  // rows start 16-byte aligned
+      if (F16) {
+        const half4 h = ldg(reinterpret_cast<const half4*>(reinterpret_cast<const _Float16*>(logits) + (size_t)t * V + rb));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lv[k][i] = (float)h[i];
+      } else {
+        const f32x4 f = ldg(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(logits) + (size_t)t * V + rb));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lv[k][i] = (float)(_Float16)f[i];
+      }
     } else {
-      vr = (float)(_Float16)ldg(reinterpret_cast<const float*>(logits) + (size_t)t * V + r);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (rb + i < r1)
+          lv[k][i] = F16 ? (float)ldg(reinterpret_cast<const _Float16*>(logits) + (size_t)t * V + rb + i)
+                         : (float)(_Float16)ldg(reinterpret_cast<const float*>(logits) + (size_t)t * V + rb + i);
+      }
     }
-    bool hit = ((ldg(seen + (r >> 5)) >> (r & 31)) & 1u) != 0;
-    if (isnew)
-      for (int j = 1; j <= t; ++j)
-        if (((isnew >> j) & 1) && r == dt[j]) hit = true;
-    const float pv = hit ? (vr > 0.f ? vr * inv_rep : vr * rep) : vr;
-    const uint64_t k = argmax_key(pv, (uint32_t)r);
-    best = k > best ? k : best;
+  }
+  // Fresh drafts that fall on this thread's logits: one pass over the drafts (bit 4k + i = logit rb_k + i).
+  uint32_t fresh = 0;
+  for (uint64_t m = isnew; m; m &= m - 1) {
+    const int e = dt[__builtin_ctzll(m)] - r0;
+    if (e >= 0 && e < ARGMAX_CHUNK && ((e & 1023) >> 2) == (int)threadIdx.x) fresh |= 1u << (4 * (e >> 10) + (e & 3));
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int rb = r0 + 1024 * k + 4 * (int)threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb + i;
+      if (r < r1) {
+        const bool hit = (((sw[k] >> (r & 31)) | (fresh >> (4 * k + i))) & 1u) != 0;
+        const float vr = lv[k][i];
+        const float pv = hit ? (vr > 0.f ? vr * inv_rep : vr * rep) : vr;
+        const uint64_t key = argmax_key(pv, (uint32_t)r);
+        best = key > best ? key : best;
+      }
+    }
   }
   best = wave_max_u64(best);
   __shared__ uint64_t red[4];

@@ -25,7 +25,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const
 }
 
 // ---------------------------------------------------------------- residual + RMS norm (norm_compute)
-// v = sum of `bands` inputs; a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
+// v = sum of `bands` inputs in band order (times v_scale when set: the split-K partials of a scaled GEMM summed as
+// its reduce kernel would); a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
 // h_new = h_old + a * v * post_w; x = fp16(h_new * rsqrt(mean(h_new^2) + eps) * norm_w).
 // One block per (row, group): blockIdx.y selects a group with its own inputs (the drafter's tap norms).
 __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
@@ -34,18 +35,66 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
   const int H = p.H;
   const float* hold = p.h_old ? p.h_old + (size_t)gi * p.group_stride + (size_t)t * H : nullptr;
   const _Float16* nw = p.norm_w + (size_t)gi * p.norm_w_stride;
-  constexpr int MAXE = 32;  // H <= 8192
-  float hv[MAXE], vv[MAXE];
-  const int ne = H / 256;
-  float s_vv = 0.f;
-  for (int k = 0; k < ne; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    hv[k] = hold ? hold[i] : 0.f;
-    float v = 0.f;
-    for (int b = 0; b < p.bands; ++b) v += p.v[(size_t)b * p.v_band_stride + (size_t)t * H + i];
-    vv[k] = v;
-    s_vv += v * v;
+  // Four consecutive columns per thread per 1024 (H <= 8192); every load is issued before the first is used.
+  constexpr int MAXK = 8;
+  const int nk = (H + 1023) / 1024;
+  f32x4 hv[MAXK], vv[MAXK];
+  half4 wn[MAXK], wp[MAXK];
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int i = 1024 * k + 4 * (int)threadIdx.x;
+    hv[k] = vv[k] = f32x4{0, 0, 0, 0};
+    wn[k] = wp[k] = half4{1, 1, 1, 1};
+    if (k < nk && i < H) {
+      if (hold) hv[k] = ldg(reinterpret_cast<const f32x4*>(hold + i));
+      wn[k] = ldg(reinterpret_cast<const half4*>(nw + i));
+      if (p.post_w) wp[k] = ldg(reinterpret_cast<const half4*>(p.post_w + i));
+    }
   }
+  // Bands eight at a time: a batch's loads are all in flight before the first add; the adds stay in band order.
+  constexpr int BB = 8;
+  for (int b0 = 0; b0 < p.bands; b0 += BB) {
+    if (nk == 2 && 4 * (int)threadIdx.x + 1024 < H) {  // H = 2048: two column groups per thread
+      f32x4 lb[BB][2];
+#pragma unroll
+      for (int bb = 0; bb < BB; ++bb) {
+        const float* vb = p.v + (size_t)min(b0 + bb, p.bands - 1) * p.v_band_stride + (size_t)t * H + 4 * threadIdx.x;
+        lb[bb][0] = ldg(reinterpret_cast<const f32x4*>(vb));
+        lb[bb][1] = ldg(reinterpret_cast<const f32x4*>(vb + 1024));
+      }
+#pragma unroll
+      for (int bb = 0; bb < BB; ++bb)
+        if (b0 + bb < p.bands) {
+          vv[0] += lb[bb][0];
+          vv[1] += lb[bb][1];
+        }
+    } else {
+      for (int b = b0; b < min(b0 + BB, p.bands); ++b) {
+        const float* vb = p.v + (size_t)b * p.v_band_stride + (size_t)t * H;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) {
+          const int i = 1024 * k + 4 * (int)threadIdx.x;
+          if (k < nk && i < H) vv[k] += ldg(reinterpret_cast<const f32x4*>(vb + i));
+        }
+      }
+    }
+  }
+  if (p.v_scale) {
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+      const int i = 1024 * k + 4 * (int)threadIdx.x;
+      if (k < nk && i < H) {
+        const half4 sc = ldg(reinterpret_cast<const half4*>(p.v_scale + i));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vv[k][j] *= (float)sc[j];
+      }
+    }
+  }
+  float s_vv = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_vv += vv[k][j] * vv[k][j];
   __shared__ float red[8];
   auto block_sum = [&](float x) -> float {
     x = wave_sum(x);
@@ -57,47 +106,73 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
   float a = 0.f;
   if (p.bands > 0) a = p.sandwich ? rsqrtf(block_sum(s_vv) / H + p.eps) : 1.f;
   float s_hh = 0.f;
-  for (int k = 0; k < ne; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    const float pw = p.post_w ? (float)p.post_w[i] : 1.f;
-    hv[k] = fmaf(vv[k] * a, pw, hv[k]);
-    s_hh += hv[k] * hv[k];
-  }
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hv[k][j] = fmaf(vv[k][j] * a, (float)wp[k][j], hv[k][j]);
+      s_hh += hv[k][j] * hv[k][j];
+    }
   const float inv = rsqrtf(block_sum(s_hh) / H + p.eps);
-  for (int k = 0; k < ne; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    const size_t o = (size_t)gi * p.group_stride + (size_t)t * H + i;
-    if (p.dst) p.dst[o] = hv[k];
-    if (p.tap) p.tap[(size_t)t * H + i] = hv[k];
-    p.x16[(size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i] = (_Float16)(hv[k] * inv * (float)nw[i]);
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int i = 1024 * k + 4 * (int)threadIdx.x;
+    if (k < nk && i < H) {
+      const size_t o = (size_t)gi * p.group_stride + (size_t)t * H + i;
+      if (p.dst) *reinterpret_cast<f32x4*>(p.dst + o) = hv[k];
+      if (p.tap) *reinterpret_cast<f32x4*>(p.tap + (size_t)t * H + i) = hv[k];
+      half4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = (_Float16)(hv[k][j] * inv * (float)wn[k][j]);
+      *reinterpret_cast<half4*>(p.x16 + (size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i) = x;
+    }
   }
 }
 
 // ---------------------------------------------------------------- gated short conv (conv_wave)
 // mix rows per channel c: [B, C, X] at 3c, 3c+1, 3c+2. bx = fp16(B*X); conv = w[K-1]*bx + sum_{k<K-1} w[k]*hist[pos-K+1+k];
 // y = fp16(C*conv); ring[pos] = bx. The history is position-indexed (ring of CONV_RING positions), so a rejected
-// token's entry is simply overwritten by a later round.
+// token's entry is simply overwritten by a later round. One thread per (token, channel): the history inside the block
+// is recomputed from the block's own mix rows (bx is a pure function of them), before it from the ring, so no thread
+// waits on another; the ring slots written (a .. a+M-1) and read (a-K+1 .. a-1) are disjoint for M + K - 1 <= CONV_RING.
 __global__ __launch_bounds__(256) void conv_kernel(const float* mix, const _Float16* conv_w, _Float16* ring, const dspark_state* st,
                                                    int M, int H, int K, _Float16* y) {
   if (stopped(st)) return;
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= H) return;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * H) return;
+  const int t = idx / H, c = idx % H;
   const int a = st->a;
-  float w[8], hist[8];
-  for (int k = 0; k < K; ++k) w[k] = (float)conv_w[(size_t)c * K + k];
-  for (int k = 0; k < K - 1; ++k) hist[k] = (float)ring[(size_t)((a - (K - 1) + k) & (CONV_RING - 1)) * H + c];
-  for (int t = 0; t < M; ++t) {
-    const float* m = mix + (size_t)t * 3 * H + 3 * c;
-    const float B = m[0], C = m[1], X = m[2];
-    const _Float16 bxh = (_Float16)(B * X);
-    const float bx = (float)bxh;
-    float conv = w[K - 1] * bx;
-    for (int k = 0; k < K - 1; ++k) conv = fmaf(w[k], hist[k], conv);
-    for (int k = 0; k + 1 < K - 1; ++k) hist[k] = hist[k + 1];
-    if (K > 1) hist[K - 2] = bx;
-    ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = bxh;
-    y[(size_t)t * H + c] = (_Float16)(C * conv);
+  constexpr int KMAX = 8;
+  float w[KMAX], bx[KMAX];
+  float C = 0.f, bx_t = 0.f;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    w[k] = 0.f;
+    bx[k] = 0.f;
+    if (k < K) {
+      w[k] = (float)conv_w[(size_t)c * K + k];
+      const int tt = t - (K - 1) + k;  // token of history slot k (k = K - 1: this token)
+      if (tt >= 0) {
+        const float* m = mix + (size_t)tt * 3 * H + 3 * c;
+        bx[k] = (float)(_Float16)(m[0] * m[2]);
+        if (k == K - 1) {
+          C = m[1];
+          bx_t = bx[k];
+        }
+      } else {
+        bx[k] = (float)ring[(size_t)((a + tt) & (CONV_RING - 1)) * H + c];
+      }
+    }
   }
+  float conv = 0.f;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k)
+    if (k == K - 1) conv = w[k] * bx[k];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k)
+    if (k < K - 1) conv = fmaf(w[k], bx[k], conv);
+  ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = (_Float16)bx_t;
+  y[(size_t)t * H + c] = (_Float16)(C * conv);
 }
 
 // ---------------------------------------------------------------- q/k norm + RoPE + K/V page write (query_fresh)
@@ -296,7 +371,7 @@ int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) 
 }
 int conv_launch(const float* mix, const void* conv_w, void* ring, const dspark_state* st, int M, int H, int K, void* y,
                 hipStream_t s) {
-  hipLaunchKernelGGL(conv_kernel, dim3((H + 255) / 256), dim3(256), 0, s, mix, (const _Float16*)conv_w, (_Float16*)ring, st,
+  hipLaunchKernelGGL(conv_kernel, dim3((M * H + 255) / 256), dim3(256), 0, s, mix, (const _Float16*)conv_w, (_Float16*)ring, st,
                      M, H, K, (_Float16*)y);
   return (int)hipGetLastError();
 }

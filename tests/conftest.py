@@ -34,5 +34,21 @@ def orc():
 
 
 @pytest.fixture(scope="session")
+def kats():
+    """Known-answer vectors held by the reference's own tests (tests/golden/reference_kats.json)."""
+    import json
+    with open(os.path.join(ROOT, "tests", "golden", "reference_kats.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="session")
+def golden():
+    """Seeded oracle vectors (tests/golden/vectors.npz, written by tests/golden/make_vectors.py)."""
+    import numpy as np
+    with np.load(os.path.join(ROOT, "tests", "golden", "vectors.npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="session")
 def host():
     return load_host()

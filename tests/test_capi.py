@@ -54,8 +54,11 @@ def test_workspace_queries_reject_bad_shapes():
     assert lib.dspark_verify_attention_workspace(ctypes.byref(args)) == 0
     args.D, args.M = 64, 65
     assert lib.dspark_verify_attention_workspace(ctypes.byref(args)) == 0
-    assert lib.dspark_gemm_i8_workspace(16, 8192, 2048) == 0          # one split: no partials
-    assert lib.dspark_gemm_i8_workspace(16, 2048, 8192) > 0           # split K
+    assert lib.dspark_gemm_i8_workspace(16, 65536, 2048) == 0         # enough 16-row strips: no split, no partials
+    for M, N, K in ((16, 2048, 8192), (9, 16384, 2048), (33, 512, 1024)):
+        ws = lib.dspark_gemm_i8_workspace(M, N, K)                    # split K: [splits][M][N] fp32 partials
+        splits = ws // (M * N * 4)
+        assert ws == splits * M * N * 4 and splits >= 2 and splits & (splits - 1) == 0, (M, N, K, ws)
     assert lib.dspark_gemm_i8_workspace(16, 2050, 8192) == 0          # N % 16
     assert lib.dspark_head_argmax_workspace(16, 16384) == 16 * 1024 * 8
 

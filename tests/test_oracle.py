@@ -51,27 +51,29 @@ def test_generators_deterministic_and_normal(orc):
 
 
 # ---------------------------------------------------------------- argmax / penalty (internal/sample/sample_test.go)
-def test_argmax_keeps_first_maximum(orc):
-    # sample_test.go:9-13
-    assert orc.argmax_first(np.array([1, 3, 3, 2], np.float32)) == 1
-    keys = [orc.argmax_key(v, i) for i, v in enumerate([1.0, 3.0, 3.0, 2.0])]
-    assert orc.key_index(max(keys)) == 1
+def test_argmax_keeps_first_maximum(orc, kats):
+    kat = kats["argmax_first_max"]  # sample_test.go:9-13
+    assert orc.argmax_first(np.array(kat["logits"], np.float32)) == kat["want"]
+    keys = [orc.argmax_key(float(v), i) for i, v in enumerate(kat["logits"])]
+    assert orc.key_index(max(keys)) == kat["want"]
 
 
-def test_repetition_penalty_signs(orc):
-    # sample_test.go:15-25
-    lg = orc.penalize_rep(np.array([2, -2, 2, -2], np.float32), np.array([0, 1], np.int32), 2.0)
-    assert lg.tolist() == [1, -4, 2, -2]
+def test_repetition_penalty_signs(orc, kats):
+    kat = kats["repetition_penalty_signs"]  # sample_test.go:15-25
+    lg = orc.penalize_rep(np.array(kat["logits"], np.float32), np.array(kat["seen"], np.int32),
+                          float(kat["repetition_penalty"]))
+    assert lg.tolist() == kat["want"]
     # the kernel form (multiply by the host's fp32 1/rep, dspark.go:575-578) gives the same on these values
     seen = np.zeros(1, np.uint32)
-    seen[0] = 0b11
-    keys = orc.verify_argmax(np.array([[2, -2, 2, -2]], np.float32), seen, [0], rep=2.0)
-    assert orc.key_index(int(keys[0])) == 2  # 1, -4, 2, -2 -> index 2
+    for t in kat["seen"]:
+        seen[0] |= np.uint32(1 << t)
+    keys = orc.verify_argmax(np.array([kat["logits"]], np.float32), seen, [0], rep=float(kat["repetition_penalty"]))
+    assert orc.key_index(int(keys[0])) == int(np.argmax(kat["want"]))
 
 
-def test_greedy_draw(orc):
-    # sample_test.go:53-57 (greedy Draw is Argmax)
-    assert orc.argmax_first(np.array([0, 9, 1], np.float32)) == 1
+def test_greedy_draw(orc, kats):
+    kat = kats["greedy_draw"]  # sample_test.go:53-57 (greedy Draw is Argmax)
+    assert orc.argmax_first(np.array(kat["logits"], np.float32)) == kat["want"]
 
 
 def test_argmax_key_orders_like_value_then_index(orc):
@@ -123,13 +125,14 @@ def test_verify_argmax_matches_numpy(orc, rep):
 
 
 # ---------------------------------------------------------------- weights (internal/weights/quant_test.go)
-def test_quantize_rows_int8_kat(orc):
-    w = orc.f32_to_f16(np.array([1, -0.5, 0.25, 0, 0, 0, 0, 0], np.float32))
-    q, s = orc.quantize_rows_int8(w, 2, 4)
+def test_quantize_rows_int8_kat(orc, kats):
+    kat = kats["quantize_rows_int8"]  # quant_test.go:9-34
+    w = orc.f32_to_f16(np.array(kat["w"], np.float32))
+    q, s = orc.quantize_rows_int8(w, kat["rows"], kat["k"])
     assert s[0] == np.float32(1.0 / 127)
-    assert q[0].tolist() == [127, -64, 32, 0]
+    assert q[0].tolist() == kat["want_q_row0"]
     assert s[1] == np.float32(1e-8) / np.float32(127)
-    assert q[1].tolist() == [0, 0, 0, 0]
+    assert q[1].tolist() == kat["want_q_row1"]
 
 
 def test_pack_rows_are_independent(orc):
