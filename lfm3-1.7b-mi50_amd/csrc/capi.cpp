@@ -156,6 +156,7 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   if (p.ksplit > 1) {
     if (!workspace || workspace_bytes < gemm_ws_bytes(M, N, K)) return DSPARK_ENOSPACE;
     p.part = static_cast<float*>(workspace);
+    p.counters = gemm_ws_counters(workspace, M, N, K);
   }
   return gemm_launch(p, true, S(stream));
 }

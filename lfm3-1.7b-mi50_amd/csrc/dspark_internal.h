@@ -46,7 +46,6 @@ struct ResNormParams {
   const float* v;               // bands of [M][H], v_band_stride apart, or nullptr
   int bands;
   size_t v_band_stride;
-  const _Float16* v_scale;      // [H] per-column factor applied to the band sum (split-K partials of a scaled GEMM)
   const _Float16* post_w;       // [H] or nullptr (1)
   const _Float16* norm_w;       // [groups][H]
   size_t norm_w_stride;
@@ -122,12 +121,13 @@ struct GemmParams {
   uint64_t* best_part;      // row-argmax keys per strip [M][N/16] (head) or nullptr
   uint64_t* best;           // [M]
   int M, N, K, ksplit, epilogue;
-  int defer_reduce;         // split-K: leave the partials for the consumer (a resnorm sums them with the scale)
+  uint32_t* counters;       // split-K arrival counter per group (zero between calls); nullptr: separate reduce kernel
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
 };
 
 void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg);
 size_t gemm_ws_bytes(int M, int N, int K);
+uint32_t* gemm_ws_counters(void* ws, int M, int N, int K);  // the counters inside a gemm_ws_bytes workspace
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
 
 size_t verify_argmax_ws(int M, int V);

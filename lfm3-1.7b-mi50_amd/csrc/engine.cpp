@@ -52,12 +52,6 @@ struct LayerW {
 
 int align16(int x) { return (x + 15) / 16 * 16; }
 
-#define CKR(x)               \
-  do {                       \
-    int _rc = (x);           \
-    if (_rc) return _rc;     \
-  } while (0)
-
 constexpr int ROUND_PLAN_BUCKET = 4096;
 
 }  // namespace
@@ -172,7 +166,7 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
 }
 
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
-         float* y32, _Float16* y16, hipStream_t st, bool defer = false) {
+         float* y32, _Float16* y16, hipStream_t st) {
   GemmParams p = {};
   p.st = e->st;
   p.x = x;
@@ -188,42 +182,19 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   if (p.ksplit > 1) {
     if (gemm_ws_bytes(M, N, K) > e->ws_gemm_bytes) return DSPARK_ENOSPACE;
     p.part = static_cast<float*>(e->ws_gemm);
-    p.defer_reduce = defer ? 1 : 0;
+    p.counters = gemm_ws_counters(e->ws_gemm, M, N, K);  // zeroed at allocation, left at zero by every call
   }
   return gemm_launch(p, true, st);
 }
 
-// A GEMM output as a resnorm input: the fp32 result, or the split-K partials with the per-row scale still to apply.
-struct VIn {
-  const float* v = nullptr;
-  int bands = 0;
-  const _Float16* scale = nullptr;
-};
-
-// GEMM whose only consumer is the next resnorm: split-K partials stay in the GEMM workspace (the resnorm reads them
-// before any later GEMM reuses it) and the reduce kernel is not launched.
-int gemm_to_resnorm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N,
-                    float* y32, VIn* out, hipStream_t st) {
-  int ks = 1, wpg = 1;
-  gemm_plan(M, N, K, true, true, &ks, &wpg);
-  CKR(gemm(e, x, M, K, w, s, N, 0, y32, nullptr, st, true));
-  if (ks > 1) {
-    *out = VIn{static_cast<const float*>(e->ws_gemm), ks, s};
-  } else {
-    *out = VIn{y32, 1, nullptr};
-  }
-  return 0;
-}
-
 // Residual + RMS norm of the B block rows.
-int resnorm(dspark_engine* e, const float* h_old, VIn v, const _Float16* post_w, const _Float16* norm_w, int sandwich,
-            float* dst, float* tap, hipStream_t s) {
+int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, const _Float16* post_w,
+            const _Float16* norm_w, int sandwich, float* dst, float* tap, hipStream_t s) {
   ResNormParams p = {};
   p.st = e->st;
   p.h_old = h_old;
-  p.v = v.v;
-  p.bands = v.bands;
-  p.v_scale = v.scale;
+  p.v = v;
+  p.bands = bands;
   p.v_band_stride = (size_t)e->B * e->d.hidden;
   p.post_w = post_w;
   p.norm_w = norm_w;
@@ -327,9 +298,8 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       p.H = H;
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
-    VIn vin;
-    CK(gemm_to_resnorm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, e->ctxv, &vin, s));
-    CK(resnorm(e, nullptr, vin, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
+    CK(gemm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s));
+    CK(resnorm(e, nullptr, e->ctxv, 1, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
     const int kvrow = 2 * d.kv_heads * d.head_dim;
     CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
     for (int j = 0; j < d.draft_layers; ++j)
@@ -339,18 +309,18 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     int cur = 0;
     for (int j = 0; j < d.draft_layers; ++j) {
       const LayerW& W = e->DL[j];
-      CK(resnorm(e, e->h[cur], j ? vin : VIn{}, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
+      CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, j ? 1 : 0, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm(e, e->x16, B, H, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s));
       CK(qkrope(e, W, e->mix, W.mix_rows, true, false, s));
       CK(attention(e, W, 1, plan_a, nullptr, s));
-      CK(gemm_to_resnorm(e, e->y16, B, H, W.out_w, W.out_s, H, e->vout, &vin, s));
-      CK(resnorm(e, e->h[cur], vin, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
+      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
+      CK(resnorm(e, e->h[cur], e->vout, 1, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
-      CK(gemm_to_resnorm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, e->w2out, &vin, s));
+      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
     }
-    CK(resnorm(e, e->h[cur], vin, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
+    CK(resnorm(e, e->h[cur], e->w2out, 1, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
     CK(gemm(e, e->x16, B, H, e->crop_w, e->crop_s, e->crop_n, 0, e->base, nullptr, s));
     MarkovParams mp = {};
     mp.st = e->st;
@@ -375,12 +345,12 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   // ---- verify
   CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
   int cur = 0;
-  VIn vin;
   for (int i = 0; i < d.n_layers; ++i) {
     const LayerW& W = e->L[i];
     const LayerW* P = i ? &e->L[i - 1] : nullptr;
     float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
-    CK(resnorm(e, e->h[cur], i ? vin : VIn{}, P ? P->post_ffn_norm : nullptr, W.op_norm, 1, e->h[cur ^ 1], tap, s));
+    CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, i ? 1 : 0, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
+               e->h[cur ^ 1], tap, s));
     cur ^= 1;
     CK(gemm(e, e->x16, B, H, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s));
     if (W.kind == 0) {
@@ -389,16 +359,16 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       CK(qkrope(e, W, e->mix, W.mix_rows, true, false, s));
       CK(attention(e, W, 0, plan_a, e->gate, s));
     }
-    CK(gemm_to_resnorm(e, e->y16, B, H, W.out_w, W.out_s, H, e->vout, &vin, s));
-    CK(resnorm(e, e->h[cur], vin, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
+    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
+    CK(resnorm(e, e->h[cur], e->vout, 1, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
     cur ^= 1;
     CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
-    CK(gemm_to_resnorm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, e->w2out, &vin, s));
+    CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
   }
   {
     const LayerW& P = e->L[d.n_layers - 1];
     float* tap = P.tap_slot >= 0 ? e->taps + (size_t)P.tap_slot * B * H : nullptr;
-    CK(resnorm(e, e->h[cur], vin, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
+    CK(resnorm(e, e->h[cur], e->w2out, 1, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
   }
   CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
   CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep));

@@ -55,6 +55,10 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
 // TB token blocks of 16. I8: weights biased int8, else fp16.
 __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st && p.st->run == 0; }
 
+constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
+constexpr int GEMM_VMCNT0 = 0x0F70;     // s_waitcnt vmcnt(0), other counters left unconstrained
+constexpr int GEMM_FIXUP_BATCH = 8;     // split partials loaded per batch by the last split
+
 // Chunks (64 columns) per batch of weight loads: 16 B per lane per chunk int8, 32 B fp16; two batches in registers.
 template <bool I8>
 constexpr int gemm_cpb() { return I8 ? 8 : 4; }
@@ -148,17 +152,54 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       if (cb + CPB < pe) compute(wb, cb + CPB, ph, pc);
     }
   }
-  if (!live) return;
-
   if (p.ksplit > 1) {
-    // partial [ks][M][N] fp32, epilogue in the reduce kernel
+    // Partials [ks][M][N] fp32. With counters, the last split of the group to arrive sums all of them in split order
+    // and runs the epilogue: partials are stored and loaded device-coherent (SC1), every store of a split is complete
+    // (vmcnt 0, then the workgroup barrier) before its arrival is counted, and the last split's loads are issued only
+    // after its own count returned ksplit - 1. It resets the counter for the next call. Without counters the reduce
+    // kernel does the sum.
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        p.part, (short)0, (int)((size_t)p.ksplit * p.M * p.N * sizeof(float)), 0x00020000);
+    if (live) {
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        const int t = 16 * tb + n;
+        if (t < p.M)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, acc[tb]), rp,
+              (uint32_t)((((size_t)ks * p.M + t) * p.N + row0 + 4 * g) * sizeof(float)), 0, GEMM_CPOL_COHERENT);
+      }
+    }
+    if (!p.counters) return;
+    __builtin_amdgcn_s_waitcnt(GEMM_VMCNT0);
+    __syncthreads();
+    __shared__ int last_s;
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(p.counters + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_s = old == (uint32_t)(p.ksplit - 1);
+      if (last_s) __hip_atomic_store(p.counters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_s || !live) return;
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
-      const int t = 16 * tb + n;
-      if (t < p.M) *reinterpret_cast<f32x4*>(p.part + ((size_t)ks * p.M + t) * p.N + row0 + 4 * g) = acc[tb];
+      const int t = min(16 * tb + n, p.M - 1);
+      u32x4 v[GEMM_FIXUP_BATCH];
+      f32x4 sum = {0, 0, 0, 0};
+      for (int k0 = 0; k0 < p.ksplit; k0 += GEMM_FIXUP_BATCH) {
+#pragma unroll
+        for (int k = 0; k < GEMM_FIXUP_BATCH; ++k)
+          v[k] = __builtin_amdgcn_raw_buffer_load_b128(
+              rp, (uint32_t)((((size_t)min(k0 + k, p.ksplit - 1) * p.M + t) * p.N + row0 + 4 * g) * sizeof(float)), 0,
+              GEMM_CPOL_COHERENT);
+#pragma unroll
+        for (int k = 0; k < GEMM_FIXUP_BATCH; ++k)
+          if (k0 + k < p.ksplit) sum += __builtin_bit_cast(f32x4, v[k]);
+      }
+      acc[tb] = sum;
     }
-    return;
   }
+  if (!live) return;
   if (p.best_part) {
     // Row argmax of this strip per token: lane holds rows row0+4g+i of token n; fold the 4 row groups.
 #pragma unroll
@@ -237,14 +278,22 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
   }
 }
 
-// Group width and split-K: the widest group (the most strips sharing one staged X) that, split along K where
-// allowed (each split keeping DSPARK_GEMM_MIN_CHUNKS chunks), still gives DSPARK_GEMM_TARGET_WGS workgroups; failing
-// that, two-strip groups with the deepest split. No split when `split` is false (the fused head argmax needs whole
+// Group width and split-K: unsplit groups of four or eight strips when they alone give DSPARK_GEMM_TARGET_WGS
+// workgroups; otherwise the widest group (the most strips sharing one staged X) that, split along K where allowed
+// (each split keeping DSPARK_GEMM_MIN_CHUNKS chunks), reaches that count; failing that, two-strip groups with the
+// deepest split. No split when `split` is false (the fused head argmax needs whole
 // rows).
 void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg) {
   (void)M;
   (void)i8;
   const int strips = N / 16, chunks = K / 64;
+  // Enough strips for unsplit groups of four or more: no partials, no reduce.
+  for (int w = DSPARK_GEMM_MAX_WPG; w >= 4; w /= 2)
+    if ((strips + w - 1) / w >= DSPARK_GEMM_TARGET_WGS) {
+      *ksplit = 1;
+      *wpg = w;
+      return;
+    }
   int ks = 1, w = 2;
   for (w = DSPARK_GEMM_MAX_WPG; w >= 2; w /= 2) {
     const int groups = (strips + w - 1) / w;
@@ -258,10 +307,19 @@ void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg) 
   *wpg = std::max(1, std::min(w, strips));
 }
 
+// Split-K workspace: partials [ks][M][N] fp32, then one arrival counter per group (256-byte aligned).
 size_t gemm_ws_bytes(int M, int N, int K) {
   int ks = 1, wpg = 1;
   gemm_plan(M, N, K, true, true, &ks, &wpg);
-  return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+  if (ks <= 1) return 0;
+  const size_t groups = (size_t)(N / 16 + wpg - 1) / wpg;
+  return (((size_t)ks * M * N * sizeof(float) + 255) / 256) * 256 + groups * sizeof(uint32_t);
+}
+
+uint32_t* gemm_ws_counters(void* ws, int M, int N, int K) {
+  int ks = 1, wpg = 1;
+  gemm_plan(M, N, K, true, true, &ks, &wpg);
+  return reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + (((size_t)ks * M * N * sizeof(float) + 255) / 256) * 256);
 }
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
@@ -269,7 +327,7 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
     launch_gemm<true>(p, s);
   else
     launch_gemm<false>(p, s);
-  if (p.ksplit > 1 && !p.defer_reduce) {
+  if (p.ksplit > 1 && !p.counters) {
     const int threads = p.M * (p.N / 4);
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, p);
   }

@@ -25,8 +25,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const
 }
 
 // ---------------------------------------------------------------- residual + RMS norm (norm_compute)
-// v = sum of `bands` inputs in band order (times v_scale when set: the split-K partials of a scaled GEMM summed as
-// its reduce kernel would); a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
+// v = sum of `bands` inputs in band order; a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
 // h_new = h_old + a * v * post_w; x = fp16(h_new * rsqrt(mean(h_new^2) + eps) * norm_w).
 // One block per (row, group): blockIdx.y selects a group with its own inputs (the drafter's tap norms).
 __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
@@ -76,17 +75,6 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
           const int i = 1024 * k + 4 * (int)threadIdx.x;
           if (k < nk && i < H) vv[k] += ldg(reinterpret_cast<const f32x4*>(vb + i));
         }
-      }
-    }
-  }
-  if (p.v_scale) {
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) {
-      const int i = 1024 * k + 4 * (int)threadIdx.x;
-      if (k < nk && i < H) {
-        const half4 sc = ldg(reinterpret_cast<const half4*>(p.v_scale + i));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) vv[k][j] *= (float)sc[j];
       }
     }
   }

@@ -119,7 +119,7 @@ class Workspace:
         torch = _torch()
         nbytes = max(int(nbytes), 256)
         if self.buf is None or self.buf.numel() < nbytes:
-            # contents need no clearing (every kernel writes what it later reads); zeros keep a dump readable
+            # zero-filled: the split-K GEMM keeps its arrival counters here (left at zero by every call)
             self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         return self.buf
 

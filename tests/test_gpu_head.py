@@ -138,6 +138,39 @@ def test_gemm_i8_matches_oracle(dev, orc, M, N, K, epilogue):
         assert np.max(np.abs(got - ref)) <= 2e-3 * max(1.0, np.max(np.abs(ref)))
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 2048, 8192), (9, 6144, 2048), (33, 512, 1024)])
+def test_gemm_split_calls_share_one_workspace(dev, orc, M, N, K):
+    """Split-K GEMMs in a row on one workspace (the last split of each row group sums the partials and resets its
+    counter): every call matches the oracle on its own inputs and repeats are bit-identical."""
+    torch = dev
+    host = load_host()
+    lib = host.lib()
+    print(f"case gemm split calls M={M} N={N} K={K}", flush=True)
+    need = lib.dspark_gemm_i8_workspace(M, N, K)
+    assert need > M * N * 4  # split: partials + counters
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    w = orc.int8_uniform(901 + N, (N, K))
+    s = orc.f32_to_f16(np.random.default_rng(N + 1).uniform(0.5, 1.5, N).astype(np.float32) / np.float32(127 * np.sqrt(K)))
+    wb = torch.from_numpy((w.astype(np.int16) + 128).astype(np.uint8)).cuda()
+    sd = f16(torch, s)
+    wso = host.Workspace()
+    wso.buf = ws
+    first = None
+    for call in range(4):
+        x = orc.normal_f16(910 + call % 3, (M, K))
+        want = orc.gemm_i8(x, w, s)
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        host.gemm_i8(f16(torch, x), wb, sd, y_f32=y, workspace=wso)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy().astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 2e-3 * np.max(np.abs(want)), f"call {call}"
+        if call == 0:
+            first = y.clone()
+        if call == 3:
+            assert torch.equal(y, first)  # same inputs as call 0: same bits
+    # a counter left non-zero would have kept every later call's groups from finishing (NaN outputs above)
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 16384, 2048), (9, 4096, 2048), (33, 1024, 512)])
 def test_head_argmax_matches_oracle(dev, orc, M, N, K):
     torch = dev
