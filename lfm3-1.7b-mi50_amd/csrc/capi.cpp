@@ -152,11 +152,15 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
-  gemm_plan(M, N, K, true, true, &p.ksplit, &p.wpg);
+  GemmPlan pl;
+  gemm_plan(M, N, K, true, true, &pl);
+  p.ksplit = pl.ksplit;
+  p.wpg = pl.wpg;
+  p.cpb = pl.cpb;
   if (p.ksplit > 1) {
-    if (!workspace || workspace_bytes < gemm_ws_bytes(M, N, K)) return DSPARK_ENOSPACE;
+    if (!workspace || workspace_bytes < gemm_ws_bytes(pl, M, N)) return DSPARK_ENOSPACE;
     p.part = static_cast<float*>(workspace);
-    p.counters = gemm_ws_counters(workspace, M, N, K);
+    p.counters = gemm_ws_counters(workspace, pl, M, N);
   }
   return gemm_launch(p, true, S(stream));
 }
@@ -178,7 +182,11 @@ int dspark_head_argmax_f16(const void* x, int32_t M, int32_t K, const void* w, i
   p.M = M;
   p.N = N;
   p.K = K;
-  gemm_plan(M, N, K, false, false, &p.ksplit, &p.wpg);
+  GemmPlan pl;
+  gemm_plan(M, N, K, false, false, &pl);
+  p.ksplit = pl.ksplit;
+  p.wpg = pl.wpg;
+  p.cpb = pl.cpb;
   p.best_part = static_cast<uint64_t*>(workspace);
   p.best = best_keys;
   return gemm_launch(p, false, S(stream));

@@ -123,11 +123,16 @@ struct GemmParams {
   int M, N, K, ksplit, epilogue;
   uint32_t* counters;       // split-K arrival counter per group (zero between calls); nullptr: separate reduce kernel
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
+  int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
 };
 
-void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg);
-size_t gemm_ws_bytes(int M, int N, int K);
-uint32_t* gemm_ws_counters(void* ws, int M, int N, int K);  // the counters inside a gemm_ws_bytes workspace
+struct GemmPlan {
+  int ksplit = 1, wpg = 1, cpb = 4;
+};
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl);
+size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N);
+size_t gemm_ws_bytes(int M, int N, int K);  // for the default split plan of an int8 GEMM
+uint32_t* gemm_ws_counters(void* ws, const GemmPlan& pl, int M, int N);  // the counters inside the workspace
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
 
 size_t verify_argmax_ws(int M, int V);

@@ -178,11 +178,15 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
-  gemm_plan(M, N, K, true, true, &p.ksplit, &p.wpg);
+  GemmPlan pl;
+  gemm_plan(M, N, K, true, true, &pl);
+  p.ksplit = pl.ksplit;
+  p.wpg = pl.wpg;
+  p.cpb = pl.cpb;
   if (p.ksplit > 1) {
-    if (gemm_ws_bytes(M, N, K) > e->ws_gemm_bytes) return DSPARK_ENOSPACE;
+    if (gemm_ws_bytes(pl, M, N) > e->ws_gemm_bytes) return DSPARK_ENOSPACE;
     p.part = static_cast<float*>(e->ws_gemm);
-    p.counters = gemm_ws_counters(e->ws_gemm, M, N, K);  // zeroed at allocation, left at zero by every call
+    p.counters = gemm_ws_counters(e->ws_gemm, pl, M, N);  // zeroed at allocation, left at zero by every call
   }
   return gemm_launch(p, true, st);
 }

@@ -59,10 +59,9 @@ constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-sc
 constexpr int GEMM_VMCNT0 = 0x0F70;     // s_waitcnt vmcnt(0), other counters left unconstrained
 constexpr int GEMM_FIXUP_BATCH = 8;     // split partials loaded per batch by the last split
 
-// Chunks (64 columns) per batch of weight loads: 16 B per lane per chunk int8, 32 B fp16; two batches in registers.
-template <bool I8>
-constexpr int gemm_cpb() { return I8 ? 8 : 4; }
+// Weight loads go in batches of CPB chunks (64 columns: 16 B per lane int8, 32 B fp16), two batches in registers.
 constexpr int GEMM_PHASE_UNITS = 32;  // X staged per phase: TB x chunks <= 32 (64 KB of LDS)
+constexpr int XR = 8;                  // X units (16 B) per thread loaded together while staging
 
 // Grid: (ceil(strips / waves per group)) groups x ksplit; each wave owns one 16-row strip and the group's K range.
 // The group stages its X slice into LDS once per phase (64 KB at most), in operand order [tb][chunk][half][lane]
@@ -70,11 +69,11 @@ constexpr int GEMM_PHASE_UNITS = 32;  // X staged per phase: TB x chunks <= 32 (
 // weights in batches of gemm_cpb chunks, the next batch in flight while the current one is multiplied. Loads past
 // the range are clamped to valid addresses and discarded, so the number of loads in flight is the same on every path
 // and the compiler's waits stay counted.
-template <int TB, bool I8>
+template <int TB, bool I8, int CPB>
 __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   if (gemm_stopped(p)) return;
   extern __shared__ u32x4 xs[];
-  constexpr int CPB = gemm_cpb<I8>(), WV = I8 ? 1 : 2, PH = GEMM_PHASE_UNITS / TB;
+  constexpr int WV = I8 ? 1 : 2, PH = GEMM_PHASE_UNITS / TB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int grp = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
@@ -130,26 +129,47 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     }
   };
 
+  // X unit u of a phase = [tb][chunk j][half h][lane l] (16 B): token min(16 tb + l % 16, M - 1) (token rows past M
+  // repeat row M - 1: their output columns are never stored, and a column of the product depends only on its own
+  // token), columns (ph + j) * 64 + 16 (l / 16) + 8 h .. + 8.
+  auto xload = [&](int ph, int pc, int u) -> u32x4 {
+    u = min(u, TB * pc * 128 - 1);
+    const int l = u & 63, h = (u >> 6) & 1, j = (u >> 7) % pc, tb = (u >> 7) / pc;
+    const int t = min(16 * tb + (l & 15), p.M - 1);
+    return ldg(reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + (ph + j) * 64 + 16 * (l >> 4) + 8 * h));
+  };
   u32x4 wa[CPB][WV], wb[CPB][WV];
   for (int ph = c0; ph < c1; ph += PH) {
     const int pc = min(PH, c1 - ph), pe = ph + pc;
-    load(wa, ph, pe);
-    // stage X[16 TB tokens][chunks ph .. ph + pc) (token rows past M repeat row M - 1: their output columns are
-    // never stored, and a column of the product depends only on its own token)
-    if (ph != c0) __syncthreads();  // every wave is done reading the previous phase
     const int units = TB * pc * 128;
-#pragma unroll 4
-    for (int u = threadIdx.x; u < units; u += blockDim.x) {
-      const int l = u & 63, h = (u >> 6) & 1, j = (u >> 7) % pc, tb = (u >> 7) / pc;
-      const int t = min(16 * tb + (l & 15), p.M - 1);
-      xs[u] = ldg(reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + (ph + j) * 64 + 16 * (l >> 4) + 8 * h));
+    // Issue order: the first XR X units of this thread, then the phase's first two weight batches, then X into LDS:
+    // the wait for X leaves the weights in flight.
+    u32x4 xr[XR];
+#pragma unroll
+    for (int i = 0; i < XR; ++i) xr[i] = xload(ph, pc, threadIdx.x + i * blockDim.x);
+    load(wa, ph, pe);
+    if (pc > CPB) load(wb, ph + CPB, pe);
+    if (ph != c0) __syncthreads();  // every wave is done reading the previous phase
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+      const int u = threadIdx.x + i * blockDim.x;
+      if (u < units) xs[u] = xr[i];
+    }
+    for (int u0 = XR * blockDim.x; u0 < units; u0 += XR * blockDim.x) {
+#pragma unroll
+      for (int i = 0; i < XR; ++i) xr[i] = xload(ph, pc, u0 + threadIdx.x + i * blockDim.x);
+#pragma unroll
+      for (int i = 0; i < XR; ++i) {
+        const int u = u0 + threadIdx.x + i * blockDim.x;
+        if (u < units) xs[u] = xr[i];
+      }
     }
     __syncthreads();
     for (int cb = ph; cb < pe; cb += 2 * CPB) {
-      if (cb + CPB < pe) load(wb, cb + CPB, pe);
       compute(wa, cb, ph, pc);
       if (cb + 2 * CPB < pe) load(wa, cb + 2 * CPB, pe);
       if (cb + CPB < pe) compute(wb, cb + CPB, ph, pc);
+      if (cb + 3 * CPB < pe) load(wb, cb + 3 * CPB, pe);
     }
   }
   if (p.ksplit > 1) {
@@ -222,7 +242,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   for (int tb = 0; tb < TB; ++tb) gemm_store(p, 16 * tb + n, row0, g, acc[tb]);
 }
 
-// Split-K reduce in index order + epilogue: one thread per 4 rows of one token.
+// Split-K reduce in index order + epilogue: one thread per 4 rows of one token, partial loads in flight in batches.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
   if (gemm_stopped(p)) return;
   const int idx = blockIdx.x * 256 + threadIdx.x;
@@ -230,7 +250,15 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
   if (idx >= p.M * groups) return;
   const int t = idx / groups, r = (idx % groups) * 4;
   f32x4 v = {0, 0, 0, 0};
-  for (int ks = 0; ks < p.ksplit; ++ks) v += *reinterpret_cast<const f32x4*>(p.part + ((size_t)ks * p.M + t) * p.N + r);
+  for (int k0 = 0; k0 < p.ksplit; k0 += GEMM_FIXUP_BATCH) {
+    f32x4 b[GEMM_FIXUP_BATCH];
+#pragma unroll
+    for (int k = 0; k < GEMM_FIXUP_BATCH; ++k)
+      b[k] = ldg(reinterpret_cast<const f32x4*>(p.part + ((size_t)min(k0 + k, p.ksplit - 1) * p.M + t) * p.N + r));
+#pragma unroll
+    for (int k = 0; k < GEMM_FIXUP_BATCH; ++k)
+      if (k0 + k < p.ksplit) v += b[k];
+  }
   // gemm_store expects the lane's 4 rows at row0 + 4g: pass row0 = r, g = 0.
   gemm_store(p, t, r, 0, v);
 }
@@ -249,18 +277,23 @@ __global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int 
 }
 
 #ifndef DSPARK_GEMM_TARGET_WGS
-#define DSPARK_GEMM_TARGET_WGS 256  // groups x splits to aim for: one workgroup per CU
+#define DSPARK_GEMM_TARGET_WGS 192  // split K until groups x splits reach this many workgroups
 #endif
 #ifndef DSPARK_GEMM_MIN_CHUNKS
-#define DSPARK_GEMM_MIN_CHUNKS 4  // a split keeps at least this many 64-column chunks
-#endif
-#ifndef DSPARK_GEMM_MAX_WPG
-#define DSPARK_GEMM_MAX_WPG 8  // widest group (waves = 16-row strips per workgroup)
+#define DSPARK_GEMM_MIN_CHUNKS 8  // a split keeps at least this many 64-column chunks
 #endif
 
 static size_t gemm_lds_bytes(int tb, int K, int ksplit) {
   const int chunks = K / 64, cpk = (chunks + ksplit - 1) / ksplit;
   return (size_t)tb * std::min(cpk, GEMM_PHASE_UNITS / tb) * 2048;
+}
+
+template <int TB, bool I8>
+static void launch_gemm_tb(const GemmParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  if (p.cpb >= 8)
+    hipLaunchKernelGGL((gemm_kernel<TB, I8, 8>), grid, block, lds, s, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<TB, I8, 4>), grid, block, lds, s, p);
 }
 
 template <bool I8>
@@ -271,58 +304,56 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
   const dim3 grid(groups * p.ksplit), block(64 * p.wpg);
   const size_t lds = gemm_lds_bytes(tb, p.K, p.ksplit);
   switch (tb) {
-    case 1: hipLaunchKernelGGL((gemm_kernel<1, I8>), grid, block, lds, s, p); break;
-    case 2: hipLaunchKernelGGL((gemm_kernel<2, I8>), grid, block, lds, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_kernel<3, I8>), grid, block, lds, s, p); break;
-    default: hipLaunchKernelGGL((gemm_kernel<4, I8>), grid, block, lds, s, p); break;
+    case 1: launch_gemm_tb<1, I8>(p, grid, block, lds, s); break;
+    case 2: launch_gemm_tb<2, I8>(p, grid, block, lds, s); break;
+    case 3: launch_gemm_tb<3, I8>(p, grid, block, lds, s); break;
+    default: launch_gemm_tb<4, I8>(p, grid, block, lds, s); break;
   }
 }
 
-// Group width and split-K: unsplit groups of four or eight strips when they alone give DSPARK_GEMM_TARGET_WGS
-// workgroups; otherwise the widest group (the most strips sharing one staged X) that, split along K where allowed
-// (each split keeping DSPARK_GEMM_MIN_CHUNKS chunks), reaches that count; failing that, two-strip groups with the
-// deepest split. No split when `split` is false (the fused head argmax needs whole
-// rows).
-void gemm_plan(int M, int N, int K, bool i8, bool split, int* ksplit, int* wpg) {
-  (void)M;
+// Plan (measured per C4 shape on MI355X, 16 and 9 tokens, in HIP graphs): groups of four 16-row strips (eight for
+// very wide heads, whose 512+ unsplit groups fill the CUs twice), split along K until groups x splits reach
+// DSPARK_GEMM_TARGET_WGS while each split keeps DSPARK_GEMM_MIN_CHUNKS chunks, and 8-chunk weight batches when a phase
+// has 16 or more chunks in groups of at most four (4-chunk batches otherwise: more workgroups per CU). No split when
+// `split` is false (the fused head argmax needs whole rows).
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl) {
   (void)i8;
-  const int strips = N / 16, chunks = K / 64;
-  // Enough strips for unsplit groups of four or more: no partials, no reduce.
-  for (int w = DSPARK_GEMM_MAX_WPG; w >= 4; w /= 2)
-    if ((strips + w - 1) / w >= DSPARK_GEMM_TARGET_WGS) {
-      *ksplit = 1;
-      *wpg = w;
-      return;
-    }
-  int ks = 1, w = 2;
-  for (w = DSPARK_GEMM_MAX_WPG; w >= 2; w /= 2) {
-    const int groups = (strips + w - 1) / w;
-    ks = 1;
-    if (split)
-      while (groups * ks < DSPARK_GEMM_TARGET_WGS && chunks / (2 * ks) >= DSPARK_GEMM_MIN_CHUNKS && ks < 32) ks *= 2;
-    if (groups * ks >= DSPARK_GEMM_TARGET_WGS) break;
-  }
-  if (w < 2) w = 2;
-  *ksplit = ks;
-  *wpg = std::max(1, std::min(w, strips));
+  const int strips = N / 16, chunks = K / 64, tb = (M + 15) / 16;
+  const int wpg = strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips));
+  const int groups = (strips + wpg - 1) / wpg;
+  int ks = 1;
+  if (split)
+    while (groups * ks < DSPARK_GEMM_TARGET_WGS && chunks / (2 * ks) >= DSPARK_GEMM_MIN_CHUNKS && ks < 32) ks *= 2;
+  const int pc = std::min((chunks + ks - 1) / ks, GEMM_PHASE_UNITS / std::max(1, std::min(4, tb)));
+  pl->ksplit = ks;
+  pl->wpg = wpg;
+  pl->cpb = (pc >= 16 && wpg <= 4) ? 8 : 4;
 }
 
 // Split-K workspace: partials [ks][M][N] fp32, then one arrival counter per group (256-byte aligned).
-size_t gemm_ws_bytes(int M, int N, int K) {
-  int ks = 1, wpg = 1;
-  gemm_plan(M, N, K, true, true, &ks, &wpg);
-  if (ks <= 1) return 0;
-  const size_t groups = (size_t)(N / 16 + wpg - 1) / wpg;
-  return (((size_t)ks * M * N * sizeof(float) + 255) / 256) * 256 + groups * sizeof(uint32_t);
+size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N) {
+  if (pl.ksplit <= 1) return 0;
+  const size_t groups = (size_t)(N / 16 + pl.wpg - 1) / pl.wpg;
+  return (((size_t)pl.ksplit * M * N * sizeof(float) + 255) / 256) * 256 + groups * sizeof(uint32_t);
 }
 
-uint32_t* gemm_ws_counters(void* ws, int M, int N, int K) {
-  int ks = 1, wpg = 1;
-  gemm_plan(M, N, K, true, true, &ks, &wpg);
-  return reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + (((size_t)ks * M * N * sizeof(float) + 255) / 256) * 256);
+size_t gemm_ws_bytes(int M, int N, int K) {
+  GemmPlan pl;
+  gemm_plan(M, N, K, true, true, &pl);
+  return gemm_ws_bytes(pl, M, N);
 }
+
+uint32_t* gemm_ws_counters(void* ws, const GemmPlan& pl, int M, int N) {
+  return reinterpret_cast<uint32_t*>(static_cast<char*>(ws) +
+                                     (((size_t)pl.ksplit * M * N * sizeof(float) + 255) / 256) * 256);
+}
+
+#ifndef DSPARK_GEMM_FIXUP
+#define DSPARK_GEMM_FIXUP 1  // 0: split-K partials summed by the reduce kernel even when counters are given
+#endif
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
+  if (!DSPARK_GEMM_FIXUP) p.counters = nullptr;
   if (i8)
     launch_gemm<true>(p, s);
   else
