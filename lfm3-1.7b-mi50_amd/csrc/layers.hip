@@ -245,6 +245,23 @@ __global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) {
 //   st->tokens[j] = prev (for j >= 1). A stop recorded by an earlier step turns the later ones into no-ops.
 // Launched as block - 1 steps, then markov_finalize writes the last token and st->M.
 __global__ __launch_bounds__(256) void markov_kernel(MarkovParams p, int j) {
+  // rows: one per thread, 256 rows per block; w2q stored row-major [N][rank]. Everything that does not depend on the
+  // previous draft (this row's first 256 w2 bytes, its scale, its base term, the confidence term) is loaded before
+  // the State and the previous step's key are read, so a step waits on one chain: key -> crop id -> w1 row.
+  constexpr int RC = 16;  // 16-byte chunks of w2 held in registers (rank <= 256 in one pass)
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  const bool live = r < p.N;
+  const int rr = live ? r : p.N - 1;
+  const int8_t* w2 = p.w2q + (size_t)rr * p.rank;
+  const int rc0 = min(RC, p.rank / 16);
+  u32x4 a4[RC];
+#pragma unroll
+  for (int c = 0; c < RC; ++c)
+    if (c < rc0) a4[c] = ldg(reinterpret_cast<const u32x4*>(w2 + 16 * c));
+  const float bz = ldg(p.base + (size_t)j * p.stride + rr);
+  const float s2 = ldg(p.w2s + rr);
+  const float bconf = ldg(p.base + (size_t)j * p.stride + p.N);
+
   dspark_state* st = p.st;
   if (stopped(st)) return;
   if (ldg(&st->M) != 0) return;  // drafting already stopped (M is set by the stop or the finalize)
@@ -258,7 +275,13 @@ __global__ __launch_bounds__(256) void markov_kernel(MarkovParams p, int j) {
     const uint64_t key = __hip_atomic_load(p.best + (j - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     prev = p.crop_ids[0xffffffffu - (uint32_t)key];
   }
-  const float conf = p.base[(size_t)j * p.stride + p.N] + p.c2[prev] + p.conf_bias;
+  const int8_t* w1 = p.w1q + (size_t)prev * p.rank;
+  u32x4 b4[RC];
+#pragma unroll
+  for (int c = 0; c < RC; ++c)
+    if (c < rc0) b4[c] = ldg(reinterpret_cast<const u32x4*>(w1 + 16 * c));
+  const float c2 = ldg(p.c2 + prev), s1 = ldg(p.w1s + prev);
+  const float conf = bconf + c2 + p.conf_bias;
   if (!(conf >= p.conf_thr)) {
     if (blockIdx.x == 0 && threadIdx.x == 0) {
       if (j >= 1) st->tokens[j] = prev;
@@ -267,24 +290,25 @@ __global__ __launch_bounds__(256) void markov_kernel(MarkovParams p, int j) {
     return;
   }
   if (blockIdx.x == 0 && threadIdx.x == 0 && j >= 1) st->tokens[j] = prev;
-  // rows: one per thread, R rows per block; w2q stored row-major [N][rank]
-  const int r = blockIdx.x * 256 + threadIdx.x;
-  uint64_t best = 0;
-  if (r < p.N) {
-    const int8_t* w2 = p.w2q + (size_t)r * p.rank;
-    const int8_t* w1 = p.w1q + (size_t)prev * p.rank;
-    int acc = 0;
-    for (int k = 0; k < p.rank; k += 16) {
-      const u32x4 a4 = ldg(reinterpret_cast<const u32x4*>(w2 + k));
-      const u32x4 b4 = ldg(reinterpret_cast<const u32x4*>(w1 + k));
-      acc = __builtin_amdgcn_sdot4(a4[0], b4[0], acc, false);
-      acc = __builtin_amdgcn_sdot4(a4[1], b4[1], acc, false);
-      acc = __builtin_amdgcn_sdot4(a4[2], b4[2], acc, false);
-      acc = __builtin_amdgcn_sdot4(a4[3], b4[3], acc, false);
+  int acc = 0;
+#pragma unroll
+  for (int c = 0; c < RC; ++c)
+    if (c < rc0) {
+      acc = __builtin_amdgcn_sdot4(a4[c][0], b4[c][0], acc, false);
+      acc = __builtin_amdgcn_sdot4(a4[c][1], b4[c][1], acc, false);
+      acc = __builtin_amdgcn_sdot4(a4[c][2], b4[c][2], acc, false);
+      acc = __builtin_amdgcn_sdot4(a4[c][3], b4[c][3], acc, false);
     }
-    const float z = fmaf((float)acc, p.w2s[r] * p.w1s[prev], p.base[(size_t)j * p.stride + r]);
-    best = argmax_key(z, (uint32_t)r);
+  for (int k = 16 * RC; k < p.rank; k += 16) {  // ranks above 256
+    const u32x4 x = ldg(reinterpret_cast<const u32x4*>(w2 + k));
+    const u32x4 y = ldg(reinterpret_cast<const u32x4*>(w1 + k));
+    acc = __builtin_amdgcn_sdot4(x[0], y[0], acc, false);
+    acc = __builtin_amdgcn_sdot4(x[1], y[1], acc, false);
+    acc = __builtin_amdgcn_sdot4(x[2], y[2], acc, false);
+    acc = __builtin_amdgcn_sdot4(x[3], y[3], acc, false);
   }
+  uint64_t best = 0;
+  if (live) best = argmax_key(fmaf((float)acc, s2 * s1, bz), (uint32_t)r);
   best = wave_max_u64(best);
   if ((threadIdx.x & 63) == 0 && best)
     __hip_atomic_fetch_max(p.best + j, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
