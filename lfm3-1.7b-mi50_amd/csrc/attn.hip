@@ -649,6 +649,9 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const _Float16* k, const 
 #ifndef DSPARK_ATTN_PF
 #define DSPARK_ATTN_PF 2
 #endif
+#ifndef DSPARK_ATTN_LDS_FILL
+#define DSPARK_ATTN_LDS_FILL 75  // LDS kernel: key splits x KV heads = this percentage of the workgroup slots
+#endif
 #ifndef DSPARK_ATTN_OCC2_MAX_PAGES
 #define DSPARK_ATTN_OCC2_MAX_PAGES 12  // pages per wave (at one workgroup per CU) below which OCC = 2 is used
 #endif
@@ -731,7 +734,9 @@ void attn_plan(AttnParams& p, int D, int cus) {
     p.OCC = nblk * pl <= 8 ? 2 : 1;
     int S = S_req;
     if (S <= 0) {
-      S = (cus * p.OCC + p.KVH - 1) / p.KVH;
+      // splits for three quarters of the workgroup slots: measured best on MI355X at 32k and 128k keys, 9 and 16
+      // tokens (the merge and per-split fixed costs outweigh the last quarter of the CUs)
+      S = (cus * p.OCC * DSPARK_ATTN_LDS_FILL / 100 + p.KVH - 1) / p.KVH;
       S = std::min(S, (p.npages + pl - 1) / pl);  // at least one step per split
     }
     S = std::max(S, (p.npages + LDS_BT_MAX - 1) / LDS_BT_MAX);
