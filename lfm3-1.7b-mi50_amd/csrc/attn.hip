@@ -382,6 +382,7 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char ring3[RING > 3 ? PL * PAGEB : 16];
   __shared__ __attribute__((aligned(16))) char trash[1024];  // destination of the padding loads
   __shared__ int32_t sm_bt[LDS_BT_MAX];                       // the split's block-table entries
+  __shared__ __attribute__((aligned(16))) char q_lds[(16 / PL) * (D / 32) * 1024];  // Q operands per row block
   if (p.st) {
     if (p.st->run == 0) return;
     attn_range(p);
@@ -393,21 +394,7 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   const int h = blockIdx.x / p.S, split = blockIdx.x % p.S;
   const int R = NRB * 16;
 
-  // Q operands of the wave's 16 rows, scaled to log2 units
   QOps<D, 1, false> qf;
-#pragma unroll
-  for (int s = 0; s < D / 32; ++s) {
-    const int r = rb * 16 + n;
-    u32x4 u = {0, 0, 0, 0};
-    if (r < p.G * p.M) {
-      const int t = r / p.G, qh = h * p.G + r % p.G;
-      u = ldg(reinterpret_cast<const u32x4*>(p.q + ((size_t)t * p.QH + qh) * D + 32 * s + 8 * g));
-    }
-    half8 q = as_half8(u);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
-    qf.r[0][s] = q;
-  }
   RowState<D, 1> rs;
 #pragma unroll
   for (int cc = 0; cc < D / 16; ++cc) rs.o[0][cc] = f32x4{0, 0, 0, 0};
@@ -479,13 +466,39 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
       page_accumulate<D, 1>(tl, rs, sc);
     }
   };
-  // Q (and the table) loads complete before the first page load is issued: a wait for them placed after the page
-  // loads would wait for the pages too (the load counter is in order).
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // The table (when staged) is in LDS before any other load is issued. Q of each row block goes to LDS with the
+  // same direct loads (the page-lane-0 wave of the block, before its first page loads: the oldest in its load
+  // counter), so the wait for Q below leaves the first steps' pages in flight. Padding rows past G*M read the last
+  // row (the merge never stores them).
+  if (paged) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if (pl == 0) {
+    const int r = min(rb * 16 + n, p.G * p.M - 1);
+    const int t = r / p.G, qh = h * p.G + r % p.G;
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.q, (short)0, (int)((size_t)p.M * p.QH * D * 2), 0x00020000);
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, DSPARK_LDSP(q_lds + (rb * (D / 32) + s) * 1024), 16,
+                                               (uint32_t)((((size_t)t * p.QH + qh) * D + 32 * s + 8 * g) * 2), 0, 0, 0);
+  }
   char* const slots[4] = {ring0, ring1, ring2, ring3};
 #pragma unroll
   for (int u = 0; u < RING - 1; ++u)
     if (u < nsteps) issue(u, slots[u]);
+  if (nsteps >= RING - 1)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((RING - 1) * LPW));
+  else if (nsteps >= 1)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
+  else
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    half8 q = *reinterpret_cast<const half8*>(q_lds + (rb * (D / 32) + s) * 1024 + lane * 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
+    qf.r[0][s] = q;
+  }
   for (int k = 0; k < nsteps; k += RING) {
 #pragma unroll
     for (int u = 0; u < RING; ++u)
