@@ -201,3 +201,68 @@ def test_engine_round_matches_oracle(dev, orc, seed):
     got_out = eng.download("out_tokens", np.int32)[:st.count]
     assert got_out.tolist() == out[:st.count].tolist()
     eng.close()
+
+
+def _greedy_chain(eng, torch, st0, n):
+    """Target-only greedy continuation: n one-token verify rounds (force_m = 1) from st0."""
+    eng.set_state(**st0)
+    for _ in range(n):
+        eng.round(1, st0["a"])
+    torch.cuda.synchronize()
+    st = eng.state()
+    assert st.count == n, (st.count, n)
+    return eng.download("out_tokens", np.int32)[:n].copy()
+
+
+@pytest.mark.parametrize("seed,wrong", [(21, ()), (22, (3, 10, 11, 20))])
+def test_planted_rounds_commit_the_greedy_chain(dev, seed, wrong):
+    """Speculative rounds commit exactly the target's greedy chain, whatever the drafts: with drafts planted from the
+    chain (force_m = -1), every round commits its drafts' accepted prefix plus the target's own next token. All
+    drafts right: each round commits block tokens. Chain positions listed in `wrong` are planted with a different
+    token: the round stops there and commits the chain token as its bonus."""
+    torch = dev
+    host = load_host()
+    desc = host.model_desc(**SMALL)
+    B = desc.block
+    eng = host.Engine(desc, 512)
+    make_weights(eng, desc, seed)
+    a, ctx_lo = 300, 150
+    setup_caches(eng, host, desc, a, ctx_lo, seed + 100)
+    st0 = dict(a=a, anchor=17, count=0, rounds_left=1 << 20, limit=eng.max_context, budget=1 << 20, eos=-1, ctx_new=1,
+               ctx_pos=a - 1, ctx_lo=ctx_lo, run=1, skip_rounds=1, stop_at=eng.max_context, ckpt_slot=-1, tokens=[17])
+    rounds = 4
+    n = (rounds + 1) * B
+    print(f"case planted rounds seed={seed} wrong={wrong}", flush=True)
+    conv = {nm: eng.download(nm, np.uint16) for nm in eng.names() if nm.startswith("conv.L")}
+    chain = _greedy_chain(eng, torch, st0, n)
+    for nm, buf in conv.items():  # the chain wrote the conv history past a: restore the history it started from
+        eng.upload(nm, buf)
+    plant = eng.download("plant", np.int32)
+    planted = chain.copy()
+    for i in wrong:
+        planted[i] = (chain[i] + 1) % desc.vocab
+    plant[a + 1:a + 1 + n] = planted
+    eng.upload("plant", plant)
+    eng.set_state(**st0)
+    commits = []
+    for _ in range(rounds):
+        before = eng.state().count
+        eng.round(-1, a)
+        torch.cuda.synchronize()
+        commits.append(eng.state().count - before)
+    st = eng.state()
+    got = eng.download("out_tokens", np.int32)[:st.count]
+    assert got.tolist() == chain[:st.count].tolist(), (got.tolist(), chain[:st.count].tolist())
+    assert st.a == a + st.count
+    if not wrong:
+        assert commits == [B] * rounds, commits
+    else:
+        # a round starting at chain index c drafts chain indices c .. c + B - 2 (draft j is plant[a' + j], the token
+        # of position a' + j); the first wrong one, w, ends the accepted prefix and the round commits w - c + 1 tokens,
+        # the last being the target's own (correct) token
+        c = 0
+        for k in commits:
+            bad = [i for i in wrong if c <= i <= c + B - 2]
+            assert k == ((bad[0] - c + 1) if bad else B), (c, k, commits)
+            c += k
+    eng.close()
