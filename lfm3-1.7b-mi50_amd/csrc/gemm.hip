@@ -57,11 +57,12 @@ __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st 
 
 constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
 constexpr int GEMM_VMCNT0 = 0x0F70;     // s_waitcnt vmcnt(0), other counters left unconstrained
+// s_waitcnt immediate: vmcnt(n) (6 bits, split low 4 / high 2), other counters left unconstrained
+#define GEMM_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
 constexpr int GEMM_FIXUP_BATCH = 8;     // split partials loaded per batch by the last split
 
 // Weight loads go in batches of CPB chunks (64 columns: 16 B per lane int8, 32 B fp16), two batches in registers.
 constexpr int GEMM_PHASE_UNITS = 32;  // X staged per phase: TB x chunks <= 32 (64 KB of LDS)
-constexpr int XR = 8;                  // X units (16 B) per thread loaded together while staging
 
 // Grid: (ceil(strips / waves per group)) groups x ksplit; each wave owns one 16-row strip and the group's K range.
 // The group stages its X slice into LDS once per phase (64 KB at most), in operand order [tb][chunk][half][lane]
@@ -129,42 +130,34 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     }
   };
 
-  // X unit u of a phase = [tb][chunk j][half h][lane l] (16 B): token min(16 tb + l % 16, M - 1) (token rows past M
-  // repeat row M - 1: their output columns are never stored, and a column of the product depends only on its own
-  // token), columns (ph + j) * 64 + 16 (l / 16) + 8 h .. + 8.
-  auto xload = [&](int ph, int pc, int u) -> u32x4 {
-    u = min(u, TB * pc * 128 - 1);
-    const int l = u & 63, h = (u >> 6) & 1, j = (u >> 7) % pc, tb = (u >> 7) / pc;
-    const int t = min(16 * tb + (l & 15), p.M - 1);
-    return ldg(reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + (ph + j) * 64 + 16 * (l >> 4) + 8 * h));
-  };
+  // X row r of a phase = [tb][chunk j][half h] (1 KB of LDS, lane l's 16 B at 16 l): token min(16 tb + l % 16, M - 1)
+  // (token rows past M repeat row M - 1: their output columns are never stored, and a column of the product depends
+  // only on its own token), columns (ph + j) * 64 + 16 (l / 16) + 8 h .. + 8. Rows go straight from global memory to
+  // LDS with direct loads (each lane gathers its 16 B), the waves taking rows in turn.
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   u32x4 wa[CPB][WV], wb[CPB][WV];
   for (int ph = c0; ph < c1; ph += PH) {
     const int pc = min(PH, c1 - ph), pe = ph + pc;
-    const int units = TB * pc * 128;
-    // Issue order: the first XR X units of this thread, then the phase's first two weight batches, then X into LDS:
-    // the wait for X leaves the weights in flight.
-    u32x4 xr[XR];
-#pragma unroll
-    for (int i = 0; i < XR; ++i) xr[i] = xload(ph, pc, threadIdx.x + i * blockDim.x);
-    load(wa, ph, pe);
-    if (pc > CPB) load(wb, ph + CPB, pe);
     if (ph != c0) __syncthreads();  // every wave is done reading the previous phase
-#pragma unroll
-    for (int i = 0; i < XR; ++i) {
-      const int u = threadIdx.x + i * blockDim.x;
-      if (u < units) xs[u] = xr[i];
+    // Issue order: this wave's X rows, then the phase's first two weight batches; the counted wait below then covers
+    // X (the oldest loads) and leaves the weights in flight.
+    for (int r = wave_u; r < TB * pc * 2; r += nw) {
+      const int h = r & 1, j = (r >> 1) % pc, tb = (r >> 1) / pc;
+      const int t = min(16 * tb + n, p.M - 1);
+      const uint32_t off = (uint32_t)(((size_t)t * p.K + (ph + j) * 64 + 16 * g + 8 * h) * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0, 0,
+                                               0);
     }
-    for (int u0 = XR * blockDim.x; u0 < units; u0 += XR * blockDim.x) {
-#pragma unroll
-      for (int i = 0; i < XR; ++i) xr[i] = xload(ph, pc, u0 + threadIdx.x + i * blockDim.x);
-#pragma unroll
-      for (int i = 0; i < XR; ++i) {
-        const int u = u0 + threadIdx.x + i * blockDim.x;
-        if (u < units) xs[u] = xr[i];
-      }
+    load(wa, ph, pe);
+    if (pc > CPB) {
+      load(wb, ph + CPB, pe);
+      __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(2 * CPB * WV));
+    } else {
+      __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPB * WV));
     }
-    __syncthreads();
+    __builtin_amdgcn_s_barrier();
     for (int cb = ph; cb < pe; cb += 2 * CPB) {
       compute(wa, cb, ph, pc);
       if (cb + 2 * CPB < pe) load(wa, cb + 2 * CPB, pe);
