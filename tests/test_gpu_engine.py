@@ -18,6 +18,13 @@ SMALL = dict(hidden=256, ffn=512, vocab=2048, n_layers=4, layer_kind=[0, 1, 0, 2
              conv_kernel=3, window=40, rope_base=1e4, rope_pairs=32, draft_layers=2, draft_ffn=512, block=8,
              max_drafts=7, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[1, 3], draft_window=100,
              ring_positions=256, mask_token=2047, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
+# The reference geometry's features at a small size: head_dim 128 with GQA 4:1, conv kernel 7, the reference's layer
+# kind pattern (conv / full / sliding), a 3-layer drafter, 9-token blocks.
+REF_SMALL = dict(hidden=512, ffn=512, vocab=2048, n_layers=6, layer_kind=[0, 0, 1, 0, 2, 0], q_heads=4, kv_heads=1,
+                 head_dim=128, conv_kernel=7, window=40, rope_base=1e6, rope_pairs=64, draft_layers=3, draft_ffn=512,
+                 block=9, max_drafts=7, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[2, 5], draft_window=100,
+                 ring_positions=256, mask_token=2047, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
+GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL}
 
 
 @pytest.fixture(scope="module")
@@ -118,12 +125,12 @@ def near_tie_ok(values, got, want, rel=1e-3):
     return abs(values[got] - values[want]) <= rel * scale
 
 
-@pytest.mark.parametrize("seed", [11, 12])
-def test_engine_round_matches_oracle(dev, orc, seed):
+@pytest.mark.parametrize("geom,seed", [("small", 11), ("small", 12), ("ref_small", 13)])
+def test_engine_round_matches_oracle(dev, orc, geom, seed):
     torch = dev
     host = load_host()
     from oracle import round as rnd
-    desc = host.model_desc(**SMALL)
+    desc = host.model_desc(**GEOMETRIES[geom])
     eng = host.Engine(desc, 512)
     weights = make_weights(eng, desc, seed)
     a, ctx_lo, ctx_new = 300, 150, 3
@@ -134,7 +141,7 @@ def test_engine_round_matches_oracle(dev, orc, seed):
                tokens=[anchor])
     eng.set_state(**st0)
     torch.cuda.synchronize()
-    print(f"case engine round seed={seed}", flush=True)
+    print(f"case engine round geom={geom} seed={seed}", flush=True)
     eng.round(0, a)
     torch.cuda.synchronize()
     B, V, N = desc.block, desc.vocab, desc.crop_rows
@@ -214,15 +221,16 @@ def _greedy_chain(eng, torch, st0, n):
     return eng.download("out_tokens", np.int32)[:n].copy()
 
 
-@pytest.mark.parametrize("seed,wrong", [(21, ()), (22, (3, 10, 11, 20))])
-def test_planted_rounds_commit_the_greedy_chain(dev, seed, wrong):
+@pytest.mark.parametrize("geom,seed,wrong", [("small", 21, ()), ("small", 22, (3, 10, 11, 20)), ("ref_small", 23, ()),
+                                             ("ref_small", 24, (0, 5, 13, 14))])
+def test_planted_rounds_commit_the_greedy_chain(dev, geom, seed, wrong):
     """Speculative rounds commit exactly the target's greedy chain, whatever the drafts: with drafts planted from the
     chain (force_m = -1), every round commits its drafts' accepted prefix plus the target's own next token. All
-    drafts right: each round commits block tokens. Chain positions listed in `wrong` are planted with a different
+    drafts right: each round commits all of its drafts plus one. Chain positions listed in `wrong` are planted with a different
     token: the round stops there and commits the chain token as its bonus."""
     torch = dev
     host = load_host()
-    desc = host.model_desc(**SMALL)
+    desc = host.model_desc(**GEOMETRIES[geom])
     B = desc.block
     eng = host.Engine(desc, 512)
     make_weights(eng, desc, seed)
@@ -232,7 +240,7 @@ def test_planted_rounds_commit_the_greedy_chain(dev, seed, wrong):
                ctx_pos=a - 1, ctx_lo=ctx_lo, run=1, skip_rounds=1, stop_at=eng.max_context, ckpt_slot=-1, tokens=[17])
     rounds = 4
     n = (rounds + 1) * B
-    print(f"case planted rounds seed={seed} wrong={wrong}", flush=True)
+    print(f"case planted rounds geom={geom} seed={seed} wrong={wrong}", flush=True)
     conv = {nm: eng.download(nm, np.uint16) for nm in eng.names() if nm.startswith("conv.L")}
     chain = _greedy_chain(eng, torch, st0, n)
     for nm, buf in conv.items():  # the chain wrote the conv history past a: restore the history it started from
@@ -254,15 +262,16 @@ def test_planted_rounds_commit_the_greedy_chain(dev, seed, wrong):
     got = eng.download("out_tokens", np.int32)[:st.count]
     assert got.tolist() == chain[:st.count].tolist(), (got.tolist(), chain[:st.count].tolist())
     assert st.a == a + st.count
+    nd = min(desc.max_drafts, B - 1)  # drafts per round (the limit and budget are far)
     if not wrong:
-        assert commits == [B] * rounds, commits
+        assert commits == [nd + 1] * rounds, commits
     else:
-        # a round starting at chain index c drafts chain indices c .. c + B - 2 (draft j is plant[a' + j], the token
+        # a round starting at chain index c drafts chain indices c .. c + nd - 1 (draft j is plant[a' + j], the token
         # of position a' + j); the first wrong one, w, ends the accepted prefix and the round commits w - c + 1 tokens,
         # the last being the target's own (correct) token
         c = 0
         for k in commits:
-            bad = [i for i in wrong if c <= i <= c + B - 2]
-            assert k == ((bad[0] - c + 1) if bad else B), (c, k, commits)
+            bad = [i for i in wrong if c <= i <= c + nd - 1]
+            assert k == ((bad[0] - c + 1) if bad else nd + 1), (c, k, commits)
             c += k
     eng.close()
