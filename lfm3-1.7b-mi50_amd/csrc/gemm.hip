@@ -130,10 +130,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     }
   };
 
-  // X row r of a phase = [tb][chunk j][half h] (1 KB of LDS, lane l's 16 B at 16 l): token min(16 tb + l % 16, M - 1)
-  // (token rows past M repeat row M - 1: their output columns are never stored, and a column of the product depends
-  // only on its own token), columns (ph + j) * 64 + 16 (l / 16) + 8 h .. + 8. Rows go straight from global memory to
-  // LDS with direct loads (each lane gathers its 16 B), the waves taking rows in turn.
+  // X row r of a phase = [tb][chunk j][half h] (1 KB of LDS, lane l's 16 B at 16 l): token 16 tb + l % 16, columns
+  // (ph + j) * 64 + 16 (l / 16) + 8 h .. + 8. Rows go straight from global memory to LDS with direct loads (each lane
+  // gathers its 16 B), the waves taking rows in turn.
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -145,10 +144,14 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     // X (the oldest loads) and leaves the weights in flight.
     for (int r = wave_u; r < TB * pc * 2; r += nw) {
       const int h = r & 1, j = (r >> 1) % pc, tb = (r >> 1) / pc;
-      const int t = min(16 * tb + n, p.M - 1);
-      const uint32_t off = (uint32_t)(((size_t)t * p.K + (ph + j) * 64 + 16 * g + 8 * h) * 2);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0, 0,
-                                               0);
+      const int t = 16 * tb + n;
+      // lanes of token rows past M load nothing: their LDS slots feed only output columns that are never stored
+      // (a column of the product depends only on its own token)
+      if (t < p.M) {
+        const uint32_t off = (uint32_t)(((size_t)t * p.K + (ph + j) * 64 + 16 * g + 8 * h) * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0,
+                                                 0, 0);
+      }
     }
     load(wa, ph, pe);
     if (pc > CPB) {
