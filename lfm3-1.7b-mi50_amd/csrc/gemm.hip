@@ -106,8 +106,35 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       }
     }
   };
-  // chunk cb + i of the phase starting at chunk ph (pc chunks staged)
+  // chunk cb + i of the phase starting at chunk ph (pc chunks staged). With one token block the batch's X operands
+  // are read from LDS before its first MFMA, so their latency is paid once per batch, not once per chunk.
   auto compute = [&](const u32x4 (&w)[CPB][WV], int cb, int ph, int pc) {
+    if constexpr (TB == 1) {
+      u32x4 xb[CPB][2];
+#pragma unroll
+      for (int i = 0; i < CPB; ++i) {
+        const int j = min(cb + i - ph, pc - 1);
+        const u32x4* xp = xs + ((size_t)j * 2) * 64 + lane;
+        xb[i][0] = xp[0];
+        xb[i][1] = xp[64];
+      }
+#pragma unroll
+      for (int i = 0; i < CPB; ++i) {
+        if (cb + i - ph < pc) {
+          half8 a[2];
+          if (I8) {
+            a[0] = i8x8_to_half8(w[i][0][0], w[i][0][1]);
+            a[1] = i8x8_to_half8(w[i][0][2], w[i][0][3]);
+          } else {
+            a[0] = as_half8(w[i][0]);
+            a[1] = as_half8(w[i][WV - 1]);
+          }
+          acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
+          acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < CPB; ++i) {
       const int j = cb + i - ph;
