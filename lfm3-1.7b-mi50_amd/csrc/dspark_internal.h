@@ -89,6 +89,9 @@ struct MarkovParams {
   const int32_t* crop_ids;      // [N]
   uint64_t* best;               // [block] argmax keys (cleared by round_begin)
   float conf_bias, conf_thr;
+  const float* table;           // [N][N] w1q[crop_ids[c]] . w2q[r] (markov_table_launch), or nullptr: steps dot w2q
+  const float* c2c;             // [N] c2[crop_ids[c]]
+  const float* s1c;             // [N] w1s[crop_ids[c]]
 };
 
 int embed_launch(const void* embed, const struct ::dspark_state* st, int mode, int mask_token, int M, int H, int V, float* h,
@@ -98,6 +101,9 @@ int conv_launch(const float* mix, const void* conv_w, void* ring, const struct :
                 void* y, hipStream_t s);
 int qkrope_launch(const QkRopeParams& p, hipStream_t s);
 int markov_launch(const MarkovParams& p, hipStream_t s);
+// Transition table of the drafter's Markov head for crop_rows N <= 16384 (steps after the first read one row of it).
+int markov_table_launch(const int8_t* w1q, const float* w1s, const float* c2, const int8_t* w2q, const int32_t* crop_ids,
+                        int N, int rank, int vocab, float* T, float* c2c, float* s1c, hipStream_t s);
 int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos,
                        int vocab, int out_cap, hipStream_t s);
 int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);

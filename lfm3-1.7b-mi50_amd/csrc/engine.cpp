@@ -68,6 +68,10 @@ struct dspark_engine {
   int32_t* crop_ids = nullptr;
   int8_t *w2q = nullptr, *w1q = nullptr;
   float *w2s = nullptr, *w1s = nullptr, *c2 = nullptr;
+  // Markov transition table [crop_rows][crop_rows] with c2 and w1s gathered by crop index (markov_table_launch);
+  // rebuilt before the next round whenever a weight it depends on may have been written
+  float *mtab = nullptr, *mc2c = nullptr, *ms1c = nullptr;
+  bool mtab_dirty = true;
   _Float16* rope = nullptr;
   int32_t* ring_bt = nullptr;
   int ring_pages = 0;
@@ -343,6 +347,9 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     mp.best = mbest;
     mp.conf_bias = d.conf_bias;
     mp.conf_thr = d.conf_thr;
+    mp.table = e->mtab;
+    mp.c2c = e->mc2c;
+    mp.s1c = e->ms1c;
     CK(markov_launch(mp, s));
     if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, s));
   }
@@ -504,6 +511,11 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->w1q = static_cast<int8_t*>(e->alloc("markov.w1q", (size_t)d.vocab * d.markov_rank, &err));
   e->w1s = static_cast<float*>(e->alloc("markov.w1s", (size_t)d.vocab * 4, &err));
   e->c2 = static_cast<float*>(e->alloc("conf_c2", (size_t)d.vocab * 4, &err));
+  if (d.crop_rows <= 16384) {
+    e->mtab = static_cast<float*>(e->alloc("", (size_t)d.crop_rows * d.crop_rows * 4, &err));
+    e->mc2c = static_cast<float*>(e->alloc("", (size_t)d.crop_rows * 4, &err));
+    e->ms1c = static_cast<float*>(e->alloc("", (size_t)d.crop_rows * 4, &err));
+  }
   e->tap_norms = h16("tap_norms", (size_t)d.n_taps * H);
   e->fc_w = u8("fc.w", (size_t)H * d.n_taps * H);
   e->fc_s = h16("fc.s", H);
@@ -587,6 +599,10 @@ int dspark_engine_tensor(dspark_engine* e, const char* name, void** ptr, size_t*
   if (!e || !name) return DSPARK_EINVAL;
   auto it = e->tensors.find(name);
   if (it == e->tensors.end()) return DSPARK_EINVAL;
+  // a pointer to a weight the Markov table is built from may be written through: rebuild before the next round
+  static const char* const table_inputs[] = {"markov.w1q", "markov.w1s", "markov.w2q", "conf_c2", "crop_ids"};
+  for (const char* n : table_inputs)
+    if (std::strcmp(name, n) == 0) e->mtab_dirty = true;
   if (ptr) *ptr = it->second.ptr;
   if (bytes) *bytes = it->second.bytes;
   return 0;
@@ -662,12 +678,27 @@ int dspark_engine_init_random(dspark_engine* e, uint64_t seed, dspark_stream_t s
   gemm_w("ckv", H);
   if (rc) return rc;
   hipLaunchKernelGGL(crop_ids_kernel, dim3((d.crop_rows + 255) / 256), dim3(256), 0, s, e->crop_ids, d.crop_rows, d.vocab);
+  e->mtab_dirty = true;
   return (int)hipGetLastError();
+}
+
+int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream) {
+  if (!e) return DSPARK_EINVAL;
+  if (!e->mtab) return 0;
+  const dspark_model_desc& d = e->d;
+  const int rc = markov_table_launch(e->w1q, e->w1s, e->c2, e->w2q, e->crop_ids, d.crop_rows, d.markov_rank, d.vocab,
+                                     e->mtab, e->mc2c, e->ms1c, reinterpret_cast<hipStream_t>(stream));
+  if (!rc) e->mtab_dirty = false;
+  return rc;
 }
 
 int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream) {
   if (!e || force_m < -1 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (e->mtab_dirty) {
+    const int rc = dspark_engine_prepare(e, stream);
+    if (rc) return rc;
+  }
   const int bucket = plan_a / ROUND_PLAN_BUCKET;
   const auto key = std::make_pair((int)force_m, bucket);
   auto it = e->graphs.find(key);

@@ -330,6 +330,144 @@ __global__ void markov_finalize(MarkovParams p) {
   st->M = drafts + 1;
 }
 
+// ---------------------------------------------------------------- drafter: the Markov chain from a transition table
+// T[c][r] = (float) (w1q[crop_ids[c]] . w2q[r]) for crop indices c, r < N: the integer dot of every step after the
+// first (whose previous token is always a crop token) depends on the weights only, so it is computed once per model
+// (exact in fp32: |dot| <= rank * 127 * 127 < 2^24). c2c[c] = c2[crop_ids[c]], s1c[c] = w1s[crop_ids[c]]. 64 x 64
+// tiles, 256 threads with 4 x 4 outputs each, rank in 256-byte slices through LDS. Crop ids outside the vocabulary
+// read row 0 (the table is built before any round checks them).
+__global__ __launch_bounds__(256) void markov_table_kernel(const int8_t* w1q, const float* w1s, const float* c2,
+                                                           const int8_t* w2q, const int32_t* crop_ids, int N, int rank,
+                                                           int vocab, float* T, float* c2c, float* s1c) {
+  constexpr int KS = 256, ROWB = KS + 16;  // rank slice and padded LDS row
+  __shared__ __attribute__((aligned(16))) int8_t As[64 * ROWB], Bs[64 * ROWB];
+  const int tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+  const int c0 = blockIdx.y * 64, q0 = blockIdx.x * 64;
+  if (blockIdx.x == 0 && tid < 64 && c0 + tid < N) {
+    int id = crop_ids[c0 + tid];
+    if (id < 0 || id >= vocab) id = 0;
+    c2c[c0 + tid] = c2[id];
+    s1c[c0 + tid] = w1s[id];
+  }
+  int acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0;
+  for (int k0 = 0; k0 < rank; k0 += KS) {
+    const int pieces = min(KS, rank - k0) / 16;
+    for (int idx = tid; idx < 64 * pieces; idx += 256) {
+      const int row = idx / pieces, pc = idx % pieces;
+      int id = crop_ids[min(c0 + row, N - 1)];
+      if (id < 0 || id >= vocab) id = 0;
+      const int r = min(q0 + row, N - 1);
+      *reinterpret_cast<u32x4*>(As + row * ROWB + 16 * pc) =
+          ldg(reinterpret_cast<const u32x4*>(w1q + (size_t)id * rank + k0 + 16 * pc));
+      *reinterpret_cast<u32x4*>(Bs + row * ROWB + 16 * pc) =
+          ldg(reinterpret_cast<const u32x4*>(w2q + (size_t)r * rank + k0 + 16 * pc));
+    }
+    __syncthreads();
+    for (int pc = 0; pc < pieces; ++pc) {
+      u32x4 av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        av[i] = *reinterpret_cast<const u32x4*>(As + (4 * ty + i) * ROWB + 16 * pc);
+        bv[i] = *reinterpret_cast<const u32x4*>(Bs + (4 * tx + i) * ROWB + 16 * pc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j] = __builtin_amdgcn_sdot4(av[i][e], bv[j][e], acc[i][j], false);
+    }
+    __syncthreads();
+  }
+  const int q = q0 + 4 * tx;
+  if (q >= N) return;  // N % 16 == 0: the 4 columns are all inside or all outside
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = c0 + 4 * ty + i;
+    if (c < N)
+      *reinterpret_cast<f32x4*>(T + (size_t)c * N + q) =
+          f32x4{(float)acc[i][0], (float)acc[i][1], (float)acc[i][2], (float)acc[i][3]};
+  }
+}
+
+// Draft steps 1 .. block - 2 and the finalize in one workgroup. Step j's previous token is the crop token of step
+// j - 1's key, so its dots are row ci of the table and its values fmaf(T[ci][r], w2s[r] * s1c[ci], base[j][r]) are
+// markov_kernel's bit for bit; the confidence test and the writes of tokens, M and the per-step keys are
+// markov_kernel's and markov_finalize's. Step 0 (previous token = the anchor, any vocabulary id) stays with
+// markov_kernel. Thread t owns rows 16 t .. 16 t + 15 (N <= 16384), so a step is one table row read with all its
+// loads in flight, then a workgroup argmax.
+constexpr int CHAIN_THREADS = 1024, CHAIN_ROWS = 16, CHAIN_MAX_N = CHAIN_THREADS * CHAIN_ROWS;
+__global__ __launch_bounds__(1024) void markov_chain_kernel(MarkovParams p) {
+  __shared__ uint64_t red[CHAIN_THREADS / 64];
+  dspark_state* st = p.st;
+  if (stopped(st)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = p.N, r0 = CHAIN_ROWS * tid;
+  const bool live = r0 < N;  // N % 16 == 0: a thread's rows are all inside or all outside
+  f32x4 s2[CHAIN_ROWS / 4];
+#pragma unroll
+  for (int i = 0; i < CHAIN_ROWS / 4; ++i)
+    s2[i] = live ? ldg(reinterpret_cast<const f32x4*>(p.w2s + r0) + i) : f32x4{0, 0, 0, 0};
+  const int a = st->a;
+  const int cap = min(min(p.max_drafts, p.block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  int M = st->M;  // nonzero when step 0's confidence test stopped drafting
+  uint64_t key = 0;
+  if (M == 0 && cap >= 1) key = __hip_atomic_load(p.best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int j = 1; j < cap && M == 0; ++j) {
+    const uint32_t ci = 0xffffffffu - (uint32_t)key;
+    const float* brow = p.base + (size_t)j * p.stride;
+    f32x4 tv[CHAIN_ROWS / 4], bv[CHAIN_ROWS / 4];
+    if (live) {
+      const f32x4* trow = reinterpret_cast<const f32x4*>(p.table + (size_t)ci * N + r0);
+#pragma unroll
+      for (int i = 0; i < CHAIN_ROWS / 4; ++i) {
+        tv[i] = ldg(trow + i);
+        bv[i] = ldg(reinterpret_cast<const f32x4*>(brow + r0) + i);
+      }
+    }
+    const int prev = ldg(p.crop_ids + ci);
+    const float s1 = ldg(p.s1c + ci);
+    const float conf = ldg(brow + N) + ldg(p.c2c + ci) + p.conf_bias;
+    if (!(conf >= p.conf_thr)) {
+      if (tid == 0) {
+        st->tokens[j] = prev;
+        st->M = j + 1;
+      }
+      M = j + 1;
+      break;
+    }
+    if (tid == 0) st->tokens[j] = prev;
+    uint64_t best = 0;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < CHAIN_ROWS / 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint64_t k = argmax_key(fmaf(tv[i][e], s2[i][e] * s1, bv[i][e]), (uint32_t)(r0 + 4 * i + e));
+          best = k > best ? k : best;
+        }
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    key = red[0];
+#pragma unroll
+    for (int w = 1; w < CHAIN_THREADS / 64; ++w) key = red[w] > key ? red[w] : key;
+    __syncthreads();  // red is rewritten by the next step
+    if (tid == 0) p.best[j] = key;
+  }
+  if (tid != 0) return;
+  st->tokens[0] = st->anchor;
+  if (M != 0) return;  // stopped by confidence: tokens and M already written
+  const int drafts = max(cap, 0);
+  if (drafts >= 1) st->tokens[drafts] = p.crop_ids[0xffffffffu - (uint32_t)key];
+  st->M = drafts + 1;
+}
+
 // ---------------------------------------------------------------- round start
 // Clears the per-round scratch the kernels fold into (argmax keys) and the draft count, marks the anchor seen
 // (dspark.hip:2432-2435). A State the buffers cannot hold -- anchor position a with a + block > max_pos, an anchor
@@ -394,8 +532,20 @@ int qkrope_launch(const QkRopeParams& p, hipStream_t s) {
 }
 int markov_launch(const MarkovParams& p, hipStream_t s) {
   const int blocks = (p.N + 255) / 256;
+  if (p.table && p.N <= CHAIN_MAX_N) {
+    if (p.block >= 2) hipLaunchKernelGGL(markov_kernel, dim3(blocks), dim3(256), 0, s, p, 0);
+    hipLaunchKernelGGL(markov_chain_kernel, dim3(1), dim3(CHAIN_THREADS), 0, s, p);
+    return (int)hipGetLastError();
+  }
   for (int j = 0; j < p.block - 1; ++j) hipLaunchKernelGGL(markov_kernel, dim3(blocks), dim3(256), 0, s, p, j);
   hipLaunchKernelGGL(markov_finalize, dim3(1), dim3(64), 0, s, p);
+  return (int)hipGetLastError();
+}
+int markov_table_launch(const int8_t* w1q, const float* w1s, const float* c2, const int8_t* w2q, const int32_t* crop_ids,
+                        int N, int rank, int vocab, float* T, float* c2c, float* s1c, hipStream_t s) {
+  if (N < 16 || N % 16 || N > CHAIN_MAX_N || rank < 16 || rank % 16) return DSPARK_EINVAL;
+  hipLaunchKernelGGL(markov_table_kernel, dim3((N + 63) / 64, (N + 63) / 64), dim3(256), 0, s, w1q, w1s, c2, w2q, crop_ids,
+                     N, rank, vocab, T, c2c, s1c);
   return (int)hipGetLastError();
 }
 int round_begin_launch(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos, int vocab,

@@ -337,6 +337,7 @@ _SIGS.update({
                                             ctypes.POINTER(ctypes.c_size_t)]),
     "dspark_engine_tensor_count": (ctypes.c_int, [ctypes.c_void_p]),
     "dspark_engine_tensor_name": (ctypes.c_char_p, [ctypes.c_void_p, ctypes.c_int32]),
+    "dspark_engine_prepare": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "dspark_engine_round": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_engine_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchArgs), ctypes.c_void_p, ctypes.c_int32,
                                             ctypes.POINTER(LaunchResult), ctypes.c_void_p]),
@@ -415,6 +416,9 @@ class Engine:
 
     def init_random(self, seed, stream=None):
         check(lib().dspark_engine_init_random(self.h, seed, stream_handle(stream)), "dspark_engine_init_random")
+
+    def prepare(self, stream=None):
+        check(lib().dspark_engine_prepare(self.h, stream_handle(stream)), "dspark_engine_prepare")
 
     def round(self, force_m=0, plan_a=0, stream=None):
         check(lib().dspark_engine_round(self.h, force_m, plan_a, stream_handle(stream)), "dspark_engine_round")

@@ -24,7 +24,13 @@ REF_SMALL = dict(hidden=512, ffn=512, vocab=2048, n_layers=6, layer_kind=[0, 0, 
                  head_dim=128, conv_kernel=7, window=40, rope_base=1e6, rope_pairs=64, draft_layers=3, draft_ffn=512,
                  block=9, max_drafts=7, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[2, 5], draft_window=100,
                  ring_positions=256, mask_token=2047, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
-GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL}
+# SMALL with the confidence term of a random half of the vocabulary (anchor aside) far below the threshold: drafting
+# stops at the first step whose previous draft is one of them, a different step from seed to seed.
+# SMALL with the full-size cropped head and Markov rank (16384 rows, rank 256): every thread of the Markov chain's
+# workgroup owns rows.
+SMALL_WIDE = dict(SMALL, vocab=32768, mask_token=32767, crop_rows=16384, markov_rank=256)
+GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE}
+STOP_ANCHOR = 17
 
 
 @pytest.fixture(scope="module")
@@ -34,7 +40,7 @@ def dev():
     return torch
 
 
-def make_weights(eng, desc, seed):
+def make_weights(eng, desc, seed, stop_half=False):
     rng = np.random.default_rng(seed)
     host = {}
     names = eng.names()
@@ -63,6 +69,10 @@ def make_weights(eng, desc, seed):
             a = np.full(nb // 4, 1 / 73.3, np.float32)
         elif n == "conf_c2":
             a = rng.uniform(-0.1, 0.1, nb // 4).astype(np.float32)
+            if stop_half:
+                low = rng.random(a.size) < 0.5
+                low[STOP_ANCHOR] = False
+                a[low] = -100.0
         elif n == "crop_ids":
             a = rng.permutation(desc.vocab)[:nb // 4].astype(np.int32)
         else:  # norms
@@ -125,17 +135,18 @@ def near_tie_ok(values, got, want, rel=1e-3):
     return abs(values[got] - values[want]) <= rel * scale
 
 
-@pytest.mark.parametrize("geom,seed", [("small", 11), ("small", 12), ("ref_small", 13)])
+@pytest.mark.parametrize("geom,seed", [("small", 11), ("small", 12), ("ref_small", 13), ("small_stop", 14),
+                                       ("small_stop", 15), ("small_stop", 16), ("small_wide", 17)])
 def test_engine_round_matches_oracle(dev, orc, geom, seed):
     torch = dev
     host = load_host()
     from oracle import round as rnd
     desc = host.model_desc(**GEOMETRIES[geom])
     eng = host.Engine(desc, 512)
-    weights = make_weights(eng, desc, seed)
+    weights = make_weights(eng, desc, seed, stop_half=geom == "small_stop")
     a, ctx_lo, ctx_new = 300, 150, 3
     C = setup_caches(eng, host, desc, a, ctx_lo, seed + 100)
-    anchor = 17
+    anchor = STOP_ANCHOR
     st0 = dict(a=a, anchor=anchor, count=0, rounds_left=1, limit=a + 40, budget=512, eos=-1, ctx_new=ctx_new,
                ctx_pos=a - ctx_new, ctx_lo=ctx_lo, run=1, skip_rounds=1, stop_at=a + 64, ckpt_slot=-1,
                tokens=[anchor])
@@ -172,6 +183,7 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
     toks, M, zs = rnd.markov(W, dict(st0), base_gpu.astype(np.float64))
     gpu_toks = [anchor] + list(st.tokens)[1:st.M]  # commit replaced tokens[0] by the bonus token
     assert st.M >= 1
+    print(f"drafted M: gpu {st.M}, oracle {M}", flush=True)
     for j in range(1, min(len(toks), len(gpu_toks))):
         if toks[j] != gpu_toks[j]:
             crop = list(weights["crop_ids"])
