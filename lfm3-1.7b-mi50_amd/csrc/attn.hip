@@ -506,36 +506,45 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // Page lanes of each row block merge as a fixed tree through LDS, ((0 + 1) + (2 + 3)): in the round of stride st
-  // lane pl with pl % 2st == st hands its state to lane pl - st. Merge `pair` (pl / 2st) of row block rb uses the
-  // area ((rb / RING) * PL / 2 + pair) of ring slot rb % RING: 16 rows of (D + 6) floats, o [16][D + 4] then m [16]
+  // Page lanes of each row block merge through LDS in one round: lanes 1 .. PL-1 store their states, then lane 0 reads
+  // all of them at once and folds them in lane order ((0 + 1) + 2) + 3. Lane q of row block rb uses the area
+  // ((rb / RING) * (PL - 1) + q - 1) of ring slot rb % RING: 16 rows of (D + 6) floats, o [16][D + 4], then m [16]
   // and l [16].
   if constexpr (PL > 1) {
     constexpr int ROWF = D + 4, AREAF = 16 * (ROWF + 2);
-    for (int st = 1; st < PL; st *= 2) {
-      __syncthreads();
-      const int pair = pl / (2 * st);
-      float* area = nullptr;
+    float* areas = nullptr;
 #pragma unroll
-      for (int i = 0; i < RING; ++i)
-        if (rb % RING == i) area = reinterpret_cast<float*>(slots[i]) + ((rb / RING) * (PL / 2) + pair) * AREAF;
-      if (pl % (2 * st) == st) {
+    for (int i = 0; i < RING; ++i)
+      if (rb % RING == i) areas = reinterpret_cast<float*>(slots[i]) + (rb / RING) * (PL - 1) * AREAF;
+    __syncthreads();  // every wave is done with the ring
+    if (pl != 0) {
+      float* area = areas + (pl - 1) * AREAF;
 #pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc) *reinterpret_cast<f32x4*>(area + n * ROWF + 16 * cc + 4 * g) = rs.o[0][cc];
-        if (g == 0) {
-          area[16 * ROWF + n] = rs.m[0];
-          area[16 * ROWF + 16 + n] = rs.ls[0][0];
-        }
+      for (int cc = 0; cc < D / 16; ++cc) *reinterpret_cast<f32x4*>(area + n * ROWF + 16 * cc + 4 * g) = rs.o[0][cc];
+      if (g == 0) {
+        area[16 * ROWF + n] = rs.m[0];
+        area[16 * ROWF + 16 + n] = rs.ls[0][0];
       }
-      __syncthreads();
-      if (pl % (2 * st) == 0) {
-        const float mb = area[16 * ROWF + n], lb = area[16 * ROWF + 16 + n];
-        const float mx = fmaxf(rs.m[0], mb);
-        const float fa = fast_exp2(rs.m[0] - mx), fb = fast_exp2(mb - mx);
+    }
+    __syncthreads();
+    if (pl == 0) {
+      f32x4 ob[PL - 1][D / 16];
+      float mb[PL - 1], lb[PL - 1];
 #pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc)
-          rs.o[0][cc] = rs.o[0][cc] * fa + *reinterpret_cast<const f32x4*>(area + n * ROWF + 16 * cc + 4 * g) * fb;
-        rs.ls[0] = rs.ls[0] * fa + f32x4{lb, lb, lb, lb} * fb;
+      for (int q = 0; q < PL - 1; ++q) {
+        const float* area = areas + q * AREAF;
+#pragma unroll
+        for (int cc = 0; cc < D / 16; ++cc) ob[q][cc] = *reinterpret_cast<const f32x4*>(area + n * ROWF + 16 * cc + 4 * g);
+        mb[q] = area[16 * ROWF + n];
+        lb[q] = area[16 * ROWF + 16 + n];
+      }
+#pragma unroll
+      for (int q = 0; q < PL - 1; ++q) {
+        const float mx = fmaxf(rs.m[0], mb[q]);
+        const float fa = fast_exp2(rs.m[0] - mx), fb = fast_exp2(mb[q] - mx);
+#pragma unroll
+        for (int cc = 0; cc < D / 16; ++cc) rs.o[0][cc] = rs.o[0][cc] * fa + ob[q][cc] * fb;
+        rs.ls[0] = rs.ls[0] * fa + f32x4{lb[q], lb[q], lb[q], lb[q]} * fb;
         rs.m[0] = mx;
       }
     }
@@ -708,7 +717,7 @@ static bool lds_shape(int D, int nblk, int* pl, int* lpw) {
   int PL = 1;
   for (int c = pl_max; c >= 1; c /= 2) {
     const size_t slot = (size_t)c * 4 * PAGE * D;
-    const size_t merge = (size_t)((nblk - 1) / RING + 1) * (c > 1 ? c / 2 : 1) * 16 * (D + 6) * 4;
+    const size_t merge = (size_t)((nblk - 1) / RING + 1) * (c > 1 ? c - 1 : 1) * 16 * (D + 6) * 4;
     if (nblk * c <= 16 && (c == 1 || merge <= slot)) {
       PL = c;
       break;
