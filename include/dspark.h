@@ -193,12 +193,15 @@ int dspark_engine_init_random(dspark_engine* e, uint64_t seed, dspark_stream_t s
 int dspark_engine_tensor(dspark_engine* e, const char* name, void** ptr, size_t* bytes);
 int dspark_engine_tensor_count(dspark_engine* e);
 const char* dspark_engine_tensor_name(dspark_engine* e, int32_t i);
-/* Build the tables derived from the weights: the drafter's Markov transition table (crop_rows <= 16384), T[c][r] =
- * w1q[crop_ids[c]] . w2q[r], from which every draft step after the first reads one row instead of the whole w2q. It
- * is enqueued by itself before the next round after dspark_engine_init_random or after a dspark_engine_tensor lookup
- * of "markov.w1q", "markov.w1s", "markov.w2q", "conf_c2" or "crop_ids"; a caller that writes those weights through a
- * pointer obtained earlier calls this before its next round. No counterpart in the reference (markov_phase,
- * dspark.hip:2322-2366, takes the dots at every step). */
+/* Build what the round reads derived from the weights: a tile-major copy of every int8 GEMM weight (each wave's
+ * weight load one contiguous 1 KB) and the drafter's Markov transition table (crop_rows <= 16384), T[c][r] =
+ * w1q[crop_ids[c]] . w2q[r], from which every draft step after the first reads one row instead of the whole w2q. What
+ * may be stale is rebuilt by itself before the next round: everything after dspark_engine_init_random, a GEMM
+ * weight's copy after a dspark_engine_tensor lookup of that weight, the table after a lookup of "markov.w1q",
+ * "markov.w1s", "markov.w2q", "conf_c2" or "crop_ids". A caller that writes weights through pointers obtained
+ * earlier calls this (it rebuilds everything) before its next round. No counterpart in the reference, whose kernel
+ * reads its own packed weights directly (dspark.go:635-659) and takes the Markov dots at every step (markov_phase,
+ * dspark.hip:2322-2366). */
 int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream);
 /* Enqueue one round on `stream`. force_m > 0 skips the drafter and verifies tokens[0..force_m) of the State as they
  * are (the reference's force_m debug mode, dspark.hip:147, 2442-2451). force_m = -1 runs the drafter, then replaces

@@ -130,6 +130,7 @@ struct GemmParams {
   uint32_t* counters;       // split-K arrival counter per group (zero between calls); nullptr: separate reduce kernel
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
   int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
+  int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
 };
 
 struct GemmPlan {
@@ -140,6 +141,8 @@ size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N);
 size_t gemm_ws_bytes(int M, int N, int K);  // for the default split plan of an int8 GEMM
 uint32_t* gemm_ws_counters(void* ws, const GemmPlan& pl, int M, int N);  // the counters inside the workspace
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
+// Tile-major copy of an int8 weight [N][K] (the layout GemmParams::tiled reads), N % 16 == 0, K % 64 == 0.
+int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s);
 
 size_t verify_argmax_ws(int M, int V);
 

@@ -72,6 +72,18 @@ struct dspark_engine {
   // rebuilt before the next round whenever a weight it depends on may have been written
   float *mtab = nullptr, *mc2c = nullptr, *ms1c = nullptr;
   bool mtab_dirty = true;
+  // Tile-major copies of the int8 GEMM weights (what the round's GEMMs read), rebuilt by dspark_engine_prepare from
+  // the row-major tensors whenever one may have been written
+  struct TiledW {
+    const uint8_t* src;
+    uint8_t* dst;
+    int N, K;
+    bool dirty;
+  };
+  std::vector<TiledW> tiles;
+  std::map<const void*, size_t> tile_of;       // row-major weight -> its tile entry
+  std::map<std::string, size_t> tile_by_name;  // tensor name -> its tile entry
+  bool tiles_dirty = true;
   _Float16* rope = nullptr;
   int32_t* ring_bt = nullptr;
   int ring_pages = 0;
@@ -110,7 +122,12 @@ struct dspark_engine {
     if (*err) return nullptr;
     void* p = nullptr;
     const size_t nb = bytes ? bytes : 16;
-    if (hipMalloc(&p, nb) != hipSuccess || hipMemset(p, 0, nb) != hipSuccess) {
+#ifdef DSPARK_ALLOC_ROUND
+    const size_t ab = (nb + (DSPARK_ALLOC_ROUND) - 1) / (DSPARK_ALLOC_ROUND) * (DSPARK_ALLOC_ROUND);
+#else
+    const size_t ab = nb;
+#endif
+    if (hipMalloc(&p, ab) != hipSuccess || hipMemset(p, 0, nb) != hipSuccess) {
       *err = DSPARK_ENOSPACE;
       return nullptr;
     }
@@ -187,6 +204,11 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
+  auto it = e->tile_of.find(w);
+  if (it != e->tile_of.end()) {
+    p.w = e->tiles[it->second].dst;
+    p.tiled = 1;
+  }
   if (p.ksplit > 1) {
     if (gemm_ws_bytes(pl, M, N) > e->ws_gemm_bytes) return DSPARK_ENOSPACE;
     p.part = static_cast<float*>(e->ws_gemm);
@@ -433,13 +455,23 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   }
   int err = 0;
   auto h16 = [&](const std::string& n, size_t count) { return static_cast<_Float16*>(e->alloc(n, count * 2, &err)); };
-  auto u8 = [&](const std::string& n, size_t count) { return static_cast<uint8_t*>(e->alloc(n, count, &err)); };
+  // an int8 GEMM weight [N][K] and its tile-major copy
+  auto u8 = [&](const std::string& n, int N, int K) {
+    uint8_t* w = static_cast<uint8_t*>(e->alloc(n, (size_t)N * K, &err));
+    uint8_t* t = static_cast<uint8_t*>(e->alloc("", (size_t)N * K, &err));
+    if (!err) {
+      e->tile_of[w] = e->tiles.size();
+      e->tile_by_name[n] = e->tiles.size();
+      e->tiles.push_back({w, t, N, K, true});
+    }
+    return w;
+  };
   const int64_t positions = (int64_t)max_context + B;
   e->kv_pages = (positions + PAGE - 1) / PAGE + 1;
   e->ring_pages = d.ring_positions / PAGE;
   e->embed = h16("embed", (size_t)d.vocab * H);
   e->final_norm = h16("final_norm", H);
-  e->head_w = u8("head.w", (size_t)d.vocab * H);
+  e->head_w = u8("head.w", d.vocab, H);
   e->head_s = h16("head.s", d.vocab);
   int tap_slot[DSPARK_MAX_LAYERS];
   for (int i = 0; i < DSPARK_MAX_LAYERS; ++i) tap_slot[i] = -1;
@@ -455,14 +487,14 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     W.post_op_norm = h16(pre + "post_op_norm", H);
     W.post_ffn_norm = h16(pre + "post_ffn_norm", H);
     W.mix_rows = W.kind == 0 ? 3 * H : align16(QH * D + 2 * KVH * D + QH);
-    W.mix_w = u8(pre + "mix.w", (size_t)W.mix_rows * H);
+    W.mix_w = u8(pre + "mix.w", W.mix_rows, H);
     W.mix_s = h16(pre + "mix.s", W.mix_rows);
-    W.out_w = u8(pre + "out.w", (size_t)H * H);
+    W.out_w = u8(pre + "out.w", H, H);
     W.out_s = h16(pre + "out.s", H);
     W.ffn = d.ffn;
-    W.w13_w = u8(pre + "w13.w", (size_t)2 * d.ffn * H);
+    W.w13_w = u8(pre + "w13.w", 2 * d.ffn, H);
     W.w13_s = h16(pre + "w13.s", 2 * d.ffn);
-    W.w2_w = u8(pre + "w2.w", (size_t)H * d.ffn);
+    W.w2_w = u8(pre + "w2.w", H, d.ffn);
     W.w2_s = h16(pre + "w2.s", H);
     if (W.kind == 0) {
       W.conv_w = h16(pre + "conv.w", (size_t)H * d.conv_kernel);
@@ -485,14 +517,14 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     W.op_norm = h16(pre + "op_norm", H);
     W.ffn_norm = h16(pre + "ffn_norm", H);
     W.mix_rows = align16(QH * D + 2 * KVH * D);
-    W.mix_w = u8(pre + "mix.w", (size_t)W.mix_rows * H);
+    W.mix_w = u8(pre + "mix.w", W.mix_rows, H);
     W.mix_s = h16(pre + "mix.s", W.mix_rows);
-    W.out_w = u8(pre + "out.w", (size_t)H * H);
+    W.out_w = u8(pre + "out.w", H, H);
     W.out_s = h16(pre + "out.s", H);
     W.ffn = d.draft_ffn;
-    W.w13_w = u8(pre + "w13.w", (size_t)2 * d.draft_ffn * H);
+    W.w13_w = u8(pre + "w13.w", 2 * d.draft_ffn, H);
     W.w13_s = h16(pre + "w13.s", 2 * d.draft_ffn);
-    W.w2_w = u8(pre + "w2.w", (size_t)H * d.draft_ffn);
+    W.w2_w = u8(pre + "w2.w", H, d.draft_ffn);
     W.w2_s = h16(pre + "w2.s", H);
     W.q_norm = h16(pre + "q_norm", D);
     W.k_norm = h16(pre + "k_norm", D);
@@ -503,7 +535,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   }
   e->draft_norm = h16("draft_norm", H);
   e->crop_n = align16(d.crop_rows + 1);
-  e->crop_w = u8("crop.w", (size_t)e->crop_n * H);
+  e->crop_w = u8("crop.w", e->crop_n, H);
   e->crop_s = h16("crop.s", e->crop_n);
   e->crop_ids = static_cast<int32_t*>(e->alloc("crop_ids", (size_t)d.crop_rows * 4, &err));
   e->w2q = static_cast<int8_t*>(e->alloc("markov.w2q", (size_t)d.crop_rows * d.markov_rank, &err));
@@ -517,11 +549,11 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     e->ms1c = static_cast<float*>(e->alloc("", (size_t)d.crop_rows * 4, &err));
   }
   e->tap_norms = h16("tap_norms", (size_t)d.n_taps * H);
-  e->fc_w = u8("fc.w", (size_t)H * d.n_taps * H);
+  e->fc_w = u8("fc.w", H, d.n_taps * H);
   e->fc_s = h16("fc.s", H);
   e->hidden_norm = h16("hidden_norm", H);
   const int ckv_rows = d.draft_layers * 2 * KVH * D;
-  e->ckv_w = u8("ckv.w", (size_t)ckv_rows * H);
+  e->ckv_w = u8("ckv.w", ckv_rows, H);
   e->ckv_s = h16("ckv.s", ckv_rows);
   e->rope = h16("rope", (size_t)(positions + 1) * D);
   // request state and activations
@@ -603,6 +635,11 @@ int dspark_engine_tensor(dspark_engine* e, const char* name, void** ptr, size_t*
   static const char* const table_inputs[] = {"markov.w1q", "markov.w1s", "markov.w2q", "conf_c2", "crop_ids"};
   for (const char* n : table_inputs)
     if (std::strcmp(name, n) == 0) e->mtab_dirty = true;
+  auto tw = e->tile_by_name.find(name);
+  if (tw != e->tile_by_name.end()) {
+    e->tiles[tw->second].dirty = true;
+    e->tiles_dirty = true;
+  }
   if (ptr) *ptr = it->second.ptr;
   if (bytes) *bytes = it->second.bytes;
   return 0;
@@ -679,24 +716,40 @@ int dspark_engine_init_random(dspark_engine* e, uint64_t seed, dspark_stream_t s
   if (rc) return rc;
   hipLaunchKernelGGL(crop_ids_kernel, dim3((d.crop_rows + 255) / 256), dim3(256), 0, s, e->crop_ids, d.crop_rows, d.vocab);
   e->mtab_dirty = true;
+  for (auto& t : e->tiles) t.dirty = true;
+  e->tiles_dirty = true;
   return (int)hipGetLastError();
 }
 
-int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream) {
-  if (!e) return DSPARK_EINVAL;
-  if (!e->mtab) return 0;
+namespace {
+// Rebuild what is derived from the weights: everything (all) or what may have changed since the last build.
+int prepare(dspark_engine* e, hipStream_t s, bool all) {
+  for (auto& t : e->tiles) {
+    if (!t.dirty && !all) continue;
+    const int rc = gemm_tile_launch(t.src, t.dst, t.N, t.K, s);
+    if (rc) return rc;
+    t.dirty = false;
+  }
+  e->tiles_dirty = false;
+  if (!e->mtab || (!e->mtab_dirty && !all)) return 0;
   const dspark_model_desc& d = e->d;
   const int rc = markov_table_launch(e->w1q, e->w1s, e->c2, e->w2q, e->crop_ids, d.crop_rows, d.markov_rank, d.vocab,
-                                     e->mtab, e->mc2c, e->ms1c, reinterpret_cast<hipStream_t>(stream));
+                                     e->mtab, e->mc2c, e->ms1c, s);
   if (!rc) e->mtab_dirty = false;
   return rc;
+}
+}  // namespace
+
+int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream) {
+  if (!e) return DSPARK_EINVAL;
+  return prepare(e, reinterpret_cast<hipStream_t>(stream), true);
 }
 
 int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream) {
   if (!e || force_m < -1 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (e->mtab_dirty) {
-    const int rc = dspark_engine_prepare(e, stream);
+  if (e->mtab_dirty || e->tiles_dirty) {
+    const int rc = prepare(e, s, false);
     if (rc) return rc;
   }
   const int bucket = plan_a / ROUND_PLAN_BUCKET;

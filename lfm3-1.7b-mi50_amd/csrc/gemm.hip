@@ -59,6 +59,7 @@ constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-sc
 constexpr int GEMM_VMCNT0 = 0x0F70;     // s_waitcnt vmcnt(0), other counters left unconstrained
 // s_waitcnt immediate: vmcnt(n) (6 bits, split low 4 / high 2), other counters left unconstrained
 #define GEMM_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
+#define GEMM_LGKMCNT0 0xC07F  // lgkmcnt(0), vmcnt and expcnt unconstrained
 constexpr int GEMM_FIXUP_BATCH = 8;     // split partials loaded per batch by the last split
 
 // Weight loads go in batches of CPB chunks (64 columns: 16 B per lane int8, 32 B fp16), two batches in registers.
@@ -91,21 +92,32 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0, 0, 0, 0};
 
-  const uint8_t* wrow = reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K * (I8 ? 1 : 2);
+  const bool tiled = I8 && p.tiled;
+  const uint8_t* wrow = tiled ? reinterpret_cast<const uint8_t*>(p.w) + (size_t)strip * chunks * 1024 + lane * 16
+                              : reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K * (I8 ? 1 : 2) + 16 * g;
+  const int cstride = tiled ? 1024 : 64;  // bytes from one 64-column chunk of the lane's row to the next
   // chunks cb .. cb + CPB - 1, clamped to the phase's last chunk ce - 1 (a re-read of a line just fetched)
   auto load = [&](u32x4 (&w)[CPB][WV], int cb, int ce) {
 #pragma unroll
     for (int i = 0; i < CPB; ++i) {
       const int c = min(cb + i, ce - 1);
       if (I8) {
-        w[i][0] = ldg_nt(reinterpret_cast<const u32x4*>(wrow + c * 64 + 16 * g));
+        w[i][0] = ldg_nt(reinterpret_cast<const u32x4*>(wrow + (size_t)c * cstride));
       } else {
-        const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * (c * 64 + 16 * g));
+        const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * c * 64 + 16 * g);  // fp16: 32 B per lane
         w[i][0] = ldg_nt(wp);
         w[i][WV - 1] = ldg_nt(wp + 1);
       }
     }
   };
+  // LDS slot of lane l's X operand in a half-h row: l, or l ^ (4 g + 2 h) when X is staged through registers (the
+  // swizzle spreads a full-line read's 16-byte pieces over every bank group; it permutes slots within the row, so the
+  // reads stay conflict-free)
+  // X goes through registers for the deep-batch plans (phases of 16+ chunks: 32-64 KB of X per workgroup, where
+  // full-line reads beat the direct loads' 16-line gathers; measured on MI355X) and by direct loads otherwise.
+  constexpr int XRG = 16;  // X loads per wave on the register path (TB * 2 * phase chunks <= 64 = XRG * 4 waves)
+  const bool xreg = CPB == 8 && nw >= 4;
+  const int xl0 = xreg ? lane ^ (4 * g) : lane, xl1 = xreg ? lane ^ (4 * g + 2) : lane;
   // chunk cb + i of the phase starting at chunk ph (pc chunks staged). With one token block the batch's X operands
   // are read from LDS before its first MFMA, so their latency is paid once per batch, not once per chunk.
   auto compute = [&](const u32x4 (&w)[CPB][WV], int cb, int ph, int pc) {
@@ -114,9 +126,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < CPB; ++i) {
         const int j = min(cb + i - ph, pc - 1);
-        const u32x4* xp = xs + ((size_t)j * 2) * 64 + lane;
-        xb[i][0] = xp[0];
-        xb[i][1] = xp[64];
+        const u32x4* xp = xs + ((size_t)j * 2) * 64;
+        xb[i][0] = xp[xl0];
+        xb[i][1] = xp[64 + xl1];
       }
 #pragma unroll
       for (int i = 0; i < CPB; ++i) {
@@ -149,9 +161,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         }
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
-          const u32x4* xb = xs + ((size_t)(tb * pc + j) * 2) * 64 + lane;
-          acc[tb] = mfma16x16x32(a[0], as_half8(xb[0]), acc[tb]);
-          acc[tb] = mfma16x16x32(a[1], as_half8(xb[64]), acc[tb]);
+          const u32x4* xb = xs + ((size_t)(tb * pc + j) * 2) * 64;
+          acc[tb] = mfma16x16x32(a[0], as_half8(xb[xl0]), acc[tb]);
+          acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + xl1]), acc[tb]);
         }
       }
     }
@@ -167,6 +179,35 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   for (int ph = c0; ph < c1; ph += PH) {
     const int pc = min(PH, c1 - ph), pe = ph + pc;
     if (ph != c0) __syncthreads();  // every wave is done reading the previous phase
+    if (xreg) {
+      // One load = 8 tokens x one 64-column chunk: lane l reads token 8 (k % 2TB) + l / 8, 16 B at column
+      // 64 j + 8 (l % 8) of chunk j = k / 2TB, so a load covers 8 whole 128-byte lines. The wave's X loads (at most
+      // XRG with four or more waves) go out before the phase's first two weight batches, so the counted wait for them
+      // leaves the weights in flight.
+      const int ninstr = TB * 2 * pc;
+      u32x4 xr[XRG];
+#pragma unroll
+      for (int i = 0; i < XRG; ++i) {
+        const int k = min(wave_u + i * nw, ninstr - 1);
+        const int t = min(8 * (k % (2 * TB)) + (lane >> 3), p.M - 1), j = k / (2 * TB);
+        xr[i] = ldg(reinterpret_cast<const u32x4*>(p.x + (size_t)t * p.K + (size_t)(ph + j) * 64 + 8 * (lane & 7)));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the X loads ahead of the weight loads in issue order
+      load(wa, ph, pe);
+      load(wb, ph + CPB, pe);  // clamped to the phase: a second batch is always issued, used when it exists
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(2 * CPB * WV));
+#pragma unroll
+      for (int i = 0; i < XRG; ++i) {
+        const int k = wave_u + i * nw;
+        const int t = 8 * (k % (2 * TB)) + (lane >> 3), j = k / (2 * TB);
+        const int q = lane & 7, gq = q >> 1, hq = q & 1;
+        if (k < ninstr && t < p.M)
+          xs[(((t >> 4) * pc + j) * 2 + hq) * 64 + (((t & 15) + 16 * gq) ^ (4 * gq + 2 * hq))] = xr[i];
+      }
+      __builtin_amdgcn_s_waitcnt(GEMM_LGKMCNT0);  // this wave's LDS writes (the weights stay in flight)
+      __builtin_amdgcn_s_barrier();
+    } else {
     // Issue order: this wave's X rows, then the phase's first two weight batches; the counted wait below then covers
     // X (the oldest loads) and leaves the weights in flight.
     for (int r = wave_u; r < TB * pc * 2; r += nw) {
@@ -188,6 +229,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPB * WV));
     }
     __builtin_amdgcn_s_barrier();
+    }
     for (int cb = ph; cb < pe; cb += 2 * CPB) {
       compute(wa, cb, ph, pc);
       if (cb + 2 * CPB < pe) load(wa, cb + 2 * CPB, pe);
@@ -297,6 +339,28 @@ __global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int 
   }
   b = wave_max_u64(b);
   if (threadIdx.x == 0) best[t] = b;
+}
+
+// Tile-major copy of an int8 weight [N][K]: tile (strip, chunk) = 1 KB with row n, bytes 16 g .. 16 g + 15 of the
+// chunk at 16 (n + 16 g), i.e. lane l's operand at 16 l, so a wave's weight load is one contiguous 1 KB.
+__global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t* src, uint8_t* dst, int N, int K) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece of the destination
+  if (i >= (size_t)N * K / 16) return;
+  const int l = (int)(i % 64), n = l % 16, g = l / 16;
+  const size_t tile = i / 64;
+  const int chunks = K / 64;
+  const size_t strip = tile / chunks;
+  const int c = (int)(tile % chunks);
+  *reinterpret_cast<u32x4*>(dst + 16 * i) =
+      ldg(reinterpret_cast<const u32x4*>(src + (strip * 16 + n) * (size_t)K + c * 64 + 16 * g));
+}
+
+int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s) {
+  if (N < 16 || N % 16 || K < 64 || K % 64) return DSPARK_EINVAL;
+  const size_t pieces = (size_t)N * K / 16;
+  hipLaunchKernelGGL(gemm_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), N, K);
+  return (int)hipGetLastError();
 }
 
 #ifndef DSPARK_GEMM_TARGET_WGS
