@@ -343,10 +343,11 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
 
 // ---------------------------------------------------------------- LDS-staged verify attention
 // A workgroup owns one (KV head, key split) and every query row of the head: NW = NRB x PL waves, wave w holds row
-// block rb = w % NRB (16 rows: token t, group member j -> row t*G + j) for page lane pl = w / NRB. Step k of the split
-// covers pages pb + k*PL + pl (pl < PL). The workgroup brings a step's PL pages from HBM into one slot of a RING-slot
-// LDS ring with direct-to-LDS buffer loads -- every page byte crosses HBM once -- and each wave reads its page lane's page
-// from LDS for its rows. RING - 1 steps are in flight while one is computed:
+// block rb = w % NRB (16 rows: token t, group member j -> row t*G + j) for page lane pl = w / NRB. A step of the split
+// is PPS = PL x PPL pages (32 KB of K+V whatever the lane count); step k covers pages pb + k*PPS + j*PL + pl
+// (j < PPL) for page lane pl. The workgroup brings a step's pages from HBM into one slot of a RING-slot LDS ring with
+// direct-to-LDS buffer loads -- every page byte crosses HBM once -- and each wave reads its page lane's PPL pages from
+// LDS for its rows. RING - 1 steps (64 KB per CU) are in flight while one is computed:
 //   step k:  s_waitcnt (this wave's loads of step k done) ; s_barrier (everyone's) ; issue step k + RING - 1 into the
 //            slot of step k - 1 (free: every wave finished step k - 1 before the barrier) ; compute step k.
 // The ring slots are separate LDS arrays selected by static index (the loop is unrolled by RING), which lets the
@@ -369,20 +370,28 @@ static_assert(RING == 3 || RING == 4, "ring of 3 or 4 slots");
 #endif
 constexpr int LDS_CPOL = DSPARK_ATTN_LDS_CPOL;
 constexpr int LDS_BT_MAX = 2048;  // pages per split the LDS kernel accepts
+constexpr int LDS_STEP_BYTES = 32768;  // K+V bytes of one ring step (4 pages at D = 64, 2 at D = 128)
+constexpr int ATTN_CPOL_COHERENT = 16;  // buffer-store cache policy SC1: device-scope coherent
 
 __device__ __forceinline__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
 #define DSPARK_LDSP(x) ((__attribute__((address_space(3))) void*)(x))
 
-template <int D, int PL, int LPW>
+template <int D, int PL, int PPL, int LPW>
 __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   constexpr int PAGEB = 4 * PAGE * D;  // K + V bytes of one (page, KV head)
   constexpr int CPG = PAGEB / 1024;    // 1 KB chunks per page: K chunks first, then V^T chunks
-  __shared__ __attribute__((aligned(16))) char ring0[PL * PAGEB], ring1[PL * PAGEB], ring2[PL * PAGEB];
-  __shared__ __attribute__((aligned(16))) char ring3[RING > 3 ? PL * PAGEB : 16];
+  constexpr int PPS = PL * PPL;        // pages per step
+  __shared__ __attribute__((aligned(16))) char ring0[PPS * PAGEB], ring1[PPS * PAGEB], ring2[PPS * PAGEB];
+  __shared__ __attribute__((aligned(16))) char ring3[RING > 3 ? PPS * PAGEB : 16];
   __shared__ __attribute__((aligned(16))) char trash[1024];  // destination of the padding loads
   __shared__ int32_t sm_bt[LDS_BT_MAX];                       // the split's block-table entries
-  __shared__ __attribute__((aligned(16))) char q_lds[(16 / PL) * (D / 32) * 1024];  // Q operands per row block
+  // Q operands of up to 16 / PL row blocks: staged in the last ring slot (not written before step 0, and every wave
+  // has read its Q before step 0's barrier) when they fit it.
+  constexpr int QBYTES = (16 / PL) * (D / 32) * 1024;
+  constexpr bool QRING = QBYTES <= PPS * PAGEB;
+  __shared__ __attribute__((aligned(16))) char q_own[QRING ? 16 : QBYTES];
+  char* const q_lds = QRING ? (RING > 3 ? ring3 : ring2) : q_own;
   if (p.st) {
     if (p.st->run == 0) return;
     attn_range(p);
@@ -407,7 +416,7 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   // split bounds are workgroup-uniform: keep them scalar so every step condition is a scalar branch
   const int pb = __builtin_amdgcn_readfirstlane(p.page0 + split * p.pps);
   const int pe = __builtin_amdgcn_readfirstlane(min(pb + p.pps, p.page0 + p.npages));
-  const int nsteps = pe > pb ? (pe - pb + PL - 1) / PL : 0;
+  const int nsteps = pe > pb ? (pe - pb + PPS - 1) / PPS : 0;
   p.full_lo = __builtin_amdgcn_readfirstlane(p.full_lo);
   p.full_hi = __builtin_amdgcn_readfirstlane(p.full_hi);
   const uint32_t koff = (uint32_t)lane * 16u, voff = (uint32_t)(n * 64 + g * 16);
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
     __syncthreads();
   }
 
-  // Step `k`'s chunks into `slot`: chunk c of [0, PL*CPG) goes to wave c % NW; every wave issues exactly LPW loads
+  // Step `k`'s chunks into `slot`: chunk c of [0, PPS*CPG) goes to wave c % NW; every wave issues exactly LPW loads
   // (chunks past the step, or of pages past the split, become out-of-range loads into `trash`), so the counted waits
   // are compile-time constants.
   auto issue = [&](int k, char* slot) {
@@ -427,11 +436,11 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
     for (int i = 0; i < LPW; ++i) {
       const int c = wave + i * NW;
       const int pp = c / CPG, cc = c % CPG;
-      const int page = pb + k * PL + pp;
+      const int page = pb + k * PPS + pp;
       const bool isv = cc >= CPG / 2;
       char* dst = trash;
       uint32_t off = 0x80000000u;
-      if (c < PL * CPG && page < pe) {
+      if (c < PPS * CPG && page < pe) {
         const int phys = paged ? __builtin_amdgcn_readfirstlane(sm_bt[page - pb]) : page;
         const uint32_t base = (uint32_t)(phys * p.KVH + h) * (uint32_t)(PAGEB / 2);
         off = isv ? base + (uint32_t)(cc - CPG / 2) * 1024u + voff : base + (uint32_t)cc * 1024u + koff;
@@ -451,19 +460,23 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
     if (k + RING - 1 < nsteps) issue(k + RING - 1, nxt);
-    const int page = pb + k * PL + pl;
-    if (page < pe) {
-      const char* src = cur + pl * PAGEB;
-      Tile<D> tl;
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        tl.k[c / (D / 32)][c % (D / 32)] = *reinterpret_cast<const half8*>(src + c * 1024 + lane * 16);
-        tl.v[c] = *reinterpret_cast<const half8*>(src + (D / 16 + c) * 1024 + lane * 16);
+    for (int j = 0; j < PPL; ++j) {
+      const int pp = j * PL + pl;
+      const int page = pb + k * PPS + pp;
+      if (page < pe) {
+        const char* src = cur + pp * PAGEB;
+        Tile<D> tl;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          tl.k[c / (D / 32)][c % (D / 32)] = *reinterpret_cast<const half8*>(src + c * 1024 + lane * 16);
+          tl.v[c] = *reinterpret_cast<const half8*>(src + (D / 16 + c) * 1024 + lane * 16);
+        }
+        f32x4 sc[1][2];
+        page_scores<D, 1, false>(tl, qf, rs.c, sc, lane);
+        page_prep<D, 1>(p, page, rb * 16, rs, sc, g, lane);
+        page_accumulate<D, 1>(tl, rs, sc);
       }
-      f32x4 sc[1][2];
-      page_scores<D, 1, false>(tl, qf, rs.c, sc, lane);
-      page_prep<D, 1>(p, page, rb * 16, rs, sc, g, lane);
-      page_accumulate<D, 1>(tl, rs, sc);
     }
   };
   // The table (when staged) is in LDS before any other load is issued. Q of each row block goes to LDS with the
@@ -550,13 +563,22 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
     }
   }
   if (pl != 0) return;
+  // The split's partial, stored device-coherent (SC1: written through to memory, so the end of the kernel has no
+  // dirty L2 lines to write back; measured 0.4-0.6 us less per C2 layer than default stores).
   const size_t slot = (size_t)h * p.S + split;
-  float* dst = p.part_acc + (slot * R + rb * 16 + n) * D;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(p.part_acc + slot * R * D, (short)0, R * D * (int)sizeof(float), 0x00020000);
 #pragma unroll
-  for (int cc = 0; cc < D / 16; ++cc) *reinterpret_cast<f32x4*>(dst + 16 * cc + 4 * g) = rs.o[0][cc];
+  for (int cc = 0; cc < D / 16; ++cc)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, rs.o[0][cc]), ra,
+                                           (uint32_t)(((rb * 16 + n) * D + 16 * cc + 4 * g) * sizeof(float)), 0,
+                                           ATTN_CPOL_COHERENT);
   if (g == 0) {
     const float L = rs.ls[0][0];
-    p.part_ml[slot * R + rb * 16 + n] = f32x2{L > 0.f ? rs.m[0] : -INFINITY, L};
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc(p.part_ml + slot * R, (short)0, R * (int)sizeof(f32x2), 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{L > 0.f ? rs.m[0] : -INFINITY, L}), rm,
+                                          (uint32_t)((rb * 16 + n) * sizeof(f32x2)), 0, ATTN_CPOL_COHERENT);
   }
 }
 #undef DSPARK_LDSP
@@ -675,7 +697,10 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const _Float16* k, const 
 #define DSPARK_ATTN_PF 2
 #endif
 #ifndef DSPARK_ATTN_LDS_FILL
-#define DSPARK_ATTN_LDS_FILL 75  // LDS kernel: key splits x KV heads = this percentage of the workgroup slots
+#define DSPARK_ATTN_LDS_FILL 75  // LDS kernel, up to 4 row blocks: key splits x KV heads = this % of the workgroup slots
+#endif
+#ifndef DSPARK_ATTN_LDS_FILL_WIDE
+#define DSPARK_ATTN_LDS_FILL_WIDE 100  // LDS kernel, 5 or more row blocks (compute-bound): the same percentage
 #endif
 #ifndef DSPARK_ATTN_OCC2_MAX_PAGES
 #define DSPARK_ATTN_OCC2_MAX_PAGES 12  // pages per wave (at one workgroup per CU) below which OCC = 2 is used
@@ -703,28 +728,32 @@ static void launch_attn(const AttnParams& p, hipStream_t s) {
   hipLaunchKernelGGL((verify_attn_kernel<D, QB, PF, OCC, QLDS>), dim3((units + 7) / 8 * 8 * p.RG), dim3(256), 0, s, p);
 }
 
-template <int D, int PL, int LPW>
+template <int D, int PL, int PPL, int LPW>
 static void launch_lds(const AttnParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((verify_attn_lds_kernel<D, PL, LPW>), dim3(p.KVH * p.S), dim3(p.nrb * PL * 64), 0, s, p);
+  hipLaunchKernelGGL((verify_attn_lds_kernel<D, PL, PPL, LPW>), dim3(p.KVH * p.S), dim3(p.nrb * PL * 64), 0, s, p);
 }
 
-// LDS-ring shape for nblk row blocks: page lanes PL (NRB * PL <= 16 waves; the page-lane merge fits the ring) and the
-// loads per wave per step LPW = ceil(chunks per page / NRB). Returns false when the register kernel is needed.
-static bool lds_shape(int D, int nblk, int* pl, int* lpw) {
+// LDS-ring shape for nblk row blocks: a step is PPS = LDS_STEP_BYTES / page bytes pages; page lanes PL (NRB * PL <= 16
+// waves; the page-lane merge fits a ring slot), PPL = PPS / PL pages per lane per step, and loads per wave per step
+// LPW = ceil(chunks per step / waves). Returns false when the register kernel is needed.
+static bool lds_shape(int D, int nblk, int* pl, int* ppl, int* lpw) {
   if (!DSPARK_ATTN_LDS || nblk < 1 || nblk > 16) return false;
-  const int cpg = D / 8;
-  const int pl_max = D == 64 ? 4 : 2;
+  const int pageb = 4 * PAGE * D, cpg = pageb / 1024;
+  int pps = LDS_STEP_BYTES / pageb;
   int PL = 1;
-  for (int c = pl_max; c >= 1; c /= 2) {
-    const size_t slot = (size_t)c * 4 * PAGE * D;
+  for (int c = pps; c >= 1; c /= 2) {
     const size_t merge = (size_t)((nblk - 1) / RING + 1) * (c > 1 ? c - 1 : 1) * 16 * (D + 6) * 4;
-    if (nblk * c <= 16 && (c == 1 || merge <= slot)) {
+    if (nblk * c <= 16 && (c == 1 || merge <= (size_t)LDS_STEP_BYTES)) {
       PL = c;
       break;
     }
   }
+  // Q staged apart from the ring (it does not fit one slot: D = 128 with one page lane) -> one page per lane per step,
+  // so ring + Q stay within the 160 KB of LDS.
+  if ((16 / PL) * (D / 32) * 1024 > pps * pageb) pps = PL;
   *pl = PL;
-  *lpw = (cpg + nblk - 1) / nblk;
+  *ppl = pps / PL;
+  *lpw = (pps * cpg + nblk * PL - 1) / (nblk * PL);
   return true;
 }
 
@@ -745,13 +774,14 @@ void attn_plan(AttnParams& p, int D, int cus) {
     p.pps = (p.npages + S - 1) / S;
     p.S = (p.npages + p.pps - 1) / p.pps;
   };
-  int pl = 0, lpw = 0;
+  int pl = 0, ppl = 0, lpw = 0;
   // LDS-ring kernel: one workgroup per (KV head, split) holding all rows; enough workgroups for every CU (two per
   // CU for small ones); splits no longer than its LDS block table.
-  if (lds_shape(D, nblk, &pl, &lpw) && (p.npages + 63) / 64 <= LDS_BT_MAX) {
+  if (lds_shape(D, nblk, &pl, &ppl, &lpw) && (p.npages + 63) / 64 <= LDS_BT_MAX) {
     p.lds = 1;
     p.nrb = nblk;
     p.pl = pl;
+    p.ppl = ppl;
     p.lpw = lpw;
     p.RG = 1;
     p.QB = 1;
@@ -759,10 +789,13 @@ void attn_plan(AttnParams& p, int D, int cus) {
     p.OCC = nblk * pl <= 8 ? 2 : 1;
     int S = S_req;
     if (S <= 0) {
-      // splits for three quarters of the workgroup slots: measured best on MI355X at 32k and 128k keys, 9 and 16
-      // tokens (the merge and per-split fixed costs outweigh the last quarter of the CUs)
-      S = (cus * p.OCC * DSPARK_ATTN_LDS_FILL / 100 + p.KVH - 1) / p.KVH;
-      S = std::min(S, (p.npages + pl - 1) / pl);  // at least one step per split
+      // Up to 4 row blocks a split streams pages at the HBM rate and three quarters of the workgroup slots measured
+      // best on MI355X (9 and 16 tokens at 32k and 128k keys: the per-split fixed costs outweigh the last quarter of
+      // the CUs). From 5 row blocks on, the per-page matrix-core and exp2 work of the NRB waves is the bound, and
+      // every CU is used (24, 33 and 64 tokens: 4-12 % faster at 32k and 128k keys).
+      const int fill = nblk <= 4 ? DSPARK_ATTN_LDS_FILL : DSPARK_ATTN_LDS_FILL_WIDE;
+      S = (cus * p.OCC * fill / 100 + p.KVH - 1) / p.KVH;
+      S = std::min(S, (p.npages + pl * ppl - 1) / (pl * ppl));  // at least one step per split
     }
     S = std::max(S, (p.npages + LDS_BT_MAX - 1) / LDS_BT_MAX);
     finish(S);
@@ -804,25 +837,28 @@ void attn_bind_workspace(AttnParams& p, int D, void* ws) {
 
 static int launch_split(const AttnParams& p, int D, hipStream_t s) {
   if (p.lds) {
-    // instantiated shapes (see lds_shape): D = 64: PL 4 (LPW 8, 4, 3, 2), 2 (LPW 2, 1), 1 (LPW 1);
-    // D = 128: PL 2 (LPW 16, 8, 6, 4, 3, 2), 1 (LPW 2, 1)
-    const int key = D * 1000 + p.pl * 100 + p.lpw;
+    // instantiated shapes (see lds_shape), as (PL, PPL, LPW): D = 64: (4, 1, 8 | 4 | 3 | 2), (2, 2, 4 | 3 | 2),
+    // (1, 4, 4 | 3 | 2); D = 128: (2, 1, 16 | 8 | 6 | 4 | 3 | 2), (1, 1, 2 | 1)
+    const int key = D * 10000 + p.pl * 1000 + p.ppl * 100 + p.lpw;
     switch (key) {
-      case 64408: launch_lds<64, 4, 8>(p, s); break;
-      case 64404: launch_lds<64, 4, 4>(p, s); break;
-      case 64403: launch_lds<64, 4, 3>(p, s); break;
-      case 64402: launch_lds<64, 4, 2>(p, s); break;
-      case 64202: launch_lds<64, 2, 2>(p, s); break;
-      case 64201: launch_lds<64, 2, 1>(p, s); break;
-      case 64101: launch_lds<64, 1, 1>(p, s); break;
-      case 128216: launch_lds<128, 2, 16>(p, s); break;
-      case 128208: launch_lds<128, 2, 8>(p, s); break;
-      case 128206: launch_lds<128, 2, 6>(p, s); break;
-      case 128204: launch_lds<128, 2, 4>(p, s); break;
-      case 128203: launch_lds<128, 2, 3>(p, s); break;
-      case 128202: launch_lds<128, 2, 2>(p, s); break;
-      case 128102: launch_lds<128, 1, 2>(p, s); break;
-      case 128101: launch_lds<128, 1, 1>(p, s); break;
+      case 644108: launch_lds<64, 4, 1, 8>(p, s); break;
+      case 644104: launch_lds<64, 4, 1, 4>(p, s); break;
+      case 644103: launch_lds<64, 4, 1, 3>(p, s); break;
+      case 644102: launch_lds<64, 4, 1, 2>(p, s); break;
+      case 642204: launch_lds<64, 2, 2, 4>(p, s); break;
+      case 642203: launch_lds<64, 2, 2, 3>(p, s); break;
+      case 642202: launch_lds<64, 2, 2, 2>(p, s); break;
+      case 641404: launch_lds<64, 1, 4, 4>(p, s); break;
+      case 641403: launch_lds<64, 1, 4, 3>(p, s); break;
+      case 641402: launch_lds<64, 1, 4, 2>(p, s); break;
+      case 1282116: launch_lds<128, 2, 1, 16>(p, s); break;
+      case 1282108: launch_lds<128, 2, 1, 8>(p, s); break;
+      case 1282106: launch_lds<128, 2, 1, 6>(p, s); break;
+      case 1282104: launch_lds<128, 2, 1, 4>(p, s); break;
+      case 1282103: launch_lds<128, 2, 1, 3>(p, s); break;
+      case 1282102: launch_lds<128, 2, 1, 2>(p, s); break;
+      case 1281102: launch_lds<128, 1, 1, 2>(p, s); break;
+      case 1281101: launch_lds<128, 1, 1, 1>(p, s); break;
       default: return DSPARK_EUNSUPPORTED;
     }
   } else if (D == 64 && p.OCC == 2) {

@@ -74,7 +74,12 @@ def run_case(torch, orc, host, M, QH, KVH, D, a, start=0, window=0, causal=True,
     (9, 16, 4, 128, 1500, 0, 0, True, False),     # reference geometry
     (9, 16, 4, 128, 1000, 745, 256, True, True),  # reference sliding layer, paged
     (16, 32, 8, 64, 5000, 0, 0, True, True),      # permuted block table
-    (33, 32, 8, 64, 2048, 0, 0, True, False),     # C5 block (M = 33)
+    (33, 32, 8, 64, 2048, 0, 0, True, False),     # C5 block (M = 33): one page lane, 4 pages per lane per step
+    (33, 32, 8, 64, 3100, 0, 0, True, True),      # same, permuted block table, ragged last step
+    (24, 32, 8, 64, 2500, 0, 0, True, True),      # 6 row blocks: two page lanes, 2 pages per lane per step
+    (64, 32, 8, 64, 1500, 200, 0, False, False),  # 16 row blocks, bidirectional block
+    (33, 16, 4, 128, 1700, 0, 0, True, True),     # reference geometry, 9 row blocks: one page per step, Q apart
+    (24, 16, 4, 128, 900, 0, 0, True, False),     # reference geometry, 6 row blocks
 ])
 def test_verify_attention_matches_oracle(dev, orc, M, QH, KVH, D, a, start, window, causal, paged):
     host = load_host()
