@@ -61,6 +61,15 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
   return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - idx);
 }
 
+// K/V page formats (one block of PAGE keys x D dims per (page, KV head)). K is stored in the operand order of
+// v_mfma_f32_16x16x32_f16: key `slot` is row n = 4 (slot / 8) + slot % 4 of key block b = (slot / 4) % 2, and dim d sits
+// in k-step d / 32 of lane n + 16 ((d % 32) / 8), element d % 8. V is stored transposed: [d][slot].
+__device__ __forceinline__ int k_page_elem(int slot, int d, int D) {
+  const int b = (slot >> 2) & 1, n = 4 * (slot >> 3) + (slot & 3);
+  return ((b * (D / 32) + d / 32) * 64 + n + 16 * ((d % 32) / 8)) * 8 + d % 8;
+}
+__device__ __forceinline__ int v_page_elem(int slot, int d) { return d * PAGE + slot; }
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
   const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);

@@ -97,8 +97,6 @@ struct MarkovParams {
 int embed_launch(const void* embed, const struct ::dspark_state* st, int mode, int mask_token, int M, int H, int V, float* h,
                  hipStream_t s);
 int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s);
-int conv_launch(const float* mix, const void* conv_w, void* ring, const struct ::dspark_state* st, int M, int H, int K,
-                void* y, hipStream_t s);
 int qkrope_launch(const QkRopeParams& p, hipStream_t s);
 int markov_launch(const MarkovParams& p, hipStream_t s);
 // Transition table of the drafter's Markov head for crop_rows N <= 16384 (steps after the first read one row of it).
@@ -131,14 +129,26 @@ struct GemmParams {
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
   int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
   int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
+  // Fused row-group epilogue (the group's scaled products go through LDS; y32 is not written):
+  //   GEMM_FUSE_QK: each group is one head of D rows of the attention mix q | k | v | gate: per-head RMS norm + RoPE,
+  //     q -> qk.q16, k and v -> the K/V pages at position st->a + t, gate rows -> qk.gate (query_fresh)
+  //   GEMM_FUSE_CONV: each group is 16 channels [B, C, X] of the conv mix (48 rows): gated short conv, y16 [M][N/3]
+  //     and the conv history ring at st->a + t (conv_wave)
+  int fuse;
+  QkRopeParams qk;
+  const _Float16* conv_w;   // [N/3][conv_k]
+  _Float16* conv_ring;      // [CONV_RING][N/3]
+  int conv_k;
 };
+constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
 
 struct GemmPlan {
   int ksplit = 1, wpg = 1, cpb = 4;
 };
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl);
+// wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV).
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0);
 size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N);
-size_t gemm_ws_bytes(int M, int N, int K);  // for the default split plan of an int8 GEMM
+size_t gemm_ws_bytes(int M, int N, int K, int wpg_req = 0);  // for the split plan of an int8 GEMM
 uint32_t* gemm_ws_counters(void* ws, const GemmPlan& pl, int M, int N);  // the counters inside the workspace
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
 // Tile-major copy of an int8 weight [N][K] (the layout GemmParams::tiled reads), N % 16 == 0, K % 64 == 0.

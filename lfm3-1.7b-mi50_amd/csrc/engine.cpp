@@ -186,8 +186,9 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
   if (r < n) ids[r] = (int32_t)(((int64_t)r * 40503 + 7) % V);
 }
 
+// `fuse` (optional) selects a fused row-group epilogue (GEMM_FUSE_QK / GEMM_FUSE_CONV) and carries its parameters.
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
-         float* y32, _Float16* y16, hipStream_t st) {
+         float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr) {
   GemmParams p = {};
   p.st = e->st;
   p.x = x;
@@ -199,8 +200,18 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
+  int wpg_req = 0;
+  if (fuse) {
+    p.fuse = fuse->fuse;
+    p.qk = fuse->qk;
+    p.conv_w = fuse->conv_w;
+    p.conv_ring = fuse->conv_ring;
+    p.conv_k = fuse->conv_k;
+    p.y32 = nullptr;
+    wpg_req = fuse->fuse == GEMM_FUSE_QK ? fuse->qk.D / 16 : 3;
+  }
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req);
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
@@ -271,7 +282,7 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   return attn_launch(p, d.head_dim, 3, s);
 }
 
-int qkrope(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode, hipStream_t s) {
+QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode) {
   const dspark_model_desc& d = e->d;
   QkRopeParams p = {};
   p.st = e->st;
@@ -294,7 +305,30 @@ int qkrope(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool w
   p.bt = Lw.bt;
   p.pos_from_ctx = ctx_mode;
   p.count_from_ctx = ctx_mode;
-  return qkrope_launch(p, s);
+  return p;
+}
+
+int qkrope(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode, hipStream_t s) {
+  return qkrope_launch(qk_params(e, Lw, mix, row, with_q, ctx_mode), s);
+}
+
+// The attention mix GEMM with q/k norm + RoPE + K/V page write fused into its epilogue (one head per group).
+int gemm_mix_qk(dspark_engine* e, const LayerW& W, hipStream_t s) {
+  GemmParams f = {};
+  f.fuse = GEMM_FUSE_QK;
+  f.qk = qk_params(e, W, nullptr, W.mix_rows, true, false);
+  return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, nullptr, s, &f);
+}
+
+// The conv mix GEMM with the gated short conv fused into its epilogue (16 channels per group); output y16.
+int gemm_mix_conv(dspark_engine* e, const LayerW& W, hipStream_t s) {
+  GemmParams f = {};
+  f.fuse = GEMM_FUSE_CONV;
+  f.conv_w = W.conv_w;
+  f.conv_ring = W.conv_ring;
+  f.conv_k = e->d.conv_kernel;
+  f.qk.st = e->st;
+  return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
 }
 
 #define CK(x)                \
@@ -341,8 +375,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       const LayerW& W = e->DL[j];
       CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, j ? 1 : 0, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
-      CK(gemm(e, e->x16, B, H, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s));
-      CK(qkrope(e, W, e->mix, W.mix_rows, true, false, s));
+      CK(gemm_mix_qk(e, W, s));
       CK(attention(e, W, 1, plan_a, nullptr, s));
       CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
       CK(resnorm(e, e->h[cur], e->vout, 1, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
@@ -385,11 +418,10 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, i ? 1 : 0, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
                e->h[cur ^ 1], tap, s));
     cur ^= 1;
-    CK(gemm(e, e->x16, B, H, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s));
     if (W.kind == 0) {
-      CK(conv_launch(e->mix, W.conv_w, W.conv_ring, e->st, B, H, d.conv_kernel, e->y16, s));
+      CK(gemm_mix_conv(e, W, s));
     } else {
-      CK(qkrope(e, W, e->mix, W.mix_rows, true, false, s));
+      CK(gemm_mix_qk(e, W, s));
       CK(attention(e, W, 0, plan_a, e->gate, s));
     }
     CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
@@ -588,7 +620,8 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   const int Ns[] = {H,        3 * H,    2 * d.ffn, 2 * d.draft_ffn, d.vocab, e->crop_n, ckv_rows,
                     align16(QH * D + 2 * KVH * D + QH), QH * D + 2 * KVH * D};
   for (int K : Ks)
-    for (int N : Ns) gws = std::max(gws, gemm_ws_bytes(B, N, K));
+    for (int N : Ns)
+      for (int wpg_req : {0, 3, D / 16}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req));
   e->ws_gemm_bytes = gws + 256;
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
   const int G = QH / KVH;

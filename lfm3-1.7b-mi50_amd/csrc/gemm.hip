@@ -55,6 +55,139 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
 // TB token blocks of 16. I8: weights biased int8, else fp16.
 __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st && p.st->run == 0; }
 
+// ---------------------------------------------------------------- fused row-group epilogues
+// The workgroup's group of R = 16 * nw rows is complete (unsplit, or summed by the last split): every wave puts its
+// scaled products into an LDS tile [token][row] (stride RS = R + 4 floats), then the group's rows are finished there.
+
+// GEMM_FUSE_QK (query_fresh, dspark.hip:999-1061): R == D, so a group is one head of q | k | v (or the gate rows).
+// One wave per token: lane l < 32 holds dims l + 32 e; q and k heads get the RMS norm (q_norm / k_norm) and RoPE at
+// position st->a + t (pairs (i, i + D/2), i < rot) and go to q16 / the K page; v heads go to the V page as they are.
+__device__ void epi_qk(const GemmParams& gp, const float* tile, int RS, int grow0, int wave, int nw, int lane) {
+  const QkRopeParams& p = gp.qk;
+  const int D = p.D, half = D / 2, ne = D / 32;
+  const int qrows = p.q16 ? p.QH * D : 0, kvrows = p.KVH * D;
+  const int a = p.st->a;
+  if (grow0 >= qrows + 2 * kvrows) {  // gate rows (one per q head), fp32 as they are
+    if (!p.gate) return;
+    const int R = 16 * nw, g0 = grow0 - qrows - 2 * kvrows;
+    for (int e = threadIdx.x; e < gp.M * R; e += 64 * nw) {
+      const int t = e / R, r = e % R;
+      if (g0 + r < p.QH) p.gate[(size_t)t * p.QH + g0 + r] = tile[t * RS + r];
+    }
+    return;
+  }
+  const int kind = grow0 < qrows ? 0 : (grow0 < qrows + kvrows ? 1 : 2);  // q, k, v
+  const int head = (grow0 - (kind == 0 ? 0 : (kind == 1 ? qrows : qrows + kvrows))) / D;
+  const _Float16* nw_ = kind == 0 ? p.q_norm : p.k_norm;
+  for (int t = wave; t < gp.M; t += nw) {
+    const float* src = tile + t * RS;
+    const int pos = a + t;
+    float v[4];
+    for (int e = 0; e < ne; ++e) v[e] = src[(lane & 31) + 32 * e];
+    if (kind == 2) {
+      if (lane < 32) {
+        const int phys = p.bt ? p.bt[pos / PAGE] : pos / PAGE;
+        _Float16* vb = p.vp + ((size_t)phys * p.KVH + head) * (D * PAGE);
+        for (int e = 0; e < ne; ++e) vb[v_page_elem(pos % PAGE, (lane & 31) + 32 * e)] = (_Float16)v[e];
+      }
+      continue;
+    }
+    float ss = 0.f;
+    for (int e = 0; e < ne; ++e) ss += v[e] * v[e];
+    ss = wave_sum(lane < 32 ? ss : 0.f);  // lanes 32..63 duplicate lanes 0..31
+    const float inv = rsqrtf(ss / D + p.eps);
+    for (int e = 0; e < ne; ++e) v[e] = v[e] * inv * (float)nw_[(lane & 31) + 32 * e];
+    const _Float16* rt = p.rope + (size_t)pos * D;
+    float r[4];
+    for (int e = 0; e < ne; ++e) r[e] = v[e];
+    for (int e = 0; e < ne / 2; ++e) {
+      const int i = (lane & 31) + 32 * e;
+      if (i < p.rot) {
+        const float c = (float)rt[i], s = (float)rt[half + i];
+        r[e] = v[e] * c - v[e + ne / 2] * s;
+        r[e + ne / 2] = v[e + ne / 2] * c + v[e] * s;
+      }
+    }
+    if (lane >= 32) continue;
+    if (kind == 0) {
+      _Float16* q = p.q16 + ((size_t)t * p.QH + head) * D;
+      for (int e = 0; e < ne; ++e) q[(lane & 31) + 32 * e] = (_Float16)r[e];
+    } else {
+      const int phys = p.bt ? p.bt[pos / PAGE] : pos / PAGE;
+      _Float16* kb = p.kp + ((size_t)phys * p.KVH + head) * (PAGE * D);
+      for (int e = 0; e < ne; ++e) kb[k_page_elem(pos % PAGE, (lane & 31) + 32 * e, D)] = (_Float16)r[e];
+    }
+  }
+}
+
+// GEMM_FUSE_CONV (conv_wave, dspark.hip:2191-2214): R == 48, so a group is 16 channels c with rows [B, C, X] at 3c ..
+// 3c + 2. One thread per (token, channel): bx = fp16(B X); conv = w[K-1] bx + sum_{k<K-1} w[k] hist[pos-K+1+k] with the
+// history inside the block recomputed from the tile and before it read from the ring; y = fp16(C conv); ring[pos] = bx.
+// Ring slots written (a .. a+M-1) and read (a-K+1 .. a-1) are disjoint for M + K - 1 <= CONV_RING.
+__device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int grow0, int R, int nthreads) {
+  const int H = p.N / 3, c0 = grow0 / 3, nch = R / 3, K = p.conv_k;
+  const int a = p.st->a;
+  for (int e = threadIdx.x; e < p.M * nch; e += nthreads) {
+    const int t = e / nch, cl = e % nch, c = c0 + cl;
+    if (c >= H) continue;
+    constexpr int KMAX = 8;
+    float w[KMAX], bx[KMAX];
+    float C = 0.f, bx_t = 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      w[k] = 0.f;
+      bx[k] = 0.f;
+      if (k < K) {
+        w[k] = (float)p.conv_w[(size_t)c * K + k];
+        const int tt = t - (K - 1) + k;
+        if (tt >= 0) {
+          const float* m = tile + tt * RS + 3 * cl;
+          bx[k] = (float)(_Float16)(m[0] * m[2]);
+          if (k == K - 1) {
+            C = m[1];
+            bx_t = bx[k];
+          }
+        } else {
+          bx[k] = (float)p.conv_ring[(size_t)((a + tt) & (CONV_RING - 1)) * H + c];
+        }
+      }
+    }
+    float conv = 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+      if (k == K - 1) conv = w[k] * bx[k];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+      if (k < K - 1) conv = fmaf(w[k], bx[k], conv);
+    p.conv_ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = (_Float16)bx_t;
+    p.y16[(size_t)t * H + c] = (_Float16)(C * conv);
+  }
+}
+
+template <int TB>
+__device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int wave, int nw, int lane,
+                                    float* tile) {
+  const int R = 16 * nw, RS = R + 4;
+  const int n = lane & 15, g = lane >> 4;
+  const int grow0 = grp * R, r = 16 * wave + 4 * g;
+  f32x4 sc = {1.f, 1.f, 1.f, 1.f};
+  if (p.scale && grow0 + r < p.N) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = (float)ldg(p.scale + grow0 + r + i);
+  }
+  __syncthreads();  // every wave is done with the X slices in LDS
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    const int t = 16 * tb + n;
+    if (t < p.M) *reinterpret_cast<f32x4*>(tile + t * RS + r) = acc[tb] * sc;
+  }
+  __syncthreads();
+  if (p.fuse == GEMM_FUSE_QK)
+    epi_qk(p, tile, RS, grow0, wave, nw, lane);
+  else
+    epi_conv(p, tile, RS, grow0, R, 64 * nw);
+}
+
 constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
 constexpr int GEMM_VMCNT0 = 0x0F70;     // s_waitcnt vmcnt(0), other counters left unconstrained
 // s_waitcnt immediate: vmcnt(n) (6 bits, split low 4 / high 2), other counters left unconstrained
@@ -265,7 +398,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       if (last_s) __hip_atomic_store(p.counters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!last_s || !live) return;
+    if (!last_s || (!live && !p.fuse)) return;
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
       const int t = min(16 * tb + n, p.M - 1);
@@ -283,6 +416,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       }
       acc[tb] = sum;
     }
+  }
+  if (p.fuse) {
+    gemm_group_epilogue<TB>(p, acc, grp, wave, nw, lane, reinterpret_cast<float*>(xs));
+    return;
   }
   if (!live) return;
   if (p.best_part) {
@@ -389,7 +526,8 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
   const int strips = p.N / 16;
   const int groups = (strips + p.wpg - 1) / p.wpg;
   const dim3 grid(groups * p.ksplit), block(64 * p.wpg);
-  const size_t lds = gemm_lds_bytes(tb, p.K, p.ksplit);
+  size_t lds = gemm_lds_bytes(tb, p.K, p.ksplit);
+  if (p.fuse) lds = std::max(lds, (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float));
   switch (tb) {
     case 1: launch_gemm_tb<1, I8>(p, grid, block, lds, s); break;
     case 2: launch_gemm_tb<2, I8>(p, grid, block, lds, s); break;
@@ -403,10 +541,10 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // DSPARK_GEMM_TARGET_WGS while each split keeps DSPARK_GEMM_MIN_CHUNKS chunks, and 8-chunk weight batches when a phase
 // has 16 or more chunks in groups of at most four (4-chunk batches otherwise: more workgroups per CU). No split when
 // `split` is false (the fused head argmax needs whole rows).
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl) {
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req) {
   (void)i8;
   const int strips = N / 16, chunks = K / 64, tb = (M + 15) / 16;
-  const int wpg = strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips));
+  const int wpg = wpg_req > 0 ? wpg_req : (strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips)));
   const int groups = (strips + wpg - 1) / wpg;
   int ks = 1;
   if (split)
@@ -424,9 +562,9 @@ size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N) {
   return (((size_t)pl.ksplit * M * N * sizeof(float) + 255) / 256) * 256 + groups * sizeof(uint32_t);
 }
 
-size_t gemm_ws_bytes(int M, int N, int K) {
+size_t gemm_ws_bytes(int M, int N, int K, int wpg_req) {
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req);
   return gemm_ws_bytes(pl, M, N);
 }
 
@@ -441,6 +579,7 @@ uint32_t* gemm_ws_counters(void* ws, const GemmPlan& pl, int M, int N) {
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
   if (!DSPARK_GEMM_FIXUP) p.counters = nullptr;
+  if (p.fuse && p.ksplit > 1 && !p.counters) return DSPARK_EINVAL;  // a fused epilogue needs the in-kernel fixup
   if (i8)
     launch_gemm<true>(p, s);
   else

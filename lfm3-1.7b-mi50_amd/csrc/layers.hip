@@ -1,8 +1,9 @@
-// Elementwise and small kernels of the DSpark round: embedding, residual + RMS norms, gated short conv, q/k norm +
-// RoPE + K/V page write, the drafter's Markov/confidence steps and the round's bookkeeping. Every kernel reads the
+// Elementwise and small kernels of the DSpark round: embedding, residual + RMS norms, q/k norm + RoPE + K/V page write
+// (the context projection's; the verify and drafter blocks run it in the mix GEMM's epilogue, as they do the gated
+// short conv), the drafter's Markov/confidence steps and the round's bookkeeping. Every kernel reads the
 // positions it needs (a, ctx_pos, ...) from the device State and returns at once when State.run is 0, so a whole
 // round is a fixed launch sequence that can be replayed without the host reading anything back.
-// Reference: norm_compute (dspark.hip:722-843), conv_wave (2191-2214), query_fresh + norm_rope (999-1061, 946-951),
+// Reference: norm_compute (dspark.hip:722-843), query_fresh + norm_rope (999-1061, 946-951),
 // embed (2463-2486), markov_phase + draft loop (2322-2366, 2633-2664), context ring write (2487-2518).
 #include "common.h"
 #include "dspark.h"
@@ -117,52 +118,6 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
   }
 }
 
-// ---------------------------------------------------------------- gated short conv (conv_wave)
-// mix rows per channel c: [B, C, X] at 3c, 3c+1, 3c+2. bx = fp16(B*X); conv = w[K-1]*bx + sum_{k<K-1} w[k]*hist[pos-K+1+k];
-// y = fp16(C*conv); ring[pos] = bx. The history is position-indexed (ring of CONV_RING positions), so a rejected
-// token's entry is simply overwritten by a later round. One thread per (token, channel): the history inside the block
-// is recomputed from the block's own mix rows (bx is a pure function of them), before it from the ring, so no thread
-// waits on another; the ring slots written (a .. a+M-1) and read (a-K+1 .. a-1) are disjoint for M + K - 1 <= CONV_RING.
-__global__ __launch_bounds__(256) void conv_kernel(const float* mix, const _Float16* conv_w, _Float16* ring, const dspark_state* st,
-                                                   int M, int H, int K, _Float16* y) {
-  if (stopped(st)) return;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= M * H) return;
-  const int t = idx / H, c = idx % H;
-  const int a = st->a;
-  constexpr int KMAX = 8;
-  float w[KMAX], bx[KMAX];
-  float C = 0.f, bx_t = 0.f;
-#pragma unroll
-  for (int k = 0; k < KMAX; ++k) {
-    w[k] = 0.f;
-    bx[k] = 0.f;
-    if (k < K) {
-      w[k] = (float)conv_w[(size_t)c * K + k];
-      const int tt = t - (K - 1) + k;  // token of history slot k (k = K - 1: this token)
-      if (tt >= 0) {
-        const float* m = mix + (size_t)tt * 3 * H + 3 * c;
-        bx[k] = (float)(_Float16)(m[0] * m[2]);
-        if (k == K - 1) {
-          C = m[1];
-          bx_t = bx[k];
-        }
-      } else {
-        bx[k] = (float)ring[(size_t)((a + tt) & (CONV_RING - 1)) * H + c];
-      }
-    }
-  }
-  float conv = 0.f;
-#pragma unroll
-  for (int k = 0; k < KMAX; ++k)
-    if (k == K - 1) conv = w[k] * bx[k];
-#pragma unroll
-  for (int k = 0; k < KMAX; ++k)
-    if (k < K - 1) conv = fmaf(w[k], bx[k], conv);
-  ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = (_Float16)bx_t;
-  y[(size_t)t * H + c] = (_Float16)(C * conv);
-}
-
 // ---------------------------------------------------------------- q/k norm + RoPE + K/V page write (query_fresh)
 // One wave per (token, head) over heads [0, QH) for q and [QH, QH + KVH) for k (v rides with k). Row layout of `mix`
 // per token: q [QH*D] | k [KVH*D] | v [KVH*D] | gate [QH] (gate optional), `row` floats apart. Position of token t:
@@ -228,12 +183,10 @@ __global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) {
   const int phys = p.bt ? p.bt[lp] : lp;
   _Float16* kb = p.kp + ((size_t)phys * p.KVH + kvh) * (PAGE * D);
   _Float16* vb = p.vp + ((size_t)phys * p.KVH + kvh) * (D * PAGE);
-  const int b = (slot >> 2) & 1, nrow = 4 * (slot >> 3) + (slot & 3);
   for (int e = 0; e < ne; ++e) {
     const int d = (lane & 31) + 32 * e;
-    const int s = d / 32, g = (d % 32) / 8, j = d % 8;
-    kb[((size_t)(b * (D / 32) + s) * 64 + nrow + 16 * g) * 8 + j] = (_Float16)r[e];
-    vb[(size_t)d * PAGE + slot] = (_Float16)vsrc[d];
+    kb[k_page_elem(slot, d, D)] = (_Float16)r[e];
+    vb[v_page_elem(slot, d)] = (_Float16)vsrc[d];
   }
 }
 
@@ -517,12 +470,6 @@ int embed_launch(const void* embed, const dspark_state* st, int mode, int mask_t
 }
 int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) {
   hipLaunchKernelGGL(resnorm_kernel, dim3(rows, groups), dim3(256), 0, s, p);
-  return (int)hipGetLastError();
-}
-int conv_launch(const float* mix, const void* conv_w, void* ring, const dspark_state* st, int M, int H, int K, void* y,
-                hipStream_t s) {
-  hipLaunchKernelGGL(conv_kernel, dim3((M * H + 255) / 256), dim3(256), 0, s, mix, (const _Float16*)conv_w, (_Float16*)ring, st,
-                     M, H, K, (_Float16*)y);
   return (int)hipGetLastError();
 }
 int qkrope_launch(const QkRopeParams& p, hipStream_t s) {
