@@ -158,9 +158,10 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
   if (p.ksplit > 1) {
+    if (gemm_groups(pl, N) > GEMM_COUNTER_SLOTS) return DSPARK_EINVAL;
     if (!workspace || workspace_bytes < gemm_ws_bytes(pl, M, N)) return DSPARK_ENOSPACE;
-    p.part = static_cast<float*>(workspace);
-    p.counters = gemm_ws_counters(workspace, pl, M, N);
+    p.part = gemm_ws_partials(workspace);
+    p.counters = gemm_ws_counters(workspace);
   }
   return gemm_launch(p, true, S(stream));
 }

@@ -29,7 +29,13 @@ REF_SMALL = dict(hidden=512, ffn=512, vocab=2048, n_layers=6, layer_kind=[0, 0, 
 # SMALL with the full-size cropped head and Markov rank (16384 rows, rank 256): every thread of the Markov chain's
 # workgroup owns rows.
 SMALL_WIDE = dict(SMALL, vocab=32768, mask_token=32767, crop_rows=16384, markov_rank=256)
-GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE}
+# Wide enough that every int8 GEMM of the round splits K across workgroups, with different split counts and shapes
+# sharing the engine's one GEMM workspace (out 2-way, w2 8-way, w13 / mix / head 2-way, fc 4-way).
+MID = dict(hidden=1024, ffn=4096, vocab=4096, n_layers=4, layer_kind=[0, 1, 0, 2], q_heads=16, kv_heads=4, head_dim=64,
+           conv_kernel=3, window=40, rope_base=1e4, rope_pairs=32, draft_layers=2, draft_ffn=2048, block=9,
+           max_drafts=8, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[1, 3], draft_window=100,
+           ring_positions=256, mask_token=4095, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
+GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE, "mid": MID}
 STOP_ANCHOR = 17
 
 
@@ -136,7 +142,8 @@ def near_tie_ok(values, got, want, rel=1e-3):
 
 
 @pytest.mark.parametrize("geom,seed", [("small", 11), ("small", 12), ("ref_small", 13), ("small_stop", 14),
-                                       ("small_stop", 15), ("small_stop", 16), ("small_wide", 17)])
+                                       ("small_stop", 15), ("small_stop", 16), ("small_wide", 17), ("mid", 18),
+                                       ("mid", 19)])
 def test_engine_round_matches_oracle(dev, orc, geom, seed):
     torch = dev
     host = load_host()
@@ -234,7 +241,7 @@ def _greedy_chain(eng, torch, st0, n):
 
 
 @pytest.mark.parametrize("geom,seed,wrong", [("small", 21, ()), ("small", 22, (3, 10, 11, 20)), ("ref_small", 23, ()),
-                                             ("ref_small", 24, (0, 5, 13, 14))])
+                                             ("ref_small", 24, (0, 5, 13, 14)), ("mid", 25, (2, 9))])
 def test_planted_rounds_commit_the_greedy_chain(dev, geom, seed, wrong):
     """Speculative rounds commit exactly the target's greedy chain, whatever the drafts: with drafts planted from the
     chain (force_m = -1), every round commits its drafts' accepted prefix plus the target's own next token. All

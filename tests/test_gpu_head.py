@@ -171,6 +171,41 @@ def test_gemm_split_calls_share_one_workspace(dev, orc, M, N, K):
     # a counter left non-zero would have kept every later call's groups from finishing (NaN outputs above)
 
 
+def test_gemm_split_shapes_share_one_workspace(dev, orc):
+    """Split-K GEMMs of different shapes and split counts in a row on one workspace (the engine's pattern: a wide
+    split writes partials where a narrower split's arrival counters would sit if counters followed the partials):
+    every call matches the oracle, and a second pass over the same calls gives the same bits."""
+    torch = dev
+    host = load_host()
+    lib = host.lib()
+    shapes = [(16, 2048, 8192), (16, 2048, 2048), (9, 6144, 2048), (16, 3104, 2048), (9, 1024, 4096), (16, 2048, 10240)]
+    need = max(lib.dspark_gemm_i8_workspace(M, N, K) for M, N, K in shapes)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    wso = host.Workspace()
+    wso.buf = ws
+    cases = []
+    for i, (M, N, K) in enumerate(shapes):
+        assert lib.dspark_gemm_i8_workspace(M, N, K) > 0  # every shape splits K
+        w = orc.int8_uniform(950 + i, (N, K))
+        s = orc.f32_to_f16(np.random.default_rng(i).uniform(0.5, 1.5, N).astype(np.float32) / np.float32(127 * np.sqrt(K)))
+        x = orc.normal_f16(960 + i, (M, K))
+        cases.append((M, N, K, w, s, x, orc.gemm_i8(x, w, s)))
+    outs = []
+    for rep in range(2):
+        for i, (M, N, K, w, s, x, want) in enumerate(cases):
+            print(f"case gemm mixed shapes pass={rep} M={M} N={N} K={K}", flush=True)
+            wb = torch.from_numpy((w.astype(np.int16) + 128).astype(np.uint8)).cuda()
+            y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+            host.gemm_i8(f16(torch, x), wb, f16(torch, s), y_f32=y, workspace=wso)
+            torch.cuda.synchronize()
+            got = y.cpu().numpy().astype(np.float64)
+            assert np.max(np.abs(got - want)) <= 2e-3 * np.max(np.abs(want)), (rep, M, N, K)
+            if rep == 0:
+                outs.append(y)
+            else:
+                assert torch.equal(y, outs[i]), (M, N, K)
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 16384, 2048), (9, 4096, 2048), (33, 1024, 512)])
 def test_head_argmax_matches_oracle(dev, orc, M, N, K):
     torch = dev
