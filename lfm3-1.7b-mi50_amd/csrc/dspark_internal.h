@@ -134,38 +134,13 @@ struct GemmParams {
   //     q -> qk.q16, k and v -> the K/V pages at position st->a + t, gate rows -> qk.gate (query_fresh)
   //   GEMM_FUSE_CONV: each group is 16 channels [B, C, X] of the conv mix (48 rows): gated short conv, y16 [M][N/3]
   //     and the conv history ring at st->a + t (conv_wave)
-  //   GEMM_FUSE_RES: the residual-norm producer below (64-row groups)
   int fuse;
   QkRopeParams qk;
   const _Float16* conv_w;   // [N/3][conv_k]
   _Float16* conv_ring;      // [CONV_RING][N/3]
   int conv_k;
-  // Sandwich RMS norm carried between two GEMMs (norm_compute: R' = R + a g with g = v * post_w, a = rsqrt(mean(v^2) +
-  // eps); x = fp16(R' * rsqrt(mean(R'^2) + eps) * norm_w)) without a norm kernel. By linearity W x is computed as
-  // inv (W x1 + a W x2) with x1 = fp16(norm_w * R), x2 = fp16(norm_w * g) and the two per-token scalars taken from
-  // per-group partial sums (v.v, R.R, R.g, g.g): sum(R'^2) = R.R + 2 a R.g + a^2 g.g.
-  //   producer (fuse = GEMM_FUSE_RES, N = H): its outputs v with res.r_in (R) and post_w / norm_w give res.g_out,
-  //     res.x1, res.x2 and res.stats_out [group][M][4]
-  //   consumer (x2 != nullptr; x = x1): scalars from res.stats (res.groups groups, width res.H); its group-0 workgroups
-  //     write R' = R + a g (R = res.r_in, g = res.g) over their K range to res.r_out (and res.tap when set)
-  const _Float16* x2;
-  struct {
-    const float* r_in;
-    const float* g;
-    const float* stats;
-    int groups, H;
-    float eps;
-    float* r_out;
-    float* tap;
-    const _Float16* post_w;
-    const _Float16* norm_w;
-    _Float16* x1;
-    _Float16* x2;
-    float* g_out;
-    float* stats_out;
-  } res;
 };
-constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2, GEMM_FUSE_RES = 3;
+constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
 
 struct GemmPlan {
   int ksplit = 1, wpg = 1, cpb = 4;

@@ -98,9 +98,6 @@ struct dspark_engine {
   float *h[2] = {nullptr, nullptr}, *mix = nullptr, *vout = nullptr, *w2out = nullptr, *ctxv = nullptr, *ckvout = nullptr,
         *taps = nullptr, *logits = nullptr, *base = nullptr, *gate = nullptr;
   _Float16 *x16 = nullptr, *q16 = nullptr, *y16 = nullptr, *a16 = nullptr;
-  // residual-norm chain between the verify GEMMs: the producer's GEMM inputs x1 / x2, g = v * post_w, partial sums
-  _Float16 *rx1 = nullptr, *rx2 = nullptr;
-  float *rg = nullptr, *rstats = nullptr;
   uint64_t* keys = nullptr;  // [B] verify best, then [B] Markov best
   void* ws_attn = nullptr;
   size_t ws_attn_bytes = 0;
@@ -210,12 +207,8 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
     p.conv_w = fuse->conv_w;
     p.conv_ring = fuse->conv_ring;
     p.conv_k = fuse->conv_k;
-    p.x2 = fuse->x2;
-    p.res = fuse->res;
-    if (fuse->fuse) p.y32 = fuse->fuse == GEMM_FUSE_RES ? y32 : nullptr;
-    wpg_req = fuse->fuse == GEMM_FUSE_QK ? fuse->qk.D / 16
-              : fuse->fuse == GEMM_FUSE_CONV ? 3
-              : fuse->fuse == GEMM_FUSE_RES ? 4 : 0;
+    p.y32 = nullptr;
+    wpg_req = fuse->fuse == GEMM_FUSE_QK ? fuse->qk.D / 16 : 3;
   }
   GemmPlan pl;
   gemm_plan(M, N, K, true, true, &pl, wpg_req);
@@ -319,50 +312,23 @@ int qkrope(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool w
   return qkrope_launch(qk_params(e, Lw, mix, row, with_q, ctx_mode), s);
 }
 
-// The residual-norm chain's consumer: x1 / x2 and the partial sums of the last producer, R' = R + a g written to
-// r_out (and tap) by the group-0 workgroups. Returns the GEMM input x1.
-const _Float16* res_consumer(dspark_engine* e, GemmParams& f, const float* r_in, float* r_out, float* tap) {
-  f.x2 = e->rx2;
-  f.res.r_in = r_in;
-  f.res.g = e->rg;
-  f.res.stats = e->rstats;
-  f.res.groups = e->d.hidden / 64;
-  f.res.H = e->d.hidden;
-  f.res.eps = e->d.eps;
-  f.res.r_out = r_out;
-  f.res.tap = tap;
-  return e->rx1;
-}
-
-// The residual-norm chain's producer: the GEMM's outputs v (N = H) with the residual R give g = v * post_w,
-// x1 = fp16(norm_w * R), x2 = fp16(norm_w * g) and the partial sums for the next consumer.
-void res_producer(dspark_engine* e, GemmParams& f, const float* r_in, const _Float16* post_w, const _Float16* norm_w) {
-  f.fuse = GEMM_FUSE_RES;
-  f.res.r_in = r_in;
-  f.res.post_w = post_w;
-  f.res.norm_w = norm_w;
-  f.res.x1 = e->rx1;
-  f.res.x2 = e->rx2;
-  f.res.g_out = e->rg;
-  f.res.stats_out = e->rstats;
-}
-
-// The attention mix GEMM with q/k norm + RoPE + K/V page write fused into its epilogue (one head per group). `f`
-// may carry the residual-norm consumer (then x is its x1).
-int gemm_mix_qk(dspark_engine* e, const LayerW& W, const _Float16* x, GemmParams f, hipStream_t s) {
+// The attention mix GEMM with q/k norm + RoPE + K/V page write fused into its epilogue (one head per group).
+int gemm_mix_qk(dspark_engine* e, const LayerW& W, hipStream_t s) {
+  GemmParams f = {};
   f.fuse = GEMM_FUSE_QK;
   f.qk = qk_params(e, W, nullptr, W.mix_rows, true, false);
-  return gemm(e, x, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, nullptr, s, &f);
+  return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, nullptr, s, &f);
 }
 
 // The conv mix GEMM with the gated short conv fused into its epilogue (16 channels per group); output y16.
-int gemm_mix_conv(dspark_engine* e, const LayerW& W, const _Float16* x, GemmParams f, hipStream_t s) {
+int gemm_mix_conv(dspark_engine* e, const LayerW& W, hipStream_t s) {
+  GemmParams f = {};
   f.fuse = GEMM_FUSE_CONV;
   f.conv_w = W.conv_w;
   f.conv_ring = W.conv_ring;
   f.conv_k = e->d.conv_kernel;
   f.qk.st = e->st;
-  return gemm(e, x, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
+  return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
 }
 
 #define CK(x)                \
@@ -409,7 +375,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       const LayerW& W = e->DL[j];
       CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, j ? 1 : 0, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
-      CK(gemm_mix_qk(e, W, e->x16, GemmParams{}, s));
+      CK(gemm_mix_qk(e, W, s));
       CK(attention(e, W, 1, plan_a, nullptr, s));
       CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
       CK(resnorm(e, e->h[cur], e->vout, 1, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
@@ -444,40 +410,25 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   }
   // ---- verify
   CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
-  // Layer 0's op norm is a norm kernel (no branch output yet); after it every sandwich norm is carried by the
-  // residual-norm chain: out and w2 GEMMs produce, the next mix / w13 GEMMs consume (and write the residual).
   int cur = 0;
   for (int i = 0; i < d.n_layers; ++i) {
     const LayerW& W = e->L[i];
     const LayerW* P = i ? &e->L[i - 1] : nullptr;
     float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
-    GemmParams mixf = {};
-    const _Float16* xin = e->x16;
-    if (i == 0)
-      CK(resnorm(e, e->h[cur], nullptr, 0, nullptr, W.op_norm, 1, e->h[cur ^ 1], tap, s));
-    else
-      xin = res_consumer(e, mixf, e->h[cur], e->h[cur ^ 1], tap);
+    CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, i ? 1 : 0, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
+               e->h[cur ^ 1], tap, s));
     cur ^= 1;
     if (W.kind == 0) {
-      CK(gemm_mix_conv(e, W, xin, mixf, s));
+      CK(gemm_mix_conv(e, W, s));
     } else {
-      CK(gemm_mix_qk(e, W, xin, mixf, s));
+      CK(gemm_mix_qk(e, W, s));
       CK(attention(e, W, 0, plan_a, e->gate, s));
     }
-    GemmParams outf = {};
-    res_producer(e, outf, e->h[cur], W.post_op_norm, W.ffn_norm);
-    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, nullptr, nullptr, s, &outf));
-    GemmParams w13f = {};
-    const _Float16* x13 = res_consumer(e, w13f, e->h[cur], e->h[cur ^ 1], nullptr);
+    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
+    CK(resnorm(e, e->h[cur], e->vout, 1, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
     cur ^= 1;
-    CK(gemm(e, x13, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, &w13f));
-    if (i + 1 < d.n_layers) {
-      GemmParams w2f = {};
-      res_producer(e, w2f, e->h[cur], W.post_ffn_norm, e->L[i + 1].op_norm);
-      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, nullptr, nullptr, s, &w2f));
-    } else {
-      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
-    }
+    CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
+    CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
   }
   {
     const LayerW& P = e->L[d.n_layers - 1];
@@ -656,10 +607,6 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->y16 = h16("y16", (size_t)B * H);
   e->vout = static_cast<float*>(e->alloc("vout", (size_t)B * H * 4, &err));
   e->a16 = h16("a16", (size_t)B * std::max(d.ffn, d.draft_ffn));
-  e->rx1 = h16("res.x1", (size_t)B * H);
-  e->rx2 = h16("res.x2", (size_t)B * H);
-  e->rg = static_cast<float*>(e->alloc("res.g", (size_t)B * H * 4, &err));
-  e->rstats = static_cast<float*>(e->alloc("res.stats", (size_t)(H / 64) * B * 16, &err));
   e->w2out = static_cast<float*>(e->alloc("w2out", (size_t)B * H * 4, &err));
   e->ctxv = static_cast<float*>(e->alloc("ctx", (size_t)B * H * 4, &err));
   e->ckvout = static_cast<float*>(e->alloc("ckv_out", (size_t)B * ckv_rows * 4, &err));

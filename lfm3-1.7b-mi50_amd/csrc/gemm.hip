@@ -164,40 +164,6 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
   }
 }
 
-// GEMM_FUSE_RES (the producer side of the residual-norm chain; 64-row groups): one wave per token, lane = row.
-// g = v * post_w, x1 = fp16(norm_w * R), x2 = fp16(norm_w * g), and the group's partial sums (v.v, R.R, R.g, g.g)
-// reduced over the 64 lanes in a fixed order. v itself goes to y32 when that is set.
-__device__ void epi_res(const GemmParams& p, const float* tile, int RS, int grow0, int wave, int nw, int lane) {
-  const int row = grow0 + lane;
-  const bool ok = row < p.N;
-  const float pw = ok ? (float)p.res.post_w[row] : 0.f, nwt = ok ? (float)p.res.norm_w[row] : 0.f;
-  for (int t = wave; t < p.M; t += nw) {
-    const size_t o = (size_t)t * p.N + row;
-    const float v = ok ? tile[t * RS + lane] : 0.f;
-    const float r = ok ? p.res.r_in[o] : 0.f;
-    const float gv = v * pw;
-    if (ok) {
-      p.res.g_out[o] = gv;
-      p.res.x1[o] = (_Float16)(nwt * r);
-      p.res.x2[o] = (_Float16)(nwt * gv);
-      if (p.y32) p.y32[o] = v;
-    }
-    const float s0 = wave_sum(v * v), s1 = wave_sum(r * r), s2 = wave_sum(r * gv), s3 = wave_sum(gv * gv);
-    if (lane == 0)
-      *reinterpret_cast<f32x4*>(p.res.stats_out + ((size_t)(grow0 / 64) * p.M + t) * 4) = f32x4{s0, s1, s2, s3};
-  }
-}
-
-// The consumer's per-token scalars of the residual-norm chain: a = rsqrt(mean(v^2) + eps), inv = rsqrt(mean(R'^2) +
-// eps) with sum(R'^2) = R.R + 2 a R.g + a^2 g.g, partial sums added in group order.
-__device__ __forceinline__ void res_scalars(const GemmParams& p, int t, float& a, float& inv) {
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int gi = 0; gi < p.res.groups; ++gi) s += ldg(reinterpret_cast<const f32x4*>(p.res.stats + ((size_t)gi * p.M + t) * 4));
-  const float H = (float)p.res.H;
-  a = rsqrtf(s[0] / H + p.res.eps);
-  inv = rsqrtf((s[1] + 2.f * a * s[2] + a * a * s[3]) / H + p.res.eps);
-}
-
 template <int TB>
 __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int wave, int nw, int lane,
                                     float* tile) {
@@ -218,10 +184,8 @@ __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB],
   __syncthreads();
   if (p.fuse == GEMM_FUSE_QK)
     epi_qk(p, tile, RS, grow0, wave, nw, lane);
-  else if (p.fuse == GEMM_FUSE_CONV)
-    epi_conv(p, tile, RS, grow0, R, 64 * nw);
   else
-    epi_res(p, tile, RS, grow0, wave, nw, lane);
+    epi_conv(p, tile, RS, grow0, R, 64 * nw);
 }
 
 constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
@@ -240,14 +204,11 @@ constexpr int GEMM_PHASE_UNITS = 32;  // X staged per phase: TB x chunks <= 32 (
 // weights in batches of gemm_cpb chunks, the next batch in flight while the current one is multiplied. Loads past
 // the range are clamped to valid addresses and discarded, so the number of loads in flight is the same on every path
 // and the compiler's waits stay counted.
-// DUAL: the consumer side of the residual-norm chain (two X operands x1 = p.x, x2 = p.x2 staged side by side, two
-// accumulators, combined per token before the split-K / epilogue path).
-template <int TB, bool I8, int CPB, bool DUAL>
+template <int TB, bool I8, int CPB>
 __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   if (gemm_stopped(p)) return;
   extern __shared__ u32x4 xs[];
   constexpr int WV = I8 ? 1 : 2, PH = GEMM_PHASE_UNITS / TB;
-  constexpr int X2OFF = DUAL ? TB * PH * 2 * 64 : 0;  // X2's slots after X1's (u32x4 units)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int grp = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
@@ -260,11 +221,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   const int cpk = (chunks + p.ksplit - 1) / p.ksplit;
   const int c0 = ks * cpk, c1 = min(chunks, c0 + cpk);
 
-  f32x4 acc[TB], acc2[DUAL ? TB : 1];
+  f32x4 acc[TB];
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0, 0, 0, 0};
-#pragma unroll
-  for (int tb = 0; tb < (DUAL ? TB : 1); ++tb) acc2[tb] = f32x4{0, 0, 0, 0};
 
   const bool tiled = I8 && p.tiled;
   const uint8_t* wrow = tiled ? reinterpret_cast<const uint8_t*>(p.w) + (size_t)strip * chunks * 1024 + lane * 16
@@ -290,23 +249,19 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   // X goes through registers for the deep-batch plans (phases of 16+ chunks: 32-64 KB of X per workgroup, where
   // full-line reads beat the direct loads' 16-line gathers; measured on MI355X) and by direct loads otherwise.
   constexpr int XRG = 16;  // X loads per wave on the register path (TB * 2 * phase chunks <= 64 = XRG * 4 waves)
-  const bool xreg = CPB == 8 && nw >= 4 && !DUAL;
+  const bool xreg = CPB == 8 && nw >= 4;
   const int xl0 = xreg ? lane ^ (4 * g) : lane, xl1 = xreg ? lane ^ (4 * g + 2) : lane;
   // chunk cb + i of the phase starting at chunk ph (pc chunks staged). With one token block the batch's X operands
   // are read from LDS before its first MFMA, so their latency is paid once per batch, not once per chunk.
   auto compute = [&](const u32x4 (&w)[CPB][WV], int cb, int ph, int pc) {
     if constexpr (TB == 1) {
-      u32x4 xb[CPB][2], xb2[DUAL ? CPB : 1][2];
+      u32x4 xb[CPB][2];
 #pragma unroll
       for (int i = 0; i < CPB; ++i) {
         const int j = min(cb + i - ph, pc - 1);
         const u32x4* xp = xs + ((size_t)j * 2) * 64;
         xb[i][0] = xp[xl0];
         xb[i][1] = xp[64 + xl1];
-        if constexpr (DUAL) {
-          xb2[i][0] = xp[X2OFF + xl0];
-          xb2[i][1] = xp[X2OFF + 64 + xl1];
-        }
       }
 #pragma unroll
       for (int i = 0; i < CPB; ++i) {
@@ -321,10 +276,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
           }
           acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
           acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
-          if constexpr (DUAL) {
-            acc2[0] = mfma16x16x32(a[0], as_half8(xb2[i][0]), acc2[0]);
-            acc2[0] = mfma16x16x32(a[1], as_half8(xb2[i][1]), acc2[0]);
-          }
         }
       }
       return;
@@ -346,10 +297,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
           const u32x4* xb = xs + ((size_t)(tb * pc + j) * 2) * 64;
           acc[tb] = mfma16x16x32(a[0], as_half8(xb[xl0]), acc[tb]);
           acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + xl1]), acc[tb]);
-          if constexpr (DUAL) {
-            acc2[tb] = mfma16x16x32(a[0], as_half8(xb[X2OFF + xl0]), acc2[tb]);
-            acc2[tb] = mfma16x16x32(a[1], as_half8(xb[X2OFF + 64 + xl1]), acc2[tb]);
-          }
         }
       }
     }
@@ -360,8 +307,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   // gathers its 16 B), the waves taking rows in turn.
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rx2 =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(DUAL ? p.x2 : p.x), (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   u32x4 wa[CPB][WV], wb[CPB][WV];
   for (int ph = c0; ph < c1; ph += PH) {
@@ -407,9 +352,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         const uint32_t off = (uint32_t)(((size_t)t * p.K + (ph + j) * 64 + 16 * g + 8 * h) * 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0,
                                                  0, 0);
-        if constexpr (DUAL)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx2, (__attribute__((address_space(3))) void*)(xs + X2OFF + r * 64), 16,
-                                                   off, 0, 0, 0);
       }
     }
     load(wa, ph, pe);
@@ -426,32 +368,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       if (cb + 2 * CPB < pe) load(wa, cb + 2 * CPB, pe);
       if (cb + CPB < pe) compute(wb, cb + CPB, ph, pc);
       if (cb + 3 * CPB < pe) load(wb, cb + 3 * CPB, pe);
-    }
-  }
-  if constexpr (DUAL) {
-    // y = inv (W x1 + a W x2) per token (the lane's token columns 16 tb + n); linear, so it commutes with the split-K
-    // sum. Group-0 workgroups (one per K range) write R' = R + a g of their K range for the next stage.
-    __shared__ float res_a[64], res_inv[64];
-    for (int t = threadIdx.x; t < p.M; t += blockDim.x) res_scalars(p, t, res_a[t], res_inv[t]);
-    __syncthreads();
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int t = min(16 * tb + n, p.M - 1);
-      acc[tb] = (acc[tb] + res_a[t] * acc2[tb]) * res_inv[t];
-    }
-    if (grp == 0 && p.res.r_out) {
-      const int k0 = c0 * 64, kq = (c1 - c0) * 16;  // float4 columns of the K range
-      for (int e = threadIdx.x; e < p.M * kq; e += blockDim.x) {
-        const int t = e / kq, k = k0 + 4 * (e % kq);
-        const size_t o = (size_t)t * p.K + k;
-        const f32x4 r = ldg(reinterpret_cast<const f32x4*>(p.res.r_in + o));
-        const f32x4 gv = ldg(reinterpret_cast<const f32x4*>(p.res.g + o));
-        f32x4 rn;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) rn[i] = fmaf(res_a[t], gv[i], r[i]);
-        *reinterpret_cast<f32x4*>(p.res.r_out + o) = rn;
-        if (p.res.tap) *reinterpret_cast<f32x4*>(p.res.tap + o) = rn;
-      }
     }
   }
   if (p.ksplit > 1) {
@@ -598,16 +514,10 @@ static size_t gemm_lds_bytes(int tb, int K, int ksplit) {
 
 template <int TB, bool I8>
 static void launch_gemm_tb(const GemmParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
-  if (I8 && p.x2) {
-    if (p.cpb >= 8)
-      hipLaunchKernelGGL((gemm_kernel<TB, I8, 8, true>), grid, block, lds, s, p);
-    else
-      hipLaunchKernelGGL((gemm_kernel<TB, I8, 4, true>), grid, block, lds, s, p);
-  } else if (p.cpb >= 8) {
-    hipLaunchKernelGGL((gemm_kernel<TB, I8, 8, false>), grid, block, lds, s, p);
-  } else {
-    hipLaunchKernelGGL((gemm_kernel<TB, I8, 4, false>), grid, block, lds, s, p);
-  }
+  if (p.cpb >= 8)
+    hipLaunchKernelGGL((gemm_kernel<TB, I8, 8>), grid, block, lds, s, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<TB, I8, 4>), grid, block, lds, s, p);
 }
 
 template <bool I8>
@@ -617,7 +527,6 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
   const int groups = (strips + p.wpg - 1) / p.wpg;
   const dim3 grid(groups * p.ksplit), block(64 * p.wpg);
   size_t lds = gemm_lds_bytes(tb, p.K, p.ksplit);
-  if (p.x2) lds = (size_t)tb * (GEMM_PHASE_UNITS / tb) * 2048 * 2;  // X1 then X2, each at its full phase size
   if (p.fuse) lds = std::max(lds, (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float));
   switch (tb) {
     case 1: launch_gemm_tb<1, I8>(p, grid, block, lds, s); break;
