@@ -157,6 +157,7 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
+  p.kw = pl.kw;
   if (p.ksplit > 1) {
     if (gemm_groups(pl, N) > GEMM_COUNTER_SLOTS) return DSPARK_EINVAL;
     if (!workspace || workspace_bytes < gemm_ws_bytes(pl, M, N)) return DSPARK_ENOSPACE;
@@ -188,6 +189,7 @@ int dspark_head_argmax_f16(const void* x, int32_t M, int32_t K, const void* w, i
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
+  p.kw = pl.kw;
   p.best_part = static_cast<uint64_t*>(workspace);
   p.best = best_keys;
   return gemm_launch(p, false, S(stream));

@@ -128,6 +128,7 @@ struct GemmParams {
   uint32_t* counters;       // split-K arrival counter per group (zero between calls); nullptr: separate reduce kernel
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
   int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
+  int kw;                   // > 0: K-sliced plan, workgroups of wpg strips x kw ranges of K (ksplit 1, gemm_plan)
   int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
   // Fused row-group epilogue (the group's scaled products go through LDS; y32 is not written):
   //   GEMM_FUSE_QK: each group is one head of D rows of the attention mix q | k | v | gate: per-head RMS norm + RoPE,
@@ -143,7 +144,7 @@ struct GemmParams {
 constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
 
 struct GemmPlan {
-  int ksplit = 1, wpg = 1, cpb = 4;
+  int ksplit = 1, wpg = 1, cpb = 4, kw = 0;
 };
 // wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV).
 void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0);

@@ -4,9 +4,11 @@
 // Layout. C^T[rows][tokens] = W[rows][K] * X^T[K][tokens] with v_mfma_f32_16x16x32_f16: a wave streams a 16-row strip
 // of W (lane l: row l%16, 16 contiguous bytes per 64-column chunk), X^T comes from the same 16-byte pieces of the
 // token rows. int8 -> fp16 is exact: byte b (= q + 128) placed under 0x64 is the half 1024 + b, minus 1152 gives q
-// (v_perm_b32 + v_pk_add_f16 per two weights). The four waves of a workgroup take interleaved K chunks of one strip
-// and reduce through LDS in a fixed order; long K splits further across workgroups with a fixed-order reduce kernel.
-// Weights are read once per call for all tokens; the kernel is HBM-bound (about 2*M flop per weight byte).
+// (v_perm_b32 + v_pk_add_f16 per two weights). Two kernels: the K-sliced kernel (up to 32 tokens) gives a workgroup
+// S strips and all of K, its S x KW waves each stream one range of K with every weight load in flight and add the
+// ranges in LDS in range order; the split kernel (any M <= 64) gives each workgroup a share of K and lets the last
+// workgroup of a row group to arrive add the split partials in split order (or a reduce kernel does). Weights are read
+// once per call for all tokens; both are HBM-bound (about 2*M flop per weight byte).
 // Reference: gemv_phase / unit_dot_r (dspark.hip:541-716), head_run<true> (2219-2318), markov argmax (2322-2366).
 #include "common.h"
 #include "dspark.h"
@@ -62,14 +64,14 @@ __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st 
 // GEMM_FUSE_QK (query_fresh, dspark.hip:999-1061): R == D, so a group is one head of q | k | v (or the gate rows).
 // One wave per token: lane l < 32 holds dims l + 32 e; q and k heads get the RMS norm (q_norm / k_norm) and RoPE at
 // position st->a + t (pairs (i, i + D/2), i < rot) and go to q16 / the K page; v heads go to the V page as they are.
-__device__ void epi_qk(const GemmParams& gp, const float* tile, int RS, int grow0, int wave, int nw, int lane) {
+__device__ void epi_qk(const GemmParams& gp, const float* tile, int RS, int grow0, int R, int wave, int nw, int lane) {
   const QkRopeParams& p = gp.qk;
   const int D = p.D, half = D / 2, ne = D / 32;
   const int qrows = p.q16 ? p.QH * D : 0, kvrows = p.KVH * D;
   const int a = p.st->a;
   if (grow0 >= qrows + 2 * kvrows) {  // gate rows (one per q head), fp32 as they are
     if (!p.gate) return;
-    const int R = 16 * nw, g0 = grow0 - qrows - 2 * kvrows;
+    const int g0 = grow0 - qrows - 2 * kvrows;
     for (int e = threadIdx.x; e < gp.M * R; e += 64 * nw) {
       const int t = e / R, r = e % R;
       if (g0 + r < p.QH) p.gate[(size_t)t * p.QH + g0 + r] = tile[t * RS + r];
@@ -164,28 +166,59 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
   }
 }
 
+// S strips per group; the waves with `holder` set hold strip s's sums (every wave of the workgroup finishes the group).
 template <int TB>
-__device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int wave, int nw, int lane,
-                                    float* tile) {
-  const int R = 16 * nw, RS = R + 4;
+__device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int s, int S, bool holder,
+                                    int lane, float* tile) {
+  const int R = 16 * S, RS = R + 4;
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int grow0 = grp * R, r = 16 * wave + 4 * g;
+  const int grow0 = grp * R, r = 16 * s + 4 * g;
   f32x4 sc = {1.f, 1.f, 1.f, 1.f};
-  if (p.scale && grow0 + r < p.N) {
+  if (holder && p.scale && grow0 + r < p.N) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[i] = (float)ldg(p.scale + grow0 + r + i);
   }
-  __syncthreads();  // every wave is done with the X slices in LDS
+  __syncthreads();  // every wave is done with the LDS it used before
+  if (holder) {
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    const int t = 16 * tb + n;
-    if (t < p.M) *reinterpret_cast<f32x4*>(tile + t * RS + r) = acc[tb] * sc;
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = 16 * tb + n;
+      if (t < p.M) *reinterpret_cast<f32x4*>(tile + t * RS + r) = acc[tb] * sc;
+    }
   }
   __syncthreads();
   if (p.fuse == GEMM_FUSE_QK)
-    epi_qk(p, tile, RS, grow0, wave, nw, lane);
+    epi_qk(p, tile, RS, grow0, R, wave, nw, lane);
   else
     epi_conv(p, tile, RS, grow0, R, 64 * nw);
+}
+
+// Finished sums of one strip (lane (n, g): rows 16 strip + 4 g + i of token 16 tb + n): the strip's row-argmax key
+// per token when the call asks for it, then the epilogue store.
+template <int TB>
+__device__ __forceinline__ void gemm_strip_out(const GemmParams& p, const f32x4 (&acc)[TB], int strip, int lane) {
+  const int n = lane & 15, g = lane >> 4, row0 = strip * 16;
+  if (p.best_part) {
+    // fold the lane's 4 rows, then the 4 row groups
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = 16 * tb + n;
+      uint64_t b = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t k = argmax_key(acc[tb][i], (uint32_t)(row0 + 4 * g + i));
+        b = k > b ? k : b;
+      }
+      uint64_t o = shfl_xor_u64(b, 16);
+      b = o > b ? o : b;
+      o = shfl_xor_u64(b, 32);
+      b = o > b ? o : b;
+      if (g == 0 && t < p.M) p.best_part[(size_t)t * (p.N / 16) + strip] = b;
+    }
+  }
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) gemm_store(p, 16 * tb + n, row0, g, acc[tb]);
 }
 
 constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
@@ -418,30 +451,154 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     }
   }
   if (p.fuse) {
-    gemm_group_epilogue<TB>(p, acc, grp, wave, nw, lane, reinterpret_cast<float*>(xs));
+    gemm_group_epilogue<TB>(p, acc, grp, wave, nw, true, lane, reinterpret_cast<float*>(xs));
     return;
   }
   if (!live) return;
-  if (p.best_part) {
-    // Row argmax of this strip per token: lane holds rows row0+4g+i of token n; fold the 4 row groups.
+  gemm_strip_out<TB>(p, acc, strip, lane);
+}
+
+// K-sliced GEMM for one workgroup of S x KW waves (S = wpg strips of 16 rows, KW = kw contiguous ranges of K): wave
+// (s, k) = (wave % S, wave / S) streams strip s over range k with every weight load of the range in flight at once, the
+// KW sums of a strip are added in LDS in range order by the k = 0 waves, and nothing leaves the workgroup before the
+// epilogue (no split partials, no arrival counters). X: XD = false stages the whole of X^T in LDS once for all waves
+// (TB * K / 64 * 2 KB <= 64 KB); XD = true (S = 1, TB = 1) has every wave load its own range of X straight into B
+// operands. Ranges longer than CPW chunks go in batches of CPW. Chunk order inside a range, then range order, fixes the
+// summation order, so results do not depend on timing.
+template <int TB, bool I8, int CPW, bool XD>
+__global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
+  if (gemm_stopped(p)) return;
+  extern __shared__ u32x4 xs[];
+  constexpr int WV = I8 ? 1 : 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int S = p.wpg, KW = p.kw;
+  const int s = wave % S, kq = wave / S;
+  const int grp = blockIdx.x;
+  const int strips = p.N / 16;
+  const int strip_raw = grp * S + s;
+  const bool live = strip_raw < strips;
+  const int strip = live ? strip_raw : strips - 1;
+  const int row0 = strip * 16;
+  const int chunks = p.K / 64;
+  const int cpk = (chunks + KW - 1) / KW;
+  const int c0 = min(chunks, kq * cpk), c1 = min(chunks, c0 + cpk);
+
+  f32x4 acc[TB];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int t = 16 * tb + n;
-      uint64_t b = 0;
+  for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0, 0, 0, 0};
+
+  const bool tiled = I8 && p.tiled;
+  const uint8_t* wrow = tiled ? reinterpret_cast<const uint8_t*>(p.w) + (size_t)strip * chunks * 1024 + lane * 16
+                              : reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K * (I8 ? 1 : 2) + 16 * g;
+  const int cstride = tiled ? 1024 : 64;
+  // chunk cb + i, clamped to the last valid chunk (a re-read of a line just fetched, discarded): the number of loads
+  // issued is CPW * WV on every path, so the counted wait for X below stays exact
+  auto load = [&](u32x4 (&w)[CPW][WV], int cb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint64_t k = argmax_key(acc[tb][i], (uint32_t)(row0 + 4 * g + i));
-        b = k > b ? k : b;
+    for (int i = 0; i < CPW; ++i) {
+      const int c = min(cb + i, max(c1, 1) - 1);
+      if (I8) {
+        w[i][0] = ldg_nt(reinterpret_cast<const u32x4*>(wrow + (size_t)c * cstride));
+      } else {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * c * 64 + 16 * g);
+        w[i][0] = ldg_nt(wp);
+        w[i][WV - 1] = ldg_nt(wp + 1);
       }
-      uint64_t o = shfl_xor_u64(b, 16);
-      b = o > b ? o : b;
-      o = shfl_xor_u64(b, 32);
-      b = o > b ? o : b;
-      if (g == 0 && t < p.M) p.best_part[(size_t)t * (p.N / 16) + strip] = b;
+    }
+  };
+  auto weights = [&](const u32x4 (&w)[WV], half8 (&a)[2]) {
+    if (I8) {
+      a[0] = i8x8_to_half8(w[0][0], w[0][1]);
+      a[1] = i8x8_to_half8(w[0][2], w[0][3]);
+    } else {
+      a[0] = as_half8(w[0]);
+      a[1] = as_half8(w[WV - 1]);
+    }
+  };
+  u32x4 w[CPW][WV];
+  if constexpr (XD) {
+    // lane (n, g): token min(n, M - 1) (rows past M feed only output columns that are never stored), 16 B at columns
+    // 64 c + 16 g and 64 c + 16 g + 8 of chunk c
+    const _Float16* xrow = p.x + (size_t)min(n, p.M - 1) * p.K + 16 * g;
+    for (int cb = c0; cb < c1; cb += CPW) {
+      u32x4 xb[CPW][2];
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        const int c = min(cb + i, c1 - 1);
+        xb[i][0] = ldg(reinterpret_cast<const u32x4*>(xrow + (size_t)c * 64));
+        xb[i][1] = ldg(reinterpret_cast<const u32x4*>(xrow + (size_t)c * 64 + 8));
+      }
+      load(w, cb);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        if (cb + i < c1) {
+          half8 a[2];
+          weights(w[i], a);
+          acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
+          acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
+        }
+      }
+    }
+  } else {
+    // X^T rows [tb][chunk][half] of 1 KB (lane l's 16 B at 16 l: token 16 tb + l % 16, columns 64 c + 16 (l / 16) +
+    // 8 h), loaded straight into LDS by the waves in turn; then this wave's first weight batch, so the counted wait
+    // covers X (the oldest loads) and leaves the weights in flight
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    for (int r = wave_u; r < TB * chunks * 2; r += nw) {
+      const int h = r & 1, j = (r >> 1) % chunks, tb = (r >> 1) / chunks;
+      const int t = 16 * tb + n;
+      if (t < p.M) {
+        const uint32_t off = (uint32_t)(((size_t)t * p.K + j * 64 + 16 * g + 8 * h) * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0,
+                                                 0, 0);
+      }
+    }
+    load(w, c0);
+    __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPW * WV));
+    __builtin_amdgcn_s_barrier();
+    for (int cb = c0; cb < c1; cb += CPW) {
+      if (cb != c0) load(w, cb);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        if (cb + i < c1) {
+          half8 a[2];
+          weights(w[i], a);
+#pragma unroll
+          for (int tb = 0; tb < TB; ++tb) {
+            const u32x4* xb = xs + ((size_t)(tb * chunks + cb + i) * 2) * 64;
+            acc[tb] = mfma16x16x32(a[0], as_half8(xb[lane]), acc[tb]);
+            acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + lane]), acc[tb]);
+          }
+        }
+      }
     }
   }
+  if (KW > 1) {
+    // ranges 1 .. KW - 1 of strip s go to LDS (over X, which every wave has finished reading); the range-0 wave adds
+    // them to its own sum in range order
+    f32x4* red = reinterpret_cast<f32x4*>(xs);
+    if (!XD) __syncthreads();
+    if (kq > 0) {
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) gemm_store(p, 16 * tb + n, row0, g, acc[tb]);
+      for (int tb = 0; tb < TB; ++tb) red[(((kq - 1) * S + s) * TB + tb) * 64 + lane] = acc[tb];
+    }
+    __syncthreads();
+    if (kq == 0) {
+      for (int k = 1; k < KW; ++k) {
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) acc[tb] += red[(((k - 1) * S + s) * TB + tb) * 64 + lane];
+      }
+    }
+  }
+  if (p.fuse) {
+    gemm_group_epilogue<TB>(p, acc, grp, s, S, kq == 0, lane, reinterpret_cast<float*>(xs));
+    return;
+  }
+  if (kq != 0 || !live) return;
+  gemm_strip_out<TB>(p, acc, strip, lane);
 }
 
 // Split-K reduce in index order + epilogue: one thread per 4 rows of one token, partial loads in flight in batches.
@@ -520,9 +677,47 @@ static void launch_gemm_tb(const GemmParams& p, dim3 grid, dim3 block, size_t ld
     hipLaunchKernelGGL((gemm_kernel<TB, I8, 4>), grid, block, lds, s, p);
 }
 
+// K-sliced launches where every wave loads its own range of X (int8, one strip per group, one token block).
+static bool gemm_sliced_xd(const GemmParams& p, bool i8) { return i8 && p.wpg == 1 && p.M <= 16; }
+
+// LDS of a K-sliced launch: X^T (unless each wave loads its own), the range sums, the fused epilogue's tile.
+static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
+  const int tb = (p.M + 15) / 16;
+  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)tb * (p.K / 64) * 2048;
+  const size_t red = (size_t)(p.kw - 1) * p.wpg * tb * 1024;
+  const size_t tile = p.fuse ? (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float) : 0;
+  return std::max(x, std::max(red, tile));
+}
+
+template <int TB, bool I8>
+static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
+  const int groups = (p.N / 16 + p.wpg - 1) / p.wpg;
+  const dim3 grid(groups), block(64 * p.wpg * p.kw);
+  const size_t lds = gemm_sliced_lds_bytes(p, I8);
+  const int cpk = (p.K / 64 + p.kw - 1) / p.kw;
+  if constexpr (I8) {
+    if (TB == 1 && gemm_sliced_xd(p, I8)) {
+      hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true>), grid, block, lds, s, p);
+      return;
+    }
+    if (cpk > 8) {  // 16-chunk batches of int8 weights: 64 VGPRs
+      hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 16, false>), grid, block, lds, s, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 8, false>), grid, block, lds, s, p);
+}
+
 template <bool I8>
 static void launch_gemm(const GemmParams& p, hipStream_t s) {
   const int tb = (p.M + 15) / 16;
+  if (p.kw > 0) {
+    if (tb == 1)
+      launch_sliced_tb<1, I8>(p, s);
+    else
+      launch_sliced_tb<2, I8>(p, s);
+    return;
+  }
   const int strips = p.N / 16;
   const int groups = (strips + p.wpg - 1) / p.wpg;
   const dim3 grid(groups * p.ksplit), block(64 * p.wpg);
@@ -541,9 +736,47 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // DSPARK_GEMM_TARGET_WGS while each split keeps DSPARK_GEMM_MIN_CHUNKS chunks, and 8-chunk weight batches when a phase
 // has 16 or more chunks in groups of at most four (4-chunk batches otherwise: more workgroups per CU). No split when
 // `split` is false (the fused head argmax needs whole rows).
+#ifndef DSPARK_GEMM_SLICED
+#define DSPARK_GEMM_SLICED 1  // 0: K-sliced plans off (split-K across workgroups instead)
+#endif
+
+// K-sliced plans (measured per shape on MI355X, 16 tokens, graph-replayed): a fused epilogue fixes S and takes
+// KW = 16 / S ranges; int8 GEMMs of one token block with at most 512 strips and K <= 4096 take S = 1 with four ranges,
+// each wave loading its own X; wider GEMMs stage X^T in LDS (at most 64 KB) with S = 16 x 1 range, 8 x 1 or 4 x 4, the
+// largest S that still gives 256 workgroups. Returns false when no sliced plan fits (the split-K plan is used).
+static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, GemmPlan* pl) {
+  const int strips = N / 16, chunks = K / 64;
+  if (!DSPARK_GEMM_SLICED || tb > 2) return false;
+  int S, KW;
+  if (wpg_req > 0) {
+    S = wpg_req;
+    KW = 16 / S;
+  } else if (i8 && tb == 1 && strips <= 512 && K <= 4096) {
+    S = 1;
+    KW = 4;
+  } else if (strips >= 16 * 256) {
+    S = 16;
+    KW = 1;
+  } else if (strips >= 8 * 256) {
+    S = 8;
+    KW = 1;
+  } else {
+    S = 4;
+    KW = 4;
+  }
+  const bool xd = i8 && S == 1 && tb == 1;
+  if (!xd && (size_t)tb * chunks * 2048 > 65536) return false;
+  pl->ksplit = 1;
+  pl->wpg = S;
+  pl->kw = std::max(1, std::min(KW, chunks));
+  pl->cpb = 8;
+  return true;
+}
+
 void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req) {
-  (void)i8;
   const int strips = N / 16, chunks = K / 64, tb = (M + 15) / 16;
+  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, pl)) return;
+  pl->kw = 0;
   const int wpg = wpg_req > 0 ? wpg_req : (strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips)));
   const int groups = (strips + wpg - 1) / wpg;
   int ks = 1;
@@ -580,6 +813,12 @@ float* gemm_ws_partials(void* ws) { return reinterpret_cast<float*>(static_cast<
 #endif
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
+  if (p.kw > 0) {
+    // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
+    const int tb = (p.M + 15) / 16;
+    if (p.ksplit != 1 || p.wpg < 1 || p.wpg * p.kw > 16 || tb > 2 || gemm_sliced_lds_bytes(p, i8) > 65536)
+      return DSPARK_EINVAL;
+  }
   if (!DSPARK_GEMM_FIXUP) p.counters = nullptr;
   if (p.fuse && p.ksplit > 1 && !p.counters) return DSPARK_EINVAL;  // a fused epilogue needs the in-kernel fixup
   if (i8)

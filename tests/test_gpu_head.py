@@ -111,9 +111,21 @@ def test_commit_stop_rules_on_device(dev, orc):
             assert getattr(gst, f) == getattr(ost, f), (kw, f)
 
 
-@pytest.mark.parametrize("M,N,K,epilogue", [(16, 8192, 2048, 0), (16, 2048, 8192, 0), (9, 1024, 2048, 1),
-                                            (16, 512, 1024, 2), (1, 64, 128, 0), (33, 256, 512, 0),
-                                            (64, 128, 256, 0)])
+@pytest.mark.parametrize("M,N,K,epilogue", [
+    (16, 12288, 2048, 0),   # K-sliced, 4 strips x 4 ranges, X^T in LDS
+    (16, 2048, 8192, 0),    # long K: split across workgroups
+    (9, 1024, 2048, 1),     # K-sliced, 1 strip x 4 ranges, each wave loads its own X, gated epilogue
+    (16, 512, 1024, 2),     # same, SiLU epilogue
+    (1, 64, 128, 0),        # two ranges of one chunk (fewer chunks than ranges)
+    (16, 1024, 192, 0),     # three chunks over four ranges: an empty range
+    (16, 2048, 4096, 0),    # own-X ranges of 16 chunks (two batches)
+    (24, 4096, 1024, 0),    # K-sliced, two token blocks
+    (16, 32768, 2048, 0),   # K-sliced, 8 strips x 1 range of 32 chunks in 16-chunk batches
+    (16, 16384, 1344, 0),   # ragged ranges: 21 chunks over 4 (X^T in LDS)
+    (16, 8192, 1344, 0),    # ragged own-X ranges
+    (33, 256, 2048, 0),     # three token blocks: K split across workgroups
+    (64, 128, 256, 0),
+])
 def test_gemm_i8_matches_oracle(dev, orc, M, N, K, epilogue):
     torch = dev
     host = load_host()
@@ -138,7 +150,7 @@ def test_gemm_i8_matches_oracle(dev, orc, M, N, K, epilogue):
         assert np.max(np.abs(got - ref)) <= 2e-3 * max(1.0, np.max(np.abs(ref)))
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 2048, 8192), (9, 6144, 2048), (33, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(33, 2048, 8192), (40, 6144, 2048), (33, 512, 1024)])
 def test_gemm_split_calls_share_one_workspace(dev, orc, M, N, K):
     """Split-K GEMMs in a row on one workspace (the last split of each row group sums the partials and resets its
     counter): every call matches the oracle on its own inputs and repeats are bit-identical."""
@@ -178,7 +190,7 @@ def test_gemm_split_shapes_share_one_workspace(dev, orc):
     torch = dev
     host = load_host()
     lib = host.lib()
-    shapes = [(16, 2048, 8192), (16, 2048, 2048), (9, 6144, 2048), (16, 3104, 2048), (9, 1024, 4096), (16, 2048, 10240)]
+    shapes = [(33, 2048, 8192), (33, 2048, 2048), (40, 6144, 2048), (48, 3104, 2048), (33, 1024, 4096), (64, 2048, 10240)]
     need = max(lib.dspark_gemm_i8_workspace(M, N, K) for M, N, K in shapes)
     ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
     wso = host.Workspace()
