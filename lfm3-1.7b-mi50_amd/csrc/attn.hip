@@ -655,7 +655,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     half4 hv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) hv[i] = (_Float16)acc[i];
-    *reinterpret_cast<half4*>(p.out16 + idx) = hv;
+    *reinterpret_cast<half4*>(p.out16 + (p.out_op ? xop_elem(t, qh * D + 4 * c4, p.out_op) : idx)) = hv;
   }
   if (p.out32) *reinterpret_cast<f32x4*>(p.out32 + idx) = acc;
 }

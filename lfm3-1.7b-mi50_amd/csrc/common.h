@@ -70,6 +70,15 @@ __device__ __forceinline__ int k_page_elem(int slot, int d, int D) {
 }
 __device__ __forceinline__ int v_page_elem(int slot, int d) { return d * PAGE + slot; }
 
+// Activations a verify GEMM reads as X ([M][K] fp16, M <= 16 tbs) in the B-operand order of v_mfma_f32_16x16x32_f16:
+// 1 KB blocks [K / 64 chunks][tbs token blocks][2 halves] of 64 lanes x 8 halves, lane 16 g + n holding token
+// 16 tb + n, columns 64 c + 16 g + 8 h .. + 7. A wave's X operand load is then one contiguous 1 KB (row-major X
+// gathers 64 bytes from each of 16 token rows). Four consecutive columns from a multiple of 4 stay contiguous.
+__device__ __forceinline__ size_t xop_elem(int t, int k, int tbs) {
+  return ((((size_t)(k >> 6) * tbs + (t >> 4)) * 2 + ((k >> 3) & 1)) * 64 + ((k >> 4) & 3) * 16 + (t & 15)) * 8 +
+         (k & 7);
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
   const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);

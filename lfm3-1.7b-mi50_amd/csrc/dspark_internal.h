@@ -24,9 +24,10 @@ struct AttnParams {
   uint32_t k_bytes, v_bytes;  // page pool sizes (range of the buffer loads; < 2 GiB)
   float* part_acc;   // [KVH][RG][S][R][D]
   f32x2_t* part_ml;  // [KVH][RG][S][R] (max, sum); max = -inf when the split saw no key of the row
-  _Float16* out16;
+  _Float16* out16;            // [M][QH][D], or operand order (xop_elem, column qh D + d) when out_op > 0
   float* out32;
   const float* gate;
+  int out_op;                 // > 0: out16 in the verify GEMM's X operand order with out_op token blocks
   int M, QH, KVH, G;
   int a, start, window, causal;
   int page0, npages, pps, S;  // logical page range and its split
@@ -53,10 +54,11 @@ struct ResNormParams {
   float eps;
   float* dst;                   // h_new [groups][M][H] or nullptr
   float* tap;                   // [M][H] or nullptr
-  _Float16* x16;                // [groups][M][x_row]
+  _Float16* x16;                // [groups][M][x_row], or operand order (xop_elem, column g x_group_stride + i) when xop
   size_t group_stride, x_group_stride;
   int x_row;
   int H;
+  int xop;                      // > 0: x16 in the verify GEMM's X operand order with xop token blocks
 };
 
 struct QkRopeParams {
@@ -129,6 +131,8 @@ struct GemmParams {
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
   int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
   int kw;                   // > 0: K-sliced plan, workgroups of wpg strips x kw ranges of K (ksplit 1, gemm_plan)
+  int xop;                  // > 0: x in operand order (xop_elem) with xop >= ceil(M / 16) token blocks; 0: row-major
+  int yop;                  // > 0: the fp16 output y16 in operand order with yop token blocks (for the next GEMM's X)
   int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
   // Fused row-group epilogue (the group's scaled products go through LDS; y32 is not written):
   //   GEMM_FUSE_QK: each group is one head of D rows of the attention mix q | k | v | gate: per-head RMS norm + RoPE,
@@ -146,14 +150,15 @@ constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
 struct GemmPlan {
   int ksplit = 1, wpg = 1, cpb = 4, kw = 0;
 };
-// wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV).
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0);
+// wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV);
+// xop: X comes in operand order (GemmParams::xop).
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0, bool xop = false);
 // Split-K workspace: GEMM_COUNTER_BYTES of arrival counters (one u32 per row group, at the same offset for every shape),
 // then the partials. Zero-filled once; every call leaves its counters at zero.
 constexpr int GEMM_COUNTER_SLOTS = 8192;
 constexpr size_t GEMM_COUNTER_BYTES = GEMM_COUNTER_SLOTS * sizeof(uint32_t);
 size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N);
-size_t gemm_ws_bytes(int M, int N, int K, int wpg_req = 0);  // for the split plan of an int8 GEMM
+size_t gemm_ws_bytes(int M, int N, int K, int wpg_req = 0, bool xop = false);  // for the plan of an int8 GEMM
 int gemm_groups(const GemmPlan& pl, int N);                  // row groups (<= GEMM_COUNTER_SLOTS for a split plan)
 uint32_t* gemm_ws_counters(void* ws);
 float* gemm_ws_partials(void* ws);

@@ -106,6 +106,7 @@ struct dspark_engine {
   void* ws_argmax = nullptr;
   size_t ws_argmax_bytes = 0;
   int x_cols = 0, mix_cols = 0, crop_n = 0;
+  int tbs = 1;  // 16-token blocks of the round: x16, y16 and a16 hold 16 tbs token rows in the GEMMs' X operand order
   int cus = 256;
   dspark_state host_st;  // launch-time uploads stay alive until the stream has consumed them
   float host_rep[2] = {1.f, 1.f};
@@ -200,6 +201,8 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
+  p.xop = e->tbs;  // every GEMM of the round reads x16, y16 or a16
+  p.yop = e->tbs;
   int wpg_req = 0;
   if (fuse) {
     p.fuse = fuse->fuse;
@@ -211,7 +214,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
     wpg_req = fuse->fuse == GEMM_FUSE_QK ? fuse->qk.D / 16 : 3;
   }
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl, wpg_req);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req, true);
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
@@ -247,6 +250,7 @@ int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, con
   p.x16 = e->x16;
   p.x_row = e->d.hidden;
   p.H = e->d.hidden;
+  p.xop = e->tbs;
   return resnorm_launch(p, e->B, 1, s);
 }
 
@@ -261,6 +265,7 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   p.bt = Lw.bt;
   p.k_bytes = p.v_bytes = (uint32_t)(Lw.kv_pages * d.kv_heads * PAGE * d.head_dim * 2);
   p.out16 = e->y16;
+  p.out_op = e->tbs;
   p.gate = gate;
   p.M = e->B;
   p.QH = d.q_heads;
@@ -361,6 +366,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       p.x_row = d.n_taps * H;
       p.x_group_stride = H;
       p.H = H;
+      p.xop = e->tbs;
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
     CK(gemm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s));
@@ -601,13 +607,14 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->mix_cols = std::max(std::max(3 * H, align16(QH * D + 2 * KVH * D + QH)), ckv_rows);
   e->h[0] = static_cast<float*>(e->alloc("h0", (size_t)B * H * 4, &err));
   e->h[1] = static_cast<float*>(e->alloc("h1", (size_t)B * H * 4, &err));
-  e->x16 = h16("x16", (size_t)B * e->x_cols);
+  e->tbs = (B + 15) / 16;
+  e->x16 = h16("x16", (size_t)16 * e->tbs * e->x_cols);
   e->mix = static_cast<float*>(e->alloc("mix", (size_t)B * e->mix_cols * 4, &err));
   e->q16 = h16("q16", (size_t)B * QH * D);
   e->gate = static_cast<float*>(e->alloc("gate", (size_t)B * QH * 4, &err));
-  e->y16 = h16("y16", (size_t)B * H);
+  e->y16 = h16("y16", (size_t)16 * e->tbs * H);
   e->vout = static_cast<float*>(e->alloc("vout", (size_t)B * H * 4, &err));
-  e->a16 = h16("a16", (size_t)B * std::max(d.ffn, d.draft_ffn));
+  e->a16 = h16("a16", (size_t)16 * e->tbs * std::max(d.ffn, d.draft_ffn));
   e->w2out = static_cast<float*>(e->alloc("w2out", (size_t)B * H * 4, &err));
   e->ctxv = static_cast<float*>(e->alloc("ctx", (size_t)B * H * 4, &err));
   e->ckvout = static_cast<float*>(e->alloc("ckv_out", (size_t)B * ckv_rows * 4, &err));
@@ -622,7 +629,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
                     align16(QH * D + 2 * KVH * D + QH), QH * D + 2 * KVH * D};
   for (int K : Ks)
     for (int N : Ns)
-      for (int wpg_req : {0, 3, D / 16}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req));
+      for (int wpg_req : {0, 3, D / 16}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req, true));
   e->ws_gemm_bytes = gws + 256;
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
   const int G = QH / KVH;

@@ -39,8 +39,8 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
     for (int i = 0; i < 4; ++i) v[i] *= (float)ldg(p.scale + r + i);
   }
   if (p.epilogue == 1) {
-    // rows (2i, 2i+1) = (gate, up): h[t][r/2 + i] = fp16(silu(gate) * up)
-    _Float16* y = p.y16 + (size_t)t * (p.N / 2) + r / 2;
+    // rows (2i, 2i+1) = (gate, up): h[t][r/2 + i] = fp16(silu(gate) * up); r/2 is even, so the pair is contiguous
+    _Float16* y = p.y16 + (p.yop ? xop_elem(t, r / 2, p.yop) : (size_t)t * (p.N / 2) + r / 2);
     y[0] = (_Float16)(silu_f(v[0]) * v[1]);
     y[1] = (_Float16)(silu_f(v[2]) * v[3]);
     return;
@@ -50,7 +50,7 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
     half4 h;
 #pragma unroll
     for (int i = 0; i < 4; ++i) h[i] = (_Float16)(p.epilogue == 2 ? silu_f(v[i]) : v[i]);
-    *reinterpret_cast<half4*>(p.y16 + (size_t)t * p.N + r) = h;
+    *reinterpret_cast<half4*>(p.y16 + (p.yop ? xop_elem(t, r, p.yop) : (size_t)t * p.N + r)) = h;
   }
 }
 
@@ -162,7 +162,7 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
     for (int k = 0; k < KMAX; ++k)
       if (k < K - 1) conv = fmaf(w[k], bx[k], conv);
     p.conv_ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = (_Float16)bx_t;
-    p.y16[(size_t)t * H + c] = (_Float16)(C * conv);
+    p.y16[p.yop ? xop_elem(t, c, p.yop) : (size_t)t * H + c] = (_Float16)(C * conv);
   }
 }
 
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   // X goes through registers for the deep-batch plans (phases of 16+ chunks: 32-64 KB of X per workgroup, where
   // full-line reads beat the direct loads' 16-line gathers; measured on MI355X) and by direct loads otherwise.
   constexpr int XRG = 16;  // X loads per wave on the register path (TB * 2 * phase chunks <= 64 = XRG * 4 waves)
-  const bool xreg = CPB == 8 && nw >= 4;
+  const bool xreg = CPB == 8 && nw >= 4 && !p.xop;
   const int xl0 = xreg ? lane ^ (4 * g) : lane, xl1 = xreg ? lane ^ (4 * g + 2) : lane;
   // chunk cb + i of the phase starting at chunk ph (pc chunks staged). With one token block the batch's X operands
   // are read from LDS before its first MFMA, so their latency is paid once per batch, not once per chunk.
@@ -338,8 +338,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   // X row r of a phase = [tb][chunk j][half h] (1 KB of LDS, lane l's 16 B at 16 l): token 16 tb + l % 16, columns
   // (ph + j) * 64 + 16 (l / 16) + 8 h .. + 8. Rows go straight from global memory to LDS with direct loads (each lane
   // gathers its 16 B), the waves taking rows in turn.
-  const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.x, (short)0, (int)((size_t)(p.xop ? 16 * p.xop : p.M) * p.K * 2), 0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   u32x4 wa[CPB][WV], wb[CPB][WV];
   for (int ph = c0; ph < c1; ph += PH) {
@@ -382,7 +382,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
       // lanes of token rows past M load nothing: their LDS slots feed only output columns that are never stored
       // (a column of the product depends only on its own token)
       if (t < p.M) {
-        const uint32_t off = (uint32_t)(((size_t)t * p.K + (ph + j) * 64 + 16 * g + 8 * h) * 2);
+        const uint32_t off = p.xop ? (uint32_t)(((((size_t)(ph + j) * p.xop + tb) * 2 + h) * 64 + lane) * 16)
+                                   : (uint32_t)(((size_t)t * p.K + (ph + j) * 64 + 16 * g + 8 * h) * 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0,
                                                  0, 0);
       }
@@ -518,16 +519,18 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
   };
   u32x4 w[CPW][WV];
   if constexpr (XD) {
-    // lane (n, g): token min(n, M - 1) (rows past M feed only output columns that are never stored), 16 B at columns
-    // 64 c + 16 g and 64 c + 16 g + 8 of chunk c
-    const _Float16* xrow = p.x + (size_t)min(n, p.M - 1) * p.K + 16 * g;
+    // lane (n, g): token n (min(n, M - 1) row-major: rows past M feed only output columns that are never stored),
+    // 16 B at columns 64 c + 16 g and 64 c + 16 g + 8 of chunk c; in operand order those are lane l's 16 B of the two
+    // 1 KB blocks of chunk c
+    const _Float16* xb0 = p.xop ? p.x + lane * 8 : p.x + (size_t)min(n, p.M - 1) * p.K + 16 * g;
+    const size_t xcs = p.xop ? (size_t)p.xop * 1024 : 64, xhs = p.xop ? 512 : 8;  // halves per chunk, per half
     for (int cb = c0; cb < c1; cb += CPW) {
       u32x4 xb[CPW][2];
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = min(cb + i, c1 - 1);
-        xb[i][0] = ldg(reinterpret_cast<const u32x4*>(xrow + (size_t)c * 64));
-        xb[i][1] = ldg(reinterpret_cast<const u32x4*>(xrow + (size_t)c * 64 + 8));
+        xb[i][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs));
+        xb[i][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + xhs));
       }
       load(w, cb);
 #pragma unroll
@@ -544,14 +547,15 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
     // X^T rows [tb][chunk][half] of 1 KB (lane l's 16 B at 16 l: token 16 tb + l % 16, columns 64 c + 16 (l / 16) +
     // 8 h), loaded straight into LDS by the waves in turn; then this wave's first weight batch, so the counted wait
     // covers X (the oldest loads) and leaves the weights in flight
-    const __amdgpu_buffer_rsrc_t rx =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.M * p.K * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.x, (short)0, (int)((size_t)(p.xop ? 16 * p.xop : p.M) * p.K * 2), 0x00020000);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     for (int r = wave_u; r < TB * chunks * 2; r += nw) {
       const int h = r & 1, j = (r >> 1) % chunks, tb = (r >> 1) / chunks;
       const int t = 16 * tb + n;
       if (t < p.M) {
-        const uint32_t off = (uint32_t)(((size_t)t * p.K + j * 64 + 16 * g + 8 * h) * 2);
+        const uint32_t off = p.xop ? (uint32_t)(((((size_t)j * p.xop + tb) * 2 + h) * 64 + lane) * 16)
+                                   : (uint32_t)(((size_t)t * p.K + j * 64 + 16 * g + 8 * h) * 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0,
                                                  0, 0);
       }
@@ -741,28 +745,25 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 #endif
 
 // K-sliced plans (measured per shape on MI355X, 16 tokens, graph-replayed): a fused epilogue fixes S and takes
-// KW = 16 / S ranges; int8 GEMMs of one token block with at most 512 strips and K <= 4096 take S = 1 with four ranges,
-// each wave loading its own X; wider GEMMs stage X^T in LDS (at most 64 KB) with S = 16 x 1 range, 8 x 1 or 4 x 4, the
-// largest S that still gives 256 workgroups. Returns false when no sliced plan fits (the split-K plan is used).
-static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, GemmPlan* pl) {
+// KW = 16 / S ranges; int8 GEMMs of one token block with at most 512 strips take S = 1, each wave loading its own X:
+// with X in operand order 4 to 8 ranges of at least 8 chunks (2048 x 2048: 4.7 us; 2048 x 8192: 9.0 us against 10.9
+// split 8 ways), with row-major X (64-byte pieces of 16 token rows per load) four ranges and only up to K = 4096;
+// wider GEMMs stage X^T in LDS (at most 64 KB) with S = max(4, strips / 256) strips per group (at most 256 groups:
+// 257 groups on 256 CUs measured 14.2 us against 10.2 for 256) and 16 / S ranges. Returns false when no sliced plan
+// fits (the split-K plan is used).
+static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, GemmPlan* pl) {
   const int strips = N / 16, chunks = K / 64;
   if (!DSPARK_GEMM_SLICED || tb > 2) return false;
   int S, KW;
   if (wpg_req > 0) {
     S = wpg_req;
     KW = 16 / S;
-  } else if (i8 && tb == 1 && strips <= 512 && K <= 4096) {
+  } else if (i8 && tb == 1 && strips <= 512 && (xop || K <= 4096)) {
     S = 1;
-    KW = 4;
-  } else if (strips >= 16 * 256) {
-    S = 16;
-    KW = 1;
-  } else if (strips >= 8 * 256) {
-    S = 8;
-    KW = 1;
+    KW = xop ? std::min(8, std::max(4, chunks / 8)) : 4;
   } else {
-    S = 4;
-    KW = 4;
+    S = std::min(16, std::max(4, (strips + 255) / 256));
+    KW = std::max(1, 16 / S);
   }
   const bool xd = i8 && S == 1 && tb == 1;
   if (!xd && (size_t)tb * chunks * 2048 > 65536) return false;
@@ -773,9 +774,9 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, GemmPla
   return true;
 }
 
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req) {
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req, bool xop) {
   const int strips = N / 16, chunks = K / 64, tb = (M + 15) / 16;
-  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, pl)) return;
+  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, xop, pl)) return;
   pl->kw = 0;
   const int wpg = wpg_req > 0 ? wpg_req : (strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips)));
   const int groups = (strips + wpg - 1) / wpg;
@@ -796,9 +797,9 @@ size_t gemm_ws_bytes(const GemmPlan& pl, int M, int N) {
   return GEMM_COUNTER_BYTES + (((size_t)pl.ksplit * M * N * sizeof(float) + 255) / 256) * 256;
 }
 
-size_t gemm_ws_bytes(int M, int N, int K, int wpg_req) {
+size_t gemm_ws_bytes(int M, int N, int K, int wpg_req, bool xop) {
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl, wpg_req);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req, xop);
   return gemm_ws_bytes(pl, M, N);
 }
 
@@ -813,6 +814,7 @@ float* gemm_ws_partials(void* ws) { return reinterpret_cast<float*>(static_cast<
 #endif
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
+  if ((p.xop && p.xop < (p.M + 15) / 16) || (p.yop && p.yop < (p.M + 15) / 16)) return DSPARK_EINVAL;
   if (p.kw > 0) {
     // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
     const int tb = (p.M + 15) / 16;

@@ -113,7 +113,9 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
       half4 x;
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[j] = (_Float16)(hv[k][j] * inv * (float)wn[k][j]);
-      *reinterpret_cast<half4*>(p.x16 + (size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i) = x;
+      const size_t xo = p.xop ? xop_elem(t, gi * (int)p.x_group_stride + i, p.xop)
+                              : (size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i;
+      *reinterpret_cast<half4*>(p.x16 + xo) = x;
     }
   }
 }

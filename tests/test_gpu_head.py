@@ -120,7 +120,9 @@ def test_commit_stop_rules_on_device(dev, orc):
     (16, 1024, 192, 0),     # three chunks over four ranges: an empty range
     (16, 2048, 4096, 0),    # own-X ranges of 16 chunks (two batches)
     (24, 4096, 1024, 0),    # K-sliced, two token blocks
-    (16, 32768, 2048, 0),   # K-sliced, 8 strips x 1 range of 32 chunks in 16-chunk batches
+    (16, 32768, 2048, 0),   # K-sliced, 8 strips x 2 ranges of 16 chunks
+    (16, 16400, 2048, 0),   # 1025 strips: 5 strips x 3 ranges (205 groups), the last group part-empty
+    (16, 65536, 1024, 0),   # 16 strips x 1 range of 16 chunks
     (16, 16384, 1344, 0),   # ragged ranges: 21 chunks over 4 (X^T in LDS)
     (16, 8192, 1344, 0),    # ragged own-X ranges
     (33, 256, 2048, 0),     # three token blocks: K split across workgroups
