@@ -79,6 +79,13 @@ struct QkRopeParams {
   int pos_from_ctx, count_from_ctx;  // positions st->ctx_pos + t, tokens t < st->ctx_new (context projection)
 };
 
+constexpr int QKROPE_BATCH = 8;
+struct QkRopeBatch {
+  QkRopeParams l[QKROPE_BATCH];  // same M, QH, KVH
+  int n;
+};
+int qkrope_batch_launch(const QkRopeBatch& b, hipStream_t s);
+
 struct MarkovParams {
   struct ::dspark_state* st;
   const float* base;            // [block][stride] crop-head outputs; column N is the confidence term
@@ -115,6 +122,17 @@ void attn_bind_workspace(AttnParams& p, int D, void* ws);
 int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);
 int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt, int KVH,
                     int D, int pos0, int n, hipStream_t s);
+
+// The State's run flag read with a vector load (issued in order with the kernel's data loads, so a kernel can put it
+// first and test it after its loads are in flight, instead of a scalar load the compiler waits for at the next use of
+// any kernel argument). 1 when there is no State. Test with run_flag_set().
+__device__ __forceinline__ int run_flag_load(const dspark_state* st) {
+  if (!st) return 1;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void*)st, (short)0, (int)sizeof(dspark_state), 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)offsetof(dspark_state, run), 0, 0);
+}
+__device__ __forceinline__ bool run_flag_set(int v) { return __builtin_amdgcn_readfirstlane(v) != 0; }
 
 struct GemmParams {
   const struct ::dspark_state* st;  // when set, a stopped round (run == 0) skips the launch's work

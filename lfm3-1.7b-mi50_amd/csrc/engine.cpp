@@ -314,10 +314,6 @@ QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int
   return p;
 }
 
-int qkrope(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode, hipStream_t s) {
-  return qkrope_launch(qk_params(e, Lw, mix, row, with_q, ctx_mode), s);
-}
-
 // The attention mix GEMM with q/k norm + RoPE + K/V page write fused into its epilogue (one head per group).
 int gemm_mix_qk(dspark_engine* e, const LayerW& W, hipStream_t s) {
   GemmParams f = {};
@@ -373,8 +369,13 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     CK(resnorm(e, nullptr, e->ctxv, 1, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
     const int kvrow = 2 * d.kv_heads * d.head_dim;
     CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
-    for (int j = 0; j < d.draft_layers; ++j)
-      CK(qkrope(e, e->DL[j], e->ckvout + (size_t)j * kvrow, d.draft_layers * kvrow, false, true, s));
+    for (int j0 = 0; j0 < d.draft_layers; j0 += QKROPE_BATCH) {  // one launch for up to 8 drafter layers
+      QkRopeBatch b = {};
+      b.n = std::min(QKROPE_BATCH, d.draft_layers - j0);
+      for (int j = 0; j < b.n; ++j)
+        b.l[j] = qk_params(e, e->DL[j0 + j], e->ckvout + (size_t)(j0 + j) * kvrow, d.draft_layers * kvrow, false, true);
+      CK(qkrope_batch_launch(b, s));
+    }
     // ---- drafter block
     CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
     int cur = 0;

@@ -468,7 +468,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 // summation order, so results do not depend on timing.
 template <int TB, bool I8, int CPW, bool XD>
 __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
-  if (gemm_stopped(p)) return;
+  // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
+  // anything is stored), so its latency overlaps theirs; a stopped round writes nothing.
+  const int run = run_flag_load(p.st);
   extern __shared__ u32x4 xs[];
   constexpr int WV = I8 ? 1 : 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -579,6 +581,10 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
         }
       }
     }
+  }
+  if (!run_flag_set(run)) {  // the same for every wave
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
   if (KW > 1) {
     // ranges 1 .. KW - 1 of strip s go to LDS (over X, which every wave has finished reading); the range-0 wave adds

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const
 // h_new = h_old + a * v * post_w; x = fp16(h_new * rsqrt(mean(h_new^2) + eps) * norm_w).
 // One block per (row, group): blockIdx.y selects a group with its own inputs (the drafter's tap norms).
 __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
-  if (stopped(p.st)) return;
+  const int run = run_flag_load(p.st);  // tested after the first loads are in flight
   const int t = blockIdx.x, gi = blockIdx.y;
   const int H = p.H;
   const float* hold = p.h_old ? p.h_old + (size_t)gi * p.group_stride + (size_t)t * H : nullptr;
@@ -50,6 +50,11 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
       wn[k] = ldg(reinterpret_cast<const half4*>(nw + i));
       if (p.post_w) wp[k] = ldg(reinterpret_cast<const half4*>(p.post_w + i));
     }
+  }
+  // a stopped round waits for the loads in flight and writes nothing
+  if (!run_flag_set(run)) {
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
   // Bands eight at a time: a batch's loads are all in flight before the first add; the adds stay in band order.
   constexpr int BB = 8;
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
 // per token: q [QH*D] | k [KVH*D] | v [KVH*D] | gate [QH] (gate optional), `row` floats apart. Position of token t:
 // base + t with base = st->a (verify, drafter block) or st->ctx_pos (context projection); tokens t >= count
 // (count = M, or st->ctx_new) are skipped.
-__global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) {
+__device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   if (stopped(p.st)) return;
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -191,6 +196,11 @@ __global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) {
     vb[v_page_elem(slot, d)] = (_Float16)vsrc[d];
   }
 }
+
+__global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) { qkrope_body(p); }
+
+// Several layers of the same shape in one launch (the context projection's drafter layers): layer blockIdx.y.
+__global__ __launch_bounds__(256) void qkrope_batch_kernel(QkRopeBatch b) { qkrope_body(b.l[blockIdx.y]); }
 
 // ---------------------------------------------------------------- drafter: Markov + confidence (markov_phase)
 // Step j (0-based) proposes draft j+1 from prev = (j == 0 ? anchor : the token of step j-1's argmax key):
@@ -477,6 +487,16 @@ int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) 
 int qkrope_launch(const QkRopeParams& p, hipStream_t s) {
   const int tasks = p.M * (p.QH + p.KVH);
   hipLaunchKernelGGL(qkrope_kernel, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
+  return (int)hipGetLastError();
+}
+
+int qkrope_batch_launch(const QkRopeBatch& b, hipStream_t s) {
+  if (b.n < 1 || b.n > QKROPE_BATCH) return DSPARK_EINVAL;
+  const QkRopeParams& p = b.l[0];
+  for (int j = 1; j < b.n; ++j)
+    if (b.l[j].M != p.M || b.l[j].QH != p.QH || b.l[j].KVH != p.KVH) return DSPARK_EINVAL;
+  const int tasks = p.M * (p.QH + p.KVH);
+  hipLaunchKernelGGL(qkrope_batch_kernel, dim3((tasks + 3) / 4, b.n), dim3(256), 0, s, b);
   return (int)hipGetLastError();
 }
 int markov_launch(const MarkovParams& p, hipStream_t s) {
