@@ -158,6 +158,7 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
   p.kw = pl.kw;
+  p.xd = pl.xd;
   if (p.ksplit > 1) {
     if (gemm_groups(pl, N) > GEMM_COUNTER_SLOTS) return DSPARK_EINVAL;
     if (!workspace || workspace_bytes < gemm_ws_bytes(pl, M, N)) return DSPARK_ENOSPACE;
@@ -190,6 +191,7 @@ int dspark_head_argmax_f16(const void* x, int32_t M, int32_t K, const void* w, i
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
   p.kw = pl.kw;
+  p.xd = pl.xd;
   p.best_part = static_cast<uint64_t*>(workspace);
   p.best = best_keys;
   return gemm_launch(p, false, S(stream));

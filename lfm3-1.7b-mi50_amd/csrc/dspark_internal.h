@@ -149,6 +149,7 @@ struct GemmParams {
   int wpg;                  // waves (16-row strips) per workgroup (gemm_plan)
   int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
   int kw;                   // > 0: K-sliced plan, workgroups of wpg strips x kw ranges of K (ksplit 1, gemm_plan)
+  int xd;                   // K-sliced, int8, one token block: each wave loads its own range of X (no LDS staging)
   int xop;                  // > 0: x in operand order (xop_elem) with xop >= ceil(M / 16) token blocks; 0: row-major
   int yop;                  // > 0: the fp16 output y16 in operand order with yop token blocks (for the next GEMM's X)
   int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
@@ -166,7 +167,7 @@ struct GemmParams {
 constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
 
 struct GemmPlan {
-  int ksplit = 1, wpg = 1, cpb = 4, kw = 0;
+  int ksplit = 1, wpg = 1, cpb = 4, kw = 0, xd = 0;
 };
 // wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV);
 // xop: X comes in operand order (GemmParams::xop).

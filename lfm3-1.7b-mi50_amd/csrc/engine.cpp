@@ -219,6 +219,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
   p.kw = pl.kw;
+  p.xd = pl.xd;
   auto it = e->tile_of.find(w);
   if (it != e->tile_of.end()) {
     p.w = e->tiles[it->second].dst;

@@ -687,8 +687,8 @@ static void launch_gemm_tb(const GemmParams& p, dim3 grid, dim3 block, size_t ld
     hipLaunchKernelGGL((gemm_kernel<TB, I8, 4>), grid, block, lds, s, p);
 }
 
-// K-sliced launches where every wave loads its own range of X (int8, one strip per group, one token block).
-static bool gemm_sliced_xd(const GemmParams& p, bool i8) { return i8 && p.wpg == 1 && p.M <= 16; }
+// K-sliced launches where every wave loads its own range of X (the plan's choice; int8, one token block).
+static bool gemm_sliced_xd(const GemmParams& p, bool i8) { return i8 && p.xd && p.M <= 16; }
 
 // LDS of a K-sliced launch: X^T (unless each wave loads its own), the range sums, the fused epilogue's tile.
 static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
@@ -746,6 +746,9 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // DSPARK_GEMM_TARGET_WGS while each split keeps DSPARK_GEMM_MIN_CHUNKS chunks, and 8-chunk weight batches when a phase
 // has 16 or more chunks in groups of at most four (4-chunk batches otherwise: more workgroups per CU). No split when
 // `split` is false (the fused head argmax needs whole rows).
+#ifndef DSPARK_GEMM_XD_MAX_S
+#define DSPARK_GEMM_XD_MAX_S 4  // groups of up to this many strips load X per wave (operand-order X) instead of via LDS
+#endif
 #ifndef DSPARK_GEMM_SLICED
 #define DSPARK_GEMM_SLICED 1  // 0: K-sliced plans off (split-K across workgroups instead)
 #endif
@@ -754,9 +757,10 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // KW = 16 / S ranges; int8 GEMMs of one token block with at most 512 strips take S = 1, each wave loading its own X:
 // with X in operand order 4 to 8 ranges of at least 8 chunks (2048 x 2048: 4.7 us; 2048 x 8192: 9.0 us against 10.9
 // split 8 ways), with row-major X (64-byte pieces of 16 token rows per load) four ranges and only up to K = 4096;
-// wider GEMMs stage X^T in LDS (at most 64 KB) with S = max(4, strips / 256) strips per group (at most 256 groups:
-// 257 groups on 256 CUs measured 14.2 us against 10.2 for 256) and 16 / S ranges. Returns false when no sliced plan
-// fits (the split-K plan is used).
+// wider GEMMs take S = max(4, strips / 256) strips per group (at most 256 groups: 257 groups on 256 CUs measured
+// 14.2 us against 10.2 for 256) and 16 / S ranges, X loaded per wave for S <= 4 with operand-order X (16384 x 2048:
+// 9.6 against 10.3 us through LDS; equal at 3104 and 6144 rows, slower for S = 5 and 16), else staged in LDS once (at
+// most 64 KB). Returns false when no sliced plan fits (the split-K plan is used).
 static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, GemmPlan* pl) {
   const int strips = N / 16, chunks = K / 64;
   if (!DSPARK_GEMM_SLICED || tb > 2) return false;
@@ -771,9 +775,10 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
   }
-  const bool xd = i8 && S == 1 && tb == 1;
+  const bool xd = i8 && tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S));
   if (!xd && (size_t)tb * chunks * 2048 > 65536) return false;
   pl->ksplit = 1;
+  pl->xd = xd;
   pl->wpg = S;
   pl->kw = std::max(1, std::min(KW, chunks));
   pl->cpb = 8;
