@@ -150,6 +150,8 @@ struct GemmParams {
   int cpb;                  // 64-column chunks per weight-load batch: 4 or 8 (gemm_plan)
   int kw;                   // > 0: K-sliced plan, workgroups of wpg strips x kw ranges of K (ksplit 1, gemm_plan)
   int xd;                   // K-sliced, int8, one token block: each wave loads its own range of X (no LDS staging)
+  int bands;                // K-sliced, > 1: K in `bands` shares over as many workgroups, band b's scaled sums to
+                            // y32 + b M N (epilogue 0, y32 only): the caller adds the bands (the norm kernel does)
   int xop;                  // > 0: x in operand order (xop_elem) with xop >= ceil(M / 16) token blocks; 0: row-major
   int yop;                  // > 0: the fp16 output y16 in operand order with yop token blocks (for the next GEMM's X)
   int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
@@ -167,11 +169,13 @@ struct GemmParams {
 constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
 
 struct GemmPlan {
-  int ksplit = 1, wpg = 1, cpb = 4, kw = 0, xd = 0;
+  int ksplit = 1, wpg = 1, cpb = 4, kw = 0, xd = 0, bands = 1;
 };
 // wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV);
-// xop: X comes in operand order (GemmParams::xop).
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0, bool xop = false);
+// xop: X comes in operand order (GemmParams::xop); max_bands > 1: the caller adds up to that many output bands
+// (GemmParams::bands).
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0, bool xop = false,
+               int max_bands = 1);
 // Split-K workspace: GEMM_COUNTER_BYTES of arrival counters (one u32 per row group, at the same offset for every shape),
 // then the partials. Zero-filled once; every call leaves its counters at zero.
 constexpr int GEMM_COUNTER_SLOTS = 8192;

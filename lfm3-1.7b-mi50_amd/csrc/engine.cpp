@@ -188,8 +188,10 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
 }
 
 // `fuse` (optional) selects a fused row-group epilogue (GEMM_FUSE_QK / GEMM_FUSE_CONV) and carries its parameters.
+// `bands` (optional): in, the most output bands the caller adds (y32 holds that many [M][N] blocks); out, the bands
+// the plan wrote.
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
-         float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr) {
+         float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr, int* bands = nullptr) {
   GemmParams p = {};
   p.st = e->st;
   p.x = x;
@@ -214,7 +216,9 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
     wpg_req = fuse->fuse == GEMM_FUSE_QK ? fuse->qk.D / 16 : 3;
   }
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl, wpg_req, true);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req, true, bands ? *bands : 1);
+  if (bands) *bands = pl.bands;
+  p.bands = pl.bands;
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
   p.cpb = pl.cpb;
@@ -334,6 +338,9 @@ int gemm_mix_conv(dspark_engine* e, const LayerW& W, hipStream_t s) {
   return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
 }
 
+// Output bands the round's norm kernels add (the w2, out and fc GEMMs may split K over that many workgroups).
+constexpr int ENGINE_BANDS = 2;
+
 #define CK(x)                \
   do {                       \
     int _rc = (x);           \
@@ -366,8 +373,9 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       p.xop = e->tbs;
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
-    CK(gemm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s));
-    CK(resnorm(e, nullptr, e->ctxv, 1, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
+    int nb = ENGINE_BANDS;
+    CK(gemm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s, nullptr, &nb));
+    CK(resnorm(e, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
     const int kvrow = 2 * d.kv_heads * d.head_dim;
     CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
     for (int j0 = 0; j0 < d.draft_layers; j0 += QKROPE_BATCH) {  // one launch for up to 8 drafter layers
@@ -379,20 +387,22 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     }
     // ---- drafter block
     CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
-    int cur = 0;
+    int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
     for (int j = 0; j < d.draft_layers; ++j) {
       const LayerW& W = e->DL[j];
-      CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, j ? 1 : 0, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
+      CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm_mix_qk(e, W, s));
       CK(attention(e, W, 1, plan_a, nullptr, s));
-      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
-      CK(resnorm(e, e->h[cur], e->vout, 1, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
+      int ob = ENGINE_BANDS;
+      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
+      CK(resnorm(e, e->h[cur], e->vout, ob, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
-      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
+      w2b = ENGINE_BANDS;
+      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
     }
-    CK(resnorm(e, e->h[cur], e->w2out, 1, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
+    CK(resnorm(e, e->h[cur], e->w2out, w2b, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
     CK(gemm(e, e->x16, B, H, e->crop_w, e->crop_s, e->crop_n, 0, e->base, nullptr, s));
     MarkovParams mp = {};
     mp.st = e->st;
@@ -419,12 +429,12 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   }
   // ---- verify
   CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
-  int cur = 0;
+  int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
   for (int i = 0; i < d.n_layers; ++i) {
     const LayerW& W = e->L[i];
     const LayerW* P = i ? &e->L[i - 1] : nullptr;
     float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
-    CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, i ? 1 : 0, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
+    CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, w2b, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
                e->h[cur ^ 1], tap, s));
     cur ^= 1;
     if (W.kind == 0) {
@@ -433,16 +443,18 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       CK(gemm_mix_qk(e, W, s));
       CK(attention(e, W, 0, plan_a, e->gate, s));
     }
-    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s));
-    CK(resnorm(e, e->h[cur], e->vout, 1, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
+    int ob = ENGINE_BANDS;
+    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
+    CK(resnorm(e, e->h[cur], e->vout, ob, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
     cur ^= 1;
     CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
-    CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s));
+    w2b = ENGINE_BANDS;
+    CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
   }
   {
     const LayerW& P = e->L[d.n_layers - 1];
     float* tap = P.tap_slot >= 0 ? e->taps + (size_t)P.tap_slot * B * H : nullptr;
-    CK(resnorm(e, e->h[cur], e->w2out, 1, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
+    CK(resnorm(e, e->h[cur], e->w2out, w2b, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
   }
   CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
   CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep));
@@ -615,10 +627,10 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->q16 = h16("q16", (size_t)B * QH * D);
   e->gate = static_cast<float*>(e->alloc("gate", (size_t)B * QH * 4, &err));
   e->y16 = h16("y16", (size_t)16 * e->tbs * H);
-  e->vout = static_cast<float*>(e->alloc("vout", (size_t)B * H * 4, &err));
+  e->vout = static_cast<float*>(e->alloc("vout", (size_t)ENGINE_BANDS * B * H * 4, &err));
   e->a16 = h16("a16", (size_t)16 * e->tbs * std::max(d.ffn, d.draft_ffn));
-  e->w2out = static_cast<float*>(e->alloc("w2out", (size_t)B * H * 4, &err));
-  e->ctxv = static_cast<float*>(e->alloc("ctx", (size_t)B * H * 4, &err));
+  e->w2out = static_cast<float*>(e->alloc("w2out", (size_t)ENGINE_BANDS * B * H * 4, &err));
+  e->ctxv = static_cast<float*>(e->alloc("ctx", (size_t)ENGINE_BANDS * B * H * 4, &err));
   e->ckvout = static_cast<float*>(e->alloc("ckv_out", (size_t)B * ckv_rows * 4, &err));
   e->taps = static_cast<float*>(e->alloc("taps", (size_t)d.n_taps * B * H * 4, &err));
   e->logits = static_cast<float*>(e->alloc("logits", (size_t)B * d.vocab * 4, &err));

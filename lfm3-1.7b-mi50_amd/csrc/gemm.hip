@@ -477,15 +477,18 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
   const int n = lane & 15, g = lane >> 4;
   const int S = p.wpg, KW = p.kw;
   const int s = wave % S, kq = wave / S;
-  const int grp = blockIdx.x;
+  const int groups = (p.N / 16 + S - 1) / S;
+  const int grp = blockIdx.x % groups, band = blockIdx.x / groups;  // band: a share of K (bands > 1)
   const int strips = p.N / 16;
   const int strip_raw = grp * S + s;
   const bool live = strip_raw < strips;
   const int strip = live ? strip_raw : strips - 1;
   const int row0 = strip * 16;
   const int chunks = p.K / 64;
-  const int cpk = (chunks + KW - 1) / KW;
-  const int c0 = min(chunks, kq * cpk), c1 = min(chunks, c0 + cpk);
+  const int cpb_ = (chunks + p.bands - 1) / p.bands;  // chunks per band
+  const int b0 = min(chunks, band * cpb_), b1 = min(chunks, b0 + cpb_);
+  const int cpk = (b1 - b0 + KW - 1) / KW;
+  const int c0 = min(b1, b0 + kq * cpk), c1 = min(b1, c0 + cpk);
 
   f32x4 acc[TB];
 #pragma unroll
@@ -552,8 +555,9 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         (void*)p.x, (short)0, (int)((size_t)(p.xop ? 16 * p.xop : p.M) * p.K * 2), 0x00020000);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    for (int r = wave_u; r < TB * chunks * 2; r += nw) {
-      const int h = r & 1, j = (r >> 1) % chunks, tb = (r >> 1) / chunks;
+    const int bc = b1 - b0;  // the band's chunks: X^T rows [tb][chunk - b0][half]
+    for (int r = wave_u; r < TB * bc * 2; r += nw) {
+      const int h = r & 1, j = b0 + (r >> 1) % bc, tb = (r >> 1) / bc;
       const int t = 16 * tb + n;
       if (t < p.M) {
         const uint32_t off = p.xop ? (uint32_t)(((((size_t)j * p.xop + tb) * 2 + h) * 64 + lane) * 16)
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
           weights(w[i], a);
 #pragma unroll
           for (int tb = 0; tb < TB; ++tb) {
-            const u32x4* xb = xs + ((size_t)(tb * chunks + cb + i) * 2) * 64;
+            const u32x4* xb = xs + ((size_t)(tb * (b1 - b0) + cb + i - b0) * 2) * 64;
             acc[tb] = mfma16x16x32(a[0], as_half8(xb[lane]), acc[tb]);
             acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + lane]), acc[tb]);
           }
@@ -608,6 +612,12 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
     return;
   }
   if (kq != 0 || !live) return;
+  if (p.bands > 1) {  // band b's scaled sums go to y32 + b M N (the consumer adds the bands in order)
+    GemmParams q = p;
+    q.y32 = p.y32 + (size_t)band * p.M * p.N;
+    gemm_strip_out<TB>(q, acc, strip, lane);
+    return;
+  }
   gemm_strip_out<TB>(p, acc, strip, lane);
 }
 
@@ -693,7 +703,8 @@ static bool gemm_sliced_xd(const GemmParams& p, bool i8) { return i8 && p.xd && 
 // LDS of a K-sliced launch: X^T (unless each wave loads its own), the range sums, the fused epilogue's tile.
 static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
   const int tb = (p.M + 15) / 16;
-  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)tb * (p.K / 64) * 2048;
+  const int bands = std::max(1, p.bands);
+  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)tb * ((p.K / 64 + bands - 1) / bands) * 2048;
   const size_t red = (size_t)(p.kw - 1) * p.wpg * tb * 1024;
   const size_t tile = p.fuse ? (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float) : 0;
   return std::max(x, std::max(red, tile));
@@ -702,7 +713,7 @@ static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
 template <int TB, bool I8>
 static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const int groups = (p.N / 16 + p.wpg - 1) / p.wpg;
-  const dim3 grid(groups), block(64 * p.wpg * p.kw);
+  const dim3 grid(groups * p.bands), block(64 * p.wpg * p.kw);
   const size_t lds = gemm_sliced_lds_bytes(p, I8);
   const int cpk = (p.K / 64 + p.kw - 1) / p.kw;
   if constexpr (I8) {
@@ -761,16 +772,19 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // 14.2 us against 10.2 for 256) and 16 / S ranges, X loaded per wave for S <= 4 with operand-order X (16384 x 2048:
 // 9.6 against 10.3 us through LDS; equal at 3104 and 6144 rows, slower for S = 5 and 16), else staged in LDS once (at
 // most 64 KB). Returns false when no sliced plan fits (the split-K plan is used).
-static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, GemmPlan* pl) {
+static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, int max_bands, GemmPlan* pl) {
   const int strips = N / 16, chunks = K / 64;
   if (!DSPARK_GEMM_SLICED || tb > 2) return false;
-  int S, KW;
+  int S, KW, bands = 1;
   if (wpg_req > 0) {
     S = wpg_req;
     KW = 16 / S;
   } else if (i8 && tb == 1 && strips <= 512 && (xop || K <= 4096)) {
     S = 1;
-    KW = xop ? std::min(8, std::max(4, chunks / 8)) : 4;
+    // fewer than 256 strips: K in bands over more workgroups when the caller adds the bands (at least 8 chunks each)
+    while (bands * 2 <= max_bands && strips * bands * 2 <= 256 && chunks / (bands * 2) >= 8) bands *= 2;
+    const int bc = chunks / bands;
+    KW = xop ? std::min(8, std::max(4, bc / 8)) : 4;
   } else {
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
@@ -778,6 +792,7 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
   const bool xd = i8 && tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S));
   if (!xd && (size_t)tb * chunks * 2048 > 65536) return false;
   pl->ksplit = 1;
+  pl->bands = bands;
   pl->xd = xd;
   pl->wpg = S;
   pl->kw = std::max(1, std::min(KW, chunks));
@@ -785,10 +800,11 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
   return true;
 }
 
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req, bool xop) {
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req, bool xop, int max_bands) {
   const int strips = N / 16, chunks = K / 64, tb = (M + 15) / 16;
-  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, xop, pl)) return;
+  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, xop, max_bands, pl)) return;
   pl->kw = 0;
+  pl->bands = 1;
   const int wpg = wpg_req > 0 ? wpg_req : (strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips)));
   const int groups = (strips + wpg - 1) / wpg;
   int ks = 1;
@@ -829,7 +845,11 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
   if (p.kw > 0) {
     // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
     const int tb = (p.M + 15) / 16;
+    if (p.bands < 1) p.bands = 1;
     if (p.ksplit != 1 || p.wpg < 1 || p.wpg * p.kw > 16 || tb > 2 || gemm_sliced_lds_bytes(p, i8) > 65536)
+      return DSPARK_EINVAL;
+    // bands: plain scaled sums into y32 only (each band its own [M][N]), nothing fused
+    if (p.bands > 1 && (p.epilogue != 0 || !p.y32 || p.y16 || p.best_part || p.fuse || p.bands > p.K / 64))
       return DSPARK_EINVAL;
   }
   if (!DSPARK_GEMM_FIXUP) p.counters = nullptr;
