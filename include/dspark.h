@@ -124,8 +124,10 @@ int dspark_accept_commit(dspark_state* st, const uint64_t* best_keys, int32_t M,
  * biased (q + 128, the reference's weights.Pack byte format, internal/weights/quant.go:66-104) with one fp16 scale per
  * output row. epilogue: 0 = y fp32 [M][N] (y_f32) and/or fp16 (y_f16); 1 = gated SiLU on row pairs (even row gate,
  * odd row up; cmd/pack/main.go:337-345): h[t][r/2] = fp16(silu(g) * u) into y_f16 [M][N/2]; 2 = SiLU: y_f16 = fp16(silu(y)).
- * One kernel launch. When K is split across workgroups the workspace holds a fixed region of arrival counters (one per
- * row group, at the same offset for every shape) followed by the split partials; the last split of a group to arrive
+ * One kernel launch. Up to 32 tokens a workgroup usually owns whole rows and sums its ranges of K in LDS: no workspace
+ * (the size query returns 0). When K is split across workgroups (more tokens, or long K) the workspace holds a fixed
+ * region of arrival counters (one per row group, at the same offset for every shape) followed by the split partials;
+ * the last split of a group to arrive
  * sums the partials in split order (the same bits every call) and applies the epilogue. Zero-fill the workspace before
  * its first use: every call leaves its counters at zero again, so one workspace serves any number of stream-ordered
  * GEMM calls of any shapes (not calls that overlap, and not other entry points in between). Replaces gemv_phase /
@@ -133,7 +135,7 @@ int dspark_accept_commit(dspark_state* st, const uint64_t* best_keys, int32_t M,
 int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* scale, int32_t N,
                    int32_t epilogue, float* y_f32, void* y_f16, void* workspace, size_t workspace_bytes,
                    dspark_stream_t stream);
-size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K); /* split-K partials + counters (0: no split) */
+size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K); /* counters + split-K partials (0: no split) */
 
 /* ---------------------------------------------------------------- cropped head + row argmax
  * y[t][r] = sum_k x[t][k] * W[r][k] (fp16 W [N][K], fp16 x [M][K], fp32 accumulation), and best_keys[t] = max key(y, r)
