@@ -784,7 +784,7 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
     // fewer than 256 strips: K in bands over more workgroups when the caller adds the bands (at least 8 chunks each)
     while (bands * 2 <= max_bands && strips * bands * 2 <= 256 && chunks / (bands * 2) >= 8) bands *= 2;
     const int bc = chunks / bands;
-    KW = xop ? std::min(8, std::max(4, bc / 8)) : 4;
+    KW = xop ? std::min(8, std::max(4, (bc + 7) / 8)) : 4;  // ranges of at most 8 chunks: one batch per wave
   } else {
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
