@@ -156,22 +156,19 @@ struct GemmParams {
   int yop;                  // > 0: the fp16 output y16 in operand order with yop token blocks (for the next GEMM's X)
   int tiled;                // int8 weights tile-major: [N / 16][K / 64][1 KB tile], lane l's 16 B at 16 l
   // Fused row-group epilogue (the group's scaled products go through LDS; y32 is not written):
-  //   GEMM_FUSE_QK: each group is one head of D rows of the attention mix q | k | v | gate: per-head RMS norm + RoPE,
-  //     q -> qk.q16, k and v -> the K/V pages at position st->a + t, gate rows -> qk.gate (query_fresh)
   //   GEMM_FUSE_CONV: each group is 16 channels [B, C, X] of the conv mix (48 rows): gated short conv, y16 [M][N/3]
   //     and the conv history ring at st->a + t (conv_wave)
   int fuse;
-  QkRopeParams qk;
   const _Float16* conv_w;   // [N/3][conv_k]
   _Float16* conv_ring;      // [CONV_RING][N/3]
   int conv_k;
 };
-constexpr int GEMM_FUSE_QK = 1, GEMM_FUSE_CONV = 2;
+constexpr int GEMM_FUSE_CONV = 2;
 
 struct GemmPlan {
   int ksplit = 1, wpg = 1, cpb = 4, kw = 0, xd = 0, bands = 1;
 };
-// wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: D / 16 for GEMM_FUSE_QK, 3 for GEMM_FUSE_CONV);
+// wpg_req > 0 fixes the strips per workgroup (a fused epilogue's group: 3 for GEMM_FUSE_CONV);
 // xop: X comes in operand order (GemmParams::xop); max_bands > 1: the caller adds up to that many output bands
 // (GemmParams::bands).
 void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0, bool xop = false,

@@ -187,7 +187,7 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
   if (r < n) ids[r] = (int32_t)(((int64_t)r * 40503 + 7) % V);
 }
 
-// `fuse` (optional) selects a fused row-group epilogue (GEMM_FUSE_QK / GEMM_FUSE_CONV) and carries its parameters.
+// `fuse` (optional) selects the fused row-group epilogue (GEMM_FUSE_CONV) and carries its parameters.
 // `bands` (optional): in, the most output bands the caller adds (y32 holds that many [M][N] blocks); out, the bands
 // the plan wrote.
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
@@ -208,12 +208,11 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   int wpg_req = 0;
   if (fuse) {
     p.fuse = fuse->fuse;
-    p.qk = fuse->qk;
     p.conv_w = fuse->conv_w;
     p.conv_ring = fuse->conv_ring;
     p.conv_k = fuse->conv_k;
     p.y32 = nullptr;
-    wpg_req = fuse->fuse == GEMM_FUSE_QK ? fuse->qk.D / 16 : 3;
+    wpg_req = 3;
   }
   GemmPlan pl;
   gemm_plan(M, N, K, true, true, &pl, wpg_req, true, bands ? *bands : 1);
@@ -319,12 +318,12 @@ QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int
   return p;
 }
 
-// The attention mix GEMM with q/k norm + RoPE + K/V page write fused into its epilogue (one head per group).
+// The attention mix GEMM, then the q/k norm + RoPE + K/V page write (qkrope). A fused epilogue needs one head per
+// workgroup: 49 workgroups for the C4 mix (10.6 us against 5.1 + 4.7 unfused) and 25 for the reference geometry's
+// 128-dim heads (14.5 us), so the two kernels are faster (measured on MI355X).
 int gemm_mix_qk(dspark_engine* e, const LayerW& W, hipStream_t s) {
-  GemmParams f = {};
-  f.fuse = GEMM_FUSE_QK;
-  f.qk = qk_params(e, W, nullptr, W.mix_rows, true, false);
-  return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, nullptr, s, &f);
+  int rc = gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s);
+  return rc ? rc : qkrope_launch(qk_params(e, W, e->mix, W.mix_rows, true, false), s);
 }
 
 // The conv mix GEMM with the gated short conv fused into its epilogue (16 channels per group); output y16.
@@ -334,7 +333,6 @@ int gemm_mix_conv(dspark_engine* e, const LayerW& W, hipStream_t s) {
   f.conv_w = W.conv_w;
   f.conv_ring = W.conv_ring;
   f.conv_k = e->d.conv_kernel;
-  f.qk.st = e->st;
   return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
 }
 
@@ -643,7 +641,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
                     align16(QH * D + 2 * KVH * D + QH), QH * D + 2 * KVH * D};
   for (int K : Ks)
     for (int N : Ns)
-      for (int wpg_req : {0, 3, D / 16}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req, true));
+      for (int wpg_req : {0, 3}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req, true));
   e->ws_gemm_bytes = gws + 256;
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
   const int G = QH / KVH;

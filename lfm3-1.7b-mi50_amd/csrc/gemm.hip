@@ -61,67 +61,6 @@ __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st 
 // The workgroup's group of R = 16 * nw rows is complete (unsplit, or summed by the last split): every wave puts its
 // scaled products into an LDS tile [token][row] (stride RS = R + 4 floats), then the group's rows are finished there.
 
-// GEMM_FUSE_QK (query_fresh, dspark.hip:999-1061): R == D, so a group is one head of q | k | v (or the gate rows).
-// One wave per token: lane l < 32 holds dims l + 32 e; q and k heads get the RMS norm (q_norm / k_norm) and RoPE at
-// position st->a + t (pairs (i, i + D/2), i < rot) and go to q16 / the K page; v heads go to the V page as they are.
-__device__ void epi_qk(const GemmParams& gp, const float* tile, int RS, int grow0, int R, int wave, int nw, int lane) {
-  const QkRopeParams& p = gp.qk;
-  const int D = p.D, half = D / 2, ne = D / 32;
-  const int qrows = p.q16 ? p.QH * D : 0, kvrows = p.KVH * D;
-  const int a = p.st->a;
-  if (grow0 >= qrows + 2 * kvrows) {  // gate rows (one per q head), fp32 as they are
-    if (!p.gate) return;
-    const int g0 = grow0 - qrows - 2 * kvrows;
-    for (int e = threadIdx.x; e < gp.M * R; e += 64 * nw) {
-      const int t = e / R, r = e % R;
-      if (g0 + r < p.QH) p.gate[(size_t)t * p.QH + g0 + r] = tile[t * RS + r];
-    }
-    return;
-  }
-  const int kind = grow0 < qrows ? 0 : (grow0 < qrows + kvrows ? 1 : 2);  // q, k, v
-  const int head = (grow0 - (kind == 0 ? 0 : (kind == 1 ? qrows : qrows + kvrows))) / D;
-  const _Float16* nw_ = kind == 0 ? p.q_norm : p.k_norm;
-  for (int t = wave; t < gp.M; t += nw) {
-    const float* src = tile + t * RS;
-    const int pos = a + t;
-    float v[4];
-    for (int e = 0; e < ne; ++e) v[e] = src[(lane & 31) + 32 * e];
-    if (kind == 2) {
-      if (lane < 32) {
-        const int phys = p.bt ? p.bt[pos / PAGE] : pos / PAGE;
-        _Float16* vb = p.vp + ((size_t)phys * p.KVH + head) * (D * PAGE);
-        for (int e = 0; e < ne; ++e) vb[v_page_elem(pos % PAGE, (lane & 31) + 32 * e)] = (_Float16)v[e];
-      }
-      continue;
-    }
-    float ss = 0.f;
-    for (int e = 0; e < ne; ++e) ss += v[e] * v[e];
-    ss = wave_sum(lane < 32 ? ss : 0.f);  // lanes 32..63 duplicate lanes 0..31
-    const float inv = rsqrtf(ss / D + p.eps);
-    for (int e = 0; e < ne; ++e) v[e] = v[e] * inv * (float)nw_[(lane & 31) + 32 * e];
-    const _Float16* rt = p.rope + (size_t)pos * D;
-    float r[4];
-    for (int e = 0; e < ne; ++e) r[e] = v[e];
-    for (int e = 0; e < ne / 2; ++e) {
-      const int i = (lane & 31) + 32 * e;
-      if (i < p.rot) {
-        const float c = (float)rt[i], s = (float)rt[half + i];
-        r[e] = v[e] * c - v[e + ne / 2] * s;
-        r[e + ne / 2] = v[e + ne / 2] * c + v[e] * s;
-      }
-    }
-    if (lane >= 32) continue;
-    if (kind == 0) {
-      _Float16* q = p.q16 + ((size_t)t * p.QH + head) * D;
-      for (int e = 0; e < ne; ++e) q[(lane & 31) + 32 * e] = (_Float16)r[e];
-    } else {
-      const int phys = p.bt ? p.bt[pos / PAGE] : pos / PAGE;
-      _Float16* kb = p.kp + ((size_t)phys * p.KVH + head) * (PAGE * D);
-      for (int e = 0; e < ne; ++e) kb[k_page_elem(pos % PAGE, (lane & 31) + 32 * e, D)] = (_Float16)r[e];
-    }
-  }
-}
-
 // GEMM_FUSE_CONV (conv_wave, dspark.hip:2191-2214): R == 48, so a group is 16 channels c with rows [B, C, X] at 3c ..
 // 3c + 2. One thread per (token, channel): bx = fp16(B X); conv = w[K-1] bx + sum_{k<K-1} w[k] hist[pos-K+1+k] with the
 // history inside the block recomputed from the tile and before it read from the ring; y = fp16(C conv); ring[pos] = bx.
@@ -188,10 +127,8 @@ __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB],
     }
   }
   __syncthreads();
-  if (p.fuse == GEMM_FUSE_QK)
-    epi_qk(p, tile, RS, grow0, R, wave, nw, lane);
-  else
-    epi_conv(p, tile, RS, grow0, R, 64 * nw);
+  (void)wave;
+  epi_conv(p, tile, RS, grow0, R, 64 * nw);
 }
 
 // Finished sums of one strip (lane (n, g): rows 16 strip + 4 g + i of token 16 tb + n): the strip's row-argmax key
