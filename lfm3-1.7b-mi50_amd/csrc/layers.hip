@@ -29,64 +29,67 @@ __global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const
 // v = sum of `bands` inputs in band order; a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
 // h_new = h_old + a * v * post_w; x = fp16(h_new * rsqrt(mean(h_new^2) + eps) * norm_w).
 // One block per (row, group): blockIdx.y selects a group with its own inputs (the drafter's tap norms).
+template <int NK, bool HAS_H>
 __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
-  const int run = run_flag_load(p.st);  // tested after the first loads are in flight
+  const int run = run_flag_load(p.st);  // tested after every load is in flight
   const int t = blockIdx.x, gi = blockIdx.y;
   const int H = p.H;
-  const float* hold = p.h_old ? p.h_old + (size_t)gi * p.group_stride + (size_t)t * H : nullptr;
+  const float* hold = HAS_H ? p.h_old + (size_t)gi * p.group_stride + (size_t)t * H : nullptr;
   const _Float16* nw = p.norm_w + (size_t)gi * p.norm_w_stride;
-  // Four consecutive columns per thread per 1024 (H <= 8192); every load is issued before the first is used.
-  constexpr int MAXK = 8;
-  const int nk = (H + 1023) / 1024;
-  f32x4 hv[MAXK], vv[MAXK];
-  half4 wn[MAXK], wp[MAXK];
+  const _Float16* pw = p.post_w ? p.post_w : nw;  // no post_w: loaded from nw and replaced by 1 below
+  // Four consecutive columns per thread per 1024 (NK = ceil(H / 1024) groups). Loads go to clamped, valid columns
+  // with no branches, so every load of the kernel is in flight before the first is used; columns past H are masked.
+  int col[NK];
+  bool ok[NK];
+  f32x4 hv[NK], vv[NK];
+  half4 wn[NK], wp[NK];
 #pragma unroll
-  for (int k = 0; k < MAXK; ++k) {
+  for (int k = 0; k < NK; ++k) {
     const int i = 1024 * k + 4 * (int)threadIdx.x;
-    hv[k] = vv[k] = f32x4{0, 0, 0, 0};
-    wn[k] = wp[k] = half4{1, 1, 1, 1};
-    if (k < nk && i < H) {
-      if (hold) hv[k] = ldg(reinterpret_cast<const f32x4*>(hold + i));
-      wn[k] = ldg(reinterpret_cast<const half4*>(nw + i));
-      if (p.post_w) wp[k] = ldg(reinterpret_cast<const half4*>(p.post_w + i));
-    }
+    ok[k] = i < H;
+    col[k] = min(i, H - 4);
+    hv[k] = HAS_H ? ldg(reinterpret_cast<const f32x4*>(hold + col[k])) : f32x4{0, 0, 0, 0};
+    wn[k] = ldg(reinterpret_cast<const half4*>(nw + col[k]));
+    wp[k] = ldg(reinterpret_cast<const half4*>(pw + col[k]));
+    vv[k] = f32x4{0, 0, 0, 0};
   }
-  // a stopped round waits for the loads in flight and writes nothing
+  // Bands BB at a time (all of a batch's loads in flight before the first add; the adds stay in band order). The
+  // first batch is outside the loop: at a loop head the compiler's wait for the previous iteration's loads would also
+  // hold the first band loads back until the loads above had arrived.
+  constexpr int BB = 2;  // the round's GEMMs write at most 2 bands
+  auto band_batch = [&](int b0) {
+    f32x4 lb[BB][NK];
+#pragma unroll
+    for (int bb = 0; bb < BB; ++bb) {
+      const float* vb = p.v + (size_t)min(b0 + bb, p.bands - 1) * p.v_band_stride + (size_t)t * H;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) lb[bb][k] = ldg(reinterpret_cast<const f32x4*>(vb + col[k]));
+    }
+#pragma unroll
+    for (int bb = 0; bb < BB; ++bb)
+      if (b0 + bb < p.bands) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) vv[k] += lb[bb][k];
+      }
+  };
+  if (p.bands > 0) band_batch(0);
+  for (int b0 = BB; b0 < p.bands; b0 += BB) band_batch(b0);
+  // the stop flag is tested once every load is in flight (a test before the band loads would hold them back by the
+  // flag's latency); a stopped round waits for the loads and writes nothing
   if (!run_flag_set(run)) {
     __builtin_amdgcn_s_waitcnt(0);
     return;
   }
-  // Bands eight at a time: a batch's loads are all in flight before the first add; the adds stay in band order.
-  constexpr int BB = 8;
-  for (int b0 = 0; b0 < p.bands; b0 += BB) {
-    if (nk == 2 && 4 * (int)threadIdx.x + 1024 < H) {  // H = 2048: two column groups per thread
-      f32x4 lb[BB][2];
+  const half4 one = {1, 1, 1, 1};
+  const f32x4 zero = {0, 0, 0, 0};
 #pragma unroll
-      for (int bb = 0; bb < BB; ++bb) {
-        const float* vb = p.v + (size_t)min(b0 + bb, p.bands - 1) * p.v_band_stride + (size_t)t * H + 4 * threadIdx.x;
-        lb[bb][0] = ldg(reinterpret_cast<const f32x4*>(vb));
-        lb[bb][1] = ldg(reinterpret_cast<const f32x4*>(vb + 1024));
-      }
-#pragma unroll
-      for (int bb = 0; bb < BB; ++bb)
-        if (b0 + bb < p.bands) {
-          vv[0] += lb[bb][0];
-          vv[1] += lb[bb][1];
-        }
-    } else {
-      for (int b = b0; b < min(b0 + BB, p.bands); ++b) {
-        const float* vb = p.v + (size_t)b * p.v_band_stride + (size_t)t * H;
-#pragma unroll
-        for (int k = 0; k < MAXK; ++k) {
-          const int i = 1024 * k + 4 * (int)threadIdx.x;
-          if (k < nk && i < H) vv[k] += ldg(reinterpret_cast<const f32x4*>(vb + i));
-        }
-      }
-    }
+  for (int k = 0; k < NK; ++k) {
+    if (!p.post_w) wp[k] = one;
+    if (!ok[k]) hv[k] = vv[k] = zero;
   }
   float s_vv = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXK; ++k)
+  for (int k = 0; k < NK; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s_vv += vv[k][j] * vv[k][j];
   __shared__ float red[8];
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
   if (p.bands > 0) a = p.sandwich ? rsqrtf(block_sum(s_vv) / H + p.eps) : 1.f;
   float s_hh = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXK; ++k)
+  for (int k = 0; k < NK; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       hv[k][j] = fmaf(vv[k][j] * a, (float)wp[k][j], hv[k][j]);
@@ -109,9 +112,9 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
     }
   const float inv = rsqrtf(block_sum(s_hh) / H + p.eps);
 #pragma unroll
-  for (int k = 0; k < MAXK; ++k) {
+  for (int k = 0; k < NK; ++k) {
     const int i = 1024 * k + 4 * (int)threadIdx.x;
-    if (k < nk && i < H) {
+    if (ok[k]) {
       const size_t o = (size_t)gi * p.group_stride + (size_t)t * H + i;
       if (p.dst) *reinterpret_cast<f32x4*>(p.dst + o) = hv[k];
       if (p.tap) *reinterpret_cast<f32x4*>(p.tap + (size_t)t * H + i) = hv[k];
@@ -480,8 +483,27 @@ int embed_launch(const void* embed, const dspark_state* st, int mode, int mask_t
   hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, (const _Float16*)embed, st, mode, mask_token, M, H, V, h);
   return (int)hipGetLastError();
 }
+template <int NK>
+static void resnorm_launch_nk(const ResNormParams& p, dim3 grid, hipStream_t s) {
+  if (p.h_old)
+    hipLaunchKernelGGL((resnorm_kernel<NK, true>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((resnorm_kernel<NK, false>), grid, dim3(256), 0, s, p);
+}
+
 int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) {
-  hipLaunchKernelGGL(resnorm_kernel, dim3(rows, groups), dim3(256), 0, s, p);
+  if (p.H < 4 || p.H % 4 || p.H > 8192) return DSPARK_EINVAL;
+  const dim3 grid(rows, groups);
+  switch ((p.H + 1023) / 1024) {
+    case 1: resnorm_launch_nk<1>(p, grid, s); break;
+    case 2: resnorm_launch_nk<2>(p, grid, s); break;
+    case 3: resnorm_launch_nk<3>(p, grid, s); break;
+    case 4: resnorm_launch_nk<4>(p, grid, s); break;
+    case 5: resnorm_launch_nk<5>(p, grid, s); break;
+    case 6: resnorm_launch_nk<6>(p, grid, s); break;
+    case 7: resnorm_launch_nk<7>(p, grid, s); break;
+    default: resnorm_launch_nk<8>(p, grid, s); break;
+  }
   return (int)hipGetLastError();
 }
 int qkrope_launch(const QkRopeParams& p, hipStream_t s) {
