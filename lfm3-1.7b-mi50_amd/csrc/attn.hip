@@ -596,7 +596,7 @@ constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
-  if (p.st && p.st->run == 0) return;
+  const int run = run_flag_load(p.st);  // tested once the partial loads are in flight
   const int hr = blockIdx.y, h = hr / p.RG, rg = hr % p.RG;
   const int R = p.R;
   const int e = blockIdx.x * (256 / COMBINE_LANES) + (int)(threadIdx.x / COMBINE_LANES);
@@ -612,6 +612,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     const bool ok = live && sp < p.S;
     ml[i] = ok ? ldg(p.part_ml + (slot0 + sp) * R + r) : f32x2{-INFINITY, 0.f};
     av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + ((slot0 + sp) * R + r) * D) + c4) : f32x4{0, 0, 0, 0};
+  }
+  if (!run_flag_set(run)) {  // a stopped round writes nothing
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0, 0, 0, 0};

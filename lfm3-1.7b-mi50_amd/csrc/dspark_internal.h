@@ -133,6 +133,12 @@ __device__ __forceinline__ int run_flag_load(const dspark_state* st) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)offsetof(dspark_state, run), 0, 0);
 }
 __device__ __forceinline__ bool run_flag_set(int v) { return __builtin_amdgcn_readfirstlane(v) != 0; }
+// Any State word by the same kind of load (byte offset `off`; st must not be null).
+__device__ __forceinline__ int state_word_load(const dspark_state* st, int off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void*)st, (short)0, (int)sizeof(dspark_state), 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 
 struct GemmParams {
   const struct ::dspark_state* st;  // when set, a stopped round (run == 0) skips the launch's work

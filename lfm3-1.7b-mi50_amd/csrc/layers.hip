@@ -134,31 +134,37 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
 // base + t with base = st->a (verify, drafter block) or st->ctx_pos (context projection); tokens t >= count
 // (count = M, or st->ctx_new) are skipped.
 __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
-  if (stopped(p.st)) return;
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int heads = p.QH + p.KVH;
   if (task >= p.M * heads) return;
   const int t = task / heads, hh = task % heads;
-  const int count = p.count_from_ctx ? p.st->ctx_new : p.M;
-  if (t >= count) return;
-  const int pos = (p.pos_from_ctx ? p.st->ctx_pos : p.st->a) + t;
-  const int D = p.D, half = D / 2;
-  const float* row = p.mix + (size_t)t * p.row;
   const bool isq = hh < p.QH;
   if (isq && !p.q16) return;
+  // The State's run flag, position base and token count are loaded by vector loads together with the row (tested
+  // and used once they are all in flight) instead of scalar loads waited for before the row is requested.
+  const int run = run_flag_load(p.st);
+  const int base_v = state_word_load(p.st, p.pos_from_ctx ? (int)offsetof(dspark_state, ctx_pos)
+                                                           : (int)offsetof(dspark_state, a));
+  const int count_v = p.count_from_ctx ? state_word_load(p.st, (int)offsetof(dspark_state, ctx_new)) : p.M;
+  const int D = p.D, half = D / 2;
+  const float* row = p.mix + (size_t)t * p.row;
   const float* src = isq ? row + (size_t)hh * D : row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)(hh - p.QH) * D;
   const _Float16* nw = isq ? p.q_norm : p.k_norm;
   // lane l holds dims l and l + 32 (D = 64) or l, l+32, l+64, l+96 (D = 128): pairs (i, i + D/2) share a lane
   constexpr int MAXE = 4;
   const int ne = D / 32;  // 2 or 4
   float v[MAXE];
-  float ss = 0.f;
-  for (int e = 0; e < ne; ++e) {
-    const int i = (lane & 31) + 32 * e;
-    v[e] = src[i];
-    ss += v[e] * v[e];
+  for (int e = 0; e < ne; ++e) v[e] = src[(lane & 31) + 32 * e];
+  if (!run_flag_set(run)) {  // a stopped round writes nothing
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
+  const int count = __builtin_amdgcn_readfirstlane(count_v);
+  if (t >= count) return;
+  const int pos = __builtin_amdgcn_readfirstlane(base_v) + t;
+  float ss = 0.f;
+  for (int e = 0; e < ne; ++e) ss += v[e] * v[e];
   // lanes 32..63 duplicate lanes 0..31; sum over the first 32 lanes
   ss = (lane < 32) ? ss : 0.f;
   ss = wave_sum(ss);
