@@ -403,8 +403,8 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 // (TB * K / 64 * 2 KB <= 64 KB); XD = true (S = 1, TB = 1) has every wave load its own range of X straight into B
 // operands. Ranges longer than CPW chunks go in batches of CPW. Chunk order inside a range, then range order, fixes the
 // summation order, so results do not depend on timing.
-template <int TB, bool I8, int CPW, bool XD>
-__global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
+template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024>
+__global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
   // anything is stored), so its latency overlaps theirs; a stopped round writes nothing.
   const int run = run_flag_load(p.st);
@@ -466,7 +466,9 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
     // 1 KB blocks of chunk c
     const _Float16* xb0 = p.xop ? p.x + lane * 8 : p.x + (size_t)min(n, p.M - 1) * p.K + 16 * g;
     const size_t xcs = p.xop ? (size_t)p.xop * 1024 : 64, xhs = p.xop ? 512 : 8;  // halves per chunk, per half
-    for (int cb = c0; cb < c1; cb += CPW) {
+    // One batch: its X and weight loads, then its products. The first batch is outside the loop: at a loop head the
+    // compiler's wait for the previous iteration's loads would also hold the first batch back behind the flag load.
+    auto batch = [&](int cb) {
       u32x4 xb[CPW][2];
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
@@ -484,6 +486,12 @@ __global__ __launch_bounds__(1024) void gemm_sliced_kernel(GemmParams p) {
           acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
         }
       }
+    };
+    if constexpr (MAXT <= 512) {  // with 128 VGPRs (1024 threads) the peeled copy spills: keep the plain loop there
+      if (c0 < c1) batch(c0);
+      for (int cb = c0 + CPW; cb < c1; cb += CPW) batch(cb);
+    } else {
+      for (int cb = c0; cb < c1; cb += CPW) batch(cb);
     }
   } else {
     // X^T rows [tb][chunk][half] of 1 KB (lane l's 16 B at 16 l: token 16 tb + l % 16, columns 64 c + 16 (l / 16) +
@@ -655,7 +663,10 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const int cpk = (p.K / 64 + p.kw - 1) / p.kw;
   if constexpr (I8) {
     if (TB == 1 && gemm_sliced_xd(p, I8)) {
-      hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true>), grid, block, lds, s, p);
+      if (block.x <= 512)  // up to 8 waves: twice the registers per wave (no spills with the first batch peeled)
+        hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512>), grid, block, lds, s, p);
+      else
+        hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true>), grid, block, lds, s, p);
       return;
     }
     if (cpk > 8) {  // 16-chunk batches of int8 weights: 64 VGPRs
