@@ -16,13 +16,38 @@ __device__ __forceinline__ bool stopped(const dspark_state* st) { return st && l
 // ---------------------------------------------------------------- embedding
 // h[t][:] = embed[token(t)][:] (fp16 -> fp32). mode 0: token(t) = st->tokens[t]; mode 1 (drafter block):
 // t == 0 ? st->anchor : mask_token. Tokens outside the vocabulary read row 0.
+// The run flag and the token come from one round trip (vector loads issued together); the row (H % 8 == 0, H <= 8192)
+// is read as 16 bytes per thread per 2048 columns, every load issued before the first store (clamped to a valid
+// column; the stores are guarded).
 __global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const dspark_state* st, int mode, int mask_token,
                                                     int M, int H, int V, float* h) {
-  if (stopped(st)) return;
   const int t = blockIdx.x;
-  int tok = mode == 0 ? st->tokens[t] : (t == 0 ? st->anchor : mask_token);
+  const int run = run_flag_load(st);
+  const int tok_v = state_word_load(st, mode == 0 ? (int)offsetof(dspark_state, tokens) + 4 * t
+                                                  : (int)offsetof(dspark_state, anchor));
+  if (!run_flag_set(run)) return;
+  int tok = __builtin_amdgcn_readfirstlane(tok_v);
+  if (mode != 0 && t != 0) tok = mask_token;
   if (tok < 0 || tok >= V) tok = 0;
-  for (int i = threadIdx.x; i < H; i += 256) h[(size_t)t * H + i] = (float)embed[(size_t)tok * H + i];
+  const _Float16* row = embed + (size_t)tok * H;
+  constexpr int G = 4;
+  half8 v[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) v[g] = ldg(reinterpret_cast<const half8*>(row + min(2048 * g + 8 * (int)threadIdx.x, H - 8)));
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int i = 2048 * g + 8 * (int)threadIdx.x;
+    if (i < H) {
+      f32x4 lo, hi;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo[j] = (float)v[g][j];
+        hi[j] = (float)v[g][4 + j];
+      }
+      *reinterpret_cast<f32x4*>(h + (size_t)t * H + i) = lo;
+      *reinterpret_cast<f32x4*>(h + (size_t)t * H + i + 4) = hi;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- residual + RMS norm (norm_compute)
@@ -486,6 +511,7 @@ __global__ void plant_kernel(dspark_state* st, const int32_t* plant, int block, 
 // ---------------------------------------------------------------- host launchers
 int embed_launch(const void* embed, const dspark_state* st, int mode, int mask_token, int M, int H, int V, float* h,
                  hipStream_t s) {
+  if (!st || H < 8 || H % 8 || H > 8192) return DSPARK_EINVAL;
   hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, (const _Float16*)embed, st, mode, mask_token, M, H, V, h);
   return (int)hipGetLastError();
 }
