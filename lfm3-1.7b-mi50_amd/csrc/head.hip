@@ -15,16 +15,48 @@ namespace dspark {
 
 constexpr int ARGMAX_CHUNK = 4096;  // logits per block
 
-template <bool F16>
+template <bool F16, bool A4>
 __global__ __launch_bounds__(256) void verify_argmax_partial(const void* logits, int M, int V, const uint32_t* seen,
                                                              const dspark_state* st, float rep, float inv_rep,
                                                              const float* rep_dev, uint64_t* part, int nchunks) {
-  if (st->run == 0) return;
+  const int run = run_flag_load(st);  // tested once the logit loads are in flight
+  const int t = blockIdx.y, chunk = blockIdx.x;
+  // Four consecutive logits per thread per 1024 (one seen word covers them). Every load of the chunk is issued before
+  // the first is used: addresses are clamped to the last logit (no branches for the compiler to wait at); positions
+  // past the chunk are dropped when the keys are formed. A4: V % 4 == 0, rows 16-byte aligned (vector loads).
+  constexpr int NK = ARGMAX_CHUNK / 1024;
+  const int r0 = chunk * ARGMAX_CHUNK, r1 = min(V, r0 + ARGMAX_CHUNK);
+  float lv[NK][4];
+  uint32_t sw[NK];
+  const float* l32 = reinterpret_cast<const float*>(logits) + (size_t)t * V;
+  const _Float16* l16 = reinterpret_cast<const _Float16*>(logits) + (size_t)t * V;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int rb = r0 + 1024 * k + 4 * (int)threadIdx.x;
+    sw[k] = ldg(seen + (min(rb, V - 1) >> 5));
+    if constexpr (A4) {
+      const int rc = min(rb, V - 4);
+      if constexpr (F16) {
+        const half4 h = ldg(reinterpret_cast<const half4*>(l16 + rc));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lv[k][i] = (float)h[i];
+      } else {
+        const f32x4 f = ldg(reinterpret_cast<const f32x4*>(l32 + rc));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lv[k][i] = (float)(_Float16)f[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rc = min(rb + i, V - 1);
+        lv[k][i] = F16 ? (float)ldg(l16 + rc) : (float)(_Float16)ldg(l32 + rc);
+      }
+    }
+  }
   if (rep_dev) {  // {rep, 1/rep} in device memory (the reference's g.rep / g.inv_rep, dspark.go:575-578)
     rep = rep_dev[0];
     inv_rep = rep_dev[1];
   }
-  const int t = blockIdx.y, chunk = blockIdx.x;
   // Drafts 1..t that were not seen before this round count as seen for this position (dspark.hip:2226-2232). Lane j
   // of wave 0 looks up draft j; a draft outside the vocabulary matches no logit (and is not looked up in seen).
   __shared__ int dt[DSPARK_MT_MAX];
@@ -42,38 +74,14 @@ __global__ __launch_bounds__(256) void verify_argmax_partial(const void* logits,
   }
   __syncthreads();
   const uint64_t isnew = isnew_s;
-  uint64_t best = 0;
-  // Four consecutive logits per thread per 1024 (one seen word covers them); every load of the chunk is issued
-  // before the first is used.
-  constexpr int NK = ARGMAX_CHUNK / 1024;
-  const int r0 = chunk * ARGMAX_CHUNK, r1 = min(V, r0 + ARGMAX_CHUNK);
-  float lv[NK][4];
-  uint32_t sw[NK];
-#pragma unroll
-  for (int k = 0; k < NK; ++k) {
-    const int rb = r0 + 1024 * k + 4 * (int)threadIdx.x;
-    sw[k] = rb < r1 ? ldg(seen + (rb >> 5)) : 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lv[k][i] = 0.f;
-    if ((V & 3) == 0 && rb + 3 < r1) {  // rows start 16-byte aligned
-      if (F16) {
-        const half4 h = ldg(reinterpret_cast<const half4*>(reinterpret_cast<const _Float16*>(logits) + (size_t)t * V + rb));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lv[k][i] = (float)h[i];
-      } else {
-        const f32x4 f = ldg(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(logits) + (size_t)t * V + rb));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lv[k][i] = (float)(_Float16)f[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (rb + i < r1)
-          lv[k][i] = F16 ? (float)ldg(reinterpret_cast<const _Float16*>(logits) + (size_t)t * V + rb + i)
-                         : (float)(_Float16)ldg(reinterpret_cast<const float*>(logits) + (size_t)t * V + rb + i);
-      }
-    }
+  // the stop flag is tested after the barrier: memory operations do not move across it, so the logit loads above stay
+  // ahead of the flag's wait (tested before them, the compiler sinks them below the test); a stopped round writes
+  // nothing
+  if (!run_flag_set(run)) {
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
   }
+  uint64_t best = 0;
   // Fresh drafts that fall on this thread's logits: one pass over the drafts (bit 4k + i = logit rb_k + i).
   uint32_t fresh = 0;
   for (uint64_t m = isnew; m; m &= m - 1) {
@@ -177,11 +185,18 @@ int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32
   const int nchunks = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
   uint64_t* part = reinterpret_cast<uint64_t*>(ws);
   if (f16)
-    hipLaunchKernelGGL(verify_argmax_partial<true>, dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st, rep,
-                       inv_rep, rep_dev, part, nchunks);
+    if (V % 4 == 0)
+      hipLaunchKernelGGL((verify_argmax_partial<true, true>), dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st,
+                         rep, inv_rep, rep_dev, part, nchunks);
+    else
+      hipLaunchKernelGGL((verify_argmax_partial<true, false>), dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st,
+                         rep, inv_rep, rep_dev, part, nchunks);
+  else if (V % 4 == 0)
+    hipLaunchKernelGGL((verify_argmax_partial<false, true>), dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st,
+                       rep, inv_rep, rep_dev, part, nchunks);
   else
-    hipLaunchKernelGGL(verify_argmax_partial<false>, dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st, rep,
-                       inv_rep, rep_dev, part, nchunks);
+    hipLaunchKernelGGL((verify_argmax_partial<false, false>), dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st,
+                       rep, inv_rep, rep_dev, part, nchunks);
   hipLaunchKernelGGL(fold_keys, dim3(M), dim3(64), 0, s, part, nchunks, best, st);
   return (int)hipGetLastError();
 }
