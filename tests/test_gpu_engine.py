@@ -29,14 +29,14 @@ REF_SMALL = dict(hidden=512, ffn=512, vocab=2048, n_layers=6, layer_kind=[0, 0, 
 # SMALL with the full-size cropped head and Markov rank (16384 rows, rank 256): every thread of the Markov chain's
 # workgroup owns rows.
 SMALL_WIDE = dict(SMALL, vocab=32768, mask_token=32767, crop_rows=16384, markov_rank=256)
-# Wider GEMMs (hidden 1024, FFN 4096): one-strip K-sliced plans with each wave loading its own X (two batches for w2's
-# 16-chunk ranges), the fused epilogues over 4 (q/k) and 5 (conv, the last range empty) ranges of K.
+# Wider GEMMs (hidden 1024, FFN 4096): one-strip K-sliced plans with each wave loading its own X, w2 and out in two K
+# bands added by the norm kernel, and the fused conv epilogue over 5 ranges of K (the last one empty).
 MID = dict(hidden=1024, ffn=4096, vocab=4096, n_layers=4, layer_kind=[0, 1, 0, 2], q_heads=16, kv_heads=4, head_dim=64,
            conv_kernel=3, window=40, rope_base=1e4, rope_pairs=32, draft_layers=2, draft_ffn=2048, block=9,
            max_drafts=8, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[1, 3], draft_window=100,
            ring_positions=256, mask_token=4095, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
-# MID with 24- and 33-token blocks: two token blocks (K-sliced GEMMs with X^T in LDS, fused epilogues over two token
-# blocks), three token blocks (K split across workgroups, the last split running the fused epilogues).
+# MID with 24- and 33-token blocks: two token blocks (K-sliced GEMMs with X^T in LDS, the fused conv epilogue over two
+# token blocks), three token blocks (K split across workgroups, the last split running the fused conv epilogue).
 MID24 = dict(MID, block=24, max_drafts=12)
 MID33 = dict(MID, block=33, max_drafts=16)
 GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE, "mid": MID,
