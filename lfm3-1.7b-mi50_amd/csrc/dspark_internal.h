@@ -194,9 +194,15 @@ int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s);
 
 size_t verify_argmax_ws(int M, int V);
 
+// fold = false: the partial keys [M][verify_argmax_chunks(V)] stay in ws for accept_commit_fold_launch to fold.
 int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32_t* seen, const dspark_state* st,
-                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev = nullptr);
+                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev = nullptr,
+                         bool fold = true);
+int verify_argmax_chunks(int V);
 int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, uint32_t* seen,
                          hipStream_t s);
+// The verify argmax's partial keys folded into best[M] (as fold_keys would), then accept + commit of State->M tokens.
+int accept_commit_fold_launch(dspark_state* st, const uint64_t* part, int nchunks, int M, uint64_t* best,
+                              int32_t* out_tokens, uint32_t* seen, hipStream_t s);
 
 }  // namespace dspark

@@ -455,8 +455,9 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     CK(resnorm(e, e->h[cur], e->w2out, w2b, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
   }
   CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
-  CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep));
-  CK(accept_commit_launch(e->st, vbest, 0, 0, e->out_tokens, e->seen, s));
+  CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep, false));
+  CK(accept_commit_fold_launch(e->st, static_cast<const uint64_t*>(e->ws_argmax), verify_argmax_chunks(d.vocab), B, vbest,
+                               e->out_tokens, e->seen, s));
   return 0;
 }
 

@@ -128,9 +128,33 @@ __global__ __launch_bounds__(64) void fold_keys(const uint64_t* part, int nchunk
 
 __device__ __forceinline__ int key_token(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
 
-__global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, const uint64_t* best, int m, int skip_now,
-                                                           int32_t* out_tokens, uint32_t* seen) {
-  if (threadIdx.x != 0 || st->run == 0) return;
+// part (optional): the verify argmax's partial keys [mfold][nchunks], folded here into best[t] first (every thread
+// loads its share at once; u64 max in LDS, order-free) instead of by a separate fold_keys launch.
+__global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uint64_t* best, int m, int skip_now,
+                                                           int32_t* out_tokens, uint32_t* seen, const uint64_t* part,
+                                                           int nchunks, int mfold) {
+  if (st->run == 0) return;
+  if (part) {
+    __shared__ unsigned long long sb[64];
+    sb[threadIdx.x] = 0;
+    __syncthreads();
+    const int n = mfold * nchunks;
+    constexpr int PB = 8;
+    for (int e0 = 0; e0 < n; e0 += 64 * PB) {
+      uint64_t v[PB];
+#pragma unroll
+      for (int i = 0; i < PB; ++i) v[i] = ldg(part + min(e0 + 64 * i + (int)threadIdx.x, n - 1));
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        const int e = e0 + 64 * i + (int)threadIdx.x;
+        if (e < n) atomicMax(&sb[e / nchunks], (unsigned long long)v[i]);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int t = 0; t < mfold; ++t) best[t] = sb[t];  // the folded keys (thread 0 reads its own writes below)
+  }
+  if (threadIdx.x != 0) return;
   if (m <= 0) m = st->M;  // rounds that drafted on the device: the verified count is in the State
   int acc = 0;
   for (int t = 0; t < m - 1; ++t) {
@@ -181,7 +205,8 @@ size_t verify_argmax_ws(int M, int V) {
 }
 
 int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32_t* seen, const dspark_state* st,
-                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev) {
+                         float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev,
+                         bool fold) {
   const int nchunks = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
   uint64_t* part = reinterpret_cast<uint64_t*>(ws);
   if (f16)
@@ -197,13 +222,24 @@ int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32
   else
     hipLaunchKernelGGL((verify_argmax_partial<false, false>), dim3(nchunks, M), dim3(256), 0, s, logits, M, V, seen, st,
                        rep, inv_rep, rep_dev, part, nchunks);
-  hipLaunchKernelGGL(fold_keys, dim3(M), dim3(64), 0, s, part, nchunks, best, st);
+  if (fold) hipLaunchKernelGGL(fold_keys, dim3(M), dim3(64), 0, s, part, nchunks, best, st);
   return (int)hipGetLastError();
 }
 
 int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, uint32_t* seen,
                          hipStream_t s) {
-  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, m, skip_now, out_tokens, seen);
+  // best is only read when no partial keys are given
+  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, const_cast<uint64_t*>(best), m, skip_now,
+                     out_tokens, seen, (const uint64_t*)nullptr, 0, 0);
+  return (int)hipGetLastError();
+}
+
+int verify_argmax_chunks(int V) { return (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
+
+int accept_commit_fold_launch(dspark_state* st, const uint64_t* part, int nchunks, int M, uint64_t* best,
+                              int32_t* out_tokens, uint32_t* seen, hipStream_t s) {
+  if (M < 1 || M > 64 || nchunks < 1) return DSPARK_EINVAL;
+  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, 0, 0, out_tokens, seen, part, nchunks, M);
   return (int)hipGetLastError();
 }
 
