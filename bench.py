@@ -118,7 +118,7 @@ def bench_c2(args, host, torch):
     for s in range(SETS):
         for l in range(L):
             a_, b_, c_, d_ = kvw[s][l]
-            host.check(lib.dspark_kv_write(a_, b_, KVH * D, c_, d_, None, KVH, D, ctx, M, sh), "kv_write")
+            host.check(lib.dspark_kv_write(a_, b_, KVH * D, c_, d_, None, n_pages, KVH, D, ctx, M, sh), "kv_write")
 
     def step(i):
         s = i % SETS

@@ -98,8 +98,10 @@ int dspark_verify_attention_combine(const dspark_attn_args* args, dspark_stream_
  * the length update alone and rollback leaves the rejected rows to be overwritten (the reference copies fresh K/V at
  * commit instead, dspark.hip:2860-2877; prefill's kv_write, kernels/ops.hip:226-251, is the same call with pos0 = 0). */
 int dspark_kv_write(const void* k, const void* v, int64_t row_stride, void* k_pages, void* v_pages,
-                    const int32_t* block_table, int32_t KVH, int32_t D, int32_t pos0, int32_t n,
+                    const int32_t* block_table, int64_t kv_pages, int32_t KVH, int32_t D, int32_t pos0, int32_t n,
                     dspark_stream_t stream);
+/* kv_pages: pages in each pool. Without a block table, pos0 + n must fit the pools (DSPARK_EINVAL otherwise); with
+ * one, a row whose table entry is outside [0, kv_pages) is not written. */
 
 /* ---------------------------------------------------------------- verify argmax (greedy head)
  * best_keys[t] = max over r < V of key(pv, r), pv the repetition-penalised fp16-rounded logit (seen[] bitmap, plus
@@ -117,7 +119,9 @@ size_t dspark_verify_argmax_workspace(int32_t M, int32_t V);
  * exactly as dspark.hip:2848-2913. `skip_now` is the round's skip flag. The KV rows of positions a..a+acc are already
  * in the pages (dspark_kv_write before attention), so the commit moves no K/V. */
 int dspark_accept_commit(dspark_state* st, const uint64_t* best_keys, int32_t M, int32_t skip_now, int32_t* out_tokens,
-                         uint32_t* seen, dspark_stream_t stream);
+                         int32_t out_cap, uint32_t* seen, dspark_stream_t stream);
+/* out_cap: int32 slots in out_tokens (>= M). A commit that would write past it (State.count + acc + 1 > out_cap)
+ * writes nothing and stops the run (State.run = 0), as a launch whose output buffer is full must stop. */
 
 /* ---------------------------------------------------------------- int8-weight verify GEMM
  * y[t][r] = scale[r] * sum_k x[t][k] * q[r][k] for t < M (M <= 64), r < N (N % 16 == 0), K % 64 == 0. Weights int8 [N][K] stored
@@ -181,11 +185,25 @@ typedef struct dspark_model_desc {
   int32_t mask_token;
   float conf_bias, conf_thr;
   float eps;               /* RMS-norm epsilon */
+  /* RoPE of the sliding-window layers (kind 2), when it differs from the table above (which serves full attention
+   * and the drafter): the reference builds base 1e6 with 32 pairs for full layers and the drafter, base 1e4 with 64
+   * pairs for sliding layers (internal/model/engine.go:333-338). rope_base_swa <= 0: sliding layers use the first. */
+  float rope_base_swa;
+  int32_t rope_pairs_swa;
+  int32_t conv_slots;      /* conv-state slots per conv layer, slot 0 the running state (engine.go:122, 138); >= 1 */
 } dspark_model_desc;
 
 typedef struct dspark_engine dspark_engine;
 
-/* Allocate weights (uninitialised) and runtime buffers for contexts up to max_context positions. */
+/* RoPE table of `positions` rows: out[p][i] = fp16(cos f), out[p][D/2 + i] = fp16(sin f) for i < D/2, with
+ * f = (double)((float)p * inv[i]), inv[i] = 1 / (float)pow(base, (float)(2 i) / D) for i < pairs and 0 beyond (a pair
+ * that does not rotate), fp16 by round-to-nearest-even. Host code, no device memory; the engine builds its tables with
+ * it. Replaces Engine.buildRope (internal/model/engine.go:428-461). */
+int dspark_rope_table(float base, int32_t pairs, int32_t head_dim, int32_t positions, uint16_t* out);
+
+/* Allocate weights (uninitialised) and runtime buffers for contexts up to max_context positions. DSPARK_EINVAL for a
+ * description outside the documented ranges, or a max_context whose per-layer K/V page pool would reach 2 GiB (the
+ * attention kernels address a pool with 32-bit byte offsets). */
 int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dspark_engine** out);
 void dspark_engine_destroy(dspark_engine* e);
 /* Random-initialise every weight on the device from `seed` (synthetic benchmarks; no host copy of the weights). */
@@ -214,11 +232,38 @@ int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream);
  * run-time a is correct; the plan is re-recorded when plan_a moves to another 4096-position bucket). */
 int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream);
 
+/* Set the repetition-penalty mask to exactly the given tokens (ids outside the vocabulary are ignored) and the
+ * penalty the next rounds use (0 = 1). Replaces Engine.InitSeen (internal/model/engine.go:617-629), which Generate
+ * calls once per request with the prompt (generate.go:105); rounds then add every token they emit. */
+int dspark_engine_init_seen(dspark_engine* e, const int32_t* tokens, int32_t n, float rep, dspark_stream_t stream);
+
+/* Drafter context seeding at prefill. capture_tap: rows of the hidden state h (fp16, row stride `row_stride` elements)
+ * of positions context .. context + tokens - 1, taken after the tapped target layer `slot`, are RMS-normed with
+ * tap_norms[slot] into the engine's capture buffer from position max(context, tap_from) on (tap_from = the first
+ * position the request captures; the buffer holds draft_window positions from it). Replaces captureTap
+ * (internal/model/dspark.go:439-459). project_prompt: the captured positions [first, end) (first = tap_from,
+ * end - first <= draft_window) through fc, the hidden norm and ckv, then per drafter layer the k norm, RoPE and the K/V
+ * rows into the drafter's ring at their positions. Replaces projectPrompt (dspark.go:461-492); beginDraft's
+ * bookkeeping (dspark.go:494-515) is the caller's: the next launch takes ctx_new = 0, ctx_pos = a, ctx_lo = first. */
+int dspark_engine_capture_tap(dspark_engine* e, int32_t slot, const void* h, int64_t row_stride, int32_t context,
+                              int32_t tokens, int32_t tap_from, dspark_stream_t stream);
+int dspark_engine_project_prompt(dspark_engine* e, int32_t first, int32_t end, dspark_stream_t stream);
+
+/* Copy conv-state slot src to slot dst in every conv layer (tensors "conv_state.L<i>", [conv_slots][H][conv_kernel-1]
+ * fp16, element (c, k) at c * (conv_kernel - 1) + k, the reference's layout, engine.go:546-547). Replaces
+ * Engine.CopyConvSlot (internal/model/prefill.go:596-606). */
+int dspark_engine_conv_copy(dspark_engine* e, int32_t src, int32_t dst, dspark_stream_t stream);
+
 /* draftLaunch: run rounds from the sequence's last token to the next 32-position block boundary (the State fields
- * a, anchor, limit, budget, eos, stop_at are set from the arguments as internal/model/dspark.go:543-566 does), then
- * copy the State and the emitted tokens back. Synchronous on `stream`. */
+ * a, anchor, limit, budget, eos, stop_at, ctx_*, miss, skip, ckpt_slot are set from the arguments as
+ * internal/model/dspark.go:543-566 does: stop_at = min(next multiple of 32 after a, max_context), limit =
+ * min(stop_at + block, max_context)), then copy the State and the emitted tokens back. Synchronous on `stream`.
+ * With conv_slot >= 0 the launch first loads the conv history of positions a - (conv_kernel - 1) .. a - 1 from that
+ * conv-state slot into the engine's position ring, and at its end writes the running state (the history before the
+ * final a) back to the slot and, when ckpt_slot >= 0 and the launch reached stop_at, the history before stop_at to
+ * ckpt_slot (dspark.hip:2415-2431, 2921-2947). conv_slot = -1 keeps the ring as the previous launch left it. */
 typedef struct dspark_launch_args {
-  int32_t a;               /* position of the anchor (= len(tokens) - 1) */
+  int32_t a;               /* position of the anchor (= len(tokens) - 1), < max_context */
   int32_t anchor;          /* token at position a */
   int32_t budget;          /* tokens this launch may emit (capped at 512) */
   int32_t eos;             /* stop token or -1 */
@@ -228,13 +273,19 @@ typedef struct dspark_launch_args {
   int32_t force_m;         /* > 0: verify-only rounds of the State's tokens (the tokens array below); -1: planted
                               drafts (see dspark_engine_round) */
   int32_t tokens[DSPARK_MT_MAX];
+  int32_t max_drafts;      /* drafts per round this launch (<= 0: the model's max_drafts); the reference's policy is
+                              7, or 3 for a request whose decode starts at position >= 57344 (dspark.go:568-571) */
+  int32_t miss, skip;      /* acceptance-miss / skip counters carried from the previous launch (dspark.go:560, 615) */
+  int32_t conv_slot;       /* running conv-state slot (the reference's step conv slot, engine.go:548), or -1 */
+  int32_t ckpt_slot;       /* conv checkpoint slot for stop_at (cache.allocConv, dspark.go:550), or -1 */
 } dspark_launch_args;
 
 typedef struct dspark_launch_result {
   int32_t count;           /* tokens emitted */
   int32_t rounds, accepted, verified;
   int32_t boundary;        /* the block boundary the launch ran to */
-  dspark_state state;      /* State after the launch */
+  int32_t ckpt_written;    /* 1: the launch reached the boundary and ckpt_slot holds the conv state there */
+  dspark_state state;      /* State after the launch (ctx_new, ctx_pos, miss, skip carry to the next launch) */
 } dspark_launch_result;
 
 int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* args, int32_t* out_tokens, int32_t max_out,

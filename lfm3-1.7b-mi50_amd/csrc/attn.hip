@@ -666,8 +666,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 
 // K/V rows of positions pos0..pos0+n-1 into the pages: one thread per (token, head, 8 dims).
 __global__ __launch_bounds__(256) void kv_write_kernel(const _Float16* k, const _Float16* v, int64_t row_stride,
-                                                       _Float16* kp, _Float16* vp, const int32_t* bt, int KVH, int D,
-                                                       int pos0, int n) {
+                                                       _Float16* kp, _Float16* vp, const int32_t* bt, int64_t kv_pages,
+                                                       int KVH, int D, int pos0, int n) {
   const int d8n = D / 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)n * KVH * d8n) return;
@@ -676,8 +676,9 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const _Float16* k, const 
   const int h = rem / d8n, d8 = rem % d8n;
   const int pos = pos0 + tok, lp = pos / PAGE, slot = pos % PAGE;
   const int phys = bt ? bt[lp] : lp;
-  const _Float16* ks = k + tok * row_stride + h * D + 8 * d8;
-  const _Float16* vs = v + tok * row_stride + h * D + 8 * d8;
+  if (phys < 0 || phys >= kv_pages) return;  // a table entry outside the pools: the row is not written
+  const _Float16* ks = k + (int64_t)tok * row_stride + h * D + 8 * d8;
+  const _Float16* vs = v + (int64_t)tok * row_stride + h * D + 8 * d8;
   // K in operand order: key `slot` is row n = 4 (slot / 8) + slot % 4 of key block b = (slot / 4) % 2; its 8 dims
   // 8 d8 .. belong to k-step s = d8 / 4 and lane n + 16 (d8 % 4).
   const int b = (slot >> 2) & 1, nrow = 4 * (slot >> 3) + (slot & 3), s = d8 >> 2, lanek = nrow + 16 * (d8 & 3);
@@ -900,13 +901,13 @@ int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
-int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt, int KVH,
-                    int D, int pos0, int n, hipStream_t s) {
+int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt,
+                    int64_t kv_pages, int KVH, int D, int pos0, int n, hipStream_t s) {
   const int64_t threads = (int64_t)n * KVH * (D / 8);
   if (threads == 0) return 0;
   hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                     (const _Float16*)k, (const _Float16*)v, row_stride, (_Float16*)kp, (_Float16*)vp, bt, KVH, D, pos0,
-                     n);
+                     (const _Float16*)k, (const _Float16*)v, row_stride, (_Float16*)kp, (_Float16*)vp, bt, kv_pages, KVH,
+                     D, pos0, n);
   return (int)hipGetLastError();
 }
 

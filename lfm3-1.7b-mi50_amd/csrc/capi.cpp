@@ -2,6 +2,10 @@
 // indexing assume is checked here, on the host, before anything is launched.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+#include <cstring>
+#include <vector>
+
 #include "dspark.h"
 #include "dspark_internal.h"
 
@@ -9,7 +13,7 @@ using namespace dspark;
 
 namespace {
 
-constexpr int ABI_VERSION = 1;
+constexpr int ABI_VERSION = 2;
 
 // Compute units of the current device (queried once per device; 256 on MI355X).
 int device_cus() {
@@ -25,6 +29,33 @@ int device_cus() {
 }
 
 hipStream_t S(dspark_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// IEEE binary32 -> binary16, round to nearest, ties to even (the host compiler's own _Float16 conversion rounds an exact
+// tie away from even, so the tables built on the host use this instead).
+uint16_t f32_to_f16(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);  // NaN
+  const int e = (int)(ax >> 23);
+  const uint32_t mant = ax & 0x7fffffu;
+  if (e >= 143) return (uint16_t)(sign | 0x7c00u);          // >= 2^16 (and infinity)
+  uint32_t q, r, half;
+  if (e >= 113) {                                          // a normal half (or overflow by rounding)
+    q = ((uint32_t)(e - 112) << 10) | (mant >> 13);
+    r = mant & 0x1fffu;
+    half = 0x1000u;
+  } else {                                                 // subnormal half: units of 2^-24
+    const int shift = 126 - e;
+    if (shift > 24) return (uint16_t)sign;
+    const uint32_t m = mant | 0x800000u;
+    q = m >> shift;
+    r = m & ((1u << shift) - 1u);
+    half = 1u << (shift - 1);
+  }
+  if (r > half || (r == half && (q & 1u))) ++q;  // a carry moves into the exponent, up to infinity
+  return (uint16_t)(sign | q);
+}
 
 bool attn_args_ok(const dspark_attn_args* a) {
   if (!a || !a->q || !a->k_pages || !a->v_pages) return false;
@@ -69,6 +100,26 @@ AttnParams attn_params(const dspark_attn_args* a) {
 extern "C" {
 
 int dspark_abi_version(void) { return ABI_VERSION; }
+
+int dspark_rope_table(float base, int32_t pairs, int32_t head_dim, int32_t positions, uint16_t* out) {
+  if (!out || !(base > 0.f) || head_dim < 2 || head_dim % 2 || pairs < 0 || pairs > head_dim / 2 || positions < 0)
+    return DSPARK_EINVAL;
+  const int D = head_dim;
+  std::vector<float> inv(D / 2, 0.f);
+  for (int i = 0; i < pairs; ++i) {
+    const float ex = (float)(2 * i) / (float)D;
+    inv[i] = 1.f / (float)std::pow((double)base, (double)ex);
+  }
+  for (int64_t p = 0; p < positions; ++p) {
+    const float t = (float)p;
+    for (int i = 0; i < D / 2; ++i) {
+      const double f = (double)(t * inv[i]);
+      out[(size_t)p * D + i] = f32_to_f16((float)std::cos(f));
+      out[(size_t)p * D + D / 2 + i] = f32_to_f16((float)std::sin(f));
+    }
+  }
+  return 0;
+}
 int dspark_page_tokens(void) { return DSPARK_PAGE_TOKENS; }
 int dspark_max_tokens(void) { return DSPARK_MT_MAX; }
 int dspark_state_bytes(void) { return (int)sizeof(dspark_state); }
@@ -103,12 +154,14 @@ int dspark_verify_attention_combine(const dspark_attn_args* a, dspark_stream_t s
 }
 
 int dspark_kv_write(const void* k, const void* v, int64_t row_stride, void* k_pages, void* v_pages,
-                    const int32_t* block_table, int32_t KVH, int32_t D, int32_t pos0, int32_t n,
+                    const int32_t* block_table, int64_t kv_pages, int32_t KVH, int32_t D, int32_t pos0, int32_t n,
                     dspark_stream_t stream) {
   if (!k || !v || !k_pages || !v_pages) return DSPARK_EINVAL;
   if ((D != 64 && D != 128) || KVH < 1 || pos0 < 0 || n < 0 || row_stride < (int64_t)KVH * D || row_stride % 8 != 0)
     return DSPARK_EINVAL;
-  return kv_write_launch(k, v, row_stride, k_pages, v_pages, block_table, KVH, D, pos0, n, S(stream));
+  if (kv_pages < 1 || (int64_t)pos0 + n > ((int64_t)1 << 31) - DSPARK_PAGE_TOKENS) return DSPARK_EINVAL;
+  if (!block_table && ((int64_t)pos0 + n + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS > kv_pages) return DSPARK_EINVAL;
+  return kv_write_launch(k, v, row_stride, k_pages, v_pages, block_table, kv_pages, KVH, D, pos0, n, S(stream));
 }
 
 size_t dspark_verify_argmax_workspace(int32_t M, int32_t V) {
@@ -125,9 +178,9 @@ int dspark_verify_argmax(const void* logits, int32_t logits_f16, int32_t M, int3
 }
 
 int dspark_accept_commit(dspark_state* st, const uint64_t* best_keys, int32_t M, int32_t skip_now, int32_t* out_tokens,
-                         uint32_t* seen, dspark_stream_t stream) {
-  if (!st || !best_keys || !out_tokens || !seen || M < 1 || M > DSPARK_MT_MAX) return DSPARK_EINVAL;
-  return accept_commit_launch(st, best_keys, M, skip_now, out_tokens, seen, S(stream));
+                         int32_t out_cap, uint32_t* seen, dspark_stream_t stream) {
+  if (!st || !best_keys || !out_tokens || !seen || M < 1 || M > DSPARK_MT_MAX || out_cap < M) return DSPARK_EINVAL;
+  return accept_commit_launch(st, best_keys, M, skip_now, out_tokens, out_cap, seen, S(stream));
 }
 
 size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K) {

@@ -97,6 +97,7 @@ struct MarkovParams {
   const float* c2;              // [vocab]
   const int32_t* crop_ids;      // [N]
   uint64_t* best;               // [block] argmax keys (cleared by round_begin)
+  const int32_t* max_drafts_dev;  // when set: the launch's draft cap (min with max_drafts), read at run time
   float conf_bias, conf_thr;
   const float* table;           // [N][N] w1q[crop_ids[c]] . w2q[r] (markov_table_launch), or nullptr: steps dot w2q
   const float* c2c;             // [N] c2[crop_ids[c]]
@@ -114,14 +115,33 @@ int markov_table_launch(const int8_t* w1q, const float* w1s, const float* c2, co
 int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos,
                        int vocab, int out_cap, hipStream_t s);
 int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);
-int plant_launch(struct ::dspark_state* st, const int32_t* plant, int block, int max_drafts, hipStream_t s);
+int plant_launch(struct ::dspark_state* st, const int32_t* plant, int block, int max_drafts, const int32_t* max_drafts_dev,
+                 hipStream_t s);
+
+// Conv state <-> the engine's position ring of conv history (CONV_RING positions x H per conv layer). The state of a
+// slot is [H][conv_k - 1] fp16 (channel-major, the reference's layout); history k of it is the position p - (conv_k - 1)
+// + k before position p. load: the ring positions before st->a from slot `slot`; store: the positions before st->a to
+// slot `slot` and, when st->ckpt_slot >= 0 and st->a >= st->stop_at, those before st->stop_at to st->ckpt_slot;
+// copy: slot src -> slot dst.
+constexpr int CONV_MAX_LAYERS = 64;
+struct ConvStateArgs {
+  _Float16* ring[CONV_MAX_LAYERS];
+  _Float16* state[CONV_MAX_LAYERS];  // [slots][H][conv_k - 1]
+  int n, H, km1, slots;
+};
+int conv_load_launch(const ConvStateArgs& a, const struct ::dspark_state* st, int slot, hipStream_t s);
+int conv_store_launch(const ConvStateArgs& a, const struct ::dspark_state* st, int slot, hipStream_t s);
+int conv_copy_launch(const ConvStateArgs& a, int src, int dst, hipStream_t s);
+// rows of fp16 h (row stride in elements) -> fp16(x * rsqrt(mean(x^2) + eps) * w) at out + row * out_stride
+int rms_rows_launch(const _Float16* h, int64_t h_stride, const _Float16* w, float eps, int H, _Float16* out,
+                    int64_t out_stride, int rows, hipStream_t s);
 size_t attn_workspace_bytes(const AttnParams& p, int D);
 // Carves the split partials out of a workspace of attn_workspace_bytes (256-byte aligned pieces).
 void attn_bind_workspace(AttnParams& p, int D, void* ws);
 // phases: 1 split pass (partials into the workspace), 2 merge of those partials, 3 both
 int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);
-int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt, int KVH,
-                    int D, int pos0, int n, hipStream_t s);
+int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt,
+                    int64_t kv_pages, int KVH, int D, int pos0, int n, hipStream_t s);
 
 // The State's run flag read with a vector load (issued in order with the kernel's data loads, so a kernel can put it
 // first and test it after its loads are in flight, instead of a scalar load the compiler waits for at the next use of
@@ -199,10 +219,10 @@ int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32
                          float rep, float inv_rep, uint64_t* best, void* ws, hipStream_t s, const float* rep_dev = nullptr,
                          bool fold = true);
 int verify_argmax_chunks(int V);
-int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, uint32_t* seen,
-                         hipStream_t s);
+int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, int out_cap,
+                         uint32_t* seen, hipStream_t s);
 // The verify argmax's partial keys folded into best[M] (as fold_keys would), then accept + commit of State->M tokens.
 int accept_commit_fold_launch(dspark_state* st, const uint64_t* part, int nchunks, int M, uint64_t* best,
-                              int32_t* out_tokens, uint32_t* seen, hipStream_t s);
+                              int32_t* out_tokens, int out_cap, uint32_t* seen, hipStream_t s);
 
 }  // namespace dspark

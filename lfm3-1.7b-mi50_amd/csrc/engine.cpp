@@ -84,16 +84,29 @@ struct dspark_engine {
   std::map<const void*, size_t> tile_of;       // row-major weight -> its tile entry
   std::map<std::string, size_t> tile_by_name;  // tensor name -> its tile entry
   bool tiles_dirty = true;
-  _Float16* rope = nullptr;
+  _Float16* rope = nullptr;      // full attention and drafter layers: [positions + 1][D] cos | sin
+  _Float16* rope_swa = nullptr;  // sliding layers (== rope when the description gives them no table of their own)
+  int rot_swa = 0;
   int32_t* ring_bt = nullptr;
   int ring_pages = 0;
   int64_t kv_pages = 0;
   // request state
   dspark_state* st = nullptr;
+  dspark_state* ast = nullptr;  // the State the kernels being enqueued read (st, or a prompt-projection chunk's)
   uint32_t* seen = nullptr;
   int32_t* out_tokens = nullptr;
   int32_t* plant = nullptr;  // planted drafts by position (force_m = -1 rounds)
-  float* rep = nullptr;  // [2]: rep, 1/rep
+  float* rep = nullptr;  // launch parameters read by the kernels: rep, 1/rep (floats 0, 1), draft cap (int32 at 2)
+  // conv state slots of every conv layer ("conv_state.L<i>") and the rings they load into / store from
+  ConvStateArgs conv = {};
+  // drafter context seeding: normed taps of captured prompt positions [tap_rows][n_taps * H] from tap_from, and one
+  // State per projection chunk (ctx_pos, ctx_new of the chunk)
+  _Float16* tapx = nullptr;
+  int tap_rows = 0, tap_from = -1;
+  dspark_state* seed_st = nullptr;
+  int seed_chunks = 0;
+  std::vector<dspark_state> host_seed;
+  std::vector<uint32_t> host_seen;
   // activations
   float *h[2] = {nullptr, nullptr}, *mix = nullptr, *vout = nullptr, *w2out = nullptr, *ctxv = nullptr, *ckvout = nullptr,
         *taps = nullptr, *logits = nullptr, *base = nullptr, *gate = nullptr;
@@ -109,7 +122,7 @@ struct dspark_engine {
   int tbs = 1;  // 16-token blocks of the round: x16, y16 and a16 hold 16 tbs token rows in the GEMMs' X operand order
   int cus = 256;
   dspark_state host_st;  // launch-time uploads stay alive until the stream has consumed them
-  float host_rep[2] = {1.f, 1.f};
+  float host_lp[4] = {1.f, 1.f, 0.f, 0.f};
   // recorded rounds: key (force_m, plan bucket) -> graph
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
   std::vector<void*> allocs;
@@ -190,10 +203,12 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
 // `fuse` (optional) selects the fused row-group epilogue (GEMM_FUSE_CONV) and carries its parameters.
 // `bands` (optional): in, the most output bands the caller adds (y32 holds that many [M][N] blocks); out, the bands
 // the plan wrote.
+// `xop` false: x is row-major [M][K] (prompt projection) instead of the round's operand order.
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
-         float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr, int* bands = nullptr) {
+         float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr, int* bands = nullptr,
+         bool xop = true) {
   GemmParams p = {};
-  p.st = e->st;
+  p.st = e->ast;
   p.x = x;
   p.w = w;
   p.scale = s;
@@ -203,7 +218,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
-  p.xop = e->tbs;  // every GEMM of the round reads x16, y16 or a16
+  p.xop = xop ? e->tbs : 0;  // every GEMM of the round reads x16, y16 or a16
   p.yop = e->tbs;
   int wpg_req = 0;
   if (fuse) {
@@ -215,7 +230,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
     wpg_req = 3;
   }
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl, wpg_req, true, bands ? *bands : 1);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req, xop, bands ? *bands : 1);
   if (bands) *bands = pl.bands;
   p.bands = pl.bands;
   p.ksplit = pl.ksplit;
@@ -240,7 +255,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
 int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, const _Float16* post_w,
             const _Float16* norm_w, int sandwich, float* dst, float* tap, hipStream_t s) {
   ResNormParams p = {};
-  p.st = e->st;
+  p.st = e->ast;
   p.h_old = h_old;
   p.v = v;
   p.bands = bands;
@@ -261,7 +276,7 @@ int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, con
 int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const float* gate, hipStream_t s) {
   const dspark_model_desc& d = e->d;
   AttnParams p = {};
-  p.st = e->st;
+  p.st = e->ast;
   p.drafter = drafter;
   p.q = e->q16;
   p.kp = Lw.kv_k;
@@ -295,17 +310,18 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
 QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode) {
   const dspark_model_desc& d = e->d;
   QkRopeParams p = {};
-  p.st = e->st;
+  p.st = e->ast;
   p.mix = mix;
   p.row = row;
   p.M = e->B;
   p.QH = d.q_heads;
   p.KVH = d.kv_heads;
   p.D = d.head_dim;
-  p.rot = d.rope_pairs;
+  // sliding layers rotate with their own table (base, pairs); full attention and the drafter with the first
+  p.rot = Lw.kind == 2 ? e->rot_swa : d.rope_pairs;
   p.q_norm = Lw.q_norm;
   p.k_norm = Lw.k_norm;
-  p.rope = e->rope;
+  p.rope = Lw.kind == 2 ? e->rope_swa : e->rope;
   p.eps = d.eps;
   p.q16 = with_q ? e->q16 : nullptr;
   p.gate = (with_q && Lw.kind != 3) ? e->gate : nullptr;
@@ -345,12 +361,35 @@ constexpr int ENGINE_BANDS = 2;
     if (_rc) return _rc;     \
   } while (0)
 
+// The context projection from its fc GEMM on (dspark.hip:2682-2705, 2487-2518; dspark.go:461-492): x_fc (the normed
+// taps of B positions, [B][n_taps * H]: the round's x16 in operand order, or row-major prompt taps) -> fc -> hidden
+// norm -> ckv -> per drafter layer k norm + RoPE, K/V rows into the drafter ring at positions State.ctx_pos + t for
+// t < State.ctx_new (of the active State).
+int enqueue_context(dspark_engine* e, const _Float16* x_fc, bool x_op, hipStream_t s) {
+  const dspark_model_desc& d = e->d;
+  const int B = e->B, H = d.hidden;
+  int nb = ENGINE_BANDS;
+  CK(gemm(e, x_fc, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s, nullptr, &nb, x_op));
+  CK(resnorm(e, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
+  const int kvrow = 2 * d.kv_heads * d.head_dim;
+  CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
+  for (int j0 = 0; j0 < d.draft_layers; j0 += QKROPE_BATCH) {  // one launch for up to 8 drafter layers
+    QkRopeBatch b = {};
+    b.n = std::min(QKROPE_BATCH, d.draft_layers - j0);
+    for (int j = 0; j < b.n; ++j)
+      b.l[j] = qk_params(e, e->DL[j0 + j], e->ckvout + (size_t)(j0 + j) * kvrow, d.draft_layers * kvrow, false, true);
+    CK(qkrope_batch_launch(b, s));
+  }
+  return 0;
+}
+
 // The round's launch sequence (see the file header).
 int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   const dspark_model_desc& d = e->d;
   const int B = e->B, H = d.hidden;
   uint64_t* vbest = e->keys;
   uint64_t* mbest = e->keys + B;
+  e->ast = e->st;
   CK(round_begin_launch(e->st, e->keys, 2 * B, e->seen, B, e->max_context + B, d.vocab, e->max_context + 2 * B, s));
   if (force_m > 0) {
     CK(force_m_launch(e->st, force_m, s));
@@ -371,18 +410,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       p.xop = e->tbs;
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
-    int nb = ENGINE_BANDS;
-    CK(gemm(e, e->x16, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s, nullptr, &nb));
-    CK(resnorm(e, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
-    const int kvrow = 2 * d.kv_heads * d.head_dim;
-    CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
-    for (int j0 = 0; j0 < d.draft_layers; j0 += QKROPE_BATCH) {  // one launch for up to 8 drafter layers
-      QkRopeBatch b = {};
-      b.n = std::min(QKROPE_BATCH, d.draft_layers - j0);
-      for (int j = 0; j < b.n; ++j)
-        b.l[j] = qk_params(e, e->DL[j0 + j], e->ckvout + (size_t)(j0 + j) * kvrow, d.draft_layers * kvrow, false, true);
-      CK(qkrope_batch_launch(b, s));
-    }
+    CK(enqueue_context(e, e->x16, true, s));
     // ---- drafter block
     CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
     int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
@@ -417,13 +445,14 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     mp.c2 = e->c2;
     mp.crop_ids = e->crop_ids;
     mp.best = mbest;
+    mp.max_drafts_dev = reinterpret_cast<const int32_t*>(e->rep + 2);
     mp.conf_bias = d.conf_bias;
     mp.conf_thr = d.conf_thr;
     mp.table = e->mtab;
     mp.c2c = e->mc2c;
     mp.s1c = e->ms1c;
     CK(markov_launch(mp, s));
-    if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, s));
+    if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, reinterpret_cast<const int32_t*>(e->rep + 2), s));
   }
   // ---- verify
   CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
@@ -457,8 +486,16 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
   CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep, false));
   CK(accept_commit_fold_launch(e->st, static_cast<const uint64_t*>(e->ws_argmax), verify_argmax_chunks(d.vocab), B, vbest,
-                               e->out_tokens, e->seen, s));
+                               e->out_tokens, e->max_context + 2 * B, e->seen, s));
   return 0;
+}
+
+int64_t kv_pages_for(const dspark_model_desc& d, int max_context) {
+  const int64_t positions = (int64_t)max_context + d.block;
+  return (positions + PAGE - 1) / PAGE + 1;
+}
+int64_t kv_pool_bytes(const dspark_model_desc& d, int max_context) {
+  return kv_pages_for(d, max_context) * d.kv_heads * PAGE * d.head_dim * 2;
 }
 
 bool desc_ok(const dspark_model_desc* d, int max_context) {
@@ -470,6 +507,9 @@ bool desc_ok(const dspark_model_desc* d, int max_context) {
   if (d->kv_heads < 1 || d->q_heads % d->kv_heads || d->q_heads * d->head_dim != d->hidden) return false;
   if (d->conv_kernel < 1 || d->conv_kernel > 8) return false;
   if (d->rope_pairs < 0 || d->rope_pairs > d->head_dim / 2) return false;
+  if (!(d->rope_base > 0.f)) return false;
+  if (d->rope_base_swa > 0.f && (d->rope_pairs_swa < 0 || d->rope_pairs_swa > d->head_dim / 2)) return false;
+  if (d->conv_slots < 0 || d->conv_slots > 65536) return false;
   if (d->draft_layers < 1 || d->block < 2 || d->block > 64 || d->max_drafts < 0 || d->max_drafts > d->block - 1) return false;
   if (d->crop_rows < 16 || d->crop_rows % 16 || d->markov_rank < 16 || d->markov_rank % 16) return false;
   if (d->crop_rows > d->vocab) return false;
@@ -479,6 +519,8 @@ bool desc_ok(const dspark_model_desc* d, int max_context) {
   if (d->ring_positions % PAGE || d->ring_positions < d->draft_window + d->block + PAGE) return false;
   if (d->mask_token < 0 || d->mask_token >= d->vocab) return false;
   if (max_context < d->block || max_context > (1 << 24)) return false;
+  // every K/V page pool below 2 GiB: the attention kernels address a pool with 32-bit byte offsets
+  if (kv_pool_bytes(*d, max_context) >= ((int64_t)1 << 31)) return false;
   int n_attn = 0;
   for (int i = 0; i < d->n_layers; ++i) {
     if (d->layer_kind[i] < 0 || d->layer_kind[i] > 2) return false;
@@ -519,7 +561,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     return w;
   };
   const int64_t positions = (int64_t)max_context + B;
-  e->kv_pages = (positions + PAGE - 1) / PAGE + 1;
+  e->kv_pages = kv_pages_for(d, max_context);
   e->ring_pages = d.ring_positions / PAGE;
   e->embed = h16("embed", (size_t)d.vocab * H);
   e->final_norm = h16("final_norm", H);
@@ -551,6 +593,13 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     if (W.kind == 0) {
       W.conv_w = h16(pre + "conv.w", (size_t)H * d.conv_kernel);
       W.conv_ring = h16("conv.L" + std::to_string(i), (size_t)CONV_RING * H);
+      const int km1 = std::max(1, d.conv_kernel - 1);
+      _Float16* cs = h16("conv_state.L" + std::to_string(i), (size_t)std::max(1, d.conv_slots) * H * km1);
+      if (e->conv.n < CONV_MAX_LAYERS) {
+        e->conv.ring[e->conv.n] = W.conv_ring;
+        e->conv.state[e->conv.n] = cs;
+        e->conv.n++;
+      }
     } else {
       W.q_norm = h16(pre + "q_norm", D);
       W.k_norm = h16(pre + "k_norm", D);
@@ -608,6 +657,18 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->ckv_w = u8("ckv.w", ckv_rows, H);
   e->ckv_s = h16("ckv.s", ckv_rows);
   e->rope = h16("rope", (size_t)(positions + 1) * D);
+  const bool own_swa = d.rope_base_swa > 0.f;
+  e->rope_swa = own_swa ? h16("rope_swa", (size_t)(positions + 1) * D) : e->rope;
+  e->rot_swa = own_swa ? d.rope_pairs_swa : d.rope_pairs;
+  e->conv.H = H;
+  e->conv.km1 = d.conv_kernel - 1;
+  e->conv.slots = std::max(1, d.conv_slots);
+  // prompt projection: captured taps of up to draft_window positions (+ one block of padding rows the last chunk's
+  // GEMM reads), one State per chunk of B positions
+  e->tap_rows = (d.draft_window + B - 1) / B * B + B;
+  e->tapx = h16("tap_x", (size_t)e->tap_rows * d.n_taps * H);
+  e->seed_chunks = e->tap_rows / B;
+  e->seed_st = static_cast<dspark_state*>(e->alloc("", (size_t)e->seed_chunks * sizeof(dspark_state), &err));
   // request state and activations
   e->st = static_cast<dspark_state*>(e->alloc("state", sizeof(dspark_state), &err));
   e->seen = static_cast<uint32_t*>(e->alloc("seen", (size_t)(d.vocab + 31) / 32 * 4, &err));
@@ -643,6 +704,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   for (int K : Ks)
     for (int N : Ns)
       for (int wpg_req : {0, 3}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req, true));
+  gws = std::max(gws, gemm_ws_bytes(B, H, d.n_taps * H, 0, false));  // the prompt projection's fc (row-major taps)
   e->ws_gemm_bytes = gws + 256;
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
   const int G = QH / KVH;
@@ -655,23 +717,21 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     delete e;
     return err;
   }
-  // drafter ring table (logical page -> ring page) and the RoPE table (cos | sin per position, fp32 frequencies
-  // rounded to fp16, as internal/model/engine.go:428-461 builds it)
+  // drafter ring table (logical page -> ring page) and the RoPE tables (dspark_rope_table)
   std::vector<int32_t> bt(bt_entries);
   for (int64_t i = 0; i < bt_entries; ++i) bt[i] = (int32_t)(i % e->ring_pages);
-  std::vector<_Float16> rope((size_t)(positions + 1) * D);
-  std::vector<float> inv(D / 2, 0.f);
-  for (int i = 0; i < d.rope_pairs; ++i) inv[i] = (float)(1.0 / std::pow((double)d.rope_base, (double)(2.f * i / D)));
-  for (int64_t pos = 0; pos <= positions; ++pos)
-    for (int i = 0; i < D / 2; ++i) {
-      const double f = (double)((float)pos * inv[i]);
-      rope[(size_t)pos * D + i] = (_Float16)(float)std::cos(f);
-      rope[(size_t)pos * D + D / 2 + i] = (_Float16)(float)std::sin(f);
-    }
-  const float rep[4] = {1.f, 1.f, 0.f, 0.f};
+  std::vector<uint16_t> rope((size_t)(positions + 1) * D), rope_swa;
+  dspark_rope_table(d.rope_base, d.rope_pairs, D, (int32_t)(positions + 1), rope.data());
+  if (own_swa) {
+    rope_swa.resize(rope.size());
+    dspark_rope_table(d.rope_base_swa, d.rope_pairs_swa, D, (int32_t)(positions + 1), rope_swa.data());
+  }
+  e->host_lp[0] = e->host_lp[1] = 1.f;
+  std::memcpy(&e->host_lp[2], &d.max_drafts, 4);
   if (hipMemcpy(e->ring_bt, bt.data(), bt.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(e->rope, rope.data(), rope.size() * 2, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(e->rep, rep, sizeof(rep), hipMemcpyHostToDevice) != hipSuccess) {
+      (own_swa && hipMemcpy(e->rope_swa, rope_swa.data(), rope_swa.size() * 2, hipMemcpyHostToDevice) != hipSuccess) ||
+      hipMemcpy(e->rep, e->host_lp, sizeof(e->host_lp), hipMemcpyHostToDevice) != hipSuccess) {
     delete e;
     return DSPARK_ENOSPACE;
   }
@@ -831,15 +891,90 @@ int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspar
   return (int)hipGraphLaunch(it->second, s);
 }
 
+int dspark_engine_init_seen(dspark_engine* e, const int32_t* tokens, int32_t n, float rep, dspark_stream_t stream) {
+  if (!e || n < 0 || (n > 0 && !tokens)) return DSPARK_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int V = e->d.vocab;
+  e->host_seen.assign((size_t)(V + 31) / 32, 0u);
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t t = tokens[i];
+    if (t >= 0 && t < V) e->host_seen[t >> 5] |= 1u << (t & 31);
+  }
+  if (rep == 0.f) rep = 1.f;
+  e->host_lp[0] = rep;
+  e->host_lp[1] = 1.f / rep;
+  if (hipMemcpyAsync(e->seen, e->host_seen.data(), e->host_seen.size() * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(e->rep, e->host_lp, 8, hipMemcpyHostToDevice, s) != hipSuccess)
+    return DSPARK_EINVAL;
+  return hipStreamSynchronize(s) == hipSuccess ? 0 : DSPARK_EINVAL;  // the host buffers are reused by the next call
+}
+
+int dspark_engine_capture_tap(dspark_engine* e, int32_t slot, const void* h, int64_t row_stride, int32_t context,
+                              int32_t tokens, int32_t tap_from, dspark_stream_t stream) {
+  if (!e || !h || slot < 0 || slot >= e->d.n_taps || context < 0 || tokens < 0 || tap_from < 0) return DSPARK_EINVAL;
+  const int H = e->d.hidden;
+  if (row_stride < H || row_stride % 4 || reinterpret_cast<uintptr_t>(h) % 8) return DSPARK_EINVAL;
+  const int first = std::max(context, tap_from);
+  const int rows = context + tokens - first;
+  if (rows <= 0) return 0;
+  if (first - tap_from + rows > e->d.draft_window) return DSPARK_EINVAL;  // beyond the capture buffer
+  e->tap_from = tap_from;
+  const _Float16* src = static_cast<const _Float16*>(h) + (size_t)(first - context) * row_stride;
+  _Float16* dst = e->tapx + (size_t)(first - tap_from) * e->d.n_taps * H + (size_t)slot * H;
+  return rms_rows_launch(src, row_stride, e->tap_norms + (size_t)slot * H, e->d.eps, H, dst, (int64_t)e->d.n_taps * H,
+                         rows, reinterpret_cast<hipStream_t>(stream));
+}
+
+int dspark_engine_project_prompt(dspark_engine* e, int32_t first, int32_t end, dspark_stream_t stream) {
+  if (!e || first < 0 || end < first || end - first > e->d.draft_window || end > e->max_context) return DSPARK_EINVAL;
+  if (end == first) return 0;
+  if (first != e->tap_from) return DSPARK_EINVAL;  // the capture buffer holds positions from tap_from
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (e->mtab_dirty || e->tiles_dirty) {
+    const int rc = prepare(e, s, false);
+    if (rc) return rc;
+  }
+  const int B = e->B, nch = (end - first + B - 1) / B;
+  if (nch > e->seed_chunks) return DSPARK_EINVAL;
+  e->host_seed.assign(nch, dspark_state{});
+  for (int c = 0; c < nch; ++c) {
+    dspark_state& t = e->host_seed[c];
+    t.run = 1;
+    t.ctx_pos = first + c * B;
+    t.ctx_new = std::min(B, end - t.ctx_pos);
+  }
+  if (hipMemcpyAsync(e->seed_st, e->host_seed.data(), nch * sizeof(dspark_state), hipMemcpyHostToDevice, s) != hipSuccess)
+    return DSPARK_EINVAL;
+  const size_t row = (size_t)e->d.n_taps * e->d.hidden;
+  int rc = 0;
+  for (int c = 0; c < nch && !rc; ++c) {
+    e->ast = e->seed_st + c;
+    rc = enqueue_context(e, e->tapx + (size_t)c * B * row, false, s);
+  }
+  e->ast = e->st;
+  if (rc) return rc;
+  return hipStreamSynchronize(s) == hipSuccess ? 0 : DSPARK_EINVAL;  // host_seed stays in use until the copy is done
+}
+
+int dspark_engine_conv_copy(dspark_engine* e, int32_t src, int32_t dst, dspark_stream_t stream) {
+  if (!e || src < 0 || dst < 0 || src >= e->conv.slots || dst >= e->conv.slots) return DSPARK_EINVAL;
+  if (src == dst) return 0;
+  return conv_copy_launch(e->conv, src, dst, reinterpret_cast<hipStream_t>(stream));
+}
+
 int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t* out_tokens, int32_t max_out,
                          dspark_launch_result* res, dspark_stream_t stream) {
-  if (!e || !a || !res || a->a < 0 || a->rounds < 1 || a->force_m < -1 || a->force_m > e->B) return DSPARK_EINVAL;
+  if (!e || !a || !res || a->a < 0 || a->a >= e->max_context || a->rounds < 1 || a->force_m < -1 || a->force_m > e->B)
+    return DSPARK_EINVAL;
   if (a->anchor < 0 || a->anchor >= e->d.vocab || a->budget < 1) return DSPARK_EINVAL;
+  if (a->conv_slot < -1 || a->conv_slot >= e->conv.slots || a->ckpt_slot < -1 || a->ckpt_slot >= e->conv.slots)
+    return DSPARK_EINVAL;
+  if (a->ckpt_slot >= 0 && a->conv_slot < 0) return DSPARK_EINVAL;  // a checkpoint needs the conv state's slots
+  if (a->ctx_new < 0 || a->ctx_new > e->B || a->ctx_lo < 0) return DSPARK_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int block_tokens = 32;  // the prefix cache's block (internal/model/engine.go:30)
   const int stop = std::min((a->a / block_tokens + 1) * block_tokens, e->max_context);
   const int limit = std::min(stop + e->B, e->max_context);
-  if (a->a + e->B > e->max_context) return DSPARK_EINVAL;
   dspark_state& st = e->host_st;
   st = dspark_state{};
   st.a = a->a;
@@ -853,20 +988,28 @@ int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t*
   st.ctx_lo = a->ctx_lo;
   st.run = 1;
   st.force_m = a->force_m;
+  st.miss = a->miss;
+  st.skip = a->skip;
   st.skip_rounds = 1;
   st.stop_at = stop;
-  st.ckpt_slot = -1;
+  st.ckpt_slot = a->ckpt_slot;
   std::memcpy(st.tokens, a->tokens, sizeof(st.tokens));
   st.tokens[0] = a->anchor;
   const float rep = a->rep == 0.f ? 1.f : a->rep;
-  e->host_rep[0] = rep;
-  e->host_rep[1] = 1.f / rep;
+  const int32_t md = a->max_drafts > 0 ? std::min(a->max_drafts, e->d.max_drafts) : e->d.max_drafts;
+  e->host_lp[0] = rep;
+  e->host_lp[1] = 1.f / rep;
+  std::memcpy(&e->host_lp[2], &md, 4);
   if (hipMemcpyAsync(e->st, &st, sizeof(st), hipMemcpyHostToDevice, s) != hipSuccess) return DSPARK_EINVAL;
-  if (hipMemcpyAsync(e->rep, e->host_rep, sizeof(e->host_rep), hipMemcpyHostToDevice, s) != hipSuccess)
+  if (hipMemcpyAsync(e->rep, e->host_lp, sizeof(e->host_lp), hipMemcpyHostToDevice, s) != hipSuccess)
     return DSPARK_EINVAL;
-  for (int r = 0; r < a->rounds; ++r) {
-    const int rc = dspark_engine_round(e, a->force_m, a->a, stream);
-    if (rc) return rc;
+  int rc = 0;
+  if (a->conv_slot >= 0) rc = conv_load_launch(e->conv, e->st, a->conv_slot, s);
+  for (int r = 0; r < a->rounds && !rc; ++r) rc = dspark_engine_round(e, a->force_m, a->a, stream);
+  if (!rc && a->conv_slot >= 0) rc = conv_store_launch(e->conv, e->st, a->conv_slot, s);
+  if (rc) {
+    (void)hipStreamSynchronize(s);  // the host copies above stay in use until the stream has consumed them
+    return rc;
   }
   if (hipMemcpyAsync(&res->state, e->st, sizeof(dspark_state), hipMemcpyDeviceToHost, s) != hipSuccess)
     return DSPARK_EINVAL;
@@ -883,6 +1026,7 @@ int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t*
   res->accepted = res->state.accepted;
   res->verified = res->state.verified;
   res->boundary = stop;
+  res->ckpt_written = (a->ckpt_slot >= 0 && res->state.a >= stop) ? 1 : 0;
   return 0;
 }
 

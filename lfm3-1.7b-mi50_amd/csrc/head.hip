@@ -131,8 +131,8 @@ __device__ __forceinline__ int key_token(uint64_t k) { return (int)(0xffffffffu 
 // part (optional): the verify argmax's partial keys [mfold][nchunks], folded here into best[t] first (every thread
 // loads its share at once; u64 max in LDS, order-free) instead of by a separate fold_keys launch.
 __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uint64_t* best, int m, int skip_now,
-                                                           int32_t* out_tokens, uint32_t* seen, const uint64_t* part,
-                                                           int nchunks, int mfold) {
+                                                           int32_t* out_tokens, int out_cap, uint32_t* seen,
+                                                           const uint64_t* part, int nchunks, int mfold) {
   if (st->run == 0) return;
   if (part) {
     __shared__ unsigned long long sb[64];
@@ -165,6 +165,10 @@ __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uin
   const int bonus = key_token(best[acc]);
   const int aa = st->a;
   int count = st->count;
+  if (count < 0 || count + commit > out_cap) {  // no room for the commit: write nothing and stop
+    st->run = 0;
+    return;
+  }
   for (int i = 1; i <= acc; ++i) out_tokens[count++] = st->tokens[i];
   out_tokens[count++] = bonus;
   for (int i = 1; i <= acc; ++i) {
@@ -226,20 +230,21 @@ int verify_argmax_launch(const void* logits, int f16, int M, int V, const uint32
   return (int)hipGetLastError();
 }
 
-int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, uint32_t* seen,
-                         hipStream_t s) {
+int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, int out_cap,
+                         uint32_t* seen, hipStream_t s) {
   // best is only read when no partial keys are given
   hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, const_cast<uint64_t*>(best), m, skip_now,
-                     out_tokens, seen, (const uint64_t*)nullptr, 0, 0);
+                     out_tokens, out_cap, seen, (const uint64_t*)nullptr, 0, 0);
   return (int)hipGetLastError();
 }
 
 int verify_argmax_chunks(int V) { return (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
 
 int accept_commit_fold_launch(dspark_state* st, const uint64_t* part, int nchunks, int M, uint64_t* best,
-                              int32_t* out_tokens, uint32_t* seen, hipStream_t s) {
+                              int32_t* out_tokens, int out_cap, uint32_t* seen, hipStream_t s) {
   if (M < 1 || M > 64 || nchunks < 1) return DSPARK_EINVAL;
-  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, 0, 0, out_tokens, seen, part, nchunks, M);
+  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, 0, 0, out_tokens, out_cap, seen, part,
+                     nchunks, M);
   return (int)hipGetLastError();
 }
 

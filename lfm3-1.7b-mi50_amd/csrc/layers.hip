@@ -13,6 +13,13 @@ namespace dspark {
 
 __device__ __forceinline__ bool stopped(const dspark_state* st) { return st && ldg(&st->run) == 0; }
 
+// Drafts a round may propose (dspark.hip:2633-2640): the model's (or the launch's, when md_dev is set) draft cap, the
+// block, the context limit and the budget.
+__device__ __forceinline__ int draft_cap(const dspark_state* st, int max_drafts, const int32_t* md_dev, int block) {
+  const int md = md_dev ? min(max_drafts, ldg(md_dev)) : max_drafts;
+  return min(min(md, block - 1), min(st->limit - st->a, st->budget - st->count) - 1);
+}
+
 // ---------------------------------------------------------------- embedding
 // h[t][:] = embed[token(t)][:] (fp16 -> fp32). mode 0: token(t) = st->tokens[t]; mode 1 (drafter block):
 // t == 0 ? st->anchor : mask_token. Tokens outside the vocabulary read row 0.
@@ -264,8 +271,7 @@ __global__ __launch_bounds__(256) void markov_kernel(MarkovParams p, int j) {
   dspark_state* st = p.st;
   if (stopped(st)) return;
   if (ldg(&st->M) != 0) return;  // drafting already stopped (M is set by the stop or the finalize)
-  const int a = st->a;
-  const int cap = min(min(p.max_drafts, p.block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  const int cap = draft_cap(st, p.max_drafts, p.max_drafts_dev, p.block);
   if (j >= cap) return;
   int prev;
   if (j == 0) {
@@ -319,8 +325,7 @@ __global__ void markov_finalize(MarkovParams p) {
   if (stopped(st) || threadIdx.x != 0) return;
   st->tokens[0] = st->anchor;
   if (st->M != 0) return;  // stopped by confidence: tokens and M already written
-  const int a = st->a;
-  const int cap = min(min(p.max_drafts, p.block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  const int cap = draft_cap(st, p.max_drafts, p.max_drafts_dev, p.block);
   const int drafts = max(cap, 0);
   if (drafts >= 1) {
     const uint64_t key = p.best[drafts - 1];
@@ -411,8 +416,7 @@ __global__ __launch_bounds__(1024) void markov_chain_kernel(MarkovParams p) {
 #pragma unroll
   for (int i = 0; i < CHAIN_ROWS / 4; ++i)
     s2[i] = live ? ldg(reinterpret_cast<const f32x4*>(p.w2s + r0) + i) : f32x4{0, 0, 0, 0};
-  const int a = st->a;
-  const int cap = min(min(p.max_drafts, p.block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  const int cap = draft_cap(st, p.max_drafts, p.max_drafts_dev, p.block);
   int M = st->M;  // nonzero when step 0's confidence test stopped drafting
   uint64_t key = 0;
   if (M == 0 && cap >= 1) key = __hip_atomic_load(p.best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -498,10 +502,11 @@ __global__ void force_m_kernel(dspark_state* st, int m) {
 // Planted drafts (benchmarks of a set acceptance rate on random-init models): after the drafter has run, its drafts
 // are replaced by plant[a + 1 .. a + M - 1], with M = 1 + the drafter's cap on drafts this round (the same cap
 // markov_kernel applies, so limit and budget still bound the round).
-__global__ void plant_kernel(dspark_state* st, const int32_t* plant, int block, int max_drafts) {
+__global__ void plant_kernel(dspark_state* st, const int32_t* plant, int block, int max_drafts,
+                             const int32_t* max_drafts_dev) {
   if (stopped(st) || threadIdx.x != 0) return;
   const int a = st->a;
-  const int cap = min(min(max_drafts, block - 1), min(st->limit - a, st->budget - st->count) - 1);
+  const int cap = draft_cap(st, max_drafts, max_drafts_dev, block);
   const int drafts = max(cap, 0);
   st->tokens[0] = st->anchor;
   for (int j = 1; j <= drafts; ++j) st->tokens[j] = plant[a + j];
@@ -576,8 +581,9 @@ int round_begin_launch(dspark_state* st, uint64_t* keys, int nkeys, uint32_t* se
   hipLaunchKernelGGL(round_begin_kernel, dim3(1), dim3(256), 0, s, st, keys, nkeys, seen, block, max_pos, vocab, out_cap);
   return (int)hipGetLastError();
 }
-int plant_launch(dspark_state* st, const int32_t* plant, int block, int max_drafts, hipStream_t s) {
-  hipLaunchKernelGGL(plant_kernel, dim3(1), dim3(64), 0, s, st, plant, block, max_drafts);
+int plant_launch(dspark_state* st, const int32_t* plant, int block, int max_drafts, const int32_t* max_drafts_dev,
+                 hipStream_t s) {
+  hipLaunchKernelGGL(plant_kernel, dim3(1), dim3(64), 0, s, st, plant, block, max_drafts, max_drafts_dev);
   return (int)hipGetLastError();
 }
 int force_m_launch(dspark_state* st, int m, hipStream_t s) {

@@ -52,14 +52,16 @@ _SIGS = {
     "dspark_verify_attention_splits": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_verify_attention_combine": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_kv_write": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_void_p]),
     "dspark_verify_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
     "dspark_verify_argmax": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "dspark_accept_commit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
-                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+                                            ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]),
     "dspark_gemm_i8_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]),
     "dspark_gemm_i8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                       ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
@@ -138,8 +140,8 @@ def kv_write(k, v, k_pages, v_pages, pos0, block_table=None, stream=None):
     KVH, D = k_pages.shape[1], k_pages.shape[3]
     row = k.stride(0)
     assert v.stride(0) == row and k.dtype == v.dtype == _torch().float16
-    rc = lib().dspark_kv_write(ptr(k), ptr(v), row, ptr(k_pages), ptr(v_pages), ptr(block_table), KVH, D, pos0, n,
-                               stream_handle(stream))
+    rc = lib().dspark_kv_write(ptr(k), ptr(v), row, ptr(k_pages), ptr(v_pages), ptr(block_table), k_pages.shape[0], KVH,
+                               D, pos0, n, stream_handle(stream))
     check(rc, "dspark_kv_write")
 
 
@@ -258,7 +260,8 @@ def verify_argmax(logits, seen, st, rep=1.0, inv_rep=None, best=None, workspace=
 
 
 def accept_commit(st, best, M, out_tokens, seen, skip_now=0, stream=None):
-    rc = lib().dspark_accept_commit(ptr(st), ptr(best), M, skip_now, ptr(out_tokens), ptr(seen), stream_handle(stream))
+    rc = lib().dspark_accept_commit(ptr(st), ptr(best), M, skip_now, ptr(out_tokens), out_tokens.numel(), ptr(seen),
+                                    stream_handle(stream))
     check(rc, "dspark_accept_commit")
 
 
@@ -314,19 +317,22 @@ class ModelDesc(ctypes.Structure):
                 ("block", ctypes.c_int32), ("max_drafts", ctypes.c_int32), ("crop_rows", ctypes.c_int32),
                 ("markov_rank", ctypes.c_int32), ("n_taps", ctypes.c_int32), ("tap_layer", ctypes.c_int32 * MAX_TAPS),
                 ("draft_window", ctypes.c_int32), ("ring_positions", ctypes.c_int32), ("mask_token", ctypes.c_int32),
-                ("conf_bias", ctypes.c_float), ("conf_thr", ctypes.c_float), ("eps", ctypes.c_float)]
+                ("conf_bias", ctypes.c_float), ("conf_thr", ctypes.c_float), ("eps", ctypes.c_float),
+                ("rope_base_swa", ctypes.c_float), ("rope_pairs_swa", ctypes.c_int32), ("conv_slots", ctypes.c_int32)]
 
 
 class LaunchArgs(ctypes.Structure):
     _fields_ = [("a", ctypes.c_int32), ("anchor", ctypes.c_int32), ("budget", ctypes.c_int32), ("eos", ctypes.c_int32),
                 ("rep", ctypes.c_float), ("rounds", ctypes.c_int32), ("ctx_new", ctypes.c_int32),
                 ("ctx_pos", ctypes.c_int32), ("ctx_lo", ctypes.c_int32), ("force_m", ctypes.c_int32),
-                ("tokens", ctypes.c_int32 * MT_MAX)]
+                ("tokens", ctypes.c_int32 * MT_MAX), ("max_drafts", ctypes.c_int32), ("miss", ctypes.c_int32),
+                ("skip", ctypes.c_int32), ("conv_slot", ctypes.c_int32), ("ckpt_slot", ctypes.c_int32)]
 
 
 class LaunchResult(ctypes.Structure):
     _fields_ = [("count", ctypes.c_int32), ("rounds", ctypes.c_int32), ("accepted", ctypes.c_int32),
-                ("verified", ctypes.c_int32), ("boundary", ctypes.c_int32), ("state", State)]
+                ("verified", ctypes.c_int32), ("boundary", ctypes.c_int32), ("ckpt_written", ctypes.c_int32),
+                ("state", State)]
 
 
 _SIGS.update({
@@ -341,11 +347,27 @@ _SIGS.update({
     "dspark_engine_round": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_engine_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchArgs), ctypes.c_void_p, ctypes.c_int32,
                                             ctypes.POINTER(LaunchResult), ctypes.c_void_p]),
+    "dspark_engine_init_seen": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_float,
+                                               ctypes.c_void_p]),
+    "dspark_engine_capture_tap": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64,
+                                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_engine_project_prompt": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_engine_conv_copy": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
 })
+
+
+def rope_table(base, pairs, head_dim, positions):
+    """The RoPE table the engine builds (uint16 fp16 bits [positions][head_dim]: cos | sin), host code of the library."""
+    import numpy as np
+    out = np.empty((positions, head_dim), np.uint16)
+    check(lib().dspark_rope_table(base, pairs, head_dim, positions, out.ctypes.data_as(ctypes.c_void_p)),
+          "dspark_rope_table")
+    return out
 
 
 def model_desc(**kw):
     d = ModelDesc()
+    d.conv_slots = 1
     for k, v in kw.items():
         if k in ("layer_kind", "tap_layer"):
             arr = getattr(d, k)
@@ -373,11 +395,14 @@ def ref_desc(block=9, max_drafts=7, vocab=128000):
     sliding-window-256 GQA attention layers, 16/4/128), hidden 2048, gated FFN 7680, vocab 128000; 3 attention-only
     drafter layers (FFN 7680) over 9-token blocks, 16384-row cropped head, Markov rank 256, taps {2, 6, 12, 18, 23},
     drafter window 2048, ring 4096. max_drafts follows the reference policy (7, or 3 from position 57344,
-    generate.go:136). Storage formats stay this build's: fp16 KV pages (the reference keeps int8 K/V records, half
-    the KV bytes) and int8 weights with per-row fp16 scales."""
+    generate.go:136). RoPE per layer kind as the reference builds it (engine.go:333-338): full attention and the
+    drafter at base 1e6 with 32 rotating pairs, sliding layers at base 1e4 with 64. Storage formats stay this build's:
+    fp16 KV pages (the reference keeps int8 K/V records, half the KV bytes) and int8 weights with per-row fp16
+    scales."""
     kinds = [0, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0]
     return model_desc(hidden=2048, ffn=7680, vocab=vocab, n_layers=24, layer_kind=kinds, q_heads=16, kv_heads=4,
-                      head_dim=128, conv_kernel=7, window=256, rope_base=1e6, rope_pairs=64, draft_layers=3,
+                      head_dim=128, conv_kernel=7, window=256, rope_base=1e6, rope_pairs=32, rope_base_swa=1e4,
+                      rope_pairs_swa=64, draft_layers=3,
                       draft_ffn=7680, block=block, max_drafts=max_drafts, crop_rows=16384, markov_rank=256, n_taps=5,
                       tap_layer=[2, 6, 12, 18, 23], draft_window=2048, ring_positions=4096, mask_token=vocab - 1,
                       conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
@@ -424,10 +449,12 @@ class Engine:
         check(lib().dspark_engine_round(self.h, force_m, plan_a, stream_handle(stream)), "dspark_engine_round")
 
     def launch(self, a, anchor, budget=512, eos=-1, rep=1.0, rounds=32, ctx_new=0, ctx_pos=0, ctx_lo=0, force_m=0,
-               tokens=(), max_out=1024, stream=None):
+               tokens=(), max_out=1024, max_drafts=0, miss=0, skip=0, conv_slot=-1, ckpt_slot=-1, stream=None):
+        """draftLaunch (dspark_engine_launch): returns (emitted tokens, LaunchResult)."""
         args = LaunchArgs()
         args.a, args.anchor, args.budget, args.eos, args.rep, args.rounds = a, anchor, budget, eos, rep, rounds
         args.ctx_new, args.ctx_pos, args.ctx_lo, args.force_m = ctx_new, ctx_pos, ctx_lo, force_m
+        args.max_drafts, args.miss, args.skip, args.conv_slot, args.ckpt_slot = max_drafts, miss, skip, conv_slot, ckpt_slot
         for i, t in enumerate(tokens):
             args.tokens[i] = int(t)
         out = (ctypes.c_int32 * max_out)()
@@ -435,6 +462,25 @@ class Engine:
         check(lib().dspark_engine_launch(self.h, ctypes.byref(args), out, max_out, ctypes.byref(res),
                                          stream_handle(stream)), "dspark_engine_launch")
         return list(out[:res.count]), res
+
+    def init_seen(self, tokens, rep=1.0, stream=None):
+        """InitSeen (dspark_engine_init_seen): the penalty mask = exactly `tokens`."""
+        arr = (ctypes.c_int32 * max(1, len(tokens)))(*[int(t) for t in tokens])
+        check(lib().dspark_engine_init_seen(self.h, arr, len(tokens), rep, stream_handle(stream)),
+              "dspark_engine_init_seen")
+
+    def capture_tap(self, slot, h, context, tap_from, stream=None):
+        """captureTap (dspark_engine_capture_tap): h = fp16 device tensor [tokens][>= hidden] of positions
+        context .. context + tokens - 1."""
+        check(lib().dspark_engine_capture_tap(self.h, slot, ptr(h), h.stride(0), context, h.shape[0], tap_from,
+                                              stream_handle(stream)), "dspark_engine_capture_tap")
+
+    def project_prompt(self, first, end, stream=None):
+        check(lib().dspark_engine_project_prompt(self.h, first, end, stream_handle(stream)),
+              "dspark_engine_project_prompt")
+
+    def conv_copy(self, src, dst, stream=None):
+        check(lib().dspark_engine_conv_copy(self.h, src, dst, stream_handle(stream)), "dspark_engine_conv_copy")
 
     # host <-> device copies of named tensors (plumbing for tests, loaders and benchmarks)
     def upload(self, name, array):

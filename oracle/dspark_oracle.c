@@ -198,6 +198,72 @@ void orc_verify_attention(const uint16_t* q, const uint16_t* k, const uint16_t* 
   free(acc);
 }
 
+/* The fp64 verify attention above with its (token, query head) rows dealt to threads (each row is computed exactly
+ * as orc_verify_attention computes it, so the outputs are the same bits); for long contexts. */
+typedef struct {
+  const uint16_t *q, *k, *v;
+  int M, QH, KVH, D, a, start, window, causal, nthreads, tid;
+  double* out;
+} attn64_job;
+
+static void* attn64_worker(void* arg) {
+  const attn64_job* j = (const attn64_job*)arg;
+  const int D = j->D;
+  double m, l;
+  double* acc = (double*)malloc(sizeof(double) * D);
+  for (int row = j->tid; row < j->M * j->QH; row += j->nthreads) {
+    const int t = row / j->QH, qh = row % j->QH;
+    const int G = j->QH / j->KVH;
+    const uint16_t* qrow = j->q + (size_t)row * D;
+    /* orc_attn_partial's arithmetic for this one row over all keys, then orc_attn_merge of the single partial */
+    const double scale = 1.0 / sqrt((double)D), log2e = 1.4426950408889634;
+    const int h = qh / G, T = j->a + j->M;
+    double mx = -INFINITY;
+    double* s = (double*)malloc(sizeof(double) * (size_t)T);
+    for (int kp = 0; kp < T; ++kp) {
+      double dot = -INFINITY;
+      if (key_valid(kp, t, j->M, j->a, j->start, j->window, j->causal)) {
+        const uint16_t* kr = j->k + ((size_t)kp * j->KVH + h) * D;
+        dot = 0.0;
+        for (int d = 0; d < D; ++d) dot += h2d(qrow[d]) * h2d(kr[d]);
+        dot *= scale * log2e;
+        if (dot > mx) mx = dot;
+      }
+      s[kp] = dot;
+    }
+    double sum = 0.0;
+    for (int d = 0; d < D; ++d) acc[d] = 0.0;
+    if (mx != -INFINITY)
+      for (int kp = 0; kp < T; ++kp) {
+        if (s[kp] == -INFINITY) continue;
+        const double p = exp2(s[kp] - mx);
+        sum += p;
+        const uint16_t* vr = j->v + ((size_t)kp * j->KVH + h) * D;
+        for (int d = 0; d < D; ++d) acc[d] += p * h2d(vr[d]);
+      }
+    free(s);
+    m = mx;
+    l = sum;
+    orc_attn_merge(1, 1, D, &m, &l, acc, j->out + (size_t)row * D);
+  }
+  free(acc);
+  return NULL;
+}
+
+void orc_verify_attention_mt(const uint16_t* q, const uint16_t* k, const uint16_t* v, int M, int QH, int KVH, int D,
+                             int a, int start, int window, int causal, double* out, int threads) {
+  if (threads < 1) threads = 1;
+  if (threads > 256) threads = 256;
+  pthread_t th[256];
+  attn64_job jobs[256];
+  for (int i = 0; i < threads; ++i) {
+    attn64_job j = {q, k, v, M, QH, KVH, D, a, start, window, causal, threads, i, out};
+    jobs[i] = j;
+    pthread_create(&th[i], NULL, attn64_worker, &jobs[i]);
+  }
+  for (int i = 0; i < threads; ++i) pthread_join(th[i], NULL);
+}
+
 /* fp32 multi-threaded restatement (same masks) used as the timed CPU baseline. */
 typedef struct {
   const uint16_t *q, *k, *v;

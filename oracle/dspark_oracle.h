@@ -56,6 +56,8 @@ void orc_attn_partial(const uint16_t* q, const uint16_t* k, const uint16_t* v, i
 /* Merge S partials [S][M*QH] (+ acc [S][M*QH][D]) -> out [M*QH][D] (dspark.hip:2148-2183; 0 if total weight 0). */
 void orc_attn_merge(int S, int rows, int D, const double* m, const double* l, const double* acc, double* out);
 /* Multi-threaded fp32 variant for the CPU baseline (same masks; threads over (kv head, token)). */
+void orc_verify_attention_mt(const uint16_t* q, const uint16_t* k, const uint16_t* v, int M, int QH, int KVH, int D,
+                             int a, int start, int window, int causal, double* out, int threads);
 void orc_verify_attention_f32_mt(const uint16_t* q, const uint16_t* k, const uint16_t* v, int M, int QH, int KVH, int D,
                                  int a, int start, int window, int causal, float* out, int threads);
 

@@ -58,6 +58,7 @@ def lib():
             "orc_attn_partial": (None, [c_u16p, c_u16p, c_u16p] + [ctypes.c_int] * 10 + [c_f64p, c_f64p, c_f64p]),
             "orc_attn_merge": (None, [ctypes.c_int] * 3 + [c_f64p, c_f64p, c_f64p, c_f64p]),
             "orc_verify_attention_f32_mt": (None, [c_u16p, c_u16p, c_u16p] + [ctypes.c_int] * 8 + [c_f32p, ctypes.c_int]),
+            "orc_verify_attention_mt": (None, [c_u16p, c_u16p, c_u16p] + [ctypes.c_int] * 8 + [c_f64p, ctypes.c_int]),
             "orc_argmax_key": (ctypes.c_uint64, [ctypes.c_float, ctypes.c_uint32]),
             "orc_key_index": (ctypes.c_uint32, [ctypes.c_uint64]),
             "orc_verify_argmax": (None, [c_f32p, ctypes.c_int, ctypes.c_int, c_u32p, c_i32p, ctypes.c_float,
@@ -165,6 +166,19 @@ def attn_merge(ms, ls, accs):
     acc = np.ascontiguousarray(np.stack(accs))
     out = np.empty((rows, D))
     lib().orc_attn_merge(S, rows, D, _p(m, c_f64p), _p(l, c_f64p), _p(acc, c_f64p), _p(out, c_f64p))
+    return out
+
+
+def verify_attention_mt(q, k, v, a, start=0, window=0, causal=True, threads=8):
+    """verify_attention (fp64, the same bits) with its rows spread over threads, for long contexts."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    M, QH, D = q.shape
+    KVH = k.shape[1]
+    assert k.shape[0] >= a + M and k.shape == v.shape
+    out = np.empty((M, QH, D), dtype=np.float64)
+    lib().orc_verify_attention_mt(_p(q, c_u16p), _p(np.ascontiguousarray(k, dtype=np.uint16), c_u16p),
+                                  _p(np.ascontiguousarray(v, dtype=np.uint16), c_u16p), M, QH, KVH, D, a, start, window,
+                                  int(causal), _p(out, c_f64p), threads)
     return out
 
 

@@ -95,6 +95,8 @@ def attn_fp16(q16, K, V, a, M, start, window, causal):
 
 
 def context_projection(W, C, st, rope):
+    """The round's context projection (sec 0): the taps of the last round's committed positions ctx_pos ..
+    ctx_pos + ctx_new - 1 (C.taps, the residual stream after each tapped layer) into the drafter rings."""
     d = W.d
     H, B = d.hidden, d.block
     n_new, pos0 = st["ctx_new"], st["ctx_pos"]
@@ -102,7 +104,29 @@ def context_projection(W, C, st, rope):
         return
     tn = W.f16("tap_norms", (d.n_taps, H))
     xs = [resnorm(C.taps[b][:B], None, None, tn[b], 0, d.eps)[1] for b in range(d.n_taps)]
-    x = np.concatenate(xs, axis=1)                         # [B][taps*H]
+    project_rows(W, C, np.concatenate(xs, axis=1)[:n_new], pos0, rope)
+
+
+def tap_rows(W, h16, slot):
+    """captureTap (dspark.go:439-459 -> ops.hip:89-101 rms_norm): fp16(h / rms(h) * tap_norms[slot]) per row."""
+    d = W.d
+    w = W.f16("tap_norms", (d.n_taps, d.hidden))[slot]
+    return resnorm(np.asarray(h16, np.float64), None, None, w, 0, d.eps)[1]
+
+
+def project_prompt(W, C, h16_taps, first, rope):
+    """captureTap + projectPrompt (dspark.go:439-492): h16_taps [n_taps][n][H] (fp16-valued hidden states after each
+    tapped layer for positions first .. first + n - 1) -> drafter ring rows of those positions."""
+    x = np.concatenate([tap_rows(W, h16_taps[b], b) for b in range(W.d.n_taps)], axis=1)
+    project_rows(W, C, x, first, rope)
+
+
+def project_rows(W, C, x, pos0, rope):
+    """x [n][n_taps * H] (normed taps, fp16-valued) -> fc -> hidden norm -> ckv -> per drafter layer k norm + RoPE
+    (the drafter's table) and v -> ring rows pos0 .. pos0 + n - 1 (dspark.hip:2682-2705, 2487-2518)."""
+    d = W.d
+    H = d.hidden
+    n_new = x.shape[0]
     fw, fs = W.gemm_w("fc", H, d.n_taps * H)
     c = gemm(x, fw, fs)
     _, x2 = resnorm(None, c, None, W.f16("hidden_norm"), 0, d.eps)
@@ -195,8 +219,10 @@ def markov(W, st, base):
     return toks, len(toks), zs
 
 
-def verify(W, C, st, tokens, rope):
-    """Logits [B][V] (fp64) of the verify pass over the B block tokens; updates K/V caches, conv rings and taps."""
+def verify(W, C, st, tokens, rope, rope_swa=None):
+    """Logits [B][V] (fp64) of the verify pass over the B block tokens; updates K/V caches, conv rings and taps.
+    Sliding layers (kind 2) rotate with rope_swa and d.rope_pairs_swa when the description gives them their own table
+    (rope_base_swa > 0; internal/model/engine.go:333-338), else with `rope` and d.rope_pairs."""
     d = W.d
     H, B, QH, KVH, D, I = d.hidden, d.block, d.q_heads, d.kv_heads, d.head_dim, d.ffn
     emb = W.f16("embed", (d.vocab, H))
@@ -235,15 +261,17 @@ def verify(W, C, st, tokens, rope):
             mix = gemm(x, mw, ms)
             qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
             K, V = C.kv[i]
+            own = kind == 2 and getattr(d, "rope_base_swa", 0) > 0
+            table = rope_swa if own else rope
+            rot = d.rope_pairs_swa if own else d.rope_pairs
             q16 = np.zeros((B, QH, D))
             for t in range(B):
                 pos = a + t
                 for qh in range(QH):
-                    q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, rope,
-                                               d.rope_pairs))
+                    q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, table, rot))
                 for hh in range(KVH):
                     o = QH * D + hh * D
-                    K[pos, hh] = f16(rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs))
+                    K[pos, hh] = f16(rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, table, rot))
                     o = QH * D + KVH * D + hh * D
                     V[pos, hh] = f16(mix[t, o:o + D])
             window = d.window if kind == 2 else 0
@@ -267,3 +295,12 @@ def verify(W, C, st, tokens, rope):
     C.taps = taps
     hw, hs = W.gemm_w("head", d.vocab, H)
     return gemm(x, hw, hs)
+
+
+def conv_state(C, layer, pos, km1, H):
+    """The conv state slot before position `pos` (dspark.hip:2921-2947): element [c][k] = history of position
+    pos - km1 + k, channel c (the reference's [H][conv_k - 1] layout, engine.go:546-547)."""
+    out = np.zeros((H, km1))
+    for k in range(km1):
+        out[:, k] = C.conv[layer][pos - km1 + k]
+    return out

@@ -26,6 +26,26 @@ def load_host():
     return mod
 
 
+def rope_numpy(base, pairs, D, positions):
+    """Engine.buildRope (internal/model/engine.go:428-461) restated in numpy: inv[i] = 1 / float32(pow(base,
+    float32(2 i) / D)) for i < pairs (0 beyond), f = float64(float32(p) * inv[i]), fp16 RNE of float32(cos f) and
+    float32(sin f). cos and sin are Python's math module's (the C library routines the library's table builder calls;
+    numpy's vectorised cos may differ in the last double bit from CPU to CPU)."""
+    import math
+    import numpy as np
+    inv = np.zeros(D // 2, np.float32)
+    for i in range(pairs):
+        ex = np.float32(2 * i) / np.float32(D)
+        inv[i] = np.float32(1.0) / np.float32(math.pow(base, float(ex)))
+    p = np.arange(positions, dtype=np.float32)[:, None]
+    f = (p * inv[None, :]).astype(np.float32).astype(np.float64)
+    flat = f.ravel()
+    cos = np.fromiter(map(math.cos, flat), np.float64, flat.size).reshape(f.shape)
+    sin = np.fromiter(map(math.sin, flat), np.float64, flat.size).reshape(f.shape)
+    return np.concatenate([cos.astype(np.float32).astype(np.float16), sin.astype(np.float32).astype(np.float16)],
+                          axis=1).view(np.uint16)
+
+
 @pytest.fixture(scope="session")
 def orc():
     from oracle import oracle

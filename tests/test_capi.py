@@ -6,7 +6,7 @@ import re
 
 import pytest
 
-from conftest import ROOT, load_host
+from conftest import ROOT, load_host, rope_numpy
 
 HEADER = os.path.join(ROOT, "include", "dspark.h")
 
@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_size_queries_and_state_layout():
     host = load_host()
     lib = host.lib()
-    assert lib.dspark_abi_version() == 1
+    assert lib.dspark_abi_version() == 2
     assert lib.dspark_page_tokens() == 32
     assert lib.dspark_max_tokens() == 64
     # 22 scalars (dspark.hip:134-157, dspark.go:52-77 sTokens == 22) then tokens[64]
@@ -76,7 +76,53 @@ def test_entry_points_refuse_invalid_arguments_without_launching():
     args = host.AttnArgs()
     args.M, args.QH, args.KVH, args.D, args.a = 16, 30, 8, 64, 10   # QH % KVH != 0
     assert lib.dspark_verify_attention(ctypes.byref(args), None) == 1001
-    assert lib.dspark_kv_write(None, None, 512, None, None, None, 8, 64, 0, 1, None) == 1001
+    assert lib.dspark_kv_write(None, None, 512, None, None, None, 100, 8, 64, 0, 1, None) == 1001
     assert lib.dspark_gemm_i8(None, 16, 2048, None, None, 8192, 0, None, None, None, 0, None) == 1001
-    assert lib.dspark_accept_commit(None, None, 9, 0, None, None, None) == 1001
+    assert lib.dspark_accept_commit(None, None, 9, 0, None, 64, None, None) == 1001
     assert lib.dspark_verify_argmax(None, 0, 9, 65536, None, None, 1.0, 1.0, None, None, 0, None) == 1001
+
+
+def test_bounds_are_checked_on_the_host():
+    """Refusals that need sizes, not just pointers: K/V rows past the page pools, an output buffer smaller than a
+    verify block, an engine whose K/V pool would reach 2 GiB (the attention kernels' 32-bit offsets). Placeholder
+    pointers are never dereferenced: every call below is refused before a launch."""
+    host = load_host()
+    lib = host.lib()
+    fake = ctypes.c_void_p(256)
+    # 10 pages hold positions 0..319: rows 300..339 overflow without a block table
+    assert lib.dspark_kv_write(fake, fake, 512, fake, fake, None, 10, 8, 64, 300, 40, None) == 1001
+    assert lib.dspark_kv_write(fake, fake, 512, fake, fake, None, 0, 8, 64, 0, 1, None) == 1001
+    # accept/commit: out_cap below the verify block
+    assert lib.dspark_accept_commit(fake, fake, 9, 0, fake, 8, fake, None) == 1001
+    # engine pools: C4 geometry pages are 8 heads x 32 keys x 64 dims x 2 B = 32 KiB, so max_context ~2M reaches 2 GiB
+    h = ctypes.c_void_p()
+    desc = host.c4_desc()
+    assert lib.dspark_engine_create(ctypes.byref(desc), 1 << 22, ctypes.byref(h)) == 1001
+    assert lib.dspark_engine_create(ctypes.byref(desc), (1 << 16) * 32, ctypes.byref(h)) == 1001
+    bad = host.ref_desc()
+    bad.rope_pairs_swa = 65  # > head_dim / 2
+    assert lib.dspark_engine_create(ctypes.byref(bad), 4096, ctypes.byref(h)) == 1001
+    bad = host.ref_desc()
+    bad.conv_slots = -1
+    assert lib.dspark_engine_create(ctypes.byref(bad), 4096, ctypes.byref(h)) == 1001
+    assert not h.value
+
+
+@pytest.mark.parametrize("base,pairs,D", [(1e6, 32, 128), (1e4, 64, 128), (1e6, 32, 64), (1e4, 16, 64)])
+def test_rope_table_matches_the_reference_formula(base, pairs, D):
+    """The library's table (what the engine uploads) against a numpy restatement, bit for bit over 70000 positions, plus
+    the closed forms: position 0 is cos 1 / sin 0, pairs past `pairs` never rotate, and the first pair's angle is the
+    position itself (inv[0] = 1)."""
+    import numpy as np
+    host = load_host()
+    n = 70000
+    got = host.rope_table(base, pairs, D, n)
+    want = rope_numpy(base, pairs, D, n)
+    assert np.array_equal(got, want)
+    f = got.view(np.float16).astype(np.float64)
+    assert np.all(f[0, :D // 2] == 1.0) and np.all(f[0, D // 2:] == 0.0)
+    assert np.all(f[:, pairs:D // 2] == 1.0) and np.all(f[:, D // 2 + pairs:] == 0.0)
+    pos = np.arange(n)
+    assert np.max(np.abs(f[:, 0] - np.cos(pos))) <= 2 ** -11 and np.max(np.abs(f[:, D // 2] - np.sin(pos))) <= 2 ** -11
+    # a wrong base or pair count is caught
+    assert not np.array_equal(host.rope_table(base * 10, pairs, D, 64), want[:64])

@@ -2,15 +2,19 @@
 the engine's C ABI, against the oracle's restatement (oracle/round.py) on a small geometry with seeded weights.
 
 Bars: drafts, verify argmax keys, acceptance and every State field bit-exact (a draft/argmax may differ only where
-the oracle's own top two values are a near tie); ring K/V, cropped-head outputs and logits within tolerances stated
-below (fp16 activations through several layers: the GPU and the oracle round at the same points, so differences are
-accumulation order and fp16 last-bit flips)."""
+the oracle's own top two values are a near tie); ring K/V, cropped-head outputs and logits within REL x the largest
+magnitude of the compared values. The GPU and the oracle round activations to fp16 at the same points; what differs is
+the fp32 accumulation order of the GEMMs, which now and then puts an fp16 activation on the other neighbour, and that
+last-bit difference carries through the later layers. Measured on MI355X over the eleven cases below: ring K/V <= 1
+fp16 ulp (<= 6e-4 x scale), cropped-head outputs <= 6.7e-4 x scale (max-abs 2.1e-3), logits <= 8.7e-4 x scale
+(max-abs 2.7e-3 .. 4.1e-3 at scale 4.2 .. 5.9): the north_star's 2e-3 max-abs holds for attention (tested alone) but
+not for logits at the end of a multi-layer fp16 forward pass."""
 import ctypes
 
 import numpy as np
 import pytest
 
-from conftest import load_host
+from conftest import load_host, rope_numpy
 
 pytestmark = pytest.mark.gpu
 
@@ -21,7 +25,8 @@ SMALL = dict(hidden=256, ffn=512, vocab=2048, n_layers=4, layer_kind=[0, 1, 0, 2
 # The reference geometry's features at a small size: head_dim 128 with GQA 4:1, conv kernel 7, the reference's layer
 # kind pattern (conv / full / sliding), a 3-layer drafter, 9-token blocks.
 REF_SMALL = dict(hidden=512, ffn=512, vocab=2048, n_layers=6, layer_kind=[0, 0, 1, 0, 2, 0], q_heads=4, kv_heads=1,
-                 head_dim=128, conv_kernel=7, window=40, rope_base=1e6, rope_pairs=64, draft_layers=3, draft_ffn=512,
+                 head_dim=128, conv_kernel=7, window=40, rope_base=1e6, rope_pairs=32, rope_base_swa=1e4,
+                 rope_pairs_swa=64, draft_layers=3, draft_ffn=512,
                  block=9, max_drafts=7, crop_rows=256, markov_rank=64, n_taps=2, tap_layer=[2, 5], draft_window=100,
                  ring_positions=256, mask_token=2047, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
 # SMALL with the confidence term of a random half of the vocabulary (anchor aside) far below the threshold: drafting
@@ -39,6 +44,7 @@ MID = dict(hidden=1024, ffn=4096, vocab=4096, n_layers=4, layer_kind=[0, 1, 0, 2
 # token blocks), three token blocks (K split across workgroups, the last split running the fused conv epilogue).
 MID24 = dict(MID, block=24, max_drafts=12)
 MID33 = dict(MID, block=33, max_drafts=16)
+REL = 1e-3  # the bar of every value comparison in the round parity test (see the module docstring)
 GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE, "mid": MID,
               "mid24": MID24, "mid33": MID33}
 STOP_ANCHOR = 17
@@ -59,7 +65,7 @@ def make_weights(eng, desc, seed, stop_half=False):
     weight_names = [n for n in names if not n.startswith(("kv.", "ring.", "conv.", "state", "seen", "out_tokens", "rep",
                                                            "h0", "h1", "x16", "mix", "q16", "gate", "y16", "vout", "a16",
                                                            "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys",
-                                                           "ws_", "rope", "ring_table"))]
+                                                           "ws_", "rope", "ring_table", "tap_x", "plant", "conv_state"))]
     for n in weight_names:
         nb = sizes[n]
         if n.endswith(".w") and not n.endswith("conv.w"):
@@ -107,9 +113,10 @@ def setup_caches(eng, host_mod, desc, a, ctx_lo, seed):
         kd = torch.from_numpy(np.ascontiguousarray(K[pos0:pos0 + n]).astype(np.float16)).cuda()
         vd = torch.from_numpy(np.ascontiguousarray(V[pos0:pos0 + n]).astype(np.float16)).cuda()
         bt = ctypes.c_void_p(eng.tensor(bt_name)[0]) if bt_name else None
+        kptr, kbytes = eng.tensor(kname)
         rc = lib.dspark_kv_write(ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()), KVH * D,
-                                 ctypes.c_void_p(eng.tensor(kname)[0]), ctypes.c_void_p(eng.tensor(vname)[0]), bt,
-                                 KVH, D, pos0, n, None)
+                                 ctypes.c_void_p(kptr), ctypes.c_void_p(eng.tensor(vname)[0]), bt,
+                                 kbytes // (KVH * 32 * D * 2), KVH, D, pos0, n, None)
         host_mod.check(rc, "kv_write")
         torch.cuda.synchronize()
 
@@ -172,7 +179,18 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
     base_gpu = eng.download("base", np.float32)[:B * ((N + 1 + 15) // 16 * 16)].reshape(B, -1)
     logits_gpu = eng.download("logits", np.float32, (B, V))
     keys_gpu = eng.download("keys", np.uint64, (2 * B,))[:B]
-    rope = rnd.h2f(eng.download("rope", np.uint16)).reshape(-1, desc.head_dim)
+    # RoPE tables: the oracle uses its own (engine.go:428-461 restated in numpy); the engine's must be the same bits
+    D = desc.head_dim
+    rope_u16 = eng.download("rope", np.uint16).reshape(-1, D)
+    want_rope = rope_numpy(desc.rope_base, desc.rope_pairs, D, rope_u16.shape[0])
+    assert np.array_equal(rope_u16, want_rope)
+    rope = rnd.h2f(want_rope)
+    rope_swa = None
+    if desc.rope_base_swa > 0:
+        swa_u16 = eng.download("rope_swa", np.uint16).reshape(-1, D)
+        want_swa = rope_numpy(desc.rope_base_swa, desc.rope_pairs_swa, D, swa_u16.shape[0])
+        assert np.array_equal(swa_u16, want_swa)
+        rope_swa = rnd.h2f(want_swa)
     W = rnd.Weights(desc, weights)
 
     # context projection -> drafter ring rows of positions ctx_pos .. ctx_pos + ctx_new - 1
@@ -181,15 +199,20 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
         -1, desc.kv_heads, 32, desc.head_dim), torch.from_numpy(eng.download("ring.D1.v", np.uint16)).view(
         torch.float16).reshape(-1, desc.kv_heads, desc.head_dim, 32), range(a - ctx_new, a),
         torch.from_numpy(eng.download("ring_table", np.int32)))
-    want_k = C.ring[1][0][a - ctx_new:a]
-    assert np.max(np.abs(kr.astype(np.float64) - want_k)) <= 2e-2 * max(1.0, np.max(np.abs(want_k)))
+    want_k, want_v = C.ring[1][0][a - ctx_new:a], C.ring[1][1][a - ctx_new:a]
+    kerr = np.max(np.abs(kr.astype(np.float64) - want_k))
+    verr = np.max(np.abs(vr.astype(np.float64) - want_v))
+    print(f"ring K max-abs {kerr:.3e} (scale {np.max(np.abs(want_k)):.2f}), ring V max-abs {verr:.3e} "
+          f"(scale {np.max(np.abs(want_v)):.2f})", flush=True)
+    assert kerr <= REL * max(1.0, np.max(np.abs(want_k)))
+    assert verr <= REL * max(1.0, np.max(np.abs(want_v)))
 
     # drafter block -> cropped head outputs
     base = rnd.drafter_block(W, C, st0, rope)
     scale = np.max(np.abs(base[:, :N + 1]))
     err = np.max(np.abs(base_gpu[:, :N + 1] - base[:, :N + 1]))
     print(f"base max-abs {err:.3e} (scale {scale:.2f})", flush=True)
-    assert err <= 2e-2 * scale
+    assert err <= REL * scale
 
     # Markov drafts from the GPU's own base: exact up to near ties
     toks, M, zs = rnd.markov(W, dict(st0), base_gpu.astype(np.float64))
@@ -206,11 +229,11 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
 
     # verify over the tokens the GPU verified
     verified = gpu_toks + list(st.tokens)[st.M:B]  # positions past M hold what the State held (verified, unused)
-    logits = rnd.verify(W, C, dict(st0, tokens=verified), verified[:B], rope)
+    logits = rnd.verify(W, C, dict(st0, tokens=verified), verified[:B], rope, rope_swa)
     lscale = np.max(np.abs(logits))
     lerr = np.max(np.abs(logits_gpu - logits))
     print(f"logits max-abs {lerr:.3e} (scale {lscale:.2f})", flush=True)
-    assert lerr <= 2e-2 * lscale
+    assert lerr <= REL * lscale
     # argmax keys on the GPU's logits are bit-exact with the oracle's key rule
     seen = eng.download("seen", np.uint32)
     want_keys = orc.verify_argmax(logits_gpu.astype(np.float32), seen, np.array(verified[:B], np.int32))

@@ -269,6 +269,18 @@ def test_attention_f32_mt_close_to_fp64(orc):
     assert np.max(np.abs(got - want)) < 2e-4
 
 
+@pytest.mark.parametrize("window,causal,start", [(0, True, 0), (40, True, 470), (0, False, 100)])
+def test_attention_mt_is_the_fp64_oracle(orc, window, causal, start):
+    """The threaded fp64 form gives the single-threaded oracle's bits (same arithmetic per row)."""
+    M, QH, KVH, D, a = 9, 16, 4, 128, 500
+    q = orc.normal_f16(61, (M, QH, D))
+    k = orc.normal_f16(62, (a + M, KVH, D))
+    v = orc.normal_f16(63, (a + M, KVH, D))
+    want = orc.verify_attention(q, k, v, a, start, window, causal)
+    got = orc.verify_attention_mt(q, k, v, a, start, window, causal, threads=5)
+    assert np.array_equal(got, want)
+
+
 # ---------------------------------------------------------------- acceptance / commit (dspark.hip:2848-2913)
 def _round(orc, tokens, best, a=1024, count=0, budget=512, stop_at=1056, eos=-1, rounds_left=32):
     st = orc.new_state(a=a, anchor=tokens[0], count=count, rounds_left=rounds_left, budget=budget, eos=eos,
