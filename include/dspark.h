@@ -92,6 +92,18 @@ int dspark_verify_attention(const dspark_attn_args* args, dspark_stream_t stream
 int dspark_verify_attention_splits(const dspark_attn_args* args, dspark_stream_t stream);
 int dspark_verify_attention_combine(const dspark_attn_args* args, dspark_stream_t stream);
 
+/* dspark_verify_attention without a workspace and without allocating anything: no counterpart in the reference; for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid device
+ * allocation). Same arguments and outputs as dspark_verify_attention except that args->workspace and
+ * args->workspace_bytes are ignored: the split partials go to a static device array of the library,
+ * DSPARK_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. Shapes whose partials need more
+ * (dspark_verify_attention_workspace > DSPARK_NOALLOC_SCRATCH_BYTES) are refused with DSPARK_ENOSPACE before any
+ * launch. The array needs no clearing (the split pass writes every partial the merge reads). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams, other threads) race; stream-ordered
+ * calls do not. */
+#define DSPARK_NOALLOC_SCRATCH_BYTES (16 << 20)
+int dspark_verify_attention_noalloc(const dspark_attn_args* args, dspark_stream_t stream);
+
 /* ---------------------------------------------------------------- KV write (append / commit)
  * Writes K/V rows for positions pos0..pos0+n-1 into the pages: k, v fp16 [n][KVH][D] (row stride `row_stride`
  * elements between tokens, >= KVH*D). Verify rounds append the drafted block's K/V before attention; commit is then

@@ -4,6 +4,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "dspark.h"
@@ -145,6 +146,46 @@ static int verify_attention_phases(const dspark_attn_args* a, int phases, dspark
 
 int dspark_verify_attention(const dspark_attn_args* a, dspark_stream_t stream) {
   return verify_attention_phases(a, 3, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- verify attention without an allocation
+// The split partials of dspark_verify_attention_noalloc live in this file-scope device array (each GPU the library runs
+// on holds its own copy until the process ends). Host code never passes the array's name to a kernel: on the host it
+// is only a stand-in, not a device address; the device address of each GPU's copy comes from hipGetSymbolAddress,
+// looked up once per device (with that device current) and kept below.
+static __device__ __align__(256) char scratch[DSPARK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[NOALLOC_MAX_DEVICES] = {nullptr};
+
+// The current device's copy of `scratch` (nullptr if the lookup failed).
+void* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    scratch_ptr[dev] = p;
+  }
+  return scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int dspark_verify_attention_noalloc(const dspark_attn_args* a, dspark_stream_t stream) {
+  if (!attn_args_ok(a)) return DSPARK_EINVAL;
+  AttnParams p = attn_params(a);
+  if (attn_workspace_bytes(p, a->D) > (size_t)DSPARK_NOALLOC_SCRATCH_BYTES) return DSPARK_ENOSPACE;
+  void* ws = scratch_for_current_device();
+  if (!ws) return DSPARK_EUNSUPPORTED;
+  attn_bind_workspace(p, a->D, ws);
+  return attn_launch(p, a->D, 3, S(stream));
 }
 int dspark_verify_attention_splits(const dspark_attn_args* a, dspark_stream_t stream) {
   return verify_attention_phases(a, 1, stream);

@@ -51,6 +51,7 @@ _SIGS = {
     "dspark_verify_attention": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_verify_attention_splits": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_verify_attention_combine": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "dspark_verify_attention_noalloc": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_kv_write": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
