@@ -10,7 +10,10 @@ Inputs are synthetic N(0,1) fp16 resident in HBM; two full KV sets (2 x 6 x 64 M
 
 Prints one JSON line (the driver's contract) with a `roofline` object for the dominant kernel (the key-split pass,
 `verify_attn_lds_kernel`) timed with HIP events on the library's stream, and a `cpu_baseline` object (the C oracle's
-fp32 multi-threaded restatement timed on a bounded sample of the same workload).
+fp32 restatement timed on a bounded sample of the same workload, on all CPUs of the job's share and on one). The same
+line carries the metric's other half, `headline_tok_s` (greedy decode tok/s of full DSpark rounds at 1k / 32k / 128k
+context, beside the reference's published MI50 numbers), and `c5_attention` (verify attention at 131072 keys for 33 and
+16 verify tokens). `--c2-only` skips those two; `--workload` selects the other configs (c3, c4, c5, tiers, ref).
 """
 import argparse
 import ctypes
@@ -53,106 +56,126 @@ def read_traffic():
         return None
 
 
-def cpu_threads():
+def cpu_info():
+    """Host CPU: model name, the host's logical CPU count and the CPUs this process may run on (the CPU share a GPU
+    job gets on the box; worker pools stay within it)."""
+    model = "unknown"
     try:
-        n = len(os.sched_getaffinity(0))
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        share = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        share = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, max(1, share)
 
 
 def cpu_baseline_c2(ctx, M, QH, KVH, D, seconds):
-    """The CPU oracle (test infrastructure, used here only as the timed baseline) on layers of the same workload."""
+    """The CPU oracle (test infrastructure, used here only as the timed baseline) on layers of the same workload: all
+    threads of this process's CPU share, then one thread."""
     import numpy as np
     from oracle import oracle as orc
     rng = np.random.default_rng(20261202)
     q = rng.standard_normal((M, QH, D)).astype(np.float16).view(np.uint16)
     k = rng.standard_normal((ctx + M, KVH, D)).astype(np.float16).view(np.uint16)
     v = rng.standard_normal((ctx + M, KVH, D)).astype(np.float16).view(np.uint16)
-    threads = cpu_threads()
-    layers = 0
-    t0 = time.perf_counter()
-    while True:
-        orc.verify_attention_f32_mt(q, k, v, ctx, threads=threads)
-        layers += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+    model, nproc, share = cpu_info()
     layer_bytes = ctx * KVH * D * 2 * 2
-    return {"value": round(layer_bytes * layers / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{layers} layers of the C2 workload (ctx {ctx}, {M} verify tokens, {QH}/{KVH} heads, d{D}) "
-                      f"through the C oracle's fp32 verify attention on {threads} threads, {el:.1f} s"}
+
+    def rate(threads, budget):
+        layers, t0 = 0, time.perf_counter()
+        while True:
+            orc.verify_attention_f32_mt(q, k, v, ctx, threads=threads)
+            layers += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return layer_bytes * layers / el / 1e9, layers, el
+
+    all_gbs, all_n, all_s = rate(share, seconds)
+    one_gbs, one_n, one_s = rate(1, seconds / 2)
+    return {"value": round(all_gbs, 3), "unit": "GB/s", "cores": share, "kind": "port",
+            "sample": f"{all_n} layers of the C2 workload (ctx {ctx}, {M} verify tokens, {QH}/{KVH} heads, d{D}) through "
+                      f"the C oracle's fp32 verify attention on {share} threads in {all_s:.1f} s; single thread: "
+                      f"{one_n} layers in {one_s:.1f} s",
+            "single_thread": round(one_gbs, 3), "host_nproc": nproc, "cpu_share": share, "cpu_model": model,
+            "note": "Go (the reference's host language) is absent on the box, so the reference's CPU path cannot run; "
+                    "the all-core figure uses the CPUs this GPU job is given (the box's share per GPU), not every "
+                    "core of the host"}
 
 
-def bench_c2(args, host, torch):
-    L, ctx, M, QH, KVH, D = 6, 32768, 16, 32, 8, 64
-    SETS = 2
+def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None):
+    """Verify attention of L GQA layers (32 q / 8 kv heads, head_dim 64) at context ctx for M verify tokens, `sets`
+    rotating KV sets (so the Infinity Cache cannot serve a step from the previous one). A step = per layer the
+    key-split pass and the merge. Returns step time, GB/s, and the split pass's average launch time."""
+    QH, KVH, D = 32, 8, 64
+    steps = steps or args.steps
+    warmup = args.warmup if warmup is None else warmup
     lib = host.lib()
     dev = "cuda"
     stream = torch.cuda.current_stream()
     sh = host.stream_handle(stream)
     n_pages = (ctx + M + 31) // 32
     g = torch.Generator(device=dev)
-    g.manual_seed(20261201 + 1)
+    g.manual_seed(20261201 + ctx + M)
 
     def rnd(*shape):
         return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(torch.float16)
 
-    kv = [[(rnd(n_pages, KVH, 32, D), rnd(n_pages, KVH, D, 32)) for _ in range(L)] for _ in range(SETS)]
+    kv = [[(rnd(n_pages, KVH, 32, D), rnd(n_pages, KVH, D, 32)) for _ in range(L)] for _ in range(sets)]
     q = [rnd(M, QH, D) for _ in range(L)]
     fk = [rnd(M, KVH, D) for _ in range(L)]
     fv = [rnd(M, KVH, D) for _ in range(L)]
     out = [torch.empty((M, QH, D), dtype=torch.float16, device=dev) for _ in range(L)]
-    argv = [[host.attn_args(q[l], kv[s][l][0], kv[s][l][1], ctx, out=out[l]) for l in range(L)] for s in range(SETS)]
+    argv = [[host.attn_args(q[l], kv[s][l][0], kv[s][l][1], ctx, out=out[l]) for l in range(L)] for s in range(sets)]
     need = lib.dspark_verify_attention_workspace(ctypes.byref(argv[0][0]))
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
-    for s in range(SETS):
+    for s in range(sets):
         for l in range(L):
             argv[s][l].workspace, argv[s][l].workspace_bytes = ws.data_ptr(), ws.numel()
-    kvw = [[(ctypes.c_void_p(fk[l].data_ptr()), ctypes.c_void_p(fv[l].data_ptr()),
-             ctypes.c_void_p(kv[s][l][0].data_ptr()), ctypes.c_void_p(kv[s][l][1].data_ptr())) for l in range(L)]
-           for s in range(SETS)]
-
     # The verified block's K/V rows go into every layer's pages once (in the full step the kernel that produces them
     # writes them); each step then re-verifies the same block.
-    for s in range(SETS):
+    for s in range(sets):
         for l in range(L):
-            a_, b_, c_, d_ = kvw[s][l]
-            host.check(lib.dspark_kv_write(a_, b_, KVH * D, c_, d_, None, n_pages, KVH, D, ctx, M, sh), "kv_write")
+            host.check(lib.dspark_kv_write(ctypes.c_void_p(fk[l].data_ptr()), ctypes.c_void_p(fv[l].data_ptr()),
+                                           KVH * D, ctypes.c_void_p(kv[s][l][0].data_ptr()),
+                                           ctypes.c_void_p(kv[s][l][1].data_ptr()), None, n_pages, KVH, D, ctx, M, sh),
+                       "kv_write")
 
     def step(i):
-        s = i % SETS
+        s = i % sets
         for l in range(L):
             host.check(lib.dspark_verify_attention(ctypes.byref(argv[s][l]), sh), "verify_attention")
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     e1.record(stream)
     torch.cuda.synchronize()
-    total_ms = e0.elapsed_time(e1)
-    ms_per_step = total_ms / args.steps
+    ms_per_step = e0.elapsed_time(e1) / steps
     layer_bytes = ctx * KVH * D * 2 * 2
-    step_bytes = L * layer_bytes
 
-    # Dominant kernel: the key-split pass (verify_attn_lds_kernel at this shape), which streams the K/V pages. Its
-    # average launch duration: the same launches back to back with nothing between them, HIP events recorded on the
-    # library's stream around all of them, elapsed / launches (launch gaps included, so this errs low). The merge
-    # kernel is timed the same way and reported beside it.
-    n_launch = args.steps * L
+    # Dominant kernel: the key-split pass (verify_attn_lds_kernel), which streams the K/V pages. Its average launch
+    # duration: the same launches back to back with nothing between them, HIP events recorded on the library's stream
+    # around all of them, elapsed / launches (launch gaps included, so this errs low). The merge kernel is timed the
+    # same way and reported beside it.
+    n_launch = steps * L
     t0, t1, t2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
     t0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         for l in range(L):
-            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
+            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % sets][l]), sh), "splits")
     t1.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         for l in range(L):
-            host.check(lib.dspark_verify_attention_combine(ctypes.byref(argv[i % SETS][l]), sh), "combine")
+            host.check(lib.dspark_verify_attention_combine(ctypes.byref(argv[i % sets][l]), sh), "combine")
     t2.record(stream)
     torch.cuda.synchronize()
     kern_avg = t0.elapsed_time(t1) / n_launch
@@ -160,24 +183,36 @@ def bench_c2(args, host, torch):
     # Per-launch brackets of the split pass (event overhead included, so these err high).
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n_launch)]
     j = 0
-    for i in range(args.steps):
+    for i in range(steps):
         for l in range(L):
             ev[j][0].record(stream)
-            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % SETS][l]), sh), "splits")
+            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % sets][l]), sh), "splits")
             ev[j][1].record(stream)
             j += 1
     torch.cuda.synchronize()
     split_br = sorted(e[0].elapsed_time(e[1]) for e in ev)
-    achieved = layer_bytes / (kern_avg * 1e-3) / 1e9
+    del kv, ws
+    torch.cuda.empty_cache()
+    return {"layers": L, "ctx": ctx, "M": M, "ms_per_step": ms_per_step, "layer_bytes": layer_bytes,
+            "step_gbs": L * layer_bytes / (ms_per_step * 1e-3) / 1e9, "split_avg_ms": kern_avg,
+            "split_gbs": layer_bytes / (kern_avg * 1e-3) / 1e9, "merge_avg_ms": combine_avg,
+            "split_bracket_median_ms": split_br[len(split_br) // 2]}
+
+
+def bench_c2(args, host, torch):
+    r = bench_attention(args, host, torch, 6, 32768, 16, 2)
+    L, ctx, M = r["layers"], r["ctx"], r["M"]
+    step_bytes = L * r["layer_bytes"]
+    achieved = r["split_gbs"]
     traffic = read_traffic()
     res = {
         "metric": METRIC,
-        "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "value": round(r["step_gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": round(r["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -186,16 +221,32 @@ def bench_c2(args, host, torch):
         "config": {"workload": "C2 verify attention (BASELINE configs[1]): 6 GQA layers, 32 q / 8 kv heads, head_dim 64, "
                                "fp16 paged K/V at context 32768, 16 verify tokens causal in block; per layer the key-split "
                                "pass and the split merge (the block's K/V appended once at setup)",
-                   "layers": L, "ctx": ctx, "verify_tokens": M, "q_heads": QH, "kv_heads": KVH, "head_dim": D,
+                   "layers": L, "ctx": ctx, "verify_tokens": M, "q_heads": 32, "kv_heads": 8, "head_dim": 64,
                    "algorithmic_bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "verify_attn_lds_kernel (key-split pass)", "algorithmic_bytes_per_launch": layer_bytes,
-                     "avg_launch_us": round(kern_avg * 1e3, 2),
-                     "bracketed_median_us": round(split_br[len(split_br) // 2] * 1e3, 2),
-                     "merge_kernel_avg_us": round(combine_avg * 1e3, 2)},
+                     "kernel": "verify_attn_lds_kernel (key-split pass)",
+                     "algorithmic_bytes_per_launch": r["layer_bytes"],
+                     "avg_launch_us": round(r["split_avg_ms"] * 1e3, 2),
+                     "bracketed_median_us": round(r["split_bracket_median_ms"] * 1e3, 2),
+                     "merge_kernel_avg_us": round(r["merge_avg_ms"] * 1e3, 2),
+                     "step_frac": round(r["step_gbs"] / HBM_PEAK_GBS, 4)},
     }
     return res
+
+
+def c5_attention_fields(args, host, torch):
+    """C5's verify attention (context 131072) for the 33-token block and for 16 tokens: 2 layers, 2 rotating KV sets
+    (4 x 268 MB)."""
+    out = []
+    for M in (33, 16):
+        r = bench_attention(args, host, torch, 2, 131072, M, 2, steps=max(4, args.steps // 2), warmup=2)
+        out.append({"ctx": 131072, "verify_tokens": M, "ms_per_layer": round(r["ms_per_step"] / 2, 5),
+                    "step_GBs": round(r["step_gbs"], 1), "step_frac": round(r["step_gbs"] / HBM_PEAK_GBS, 4),
+                    "split_avg_us": round(r["split_avg_ms"] * 1e3, 2), "split_GBs": round(r["split_gbs"], 1),
+                    "split_frac": round(r["split_gbs"] / HBM_PEAK_GBS, 4),
+                    "merge_avg_us": round(r["merge_avg_ms"] * 1e3, 2)})
+    return out
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
@@ -466,9 +517,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy"])
+    ap.add_argument("--c2-only", action="store_true",
+                    help="default workload without the headline tiers and the C5 attention fields")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -489,6 +542,23 @@ def main():
         print(json.dumps(bench_engine(args, host, torch, args.workload)), flush=True)
         return
     res = bench_c2(args, host, torch)
+    if not args.c2_only:
+        # The metric's other half: greedy decode tok/s at 1k / 32k / 128k (DSpark rounds of the C4-geometry model with
+        # the reference's 9-token verify block, drafts planted at the MI50's committed tokens per round), and C5's
+        # verify attention at 128k.
+        targs = argparse.Namespace(**vars(args))
+        targs.steps, targs.warmup = min(args.steps, 20), min(args.warmup, 5)
+        tiers = bench_engine(targs, host, torch, "tiers")
+        res["headline_tok_s"] = {
+            "model": "C4 geometry (16 layers: 10 conv k=3 + 6 GQA 32/8/64, H 2048, FFN 8192, vocab 65536, int8 "
+                     "weights; 4-layer drafter), random-init, block 9 (the reference's verify block)",
+            "rounds": targs.steps, "warmup": targs.warmup,
+            "tiers": [{k: c[k] for k in ("ctx", "ms_per_round", "tokens_per_round", "tok_s", "tok_s_at_mi50_tau",
+                                         "mi50_tok_s", "vs_mi50", "planted_tau_expected")} for c in tiers["cases"]],
+            "note": "tok_s_at_mi50_tau = the MI50's measured committed tokens per round (benchmarks/"
+                    "verify_attention.txt:54-58) / this round time; a round verifies the same tokens whatever is "
+                    "accepted, so its time does not depend on the draws; tok_s is the rate of the planted draws"}
+        res["c5_attention"] = c5_attention_fields(args, host, torch)
     if not args.no_cpu:
         sys.path.insert(0, ROOT)
         res["cpu_baseline"] = cpu_baseline_c2(32768, 16, 32, 8, 64, args.cpu_seconds)
