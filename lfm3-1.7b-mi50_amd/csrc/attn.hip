@@ -377,8 +377,12 @@ __device__ __forceinline__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((
 
 #define DSPARK_LDSP(x) ((__attribute__((address_space(3))) void*)(x))
 
-template <int D, int PL, int PPL, int LPW>
-__global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
+// QB row blocks per wave: wave w is row group rg = w % NRG (row blocks rg QB .. rg QB + QB - 1, past NRB padding) of
+// page lane pl = w / NRG. With QB > 1 fewer waves share each page (LDS reads per step fall by QB) and the waves can be
+// a multiple of four (one share per SIMD: 9 row blocks as 3 groups of 3 x 4 page lanes = 12 waves, where 9 waves of
+// one block each left one SIMD a third more work than the others).
+template <int D, int QB, int PL, int PPL, int LPW, int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p) {
   constexpr int PAGEB = 4 * PAGE * D;  // K + V bytes of one (page, KV head)
   constexpr int CPG = PAGEB / 1024;    // 1 KB chunks per page: K chunks first, then V^T chunks
   constexpr int PPS = PL * PPL;        // pages per step
@@ -386,9 +390,9 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char ring3[RING > 3 ? PPS * PAGEB : 16];
   __shared__ __attribute__((aligned(16))) char trash[1024];  // destination of the padding loads
   __shared__ int32_t sm_bt[LDS_BT_MAX];                       // the split's block-table entries
-  // Q operands of up to 16 / PL row blocks: staged in the last ring slot (not written before step 0, and every wave
+  // Q operands of up to MAXW / PL row groups: staged in the last ring slot (not written before step 0, and every wave
   // has read its Q before step 0's barrier) when they fit it.
-  constexpr int QBYTES = (16 / PL) * (D / 32) * 1024;
+  constexpr int QBYTES = (MAXW / PL) * QB * (D / 32) * 1024;
   constexpr bool QRING = QBYTES <= PPS * PAGEB;
   __shared__ __attribute__((aligned(16))) char q_own[QRING ? 16 : QBYTES];
   char* const q_lds = QRING ? (RING > 3 ? ring3 : ring2) : q_own;
@@ -398,18 +402,21 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   }
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int NRB = p.nrb, NW = NRB * PL;
-  const int rb = wave % NRB, pl = wave / NRB;
+  const int NRB = p.nrb, NRG = p.nrg, NW = NRG * PL;
+  const int rg = wave % NRG, pl = wave / NRG;
   const int h = blockIdx.x / p.S, split = blockIdx.x % p.S;
   const int R = NRB * 16;
 
-  QOps<D, 1, false> qf;
-  RowState<D, 1> rs;
+  QOps<D, QB, false> qf;
+  RowState<D, QB> rs;
 #pragma unroll
-  for (int cc = 0; cc < D / 16; ++cc) rs.o[0][cc] = f32x4{0, 0, 0, 0};
-  rs.ls[0] = f32x4{0, 0, 0, 0};
-  rs.m[0] = M_INIT;
-  rs.c[0] = f32x4{0, 0, 0, 0};
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) rs.o[qb][cc] = f32x4{0, 0, 0, 0};
+    rs.ls[qb] = f32x4{0, 0, 0, 0};
+    rs.m[qb] = M_INIT;
+    rs.c[qb] = f32x4{0, 0, 0, 0};
+  }
 
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)p.kp, (short)0, (int)p.k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)p.vp, (short)0, (int)p.v_bytes, 0x00020000);
@@ -472,10 +479,10 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
           tl.k[c / (D / 32)][c % (D / 32)] = *reinterpret_cast<const half8*>(src + c * 1024 + lane * 16);
           tl.v[c] = *reinterpret_cast<const half8*>(src + (D / 16 + c) * 1024 + lane * 16);
         }
-        f32x4 sc[1][2];
-        page_scores<D, 1, false>(tl, qf, rs.c, sc, lane);
-        page_prep<D, 1>(p, page, rb * 16, rs, sc, g, lane);
-        page_accumulate<D, 1>(tl, rs, sc);
+        f32x4 sc[QB][2];
+        page_scores<D, QB, false>(tl, qf, rs.c, sc, lane);
+        page_prep<D, QB>(p, page, rg * QB * 16, rs, sc, g, lane);
+        page_accumulate<D, QB>(tl, rs, sc);
       }
     }
   };
@@ -485,14 +492,18 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   // row (the merge never stores them).
   if (paged) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   if (pl == 0) {
-    const int r = min(rb * 16 + n, p.G * p.M - 1);
-    const int t = r / p.G, qh = h * p.G + r % p.G;
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.q, (short)0, (int)((size_t)p.M * p.QH * D * 2), 0x00020000);
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, DSPARK_LDSP(q_lds + (rb * (D / 32) + s) * 1024), 16,
-                                               (uint32_t)((((size_t)t * p.QH + qh) * D + 32 * s + 8 * g) * 2), 0, 0, 0);
+    for (int qb = 0; qb < QB; ++qb) {
+      const int rb = rg * QB + qb;
+      const int r = min(rb * 16 + n, p.G * p.M - 1);
+      const int t = r / p.G, qh = h * p.G + r % p.G;
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, DSPARK_LDSP(q_lds + (rb * (D / 32) + s) * 1024), 16,
+                                                 (uint32_t)((((size_t)t * p.QH + qh) * D + 32 * s + 8 * g) * 2), 0, 0, 0);
+    }
   }
   char* const slots[4] = {ring0, ring1, ring2, ring3};
 #pragma unroll
@@ -506,12 +517,14 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __builtin_amdgcn_s_barrier();
 #pragma unroll
-  for (int s = 0; s < D / 32; ++s) {
-    half8 q = *reinterpret_cast<const half8*>(q_lds + (rb * (D / 32) + s) * 1024 + lane * 16);
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
-    qf.r[0][s] = q;
-  }
+    for (int s = 0; s < D / 32; ++s) {
+      half8 q = *reinterpret_cast<const half8*>(q_lds + ((rg * QB + qb) * (D / 32) + s) * 1024 + lane * 16);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
+      qf.r[qb][s] = q;
+    }
   for (int k = 0; k < nsteps; k += RING) {
 #pragma unroll
     for (int u = 0; u < RING; ++u)
@@ -519,47 +532,55 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // Page lanes of each row block merge through LDS in one round: lanes 1 .. PL-1 store their states, then lane 0 reads
-  // all of them at once and folds them in lane order ((0 + 1) + 2) + 3. Lane q of row block rb uses the area
-  // ((rb / RING) * (PL - 1) + q - 1) of ring slot rb % RING: 16 rows of (D + 6) floats, o [16][D + 4], then m [16]
-  // and l [16].
+  // Page lanes merge through LDS as a tree: at level `half` (PL / 2, ..., 1) lanes half .. 2 half - 1 store their
+  // states and lane q < half folds in lane q + half's -- ((0 + 2) + (1 + 3)) for four lanes, a fixed order. The state
+  // of row block rb stored by lane q + half goes to area q * NRG QB + rb, area i at (i / RING) AREAF floats into ring
+  // slot i % RING: 16 rows of (D + 6) floats, o [16][D + 4], then m [16] and l [16] (the host plan checks that
+  // PL / 2 x NRG x QB areas fit the ring).
   if constexpr (PL > 1) {
     constexpr int ROWF = D + 4, AREAF = 16 * (ROWF + 2);
-    float* areas = nullptr;
+    const int NRGQ = NRG * QB;
+    auto area_of = [&](int i) -> float* {
+      float* a = nullptr;
 #pragma unroll
-    for (int i = 0; i < RING; ++i)
-      if (rb % RING == i) areas = reinterpret_cast<float*>(slots[i]) + (rb / RING) * (PL - 1) * AREAF;
+      for (int k = 0; k < RING; ++k)
+        if (i % RING == k) a = reinterpret_cast<float*>(slots[k]) + (i / RING) * AREAF;
+      return a;
+    };
     __syncthreads();  // every wave is done with the ring
-    if (pl != 0) {
-      float* area = areas + (pl - 1) * AREAF;
 #pragma unroll
-      for (int cc = 0; cc < D / 16; ++cc) *reinterpret_cast<f32x4*>(area + n * ROWF + 16 * cc + 4 * g) = rs.o[0][cc];
-      if (g == 0) {
-        area[16 * ROWF + n] = rs.m[0];
-        area[16 * ROWF + 16 + n] = rs.ls[0][0];
+    for (int half = PL / 2; half >= 1; half /= 2) {
+      if (pl >= half && pl < 2 * half) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          float* area = area_of((pl - half) * NRGQ + rg * QB + qb);
+#pragma unroll
+          for (int cc = 0; cc < D / 16; ++cc)
+            *reinterpret_cast<f32x4*>(area + n * ROWF + 16 * cc + 4 * g) = rs.o[qb][cc];
+          if (g == 0) {
+            area[16 * ROWF + n] = rs.m[qb];
+            area[16 * ROWF + 16 + n] = rs.ls[qb][0];
+          }
+        }
       }
-    }
-    __syncthreads();
-    if (pl == 0) {
-      f32x4 ob[PL - 1][D / 16];
-      float mb[PL - 1], lb[PL - 1];
+      __syncthreads();
+      if (pl < half) {
 #pragma unroll
-      for (int q = 0; q < PL - 1; ++q) {
-        const float* area = areas + q * AREAF;
+        for (int qb = 0; qb < QB; ++qb) {
+          const float* area = area_of(pl * NRGQ + rg * QB + qb);
+          f32x4 ob[D / 16];
 #pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc) ob[q][cc] = *reinterpret_cast<const f32x4*>(area + n * ROWF + 16 * cc + 4 * g);
-        mb[q] = area[16 * ROWF + n];
-        lb[q] = area[16 * ROWF + 16 + n];
+          for (int cc = 0; cc < D / 16; ++cc) ob[cc] = *reinterpret_cast<const f32x4*>(area + n * ROWF + 16 * cc + 4 * g);
+          const float mb = area[16 * ROWF + n], lb = area[16 * ROWF + 16 + n];
+          const float mx = fmaxf(rs.m[qb], mb);
+          const float fa = fast_exp2(rs.m[qb] - mx), fb = fast_exp2(mb - mx);
+#pragma unroll
+          for (int cc = 0; cc < D / 16; ++cc) rs.o[qb][cc] = rs.o[qb][cc] * fa + ob[cc] * fb;
+          rs.ls[qb] = rs.ls[qb] * fa + f32x4{lb, lb, lb, lb} * fb;
+          rs.m[qb] = mx;
+        }
       }
-#pragma unroll
-      for (int q = 0; q < PL - 1; ++q) {
-        const float mx = fmaxf(rs.m[0], mb[q]);
-        const float fa = fast_exp2(rs.m[0] - mx), fb = fast_exp2(mb[q] - mx);
-#pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc) rs.o[0][cc] = rs.o[0][cc] * fa + ob[q][cc] * fb;
-        rs.ls[0] = rs.ls[0] * fa + f32x4{lb[q], lb[q], lb[q], lb[q]} * fb;
-        rs.m[0] = mx;
-      }
+      __syncthreads();  // the areas are rewritten by the next level
     }
   }
   if (pl != 0) return;
@@ -568,17 +589,22 @@ __global__ __launch_bounds__(1024) void verify_attn_lds_kernel(AttnParams p) {
   const size_t slot = (size_t)h * p.S + split;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(p.part_acc + slot * R * D, (short)0, R * D * (int)sizeof(float), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rm =
+      __builtin_amdgcn_make_buffer_rsrc(p.part_ml + slot * R, (short)0, R * (int)sizeof(f32x2), 0x00020000);
 #pragma unroll
-  for (int cc = 0; cc < D / 16; ++cc)
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, rs.o[0][cc]), ra,
-                                           (uint32_t)(((rb * 16 + n) * D + 16 * cc + 4 * g) * sizeof(float)), 0,
-                                           ATTN_CPOL_COHERENT);
-  if (g == 0) {
-    const float L = rs.ls[0][0];
-    const __amdgpu_buffer_rsrc_t rm =
-        __builtin_amdgcn_make_buffer_rsrc(p.part_ml + slot * R, (short)0, R * (int)sizeof(f32x2), 0x00020000);
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{L > 0.f ? rs.m[0] : -INFINITY, L}), rm,
-                                          (uint32_t)((rb * 16 + n) * sizeof(f32x2)), 0, ATTN_CPOL_COHERENT);
+  for (int qb = 0; qb < QB; ++qb) {
+    const int rb = rg * QB + qb;
+    if (rb >= NRB) break;  // padding row blocks of the last group
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, rs.o[qb][cc]), ra,
+                                             (uint32_t)(((rb * 16 + n) * D + 16 * cc + 4 * g) * sizeof(float)), 0,
+                                             ATTN_CPOL_COHERENT);
+    if (g == 0) {
+      const float L = rs.ls[qb][0];
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{L > 0.f ? rs.m[qb] : -INFINITY, L}), rm,
+                                            (uint32_t)((rb * 16 + n) * sizeof(f32x2)), 0, ATTN_CPOL_COHERENT);
+    }
   }
 }
 #undef DSPARK_LDSP
@@ -733,22 +759,37 @@ static void launch_attn(const AttnParams& p, hipStream_t s) {
   hipLaunchKernelGGL((verify_attn_kernel<D, QB, PF, OCC, QLDS>), dim3((units + 7) / 8 * 8 * p.RG), dim3(256), 0, s, p);
 }
 
-template <int D, int PL, int PPL, int LPW>
+template <int D, int QB, int PL, int PPL, int LPW, int MAXW>
 static void launch_lds(const AttnParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((verify_attn_lds_kernel<D, PL, PPL, LPW>), dim3(p.KVH * p.S), dim3(p.nrb * PL * 64), 0, s, p);
+  hipLaunchKernelGGL((verify_attn_lds_kernel<D, QB, PL, PPL, LPW, MAXW>), dim3(p.KVH * p.S), dim3(p.nrg * PL * 64), 0, s,
+                     p);
 }
 
-// LDS-ring shape for nblk row blocks: a step is PPS = LDS_STEP_BYTES / page bytes pages; page lanes PL (NRB * PL <= 16
-// waves; the page-lane merge fits a ring slot), PPL = PPS / PL pages per lane per step, and loads per wave per step
-// LPW = ceil(chunks per step / waves). Returns false when the register kernel is needed.
-static bool lds_shape(int D, int nblk, int* pl, int* ppl, int* lpw) {
+#ifndef DSPARK_ATTN_QB3
+#define DSPARK_ATTN_QB3 1  // 0: 9 row blocks as 9 waves of one block (the QB = 1 shape)
+#endif
+
+// LDS-ring shape for nblk row blocks: a step is PPS = LDS_STEP_BYTES / page bytes pages; QB row blocks per wave in
+// NRG = ceil(nblk / QB) row groups; page lanes PL (NRG * PL <= 16 waves; the page-lane merge's PL / 2 x NRG x QB
+// areas fit the ring), PPL = PPS / PL pages per lane per step, and loads per wave per step LPW = ceil(chunks per step /
+// waves). QB = 3 for 9 row blocks at D = 64 (33 tokens x 4 query heads: 3 groups x 4 page lanes = 12 waves, three per
+// SIMD, each reading one page per step), QB = 1 otherwise. Returns false when the register kernel is needed.
+static bool lds_shape(int D, int nblk, int* qb, int* nrg, int* pl, int* ppl, int* lpw) {
   if (!DSPARK_ATTN_LDS || nblk < 1 || nblk > 16) return false;
   const int pageb = 4 * PAGE * D, cpg = pageb / 1024;
   int pps = LDS_STEP_BYTES / pageb;
+  const size_t areaf = 16 * (D + 6) * 4, areas_in_ring = (size_t)RING * (LDS_STEP_BYTES / areaf);
+  if (DSPARK_ATTN_QB3 && D == 64 && nblk == 9) {
+    *qb = 3;
+    *nrg = 3;
+    *pl = 4;
+    *ppl = pps / 4;
+    *lpw = (pps * cpg + 11) / 12;
+    return (size_t)(4 / 2) * 9 <= areas_in_ring;
+  }
   int PL = 1;
   for (int c = pps; c >= 1; c /= 2) {
-    const size_t merge = (size_t)((nblk - 1) / RING + 1) * (c > 1 ? c - 1 : 1) * 16 * (D + 6) * 4;
-    if (nblk * c <= 16 && (c == 1 || merge <= (size_t)LDS_STEP_BYTES)) {
+    if (nblk * c <= 16 && (c == 1 || (size_t)(c / 2) * nblk <= areas_in_ring)) {
       PL = c;
       break;
     }
@@ -756,6 +797,8 @@ static bool lds_shape(int D, int nblk, int* pl, int* ppl, int* lpw) {
   // Q staged apart from the ring (it does not fit one slot: D = 128 with one page lane) -> one page per lane per step,
   // so ring + Q stay within the 160 KB of LDS.
   if ((16 / PL) * (D / 32) * 1024 > pps * pageb) pps = PL;
+  *qb = 1;
+  *nrg = nblk;
   *pl = PL;
   *ppl = pps / PL;
   *lpw = (pps * cpg + nblk * PL - 1) / (nblk * PL);
@@ -779,19 +822,21 @@ void attn_plan(AttnParams& p, int D, int cus) {
     p.pps = (p.npages + S - 1) / S;
     p.S = (p.npages + p.pps - 1) / p.pps;
   };
-  int pl = 0, ppl = 0, lpw = 0;
+  int qb = 1, nrg = 0, pl = 0, ppl = 0, lpw = 0;
   // LDS-ring kernel: one workgroup per (KV head, split) holding all rows; enough workgroups for every CU (two per
   // CU for small ones); splits no longer than its LDS block table.
-  if (lds_shape(D, nblk, &pl, &ppl, &lpw) && (p.npages + 63) / 64 <= LDS_BT_MAX) {
+  if (lds_shape(D, nblk, &qb, &nrg, &pl, &ppl, &lpw) && (p.npages + 63) / 64 <= LDS_BT_MAX) {
     p.lds = 1;
     p.nrb = nblk;
+    p.qb = qb;
+    p.nrg = nrg;
     p.pl = pl;
     p.ppl = ppl;
     p.lpw = lpw;
     p.RG = 1;
     p.QB = 1;
     p.R = 16 * nblk;
-    p.OCC = nblk * pl <= 8 ? 2 : 1;
+    p.OCC = nrg * pl <= 8 ? 2 : 1;
     int S = S_req;
     if (S <= 0) {
       // Up to 4 row blocks a split streams pages at the HBM rate and three quarters of the workgroup slots measured
@@ -844,26 +889,32 @@ static int launch_split(const AttnParams& p, int D, hipStream_t s) {
   if (p.lds) {
     // instantiated shapes (see lds_shape), as (PL, PPL, LPW): D = 64: (4, 1, 8 | 4 | 3 | 2), (2, 2, 4 | 3 | 2),
     // (1, 4, 4 | 3 | 2); D = 128: (2, 1, 16 | 8 | 6 | 4 | 3 | 2), (1, 1, 2 | 1)
+    if (p.qb == 3) {
+      if (D != 64 || p.nrg != 3 || p.pl != 4 || p.ppl != 1 || p.lpw != 3) return DSPARK_EUNSUPPORTED;
+      launch_lds<64, 3, 4, 1, 3, 12>(p, s);
+      return 0;
+    }
+    if (p.qb != 1) return DSPARK_EUNSUPPORTED;
     const int key = D * 10000 + p.pl * 1000 + p.ppl * 100 + p.lpw;
     switch (key) {
-      case 644108: launch_lds<64, 4, 1, 8>(p, s); break;
-      case 644104: launch_lds<64, 4, 1, 4>(p, s); break;
-      case 644103: launch_lds<64, 4, 1, 3>(p, s); break;
-      case 644102: launch_lds<64, 4, 1, 2>(p, s); break;
-      case 642204: launch_lds<64, 2, 2, 4>(p, s); break;
-      case 642203: launch_lds<64, 2, 2, 3>(p, s); break;
-      case 642202: launch_lds<64, 2, 2, 2>(p, s); break;
-      case 641404: launch_lds<64, 1, 4, 4>(p, s); break;
-      case 641403: launch_lds<64, 1, 4, 3>(p, s); break;
-      case 641402: launch_lds<64, 1, 4, 2>(p, s); break;
-      case 1282116: launch_lds<128, 2, 1, 16>(p, s); break;
-      case 1282108: launch_lds<128, 2, 1, 8>(p, s); break;
-      case 1282106: launch_lds<128, 2, 1, 6>(p, s); break;
-      case 1282104: launch_lds<128, 2, 1, 4>(p, s); break;
-      case 1282103: launch_lds<128, 2, 1, 3>(p, s); break;
-      case 1282102: launch_lds<128, 2, 1, 2>(p, s); break;
-      case 1281102: launch_lds<128, 1, 1, 2>(p, s); break;
-      case 1281101: launch_lds<128, 1, 1, 1>(p, s); break;
+      case 644108: launch_lds<64, 1, 4, 1, 8, 16>(p, s); break;
+      case 644104: launch_lds<64, 1, 4, 1, 4, 16>(p, s); break;
+      case 644103: launch_lds<64, 1, 4, 1, 3, 16>(p, s); break;
+      case 644102: launch_lds<64, 1, 4, 1, 2, 16>(p, s); break;
+      case 642204: launch_lds<64, 1, 2, 2, 4, 16>(p, s); break;
+      case 642203: launch_lds<64, 1, 2, 2, 3, 16>(p, s); break;
+      case 642202: launch_lds<64, 1, 2, 2, 2, 16>(p, s); break;
+      case 641404: launch_lds<64, 1, 1, 4, 4, 16>(p, s); break;
+      case 641403: launch_lds<64, 1, 1, 4, 3, 16>(p, s); break;
+      case 641402: launch_lds<64, 1, 1, 4, 2, 16>(p, s); break;
+      case 1282116: launch_lds<128, 1, 2, 1, 16, 16>(p, s); break;
+      case 1282108: launch_lds<128, 1, 2, 1, 8, 16>(p, s); break;
+      case 1282106: launch_lds<128, 1, 2, 1, 6, 16>(p, s); break;
+      case 1282104: launch_lds<128, 1, 2, 1, 4, 16>(p, s); break;
+      case 1282103: launch_lds<128, 1, 2, 1, 3, 16>(p, s); break;
+      case 1282102: launch_lds<128, 1, 2, 1, 2, 16>(p, s); break;
+      case 1281102: launch_lds<128, 1, 1, 1, 2, 16>(p, s); break;
+      case 1281101: launch_lds<128, 1, 1, 1, 1, 16>(p, s); break;
       default: return DSPARK_EUNSUPPORTED;
     }
   } else if (D == 64 && p.OCC == 2) {

@@ -33,6 +33,7 @@ struct AttnParams {
   int page0, npages, pps, S;  // logical page range and its split
   int RG, QB, R, OCC;         // row groups, 16-row blocks per wave, rows per group, workgroups per CU
   int lds, nrb, pl, ppl, lpw; // LDS-ring kernel: row blocks, page lanes, pages per lane per step, loads per wave per step
+  int qb, nrg;                // LDS-ring kernel: row blocks per wave, row groups (waves per page lane, nrg * qb >= nrb)
   int full_lo, full_hi;       // pages inside [full_lo, full_hi] need no mask
   float c;                    // log2(e) / sqrt(D)
 };
