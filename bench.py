@@ -386,6 +386,29 @@ def greedy_chain(eng, host, torch, a0, anchor, n):
     return chain
 
 
+def phase_times(eng, host, torch, mode, a0, anchor, rounds=5):
+    """Mean microseconds per round of each phase, from traced rounds (the phase trace, dspark_engine_trace): the time
+    from the previous mark to the phase's own mark; traced rounds carry one extra kernel per mark."""
+    import collections
+    engine_state(eng, a0, anchor)
+    eng.trace(True)
+    for _ in range(rounds):
+        eng.round(mode, a0)
+    torch.cuda.synchronize()
+    marks = eng.trace_read()
+    eng.trace(False)
+    acc = collections.OrderedDict()
+    for (r0, _, c0), (r1, p1, c1) in zip(marks, marks[1:]):
+        if r1 != r0:
+            continue
+        name = host.trace_phase_name(p1)
+        if name.startswith("verify_L"):
+            name = "verify_layers"
+        acc[name] = acc.get(name, 0.0) + (c1 - c0) / 1e3
+    nr = len({r for (r, _, _) in marks}) or 1
+    return {k: round(v / nr, 1) for k, v in acc.items()}
+
+
 def run_rounds(eng, torch, mode, a0, anchor, warmup, rounds, hist=False):
     """Timed rounds from position a0; returns (ms per round, committed tokens per round, per-round accepted)."""
     stream = torch.cuda.current_stream()
@@ -475,6 +498,7 @@ def bench_engine(args, host, torch, workload):
             rec["planted_p"] = round(p, 4)
             rec["planted_tau_expected"] = round(1 + sum(p ** k for k in range(1, desc.max_drafts + 1)), 3)
             rec["max_drafts"] = desc.max_drafts
+        rec["phase_us"] = phase_times(eng, host, torch, 0 if plant is None else -1, a0, anchor)
         rec.update({"ms_per_round": round(ms, 4), "tokens_per_round": round(committed, 3),
                     "tok_s": round(committed / (ms * 1e-3), 1)})
         if isinstance(plant, tuple):

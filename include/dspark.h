@@ -303,6 +303,27 @@ typedef struct dspark_launch_result {
 int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* args, int32_t* out_tokens, int32_t max_out,
                          dspark_launch_result* result, dspark_stream_t stream);
 
+/* Phase tracing. With tracing on, every round records a mark after each of its phases (the round's HIP graph gains a
+ * one-thread kernel per mark that stores the GPU's constant-rate clock; marks cost about a kernel launch each, so
+ * traced rounds run a little slower). dspark_engine_trace_read copies the marks recorded since tracing was turned on:
+ * out[2 i] = phase (DSPARK_TRACE_* below; verify layer L is DSPARK_TRACE_VERIFY_LAYER + L) | round << 32, out[2 i + 1]
+ * = the clock in nanoseconds; *n = the number of marks (at most DSPARK_TRACE_MAX_MARKS are kept). The difference of
+ * consecutive marks is the time of a phase. Replaces the reference's trace buffer (trace_mark, dspark.hip:384-391;
+ * LFM3_DS_TRACE, internal/model/dstrace.go). */
+enum {
+  DSPARK_TRACE_BEGIN = 0,        /* round started (State checked, keys cleared) */
+  DSPARK_TRACE_CONTEXT = 1,      /* context projection into the drafter ring */
+  DSPARK_TRACE_DRAFTER = 2,      /* drafter layers */
+  DSPARK_TRACE_CROP_HEAD = 3,    /* cropped head */
+  DSPARK_TRACE_MARKOV = 4,       /* Markov / confidence drafts */
+  DSPARK_TRACE_LM_HEAD = 5,      /* final norm + LM head */
+  DSPARK_TRACE_COMMIT = 6,       /* argmax + acceptance + commit */
+  DSPARK_TRACE_VERIFY_LAYER = 16 /* + L: target layer L of the verify pass */
+};
+#define DSPARK_TRACE_MAX_MARKS 65536
+int dspark_engine_trace(dspark_engine* e, int32_t enable, dspark_stream_t stream);
+int dspark_engine_trace_read(dspark_engine* e, uint64_t* out, int32_t cap, int32_t* n);
+
 /* token id of an argmax key */
 static inline int32_t dspark_key_token(uint64_t key) { return (int32_t)(0xFFFFFFFFu - (uint32_t)key); }
 

@@ -125,6 +125,9 @@ struct dspark_engine {
   float host_lp[4] = {1.f, 1.f, 0.f, 0.f};
   // recorded rounds: key (force_m, plan bucket) -> graph
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  // phase tracing: marks [2 + 2 DSPARK_TRACE_MAX_MARKS] u64 (count, round | active, then (phase, clock) pairs)
+  uint64_t* trace = nullptr;
+  bool trace_on = false;
   std::vector<void*> allocs;
 
   ~dspark_engine() {
@@ -361,6 +364,12 @@ constexpr int ENGINE_BANDS = 2;
     if (_rc) return _rc;     \
   } while (0)
 
+// A trace mark after a phase (tracing rounds only): one thread stores (phase | round << 32, clock).
+int mark(dspark_engine* e, int phase, hipStream_t s) {
+  if (!e->trace_on) return 0;
+  return trace_mark_launch(e->trace, e->st, phase, phase == DSPARK_TRACE_BEGIN, DSPARK_TRACE_MAX_MARKS, s);
+}
+
 // The context projection from its fc GEMM on (dspark.hip:2682-2705, 2487-2518; dspark.go:461-492): x_fc (the normed
 // taps of B positions, [B][n_taps * H]: the round's x16 in operand order, or row-major prompt taps) -> fc -> hidden
 // norm -> ckv -> per drafter layer k norm + RoPE, K/V rows into the drafter ring at positions State.ctx_pos + t for
@@ -391,6 +400,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
   uint64_t* mbest = e->keys + B;
   e->ast = e->st;
   CK(round_begin_launch(e->st, e->keys, 2 * B, e->seen, B, e->max_context + B, d.vocab, e->max_context + 2 * B, s));
+  CK(mark(e, DSPARK_TRACE_BEGIN, s));
   if (force_m > 0) {
     CK(force_m_launch(e->st, force_m, s));
   } else {
@@ -411,6 +421,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
     CK(enqueue_context(e, e->x16, true, s));
+    CK(mark(e, DSPARK_TRACE_CONTEXT, s));
     // ---- drafter block
     CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
     int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
@@ -428,8 +439,10 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
       w2b = ENGINE_BANDS;
       CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
     }
+    CK(mark(e, DSPARK_TRACE_DRAFTER, s));
     CK(resnorm(e, e->h[cur], e->w2out, w2b, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
     CK(gemm(e, e->x16, B, H, e->crop_w, e->crop_s, e->crop_n, 0, e->base, nullptr, s));
+    CK(mark(e, DSPARK_TRACE_CROP_HEAD, s));
     MarkovParams mp = {};
     mp.st = e->st;
     mp.base = e->base;
@@ -453,6 +466,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     mp.s1c = e->ms1c;
     CK(markov_launch(mp, s));
     if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, reinterpret_cast<const int32_t*>(e->rep + 2), s));
+    CK(mark(e, DSPARK_TRACE_MARKOV, s));
   }
   // ---- verify
   CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
@@ -477,6 +491,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
     w2b = ENGINE_BANDS;
     CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
+    CK(mark(e, DSPARK_TRACE_VERIFY_LAYER + i, s));
   }
   {
     const LayerW& P = e->L[d.n_layers - 1];
@@ -484,9 +499,11 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     CK(resnorm(e, e->h[cur], e->w2out, w2b, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
   }
   CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
+  CK(mark(e, DSPARK_TRACE_LM_HEAD, s));
   CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep, false));
   CK(accept_commit_fold_launch(e->st, static_cast<const uint64_t*>(e->ws_argmax), verify_argmax_chunks(d.vocab), B, vbest,
                                e->out_tokens, e->max_context + 2 * B, e->seen, s));
+  CK(mark(e, DSPARK_TRACE_COMMIT, s));
   return 0;
 }
 
@@ -677,6 +694,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->out_tokens = static_cast<int32_t*>(e->alloc("out_tokens", (size_t)(max_context + 2 * B) * 4, &err));
   e->plant = static_cast<int32_t*>(e->alloc("plant", (size_t)(positions + B + 1) * 4, &err));
   e->rep = static_cast<float*>(e->alloc("rep", 16, &err));
+  e->trace = static_cast<uint64_t*>(e->alloc("trace", (size_t)(2 + 2 * DSPARK_TRACE_MAX_MARKS) * 8, &err));
   e->x_cols = std::max(std::max(H, d.n_taps * H), std::max(d.ffn, d.draft_ffn));
   e->mix_cols = std::max(std::max(3 * H, align16(QH * D + 2 * KVH * D + QH)), ckv_rows);
   e->h[0] = static_cast<float*>(e->alloc("h0", (size_t)B * H * 4, &err));
@@ -867,7 +885,7 @@ int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspar
     if (rc) return rc;
   }
   const int bucket = plan_a / ROUND_PLAN_BUCKET;
-  const auto key = std::make_pair((int)force_m, bucket);
+  const auto key = std::make_pair((int)force_m + (e->trace_on ? 1000 : 0), bucket);
   auto it = e->graphs.find(key);
   if (it == e->graphs.end()) {
     // Record the round on a private stream (capture needs a non-default stream), then replay it on `stream`.
@@ -960,6 +978,31 @@ int dspark_engine_conv_copy(dspark_engine* e, int32_t src, int32_t dst, dspark_s
   if (!e || src < 0 || dst < 0 || src >= e->conv.slots || dst >= e->conv.slots) return DSPARK_EINVAL;
   if (src == dst) return 0;
   return conv_copy_launch(e->conv, src, dst, reinterpret_cast<hipStream_t>(stream));
+}
+
+int dspark_engine_trace(dspark_engine* e, int32_t enable, dspark_stream_t stream) {
+  if (!e) return DSPARK_EINVAL;
+  e->trace_on = enable != 0;
+  if (!e->trace_on) return 0;
+  // a fresh trace: count and round counter to zero (outside any graph)
+  return (int)hipMemsetAsync(e->trace, 0, 16, reinterpret_cast<hipStream_t>(stream));
+}
+
+int dspark_engine_trace_read(dspark_engine* e, uint64_t* out, int32_t cap, int32_t* n) {
+  if (!e || !n || cap < 0 || (cap > 0 && !out)) return DSPARK_EINVAL;
+  if (hipDeviceSynchronize() != hipSuccess) return DSPARK_EINVAL;
+  uint64_t head[2];
+  if (hipMemcpy(head, e->trace, 16, hipMemcpyDeviceToHost) != hipSuccess) return DSPARK_EINVAL;
+  const int total = (int)std::min<uint64_t>(head[0], DSPARK_TRACE_MAX_MARKS);
+  *n = total;
+  const int k = std::min(total, cap);
+  if (k > 0 && hipMemcpy(out, e->trace + 2, (size_t)k * 16, hipMemcpyDeviceToHost) != hipSuccess) return DSPARK_EINVAL;
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
+      khz <= 0)
+    return DSPARK_EUNSUPPORTED;
+  for (int i = 0; i < k; ++i) out[2 * i + 1] = (uint64_t)((double)out[2 * i + 1] * 1e6 / khz);  // ticks -> ns
+  return 0;
 }
 
 int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t* out_tokens, int32_t max_out,

@@ -499,6 +499,31 @@ __global__ void force_m_kernel(dspark_state* st, int m) {
   st->M = m;
 }
 
+// Phase trace mark (one thread; stream order makes the marks of a round sequential, so no atomics): the clock is the
+// constant-rate wall clock, read first. buf[1] = rounds opened << 1 | whether the current round runs.
+__global__ void trace_mark_kernel(uint64_t* buf, const dspark_state* st, int phase, int begin, int max_marks) {
+  if (threadIdx.x != 0) return;
+  const uint64_t clk = wall_clock64();
+  if (begin) {
+    const uint64_t active = st->run != 0 ? 1 : 0;
+    buf[1] = (((buf[1] >> 1) + active) << 1) | active;
+    if (!active) return;
+  } else if (!(buf[1] & 1)) {
+    return;
+  }
+  const uint64_t round = (buf[1] >> 1) - 1, i = buf[0];
+  if (i < (uint64_t)max_marks) {
+    buf[2 + 2 * i] = (uint64_t)(uint32_t)phase | (round << 32);
+    buf[3 + 2 * i] = clk;
+  }
+  buf[0] = i + 1;
+}
+
+int trace_mark_launch(uint64_t* buf, const dspark_state* st, int phase, int begin, int max_marks, hipStream_t s) {
+  hipLaunchKernelGGL(trace_mark_kernel, dim3(1), dim3(64), 0, s, buf, st, phase, begin, max_marks);
+  return (int)hipGetLastError();
+}
+
 // Planted drafts (benchmarks of a set acceptance rate on random-init models): after the drafter has run, its drafts
 // are replaced by plant[a + 1 .. a + M - 1], with M = 1 + the drafter's cap on drafts this round (the same cap
 // markov_kernel applies, so limit and budget still bound the round).

@@ -354,7 +354,17 @@ _SIGS.update({
                                                  ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_engine_project_prompt": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_engine_conv_copy": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_engine_trace": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_engine_trace_read": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                                ctypes.POINTER(ctypes.c_int32)]),
 })
+
+TRACE_PHASES = {0: "begin", 1: "context", 2: "drafter", 3: "crop_head", 4: "markov", 5: "lm_head", 6: "commit"}
+TRACE_VERIFY_LAYER = 16
+
+
+def trace_phase_name(phase):
+    return TRACE_PHASES.get(phase, f"verify_L{phase - TRACE_VERIFY_LAYER}")
 
 
 def rope_table(base, pairs, head_dim, positions):
@@ -479,6 +489,20 @@ class Engine:
     def project_prompt(self, first, end, stream=None):
         check(lib().dspark_engine_project_prompt(self.h, first, end, stream_handle(stream)),
               "dspark_engine_project_prompt")
+
+    def trace(self, enable=True, stream=None):
+        """Phase tracing on (a fresh trace) or off for the rounds enqueued after this call."""
+        check(lib().dspark_engine_trace(self.h, int(enable), stream_handle(stream)), "dspark_engine_trace")
+
+    def trace_read(self, cap=65536):
+        """The marks since tracing was turned on: list of (round, phase, clock ns)."""
+        import numpy as np
+        out = np.zeros(2 * cap, np.uint64)
+        n = ctypes.c_int32()
+        check(lib().dspark_engine_trace_read(self.h, out.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(n)),
+              "dspark_engine_trace_read")
+        k = min(n.value, cap)
+        return [(int(out[2 * i]) >> 32, int(out[2 * i]) & 0xFFFFFFFF, int(out[2 * i + 1])) for i in range(k)]
 
     def conv_copy(self, src, dst, stream=None):
         check(lib().dspark_engine_conv_copy(self.h, src, dst, stream_handle(stream)), "dspark_engine_conv_copy")

@@ -336,3 +336,45 @@ def test_init_seen(dev):
     torch.cuda.synchronize()
     assert not eng.download("seen", np.uint32).any() and eng.download("rep", np.float32)[0] == 1.0
     eng.close()
+
+
+def test_phase_trace(dev):
+    """Traced rounds record every phase in order (begin, context, drafter, crop head, Markov, each verify layer, LM head,
+    commit) with a non-decreasing clock, number the rounds that run, record nothing for a stopped round, and commit
+    the same tokens as untraced rounds from the same start."""
+    torch = dev
+    host = load_host()
+    desc = host.model_desc(**GEOMETRIES["small"])
+    eng = host.Engine(desc, 512)
+    make_weights(eng, desc, 45)
+    setup_caches(eng, host, desc, A0, CTX_LO, 145)
+    print("case phase trace", flush=True)
+    rings = conv_rings(eng)
+    st0 = dict(a=A0, anchor=ANCHOR, count=0, rounds_left=3, limit=eng.max_context, budget=512, eos=-1, ctx_new=1,
+               ctx_pos=A0 - 1, ctx_lo=CTX_LO, run=1, skip_rounds=1, stop_at=eng.max_context, ckpt_slot=-1,
+               tokens=[ANCHOR])
+    outs = []
+    for traced in (False, True):
+        for nm, buf in rings.items():
+            eng.upload(nm, buf)
+        eng.init_seen([])
+        eng.set_state(**st0)
+        eng.trace(traced)
+        for _ in range(4):  # the fourth round finds run == 0 (rounds_left was 3)
+            eng.round(0, A0)
+        torch.cuda.synchronize()
+        st = eng.state()
+        outs.append((st.count, eng.download("out_tokens", np.int32)[:st.count].tolist(),
+                     [getattr(st, f) for f in host.STATE_FIELDS]))
+    assert outs[0] == outs[1]
+    marks = eng.trace_read()
+    eng.trace(False)
+    per_round = [host.TRACE_PHASES[p] for p in (0, 1, 2, 3, 4)] + \
+        [f"verify_L{i}" for i in range(desc.n_layers)] + ["lm_head", "commit"]
+    assert len(marks) == 3 * len(per_round), len(marks)
+    for r in range(3):
+        got = [host.trace_phase_name(p) for (rr, p, _) in marks[r * len(per_round):(r + 1) * len(per_round)]]
+        assert got == per_round and all(rr == r for (rr, _, _) in marks[r * len(per_round):(r + 1) * len(per_round)])
+    clocks = [c for (_, _, c) in marks]
+    assert all(b >= a for a, b in zip(clocks, clocks[1:])) and clocks[-1] > clocks[0]
+    eng.close()
