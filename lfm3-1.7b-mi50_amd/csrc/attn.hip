@@ -610,13 +610,15 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
 #undef DSPARK_LDSP
 
 // ---------------------------------------------------------------- merge of the split partials
-// Four lanes per output quad (row r, dims 4 c4 .. + 3): lane j takes splits j, j + 4, ... with all its loads in flight
-// and merges them as an online log-sum-exp (m = max, l = sum f_s l_s, acc = sum f_s acc_s, f_s = exp2(m_s - m)); the
-// four lanes then merge in the fixed order ((0 + 1) + 2) + 3, so outputs are bit-identical run to run. o = acc / l (0
-// when nothing was visible), times the optional sigmoid gate, stored fp16 and/or fp32. blockIdx.y = KV head x row
-// group. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
+// COMBINE_LANES lanes per output quad (row r, dims 4 c4 .. + 3): lane j takes splits j, j + COMBINE_LANES, ... with
+// all its loads in flight and merges them as a log-sum-exp (m = max, l = sum f_s l_s, acc = sum f_s acc_s,
+// f_s = exp2(m_s - m)); the lanes then merge pairwise in a fixed tree (lanes 1, 2, 4 apart), so outputs are
+// bit-identical run to run. o = acc / l (0 when nothing was visible), times the optional sigmoid gate, stored fp16
+// and/or fp32. blockIdx.y = KV head x row group. Eight lanes of at most 8 splits each measured 3.6-3.9 us per C2 merge
+// against 4.4 us for four lanes of 16. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60
+// workgroups' key ranges).
 #ifndef DSPARK_ATTN_COMBINE_LANES
-#define DSPARK_ATTN_COMBINE_LANES 4
+#define DSPARK_ATTN_COMBINE_LANES 8
 #endif
 constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 64 / COMBINE_LANES;  // S <= 64
 
@@ -655,16 +657,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
       acc += f * av[i];
     }
   }
-  // lanes 1..3 hand their own (unmerged) states to lane 0 of the quad
-  const int base_lane = (int)(threadIdx.x & 63) & ~(COMBINE_LANES - 1);
-  const float m_own = m, l_own = l;
-  const f32x4 a_own = acc;
 #pragma unroll
-  for (int k = 1; k < COMBINE_LANES; ++k) {
-    const float mk = __shfl(m_own, base_lane + k), lk = __shfl(l_own, base_lane + k);
+  for (int off = 1; off < COMBINE_LANES; off <<= 1) {
+    const float mk = __shfl_xor(m, off), lk = __shfl_xor(l, off);
     f32x4 ak;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ak[i] = __shfl(a_own[i], base_lane + k);
+    for (int i = 0; i < 4; ++i) ak[i] = __shfl_xor(acc[i], off);
     const float mx = fmaxf(m, mk);
     if (mx > -INFINITY) {
       const float fa = m == -INFINITY ? 0.f : fast_exp2(m - mx), fb = mk == -INFINITY ? 0.f : fast_exp2(mk - mx);
