@@ -137,7 +137,9 @@ __device__ __forceinline__ void page_prep(const AttnParams& p, int lpage, int ro
   for (int qb = 0; qb < QB; ++qb) {
     const f32x4 a = s[qb][0], b = s[qb][1];
     tmax[qb] = fmaxf(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])), fmaxf(fmaxf(b[0], b[1]), fmaxf(b[2], b[3])));
-    need = need || (rs.m[qb] == M_INIT ? tmax[qb] > -INFINITY : tmax[qb] > TAU);
+    // bitwise, not ||: a short-circuit here compiles to exec-mask branches on every page
+    const float thr = rs.m[qb] == M_INIT ? -INFINITY : TAU;
+    need = need | (tmax[qb] > thr);
   }
   if (__builtin_amdgcn_ballot_w64(need) != 0) {
     // Some row passed its running max by more than TAU (or saw its first key): move that row's max up to its page
