@@ -13,7 +13,8 @@ Prints one JSON line (the driver's contract) with a `roofline` object for the do
 fp32 restatement timed on a bounded sample of the same workload, on all CPUs of the job's share and on one). The same
 line carries the metric's other half, `headline_tok_s` (greedy decode tok/s of full DSpark rounds at 1k / 32k / 128k
 context, beside the reference's published MI50 numbers), and `c5_attention` (verify attention at 131072 keys for 33 and
-16 verify tokens). `--c2-only` skips those two; `--workload` selects the other configs (c3, c4, c5, tiers, ref).
+16 verify tokens). `--c2-only` skips those two; `--workload` selects the other configs (c3, c4, c5, tiers, ref), or
+verify attention alone at any context and block (`attn`, `--ctx`, `--tokens`).
 """
 import argparse
 import ctypes
@@ -543,7 +544,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy", "attn"])
+    ap.add_argument("--ctx", type=int, default=131072, help="attn workload: context (keys before the block)")
+    ap.add_argument("--tokens", type=int, default=33, help="attn workload: verify tokens (M)")
+    ap.add_argument("--layers", type=int, default=2, help="attn workload: layers per step")
     ap.add_argument("--c2-only", action="store_true",
                     help="default workload without the headline tiers and the C5 attention fields")
     args = ap.parse_args()
@@ -561,6 +565,16 @@ def main():
     host = load_host()
     if args.workload == "c3":
         print(json.dumps(bench_c3(args, host, torch)), flush=True)
+        return
+    if args.workload == "attn":
+        # verify attention alone (the C2 kernels) at any context and block: what the C5 attention profiles run
+        r = bench_attention(args, host, torch, args.layers, args.ctx, args.tokens, 2)
+        print(json.dumps({"metric": "verify attention HBM GB/s", "workload": "attn", "ctx": args.ctx,
+                          "verify_tokens": args.tokens, "layers": args.layers, "steps": args.steps,
+                          "ms_per_layer": round(r["ms_per_step"] / args.layers, 5),
+                          "step_GBs": round(r["step_gbs"], 1), "split_avg_us": round(r["split_avg_ms"] * 1e3, 2),
+                          "split_frac": round(r["split_gbs"] / HBM_PEAK_GBS, 4),
+                          "merge_avg_us": round(r["merge_avg_ms"] * 1e3, 2)}), flush=True)
         return
     if args.workload in ("c4", "c5", "tiers", "ref"):
         print(json.dumps(bench_engine(args, host, torch, args.workload)), flush=True)
