@@ -410,6 +410,25 @@ def phase_times(eng, host, torch, mode, a0, anchor, rounds=5):
     return {k: round(v / nr, 1) for k, v in acc.items()}
 
 
+def round_bytes(eng, desc, a):
+    """Algorithmic HBM bytes of one round at anchor position a: every GEMM weight and scale (int8 target and drafter
+    layers, LM head, fp16 cropped head, conv taps) read once; the K/V each attention layer reads (full layers: the a
+    cached positions plus the block; sliding layers: the window plus the block; drafter layers: the ring window plus
+    the block); one Markov table row and one cropped-head row per draft step. Returns (round bytes, target K/V bytes)."""
+    w = sum(eng.tensor(n)[1] for n in eng.names() if n.endswith((".w", ".s")) and not n.startswith("markov."))
+    B = desc.block
+    row = desc.kv_heads * desc.head_dim * 2 * 2  # K and V bytes per position
+    kv = 0
+    for i in range(desc.n_layers):
+        if desc.layer_kind[i] == 1:
+            kv += (a + B) * row
+        elif desc.layer_kind[i] == 2:
+            kv += (min(desc.window, a) + B) * row
+    ring = desc.draft_layers * (min(desc.draft_window, a) + B) * row
+    chain = desc.max_drafts * 2 * desc.crop_rows * 4
+    return w + kv + ring + chain, kv
+
+
 def run_rounds(eng, torch, mode, a0, anchor, warmup, rounds, hist=False):
     """Timed rounds from position a0; returns (ms per round, committed tokens per round, per-round accepted)."""
     stream = torch.cuda.current_stream()
@@ -502,6 +521,9 @@ def bench_engine(args, host, torch, workload):
         rec["phase_us"] = phase_times(eng, host, torch, 0 if plant is None else -1, a0, anchor)
         rec.update({"ms_per_round": round(ms, 4), "tokens_per_round": round(committed, 3),
                     "tok_s": round(committed / (ms * 1e-3), 1)})
+        rb, kvb = round_bytes(eng, desc, a0)
+        rec.update({"round_bytes": rb, "verify_kv_bytes": kvb, "round_GBs": round(rb / (ms * 1e-3) / 1e9, 1),
+                    "round_frac": round(rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
         if isinstance(plant, tuple):
             # A round verifies the same tokens whatever is accepted, so its time does not depend on the draws: the
             # rate at exactly the MI50's committed tokens per round is tau / round time (the realised rate above
