@@ -399,10 +399,11 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 // K-sliced GEMM for one workgroup of S x KW waves (S = wpg strips of 16 rows, KW = kw contiguous ranges of K): wave
 // (s, k) = (wave % S, wave / S) streams strip s over range k with every weight load of the range in flight at once, the
 // KW sums of a strip are added in LDS in range order by the k = 0 waves, and nothing leaves the workgroup before the
-// epilogue (no split partials, no arrival counters). X: XD = false stages the whole of X^T in LDS once for all waves
-// (TB * K / 64 * 2 KB <= 64 KB); XD = true (S = 1, TB = 1) has every wave load its own range of X straight into B
-// operands. Ranges longer than CPW chunks go in batches of CPW. Chunk order inside a range, then range order, fixes the
-// summation order, so results do not depend on timing.
+// epilogue (no split partials, no arrival counters). X: XD = false stages X^T of the band in LDS for all waves, every
+// token block at once when that is at most 64 KB, else one token block (at most 64 KB) per pass with the range's
+// weights held in registers (up to 4 token blocks); XD = true (TB = 1) has every wave load its own range of X straight
+// into B operands. Ranges longer than CPW chunks go in batches of CPW. Chunk order inside a range, then range order,
+// fixes the summation order, so results do not depend on timing.
 template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
@@ -496,34 +497,63 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   } else {
     // X^T rows [tb][chunk][half] of 1 KB (lane l's 16 B at 16 l: token 16 tb + l % 16, columns 64 c + 16 (l / 16) +
     // 8 h), loaded straight into LDS by the waves in turn; then this wave's first weight batch, so the counted wait
-    // covers X (the oldest loads) and leaves the weights in flight
+    // covers X (the oldest loads) and leaves the weights in flight. At most 64 KB of X^T at a time: when the band's
+    // X^T for every token block does not fit, the token blocks come one per pass, and the range's weights (one batch:
+    // the plan keeps the range within CPW chunks) stay in registers across the passes.
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         (void*)p.x, (short)0, (int)((size_t)(p.xop ? 16 * p.xop : p.M) * p.K * 2), 0x00020000);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const int bc = b1 - b0;  // the band's chunks: X^T rows [tb][chunk - b0][half]
-    for (int r = wave_u; r < TB * bc * 2; r += nw) {
-      const int h = r & 1, j = b0 + (r >> 1) % bc, tb = (r >> 1) / bc;
-      const int t = 16 * tb + n;
-      if (t < p.M) {
-        const uint32_t off = p.xop ? (uint32_t)(((((size_t)j * p.xop + tb) * 2 + h) * 64 + lane) * 16)
-                                   : (uint32_t)(((size_t)t * p.K + j * 64 + 16 * g + 8 * h) * 2);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off, 0,
-                                                 0, 0);
+    const int bc = b1 - b0;  // the band's chunks: X^T rows [tb - t0][chunk - b0][half]
+    const bool all = TB * cpb_ <= 32;  // every token block's X^T in one 64 KB stage (the host sizes LDS the same way)
+    auto stage = [&](int t0) {
+      const int nt = all ? TB : 1;
+      for (int r = wave_u; r < nt * bc * 2; r += nw) {
+        const int h = r & 1, j = b0 + (r >> 1) % bc, tb = t0 + (r >> 1) / bc;
+        const int t = 16 * tb + n;
+        if (t < p.M) {
+          const uint32_t off = p.xop ? (uint32_t)(((((size_t)j * p.xop + tb) * 2 + h) * 64 + lane) * 16)
+                                     : (uint32_t)(((size_t)t * p.K + j * 64 + 16 * g + 8 * h) * 2);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(xs + r * 64), 16, off,
+                                                   0, 0, 0);
+        }
       }
-    }
+    };
+    stage(0);
     load(w, c0);
     __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPW * WV));
     __builtin_amdgcn_s_barrier();
-    for (int cb = c0; cb < c1; cb += CPW) {
-      if (cb != c0) load(w, cb);
+    if (all || CPW > 8) {  // (16-chunk batches: the plan never takes passes)
+      for (int cb = c0; cb < c1; cb += CPW) {
+        if (cb != c0) load(w, cb);
 #pragma unroll
-      for (int i = 0; i < CPW; ++i) {
-        if (cb + i < c1) {
-          half8 a[2];
-          weights(w[i], a);
+        for (int i = 0; i < CPW; ++i) {
+          if (cb + i < c1) {
+            half8 a[2];
+            weights(w[i], a);
 #pragma unroll
-          for (int tb = 0; tb < TB; ++tb) {
-            const u32x4* xb = xs + ((size_t)(tb * (b1 - b0) + cb + i - b0) * 2) * 64;
+            for (int tb = 0; tb < TB; ++tb) {
+              const u32x4* xb = xs + ((size_t)(tb * bc + cb + i - b0) * 2) * 64;
+              acc[tb] = mfma16x16x32(a[0], as_half8(xb[lane]), acc[tb]);
+              acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + lane]), acc[tb]);
+            }
+          }
+        }
+      }
+    } else if constexpr (CPW <= 8) {
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        if (tb > 0) {
+          __syncthreads();  // every wave is done with the previous pass's X^T
+          stage(tb);
+          __builtin_amdgcn_s_waitcnt(0);
+          __builtin_amdgcn_s_barrier();
+        }
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+          if (c0 + i < c1) {
+            half8 a[2];
+            weights(w[i], a);
+            const u32x4* xb = xs + ((size_t)(c0 + i - b0) * 2) * 64;
             acc[tb] = mfma16x16x32(a[0], as_half8(xb[lane]), acc[tb]);
             acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + lane]), acc[tb]);
           }
@@ -649,7 +679,8 @@ static bool gemm_sliced_xd(const GemmParams& p, bool i8) { return i8 && p.xd && 
 static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
   const int tb = (p.M + 15) / 16;
   const int bands = std::max(1, p.bands);
-  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)tb * ((p.K / 64 + bands - 1) / bands) * 2048;
+  const int bc = (p.K / 64 + bands - 1) / bands;  // X^T of the token blocks of one pass (all of them when they fit)
+  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)(tb * bc <= 32 ? tb : 1) * bc * 2048;
   const size_t red = (size_t)(p.kw - 1) * p.wpg * tb * 1024;
   const size_t tile = p.fuse ? (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float) : 0;
   return std::max(x, std::max(red, tile));
@@ -660,7 +691,7 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const int groups = (p.N / 16 + p.wpg - 1) / p.wpg;
   const dim3 grid(groups * p.bands), block(64 * p.wpg * p.kw);
   const size_t lds = gemm_sliced_lds_bytes(p, I8);
-  const int cpk = (p.K / 64 + p.kw - 1) / p.kw;
+  const int cpk = ((p.K / 64 + p.bands - 1) / p.bands + p.kw - 1) / p.kw;  // chunks per range (of the band's)
   if constexpr (I8) {
     if (TB == 1 && gemm_sliced_xd(p, I8)) {
       if (block.x <= 512)  // up to 8 waves: twice the registers per wave (no spills with the first batch peeled)
@@ -669,9 +700,11 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true>), grid, block, lds, s, p);
       return;
     }
-    if (cpk > 8) {  // 16-chunk batches of int8 weights: 64 VGPRs
-      hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 16, false>), grid, block, lds, s, p);
-      return;
+    if constexpr (TB <= 2) {
+      if (cpk > 8) {  // 16-chunk batches of int8 weights: 64 VGPRs (the plan keeps 3 or 4 token blocks within 8)
+        hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 16, false>), grid, block, lds, s, p);
+        return;
+      }
     }
   }
   hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 8, false>), grid, block, lds, s, p);
@@ -681,10 +714,12 @@ template <bool I8>
 static void launch_gemm(const GemmParams& p, hipStream_t s) {
   const int tb = (p.M + 15) / 16;
   if (p.kw > 0) {
-    if (tb == 1)
-      launch_sliced_tb<1, I8>(p, s);
-    else
-      launch_sliced_tb<2, I8>(p, s);
+    switch (tb) {
+      case 1: launch_sliced_tb<1, I8>(p, s); break;
+      case 2: launch_sliced_tb<2, I8>(p, s); break;
+      case 3: launch_sliced_tb<3, I8>(p, s); break;
+      default: launch_sliced_tb<4, I8>(p, s); break;
+    }
     return;
   }
   const int strips = p.N / 16;
@@ -719,26 +754,32 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // wider GEMMs take S = max(4, strips / 256) strips per group (at most 256 groups: 257 groups on 256 CUs measured
 // 14.2 us against 10.2 for 256) and 16 / S ranges, X loaded per wave for S <= 4 with operand-order X (16384 x 2048:
 // 9.6 against 10.3 us through LDS; equal at 3104 and 6144 rows, slower for S = 5 and 16), else staged in LDS once (at
-// most 64 KB). Returns false when no sliced plan fits (the split-K plan is used).
+// most 64 KB). Two to four token blocks (X through LDS) take the same groups, one token block's X^T per pass when all
+// of them exceed 64 KB (band at most 32 chunks, ranges of at most 8 chunks): 33 tokens, C5 round 2.19 -> 2.02 ms
+// against the split-K kernel. Returns false when no sliced plan fits (the split-K plan is used).
 static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, int max_bands, GemmPlan* pl) {
   const int strips = N / 16, chunks = K / 64;
-  if (!DSPARK_GEMM_SLICED || tb > 2) return false;
+  if (!DSPARK_GEMM_SLICED || tb > 4) return false;
   int S, KW, bands = 1;
   if (wpg_req > 0) {
     S = wpg_req;
     KW = 16 / S;
-  } else if (i8 && tb == 1 && strips <= 512 && (xop || K <= 4096)) {
+  } else if (i8 && strips <= 512 && (xop || K <= 4096)) {
     S = 1;
     // fewer than 256 strips: K in bands over more workgroups when the caller adds the bands (at least 8 chunks each)
     while (bands * 2 <= max_bands && strips * bands * 2 <= 256 && chunks / (bands * 2) >= 8) bands *= 2;
     const int bc = chunks / bands;
-    KW = xop ? std::min(8, std::max(4, (bc + 7) / 8)) : 4;  // ranges of at most 8 chunks: one batch per wave
+    // ranges of at most 8 chunks: one batch per wave (row-major X with one token block: four ranges)
+    KW = xop || tb > 1 ? std::min(8, std::max(4, (bc + 7) / 8)) : 4;
   } else {
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
   }
   const bool xd = i8 && tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S));
-  if (!xd && (size_t)tb * chunks * 2048 > 65536) return false;
+  // X^T through LDS: all token blocks at once when they fit 64 KB, else one token block per pass, each pass's X^T
+  // within 64 KB and each range within one 8-chunk batch (its weights stay in registers)
+  const int bc = (chunks + bands - 1) / bands, cpk = (bc + KW - 1) / std::max(1, KW);
+  if (!xd && (((size_t)tb * bc * 2048 > 65536 && (bc > 32 || cpk > 8)) || (tb > 2 && cpk > 8))) return false;
   pl->ksplit = 1;
   pl->bands = bands;
   pl->xd = xd;
@@ -794,7 +835,11 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
     // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
     const int tb = (p.M + 15) / 16;
     if (p.bands < 1) p.bands = 1;
-    if (p.ksplit != 1 || p.wpg < 1 || p.wpg * p.kw > 16 || tb > 2 || gemm_sliced_lds_bytes(p, i8) > 65536)
+    if (p.ksplit != 1 || p.wpg < 1 || p.wpg * p.kw > 16 || tb > 4 || gemm_sliced_lds_bytes(p, i8) > 65536)
+      return DSPARK_EINVAL;
+    // X^T in passes (it does not fit LDS for every token block at once): each range within one batch of weights
+    const int bc = (p.K / 64 + p.bands - 1) / p.bands, cpk = (bc + p.kw - 1) / p.kw;
+    if (!gemm_sliced_xd(p, i8) && (((size_t)tb * bc * 2048 > 65536 && (bc > 32 || cpk > 8)) || (tb > 2 && cpk > 8)))
       return DSPARK_EINVAL;
     // bands: plain scaled sums into y32 only (each band its own [M][N]), nothing fused
     if (p.bands > 1 && (p.epilogue != 0 || !p.y32 || p.y16 || p.best_part || p.fuse || p.bands > p.K / 64))
