@@ -10,6 +10,8 @@
 // workgroup of a row group to arrive add the split partials in split order (or a reduce kernel does). Weights are read
 // once per call for all tokens; both are HBM-bound (about 2*M flop per weight byte).
 // Reference: gemv_phase / unit_dot_r (dspark.hip:541-716), head_run<true> (2219-2318), markov argmax (2322-2366).
+#include <type_traits>
+
 #include "common.h"
 #include "dspark.h"
 #include "dspark_internal.h"
@@ -52,6 +54,14 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
     for (int i = 0; i < 4; ++i) h[i] = (_Float16)(p.epilogue == 2 ? silu_f(v[i]) : v[i]);
     *reinterpret_cast<half4*>(p.y16 + (p.yop ? xop_elem(t, r, p.yop) : (size_t)t * p.N + r)) = h;
   }
+}
+
+// X^T of a band staged in LDS by the K-sliced kernel (bytes): every token block at once when that fits, else passes
+// of two token blocks, else of one (each token block's X^T is the band's chunks x 2 KB).
+constexpr int GEMM_X_LDS = 131072;
+__host__ __device__ inline int gemm_pass_tbs(int tb, int band_chunks) {
+  if (tb * band_chunks * 2048 <= GEMM_X_LDS) return tb;
+  return 2 * band_chunks * 2048 <= GEMM_X_LDS ? 2 : 1;
 }
 
 // TB token blocks of 16. I8: weights biased int8, else fp16.
@@ -504,9 +514,9 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
         (void*)p.x, (short)0, (int)((size_t)(p.xop ? 16 * p.xop : p.M) * p.K * 2), 0x00020000);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const int bc = b1 - b0;  // the band's chunks: X^T rows [tb - t0][chunk - b0][half]
-    const bool all = TB * cpb_ <= 32;  // every token block's X^T in one 64 KB stage (the host sizes LDS the same way)
-    auto stage = [&](int t0) {
-      const int nt = all ? TB : 1;
+    const int tbp = gemm_pass_tbs(TB, cpb_);  // token blocks per stage (the host sizes LDS the same way)
+    const bool all = tbp >= TB;
+    auto stage = [&](int t0, int nt) {
       for (int r = wave_u; r < nt * bc * 2; r += nw) {
         const int h = r & 1, j = b0 + (r >> 1) % bc, tb = t0 + (r >> 1) / bc;
         const int t = 16 * tb + n;
@@ -518,7 +528,7 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
         }
       }
     };
-    stage(0);
+    stage(0, min(tbp, TB));
     load(w, c0);
     __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPW * WV));
     __builtin_amdgcn_s_barrier();
@@ -540,25 +550,38 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
         }
       }
     } else if constexpr (CPW <= 8) {
+      // passes of PT token blocks (static indices throughout): PT = 2 when two fit, else 1
+      auto passes = [&](auto pt) {
+        constexpr int PT = decltype(pt)::value;
 #pragma unroll
-      for (int tb = 0; tb < TB; ++tb) {
-        if (tb > 0) {
-          __syncthreads();  // every wave is done with the previous pass's X^T
-          stage(tb);
-          __builtin_amdgcn_s_waitcnt(0);
-          __builtin_amdgcn_s_barrier();
-        }
+        for (int t0 = 0; t0 < TB; t0 += PT) {
+          if (t0 > 0) {
+            __syncthreads();  // every wave is done with the previous pass's X^T
+            stage(t0, min(PT, TB - t0));
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_s_barrier();
+          }
 #pragma unroll
-        for (int i = 0; i < CPW; ++i) {
-          if (c0 + i < c1) {
-            half8 a[2];
-            weights(w[i], a);
-            const u32x4* xb = xs + ((size_t)(c0 + i - b0) * 2) * 64;
-            acc[tb] = mfma16x16x32(a[0], as_half8(xb[lane]), acc[tb]);
-            acc[tb] = mfma16x16x32(a[1], as_half8(xb[64 + lane]), acc[tb]);
+          for (int i = 0; i < CPW; ++i) {
+            if (c0 + i < c1) {
+              half8 a[2];
+              weights(w[i], a);
+#pragma unroll
+              for (int u = 0; u < PT; ++u) {
+                if (t0 + u < TB) {
+                  const u32x4* xb = xs + ((size_t)(u * bc + c0 + i - b0) * 2) * 64;
+                  acc[t0 + u] = mfma16x16x32(a[0], as_half8(xb[lane]), acc[t0 + u]);
+                  acc[t0 + u] = mfma16x16x32(a[1], as_half8(xb[64 + lane]), acc[t0 + u]);
+                }
+              }
+            }
           }
         }
-      }
+      };
+      if (tbp >= 2)
+        passes(std::integral_constant<int, 2>{});
+      else
+        passes(std::integral_constant<int, 1>{});
     }
   }
   if (!run_flag_set(run)) {  // the same for every wave
@@ -680,10 +703,18 @@ static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
   const int tb = (p.M + 15) / 16;
   const int bands = std::max(1, p.bands);
   const int bc = (p.K / 64 + bands - 1) / bands;  // X^T of the token blocks of one pass (all of them when they fit)
-  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)(tb * bc <= 32 ? tb : 1) * bc * 2048;
+  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)gemm_pass_tbs(tb, bc) * bc * 2048;
   const size_t red = (size_t)(p.kw - 1) * p.wpg * tb * 1024;
   const size_t tile = p.fuse ? (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float) : 0;
   return std::max(x, std::max(red, tile));
+}
+
+// Dynamic LDS above 64 KB (X^T passes of up to 128 KB): the kernel's limit is raised first (on the current device).
+template <typename F>
+static void allow_lds(F* kernel, size_t lds) {
+  if (lds > 65536)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
 }
 
 template <int TB, bool I8>
@@ -702,11 +733,13 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
     }
     if constexpr (TB <= 2) {
       if (cpk > 8) {  // 16-chunk batches of int8 weights: 64 VGPRs (the plan keeps 3 or 4 token blocks within 8)
+        allow_lds(gemm_sliced_kernel<TB, I8, 16, false>, lds);
         hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 16, false>), grid, block, lds, s, p);
         return;
       }
     }
   }
+  allow_lds(gemm_sliced_kernel<TB, I8, 8, false>, lds);
   hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 8, false>), grid, block, lds, s, p);
 }
 
@@ -754,9 +787,10 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // wider GEMMs take S = max(4, strips / 256) strips per group (at most 256 groups: 257 groups on 256 CUs measured
 // 14.2 us against 10.2 for 256) and 16 / S ranges, X loaded per wave for S <= 4 with operand-order X (16384 x 2048:
 // 9.6 against 10.3 us through LDS; equal at 3104 and 6144 rows, slower for S = 5 and 16), else staged in LDS once (at
-// most 64 KB). Two to four token blocks (X through LDS) take the same groups, one token block's X^T per pass when all
-// of them exceed 64 KB (band at most 32 chunks, ranges of at most 8 chunks): 33 tokens, C5 round 2.19 -> 2.02 ms
-// against the split-K kernel. Returns false when no sliced plan fits (the split-K plan is used).
+// most 64 KB). Two to four token blocks (X through LDS) take the same groups, X^T in passes of two or one token blocks
+// of at most 128 KB when all of them do not fit (ranges of at most 8 chunks): 33 tokens, C5 round 2.19 -> 1.95 ms
+// against the split-K kernel (2.02 with 64 KB passes of one token block). Returns false when no sliced plan fits (the
+// split-K plan is used).
 static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, int max_bands, GemmPlan* pl) {
   const int strips = N / 16, chunks = K / 64;
   if (!DSPARK_GEMM_SLICED || tb > 4) return false;
@@ -779,7 +813,8 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
   // X^T through LDS: all token blocks at once when they fit 64 KB, else one token block per pass, each pass's X^T
   // within 64 KB and each range within one 8-chunk batch (its weights stay in registers)
   const int bc = (chunks + bands - 1) / bands, cpk = (bc + KW - 1) / std::max(1, KW);
-  if (!xd && (((size_t)tb * bc * 2048 > 65536 && (bc > 32 || cpk > 8)) || (tb > 2 && cpk > 8))) return false;
+  const int tp = gemm_pass_tbs(tb, bc);
+  if (!xd && ((size_t)tp * bc * 2048 > GEMM_X_LDS || (tp < tb && cpk > 8) || (tb > 2 && cpk > 8))) return false;
   pl->ksplit = 1;
   pl->bands = bands;
   pl->xd = xd;
@@ -835,11 +870,12 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
     // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
     const int tb = (p.M + 15) / 16;
     if (p.bands < 1) p.bands = 1;
-    if (p.ksplit != 1 || p.wpg < 1 || p.wpg * p.kw > 16 || tb > 4 || gemm_sliced_lds_bytes(p, i8) > 65536)
+    if (p.ksplit != 1 || p.wpg < 1 || p.wpg * p.kw > 16 || tb > 4 || gemm_sliced_lds_bytes(p, i8) > GEMM_X_LDS)
       return DSPARK_EINVAL;
     // X^T in passes (it does not fit LDS for every token block at once): each range within one batch of weights
     const int bc = (p.K / 64 + p.bands - 1) / p.bands, cpk = (bc + p.kw - 1) / p.kw;
-    if (!gemm_sliced_xd(p, i8) && (((size_t)tb * bc * 2048 > 65536 && (bc > 32 || cpk > 8)) || (tb > 2 && cpk > 8)))
+    const int tp = gemm_pass_tbs(tb, bc);
+    if (!gemm_sliced_xd(p, i8) && ((size_t)tp * bc * 2048 > GEMM_X_LDS || (tp < tb && cpk > 8) || (tb > 2 && cpk > 8)))
       return DSPARK_EINVAL;
     // bands: plain scaled sums into y32 only (each band its own [M][N]), nothing fused
     if (p.bands > 1 && (p.epilogue != 0 || !p.y32 || p.y16 || p.best_part || p.fuse || p.bands > p.K / 64))

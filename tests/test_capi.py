@@ -55,11 +55,11 @@ def test_workspace_queries_reject_bad_shapes():
     args.D, args.M = 64, 65
     assert lib.dspark_verify_attention_workspace(ctypes.byref(args)) == 0
     assert lib.dspark_gemm_i8_workspace(16, 65536, 2048) == 0         # enough 16-row strips: no split, no partials
-    # K ranges summed inside one workgroup (3 or 4 token blocks: X^T one token block per pass)
+    # K ranges summed inside one workgroup (2 to 4 token blocks: X^T in passes of one or two token blocks)
     for M, N, K in ((16, 2048, 2048), (9, 6144, 2048), (24, 4096, 1024), (1, 64, 128), (40, 6144, 2048),
-                    (33, 512, 1024), (64, 16384, 2048)):
+                    (33, 512, 1024), (64, 16384, 2048), (40, 1024, 4096)):
         assert lib.dspark_gemm_i8_workspace(M, N, K) == 0, (M, N, K)
-    for M, N, K in ((33, 2048, 8192), (40, 1024, 4096), (48, 4096, 8192)):
+    for M, N, K in ((33, 2048, 8192), (40, 1024, 8192), (48, 4096, 8192)):
         # split K: a fixed region of 8192 u32 arrival counters (the same offset for every shape), then the
         # [splits][M][N] fp32 partials, 256-byte rounded
         ws = lib.dspark_gemm_i8_workspace(M, N, K)

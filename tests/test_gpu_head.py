@@ -131,7 +131,8 @@ def test_commit_stop_rules_on_device(dev, orc):
     (48, 16384, 2048, 2),   # three token blocks, 4 strips x 4 ranges, SiLU epilogue
     (64, 2048, 2048, 0),    # four token blocks
     (36, 1024, 1344, 0),    # passes over ragged ranges (21 chunks over 4)
-    (33, 1024, 4096, 0),    # X^T of one token block over 64 KB: K split across workgroups
+    (33, 1024, 4096, 0),    # one token block's X^T per pass (128 KB)
+    (33, 1024, 8192, 0),    # X^T of one token block over 128 KB: K split across workgroups
     (64, 128, 256, 0),
 ])
 def test_gemm_i8_matches_oracle(dev, orc, M, N, K, epilogue):
@@ -158,7 +159,7 @@ def test_gemm_i8_matches_oracle(dev, orc, M, N, K, epilogue):
         assert np.max(np.abs(got - ref)) <= 2e-3 * max(1.0, np.max(np.abs(ref)))
 
 
-@pytest.mark.parametrize("M,N,K", [(33, 2048, 8192), (40, 1024, 4096), (33, 512, 8192)])
+@pytest.mark.parametrize("M,N,K", [(33, 2048, 8192), (40, 1024, 8192), (33, 512, 8192)])
 def test_gemm_split_calls_share_one_workspace(dev, orc, M, N, K):
     """Split-K GEMMs in a row on one workspace (the last split of each row group sums the partials and resets its
     counter): every call matches the oracle on its own inputs and repeats are bit-identical."""
@@ -198,7 +199,7 @@ def test_gemm_split_shapes_share_one_workspace(dev, orc):
     torch = dev
     host = load_host()
     lib = host.lib()
-    shapes = [(33, 2048, 8192), (33, 2048, 4096), (40, 6144, 4096), (48, 3104, 4096), (33, 1024, 4096), (64, 2048, 10240)]
+    shapes = [(33, 2048, 8192), (33, 2048, 10240), (40, 6144, 8192), (48, 3104, 8192), (33, 1024, 6144), (64, 2048, 10240)]
     need = max(lib.dspark_gemm_i8_workspace(M, N, K) for M, N, K in shapes)
     ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
     wso = host.Workspace()
