@@ -759,10 +759,13 @@ static void launch_attn(const AttnParams& p, hipStream_t s) {
   hipLaunchKernelGGL((verify_attn_kernel<D, QB, PF, OCC, QLDS>), dim3((units + 7) / 8 * 8 * p.RG), dim3(256), 0, s, p);
 }
 
+// MAXW: the most waves a plan of this shape launches (the launch bound, so the register budget is the shape's own).
 template <int D, int QB, int PL, int PPL, int LPW, int MAXW>
-static void launch_lds(const AttnParams& p, hipStream_t s) {
+static int launch_lds(const AttnParams& p, hipStream_t s) {
+  if (p.nrg * PL > MAXW) return DSPARK_EUNSUPPORTED;
   hipLaunchKernelGGL((verify_attn_lds_kernel<D, QB, PL, PPL, LPW, MAXW>), dim3(p.KVH * p.S), dim3(p.nrg * PL * 64), 0, s,
                      p);
+  return 0;
 }
 
 #ifndef DSPARK_ATTN_QB3
@@ -891,30 +894,29 @@ static int launch_split(const AttnParams& p, int D, hipStream_t s) {
     // (1, 4, 4 | 3 | 2); D = 128: (2, 1, 16 | 8 | 6 | 4 | 3 | 2), (1, 1, 2 | 1)
     if (p.qb == 3) {
       if (D != 64 || p.nrg != 3 || p.pl != 4 || p.ppl != 1 || p.lpw != 3) return DSPARK_EUNSUPPORTED;
-      launch_lds<64, 3, 4, 1, 3, 12>(p, s);
-      return 0;
+      return launch_lds<64, 3, 4, 1, 3, 12>(p, s);
     }
     if (p.qb != 1) return DSPARK_EUNSUPPORTED;
     const int key = D * 10000 + p.pl * 1000 + p.ppl * 100 + p.lpw;
     switch (key) {
-      case 644108: launch_lds<64, 1, 4, 1, 8, 16>(p, s); break;
-      case 644104: launch_lds<64, 1, 4, 1, 4, 16>(p, s); break;
-      case 644103: launch_lds<64, 1, 4, 1, 3, 16>(p, s); break;
-      case 644102: launch_lds<64, 1, 4, 1, 2, 16>(p, s); break;
-      case 642204: launch_lds<64, 1, 2, 2, 4, 16>(p, s); break;
-      case 642203: launch_lds<64, 1, 2, 2, 3, 16>(p, s); break;
-      case 642202: launch_lds<64, 1, 2, 2, 2, 16>(p, s); break;
-      case 641404: launch_lds<64, 1, 1, 4, 4, 16>(p, s); break;
-      case 641403: launch_lds<64, 1, 1, 4, 3, 16>(p, s); break;
-      case 641402: launch_lds<64, 1, 1, 4, 2, 16>(p, s); break;
-      case 1282116: launch_lds<128, 1, 2, 1, 16, 16>(p, s); break;
-      case 1282108: launch_lds<128, 1, 2, 1, 8, 16>(p, s); break;
-      case 1282106: launch_lds<128, 1, 2, 1, 6, 16>(p, s); break;
-      case 1282104: launch_lds<128, 1, 2, 1, 4, 16>(p, s); break;
-      case 1282103: launch_lds<128, 1, 2, 1, 3, 16>(p, s); break;
-      case 1282102: launch_lds<128, 1, 2, 1, 2, 16>(p, s); break;
-      case 1281102: launch_lds<128, 1, 1, 1, 2, 16>(p, s); break;
-      case 1281101: launch_lds<128, 1, 1, 1, 1, 16>(p, s); break;
+      case 644108: return launch_lds<64, 1, 4, 1, 8, 16>(p, s);
+      case 644104: return launch_lds<64, 1, 4, 1, 4, 16>(p, s);
+      case 644103: return launch_lds<64, 1, 4, 1, 3, 16>(p, s);
+      case 644102: return launch_lds<64, 1, 4, 1, 2, 16>(p, s);
+      case 642204: return launch_lds<64, 1, 2, 2, 4, 16>(p, s);
+      case 642203: return launch_lds<64, 1, 2, 2, 3, 16>(p, s);
+      case 642202: return launch_lds<64, 1, 2, 2, 2, 16>(p, s);
+      case 641404: return launch_lds<64, 1, 1, 4, 4, 16>(p, s);
+      case 641403: return launch_lds<64, 1, 1, 4, 3, 16>(p, s);
+      case 641402: return launch_lds<64, 1, 1, 4, 2, 16>(p, s);
+      case 1282116: return launch_lds<128, 1, 2, 1, 16, 4>(p, s);
+      case 1282108: return launch_lds<128, 1, 2, 1, 8, 4>(p, s);
+      case 1282106: return launch_lds<128, 1, 2, 1, 6, 8>(p, s);
+      case 1282104: return launch_lds<128, 1, 2, 1, 4, 12>(p, s);
+      case 1282103: return launch_lds<128, 1, 2, 1, 3, 16>(p, s);
+      case 1282102: return launch_lds<128, 1, 2, 1, 2, 16>(p, s);
+      case 1281102: return launch_lds<128, 1, 1, 1, 2, 16>(p, s);
+      case 1281101: return launch_lds<128, 1, 1, 1, 1, 16>(p, s);
       default: return DSPARK_EUNSUPPORTED;
     }
   } else if (D == 64 && p.OCC == 2) {
