@@ -115,6 +115,31 @@ int dspark_kv_write(const void* k, const void* v, int64_t row_stride, void* k_pa
 /* kv_pages: pages in each pool. Without a block table, pos0 + n must fit the pools (DSPARK_EINVAL otherwise); with
  * one, a row whose table entry is outside [0, kv_pages) is not written. */
 
+/* ---------------------------------------------------------------- int8 K/V records (the reference's KV format)
+ * Per (position, KV head) one record of DSPARK_REC_BYTES = 264 bytes, K int8[128] | f32 k scale | V int8[128] |
+ * f32 v scale, in pages of 32 positions laid out [page][slot][KV head][record] (KVBlock = 32 x KVH x 264 bytes), a
+ * logical page (position / 32) mapped to a physical page by an int32 block table (NULL = identity). This is the
+ * layout the reference's prefill and commit write (internal/model/engine.go:30-32, kernels/ops.hip:226-251,
+ * dspark.hip:2860-2877), so a cache filled by the reference's writers is read as it is. */
+#define DSPARK_REC_BYTES 264
+/* Records of positions pos0 .. pos0+n-1 from fp32 k, v rows [n][row_stride] (head h at h * 128; K already normed and
+ * rotated), each quantized as quantize_pair (ops.hip:212-224): scale = max(amax / 127, 1e-6), q = x * (1 / scale)
+ * rounded half away from zero, clamped to [-128, 127]. Replaces kv_write (ops.hip:235-251) and the verified rows'
+ * records of query_fresh (dspark.hip:1036-1046). Without a block table pos0 + n must fit the pool (DSPARK_EINVAL
+ * otherwise); with one, a position whose entry is outside [0, kv_pages) is not written. */
+int dspark_kv_write_rec(const float* k, const float* v, int64_t row_stride, void* pages, const int32_t* block_table,
+                        int64_t kv_pages, int32_t KVH, int32_t pos0, int32_t n, dspark_stream_t stream);
+/* dspark_verify_attention over a record pool: args->k_pages is the pool (kv_pages pages of 32 x KVH x 264 bytes, under
+ * 2 GiB), args->v_pages must be NULL, D = 128 and KVH = 4 (the reference geometry), QH / KVH x M <= 64 rows per KV
+ * head (16 verify tokens; the reference verifies at most 9). The reference's int8 numerics: Q quantized per 32-dim group (scale = max(amax / 127, 1e-20), q8 =
+ * rint(q * rcp(scale))), exact int8 dot products scaled by the group and key scales, P = fp16(p * v scale * 2^k) on
+ * int8 V, fp32 accumulation; the result is the softmax attention of those int8 Q/K/V within the reference's own error
+ * (benchmarks/verify_attention.txt). Splits and merge as dspark_verify_attention (same workspace contract).
+ * Replaces attention_pass / attention_v2 / attention_v3 over the int8 cache (dspark.hip:1070-1412, 1488-2130) and
+ * combine_phase (2132-2185). */
+size_t dspark_verify_attention_rec_workspace(const dspark_attn_args* args);
+int dspark_verify_attention_rec(const dspark_attn_args* args, dspark_stream_t stream);
+
 /* ---------------------------------------------------------------- verify argmax (greedy head)
  * best_keys[t] = max over r < V of key(pv, r), pv the repetition-penalised fp16-rounded logit (seen[] bitmap, plus
  * drafts tokens[1..t] not yet seen), key = ordered float bits << 32 | (0xFFFFFFFF - r). logits fp32 [M][V] or fp16

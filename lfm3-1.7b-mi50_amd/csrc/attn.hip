@@ -23,6 +23,7 @@
 #include "common.h"
 #include "dspark.h"
 #include "dspark_internal.h"
+#include "attn_range.h"
 
 namespace dspark {
 
@@ -179,28 +180,6 @@ __device__ __forceinline__ void page_accumulate(const Tile<D>& tl, RowState<D, Q
     for (int cc = 0; cc < D / 16; ++cc) rs.o[qb][cc] = mfma16x16x32(tl.v[cc], pp, rs.o[qb][cc]);
     rs.ls[qb] = mfma16x16x32(ones, pp, rs.ls[qb]);
   }
-}
-
-// Page range, pages per split and unmasked range from a (the host plan evaluated with the State's a at run time).
-__device__ void attn_range(AttnParams& p) {
-  const int a = p.st->a;
-  p.a = a;
-  if (p.drafter) {
-    // drafter ring: context [max(ctx_lo, a - window), a) for every block token, block keys in both directions
-    p.start = max(p.st->ctx_lo, a - p.window);
-    p.window = 0;
-    p.causal = 0;
-  } else if (p.window > 0) {
-    p.start = max(0, a - p.window + 1);
-  }
-  const int lo0 = max(p.start, p.window > 0 ? a - p.window + 1 : 0);
-  const int lo_last = max(p.start, p.window > 0 ? a + p.M - p.window : 0);
-  const int hi_last = a + p.M - 1;
-  p.full_lo = lo_last;
-  p.full_hi = p.causal ? a : hi_last;
-  p.page0 = lo0 / PAGE;
-  p.npages = hi_last / PAGE - p.page0 + 1;
-  p.pps = (p.npages + p.S - 1) / p.S;
 }
 
 template <int D, int QB, int PF, int OCC, bool QLDS>
@@ -375,7 +354,6 @@ constexpr int LDS_BT_MAX = 2048;  // pages per split the LDS kernel accepts
 constexpr int LDS_STEP_BYTES = 32768;  // K+V bytes of one ring step (4 pages at D = 64, 2 at D = 128)
 constexpr int ATTN_CPOL_COHERENT = 16;  // buffer-store cache policy SC1: device-scope coherent
 
-__device__ __forceinline__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
 #define DSPARK_LDSP(x) ((__attribute__((address_space(3))) void*)(x))
 
@@ -622,7 +600,7 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
 #ifndef DSPARK_ATTN_COMBINE_LANES
 #define DSPARK_ATTN_COMBINE_LANES 8
 #endif
-constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 64 / COMBINE_LANES;  // S <= 64
+constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 64 / COMBINE_LANES;
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
@@ -634,29 +612,38 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
   const bool live = e < R * D / 4;
   const int r = live ? e / (D / 4) : 0, c4 = e % (D / 4);
   const size_t slot0 = (size_t)hr * p.S;
-  f32x2 ml[COMBINE_MAX_PER_LANE];
-  f32x4 av[COMBINE_MAX_PER_LANE];
-#pragma unroll
-  for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
-    const int sp = j + COMBINE_LANES * i;
-    const bool ok = live && sp < p.S;
-    ml[i] = ok ? ldg(p.part_ml + (slot0 + sp) * R + r) : f32x2{-INFINITY, 0.f};
-    av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + ((slot0 + sp) * R + r) * D) + c4) : f32x4{0, 0, 0, 0};
-  }
-  if (!run_flag_set(run)) {  // a stopped round writes nothing
-    __builtin_amdgcn_s_waitcnt(0);
-    return;
-  }
+  // Splits in batches of COMBINE_LANES x COMBINE_MAX_PER_LANE (one batch up to 64 splits): a lane's loads of a batch
+  // are all in flight before the first is used, and each batch folds into the lane's running (m, l, acc).
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-  for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) m = fmaxf(m, ml[i][0]);
-  if (m > -INFINITY) {
+  for (int b0 = 0; b0 < p.S; b0 += COMBINE_LANES * COMBINE_MAX_PER_LANE) {
+    f32x2 ml[COMBINE_MAX_PER_LANE];
+    f32x4 av[COMBINE_MAX_PER_LANE];
 #pragma unroll
     for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
-      const float f = ml[i][0] == -INFINITY ? 0.f : fast_exp2(ml[i][0] - m);
-      l = fmaf(f, ml[i][1], l);
-      acc += f * av[i];
+      const int sp = b0 + j + COMBINE_LANES * i;
+      const bool ok = live && sp < p.S;
+      ml[i] = ok ? ldg(p.part_ml + (slot0 + sp) * R + r) : f32x2{-INFINITY, 0.f};
+      av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + ((slot0 + sp) * R + r) * D) + c4) : f32x4{0, 0, 0, 0};
+    }
+    if (!run_flag_set(run)) {  // a stopped round writes nothing
+      __builtin_amdgcn_s_waitcnt(0);
+      return;
+    }
+    float mb = m;
+#pragma unroll
+    for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) mb = fmaxf(mb, ml[i][0]);
+    if (mb > -INFINITY) {
+      const float fr = m == -INFINITY ? 0.f : fast_exp2(m - mb);  // the running state rescaled to the batch max
+      l *= fr;
+      acc *= fr;
+      m = mb;
+#pragma unroll
+      for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
+        const float f = ml[i][0] == -INFINITY ? 0.f : fast_exp2(ml[i][0] - m);
+        l = fmaf(f, ml[i][1], l);
+        acc += f * av[i];
+      }
     }
   }
 #pragma unroll

@@ -205,6 +205,73 @@ int dspark_kv_write(const void* k, const void* v, int64_t row_stride, void* k_pa
   return kv_write_launch(k, v, row_stride, k_pages, v_pages, block_table, kv_pages, KVH, D, pos0, n, S(stream));
 }
 
+// ---------------------------------------------------------------- int8 K/V records
+static bool rec_args_ok(const dspark_attn_args* a) {
+  if (!a || !a->q || !a->k_pages || a->v_pages) return false;
+  if (!a->out && !a->out_f32) return false;
+  if (a->D != 128 || a->KVH != 4 || a->QH < a->KVH || a->QH % a->KVH != 0) return false;
+  if (a->M < 1 || a->M > DSPARK_MT_MAX || (int64_t)a->QH / a->KVH * a->M > 4 * 16) return false;
+  if (a->a < 0 || a->start < 0 || a->window < 0 || a->start > a->a + a->M - 1) return false;
+  if (a->splits < 0) return false;
+  if (a->kv_pages < 1 || a->kv_pages * DSPARK_PAGE_TOKENS * a->KVH * DSPARK_REC_BYTES >= (int64_t)1 << 31) return false;
+  if (!a->block_table && a->kv_pages < (a->a + a->M + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS) return false;
+  return true;
+}
+
+static AttnParams rec_params(const dspark_attn_args* a) {
+  AttnParams p = {};
+  p.q = static_cast<const _Float16*>(a->q);
+  p.kp = static_cast<const _Float16*>(a->k_pages);
+  p.bt = a->block_table;
+  p.k_bytes = (uint32_t)(a->kv_pages * DSPARK_PAGE_TOKENS * a->KVH * DSPARK_REC_BYTES);
+  p.out16 = static_cast<_Float16*>(a->out);
+  p.out32 = a->out_f32;
+  p.gate = a->gate;
+  p.M = a->M;
+  p.QH = a->QH;
+  p.KVH = a->KVH;
+  p.G = a->QH / a->KVH;
+  p.a = a->a;
+  p.start = a->start;
+  p.window = a->window;
+  p.causal = a->causal ? 1 : 0;
+  p.S = a->splits;
+  attn_rec_plan(p, device_cus());
+  return p;
+}
+
+size_t dspark_verify_attention_rec_workspace(const dspark_attn_args* a) {
+  if (!a) return 0;
+  dspark_attn_args b = *a;
+  if (!b.q) {  // size only
+    b.q = b.k_pages = b.out = reinterpret_cast<void*>(1);
+    b.v_pages = nullptr;
+  }
+  if (b.kv_pages == 0) b.kv_pages = (b.a + b.M + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS;
+  if (!rec_args_ok(&b)) return 0;
+  AttnParams p = rec_params(&b);
+  return attn_workspace_bytes(p, 128);
+}
+
+int dspark_verify_attention_rec(const dspark_attn_args* a, dspark_stream_t stream) {
+  if (!rec_args_ok(a)) return DSPARK_EINVAL;
+  AttnParams p = rec_params(a);
+  const size_t need = attn_workspace_bytes(p, 128);
+  if (!a->workspace || a->workspace_bytes < need) return DSPARK_ENOSPACE;
+  attn_bind_workspace(p, 128, a->workspace);
+  return attn_rec_launch(p, 3, S(stream));
+}
+
+int dspark_kv_write_rec(const float* k, const float* v, int64_t row_stride, void* pages, const int32_t* block_table,
+                        int64_t kv_pages, int32_t KVH, int32_t pos0, int32_t n, dspark_stream_t stream) {
+  if (!k || !v || !pages) return DSPARK_EINVAL;
+  if (KVH < 1 || pos0 < 0 || n < 0 || row_stride < (int64_t)KVH * 128 || row_stride % 2 != 0) return DSPARK_EINVAL;
+  if (kv_pages < 1 || (int64_t)pos0 + n > ((int64_t)1 << 31) - DSPARK_PAGE_TOKENS) return DSPARK_EINVAL;
+  if ((int64_t)n * KVH > ((int64_t)1 << 31) - 4) return DSPARK_EINVAL;
+  if (!block_table && ((int64_t)pos0 + n + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS > kv_pages) return DSPARK_EINVAL;
+  return kv_write_rec_launch(k, v, row_stride, pages, block_table, kv_pages, KVH, pos0, n, S(stream));
+}
+
 size_t dspark_verify_argmax_workspace(int32_t M, int32_t V) {
   if (M < 1 || M > DSPARK_MT_MAX || V < 1) return 0;
   return verify_argmax_ws(M, V);

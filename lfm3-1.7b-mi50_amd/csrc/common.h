@@ -42,6 +42,10 @@ __device__ __forceinline__ T ldg_nt(const T* p) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// s_waitcnt immediates (gfx9 encoding): vmcnt(n) with expcnt and lgkmcnt left at their maxima; lgkmcnt(0) alone.
+__device__ __forceinline__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+constexpr int LGKMCNT0_IMM = 0xC07F;
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));

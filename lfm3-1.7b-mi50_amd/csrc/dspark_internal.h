@@ -39,8 +39,7 @@ struct AttnParams {
 };
 
 void attn_plan(AttnParams& p, int D, int cus);
-// The same plan evaluated on the device from the State's a: page range, pages per split, unmasked range.
-__device__ void attn_range(AttnParams& p);
+// attn_range (attn_range.h): the same plan evaluated on the device from the State's a.
 
 struct ResNormParams {
   const struct ::dspark_state* st;
@@ -146,6 +145,16 @@ void attn_bind_workspace(AttnParams& p, int D, void* ws);
 int attn_launch(AttnParams& p, int D, int phases, hipStream_t s);
 int kv_write_launch(const void* k, const void* v, int64_t row_stride, void* kp, void* vp, const int32_t* bt,
                     int64_t kv_pages, int KVH, int D, int pos0, int n, hipStream_t s);
+
+// Verify attention over int8 K/V records (attn_rec.hip): D = 128, 4 KV heads, one workgroup per key split of all heads,
+// up to ATTN_REC_MAX_SPLITS splits (the merge takes any split count); same partial format and merge as the fp16 path
+// (the workspace size is attn_workspace_bytes(p, 128) of the planned p).
+constexpr int ATTN_REC_MAX_SPLITS = 256;
+void attn_rec_plan(AttnParams& p, int cus);
+int attn_rec_launch(AttnParams& p, int phases, hipStream_t s);
+// quantize_pair records of positions pos0 .. pos0 + n - 1 from fp32 k, v rows ([n][row_stride], head h at h * 128).
+int kv_write_rec_launch(const float* k, const float* v, int64_t row_stride, void* pages, const int32_t* bt,
+                        int64_t kv_pages, int KVH, int pos0, int n, hipStream_t s);
 
 // The State's run flag read with a vector load (issued in order with the kernel's data loads, so a kernel can put it
 // first and test it after its loads are in flight, instead of a scalar load the compiler waits for at the next use of

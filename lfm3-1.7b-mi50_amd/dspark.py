@@ -55,6 +55,11 @@ _SIGS = {
     "dspark_kv_write": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_kv_write_rec": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                           ctypes.c_int32, ctypes.c_void_p]),
+    "dspark_verify_attention_rec_workspace": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
+    "dspark_verify_attention_rec": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                          ctypes.c_void_p]),
     "dspark_verify_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
@@ -219,6 +224,59 @@ def verify_attention(q, k_pages, v_pages, a, start=0, window=0, causal=True, out
     ws = (workspace or Workspace(q.device)).get(need)
     args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     check(lib().dspark_verify_attention(ctypes.byref(args), stream_handle(stream)), "dspark_verify_attention")
+    return out, out_f32
+
+
+# ---------------------------------------------------------------- int8 K/V records
+REC_BYTES = 264
+
+
+def rec_pages_alloc(n_pages, KVH, device="cuda"):
+    """A record pool: [n_pages][32 slots][KVH][264 bytes] (internal/model/engine.go:30-32)."""
+    return _torch().zeros((n_pages, PAGE, KVH, REC_BYTES), dtype=_torch().uint8, device=device)
+
+
+def kv_write_rec(k, v, pages, pos0, block_table=None, stream=None):
+    """k, v: fp32 [n][KVH][128] (or [n][row], row >= KVH*128) device tensors -> quantize_pair records."""
+    torch = _torch()
+    n = k.shape[0]
+    KVH = pages.shape[2]
+    row = k.stride(0)
+    assert v.stride(0) == row and k.dtype == v.dtype == torch.float32 and pages.dtype == torch.uint8
+    rc = lib().dspark_kv_write_rec(ptr(k), ptr(v), row, ptr(pages), ptr(block_table), pages.shape[0], KVH, pos0, n,
+                                   stream_handle(stream))
+    check(rc, "dspark_kv_write_rec")
+
+
+def rec_attn_args(q, pages, a, start=0, window=0, causal=True, out=None, out_f32=None, gate=None, block_table=None,
+                  splits=0):
+    M, QH, D = q.shape
+    args = AttnArgs()
+    args.q, args.k_pages, args.v_pages = q.data_ptr(), pages.data_ptr(), None
+    args.block_table = block_table.data_ptr() if block_table is not None else None
+    args.kv_pages = pages.shape[0]
+    args.out = out.data_ptr() if out is not None else None
+    args.out_f32 = out_f32.data_ptr() if out_f32 is not None else None
+    args.gate = gate.data_ptr() if gate is not None else None
+    args.M, args.QH, args.KVH, args.D = M, QH, pages.shape[2], D
+    args.a, args.start, args.window, args.causal, args.splits = a, start, window, int(causal), splits
+    return args
+
+
+def verify_attention_rec(q, pages, a, start=0, window=0, causal=True, out=None, out_f32=None, gate=None,
+                         block_table=None, splits=0, workspace=None, stream=None):
+    """q fp16 [M][QH][128]; pages: a record pool holding positions 0..a+M-1."""
+    torch = _torch()
+    M, QH, D = q.shape
+    if out is None and out_f32 is None:
+        out = torch.empty((M, QH, D), dtype=torch.float16, device=q.device)
+    args = rec_attn_args(q, pages, a, start, window, causal, out, out_f32, gate, block_table, splits)
+    need = lib().dspark_verify_attention_rec_workspace(ctypes.byref(args))
+    if need == 0:
+        raise DsparkError("dspark_verify_attention_rec_workspace rejected the arguments")
+    ws = (workspace or Workspace(q.device)).get(need)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    check(lib().dspark_verify_attention_rec(ctypes.byref(args), stream_handle(stream)), "dspark_verify_attention_rec")
     return out, out_f32
 
 

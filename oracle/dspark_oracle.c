@@ -450,6 +450,160 @@ void orc_kv_commit(uint16_t* cache, const uint16_t* fresh, int a, int acc, int r
   for (int c = 0; c <= acc; ++c) memcpy(cache + (size_t)(a + c) * row, fresh + (size_t)c * row, sizeof(uint16_t) * row);
 }
 
+/* ------------------------------------------------------------------ int8 K/V records (reference KV format) */
+
+/* quantize_pair, kernels/ops.hip:212-224 (= dspark.hip:933-944): amax over the D values, scale = max(amax / 127, 1e-6),
+ * inv = 1 / scale, a = x * inv, a + 0.5 (a >= 0) or a - 0.5, clamped to [-128, 127], truncated. Each step is one IEEE
+ * binary32 operation; `volatile` keeps the compiler from fusing the multiply and the add. Returns the scale. */
+float orc_rec_quantize(const float* x, int D, int8_t* q) {
+  float amax = 0.f;
+  for (int i = 0; i < D; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  volatile float scale = fmaxf(amax / 127.f, 1e-6f);
+  volatile float inv = 1.f / scale;
+  for (int i = 0; i < D; ++i) {
+    volatile float a = x[i] * inv;
+    volatile float r = a >= 0.f ? a + 0.5f : a - 0.5f;
+    q[i] = (int8_t)truncf(fminf(fmaxf(r, -128.f), 127.f));
+  }
+  return scale;
+}
+
+/* kv_write, kernels/ops.hip:235-251, with the engine's layout (internal/model/engine.go:30-32: KVBlock = 32 KVH Rec,
+ * kv_head = Rec, kv_slot = KVH Rec): record of (pos, h) at page bt[pos / 32] (identity without a table), offset
+ * ((pos % 32) KVH + h) Rec; K int8[128] | f32 k scale | V int8[128] | f32 v scale. k, v: fp32 [n][KVH][128]. */
+void orc_kv_write_rec(const float* k, const float* v, int n, int KVH, int pos0, const int32_t* bt, uint8_t* pages) {
+  const int D = 128, rec = 2 * D + 8;
+  for (int t = 0; t < n; ++t) {
+    const int pos = pos0 + t;
+    const int phys = bt ? bt[pos / 32] : pos / 32;
+    for (int h = 0; h < KVH; ++h) {
+      uint8_t* r = pages + (size_t)phys * 32 * KVH * rec + ((size_t)(pos % 32) * KVH + h) * rec;
+      const float ks = orc_rec_quantize(k + ((size_t)t * KVH + h) * D, D, (int8_t*)r);
+      const float vs = orc_rec_quantize(v + ((size_t)t * KVH + h) * D, D, (int8_t*)(r + D + 4));
+      memcpy(r + D, &ks, 4);
+      memcpy(r + 2 * D + 4, &vs, 4);
+    }
+  }
+}
+
+/* Query quantization of the int8 attention, query_fresh (dspark.hip:1020-1035): per 32-dim group
+ * s = max(amax / 127, 1e-20), q8 = rint(q * (1 / s)) (the reference multiplies by the hardware reciprocal of s, within
+ * one ulp of 1 / s, so a value that lands within an ulp of a rounding boundary can differ by one unit). q fp16
+ * [rows][D]; q8 [rows][D]; qs [rows][D / 32]. */
+void orc_rec_quantize_q(const uint16_t* q, int rows, int D, int8_t* q8, float* qs) {
+  for (int r = 0; r < rows; ++r)
+    for (int g = 0; g < D / 32; ++g) {
+      const uint16_t* src = q + (size_t)r * D + 32 * g;
+      float amax = 0.f;
+      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(orc_f16_to_f32(src[i])));
+      volatile float s = fmaxf(amax / 127.f, 1e-20f);
+      volatile float inv = 1.f / s;
+      for (int i = 0; i < 32; ++i) {
+        volatile float a = orc_f16_to_f32(src[i]) * inv;
+        q8[(size_t)r * D + 32 * g + i] = (int8_t)nearbyintf(a);
+      }
+      qs[(size_t)r * (D / 32) + g] = s;
+    }
+}
+
+/* fp64 attention over dequantized values: q [M][QH][D], k, v [T][KVH][D] as doubles; the masks and merge of
+ * orc_verify_attention (dspark.hip:1308-1312, 2006-2012). */
+void orc_verify_attention_d(const double* q, const double* k, const double* v, int M, int QH, int KVH, int D, int a,
+                            int start, int window, int causal, double* out) {
+  const int G = QH / KVH, T = a + M;
+  const double scale = 1.0 / sqrt((double)D), log2e = 1.4426950408889634;
+  double* s = (double*)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+  for (int t = 0; t < M; ++t)
+    for (int qh = 0; qh < QH; ++qh) {
+      const int h = qh / G, row = t * QH + qh;
+      const double* qr = q + (size_t)row * D;
+      double mx = -INFINITY;
+      for (int kp = 0; kp < T; ++kp) {
+        double dot = -INFINITY;
+        if (key_valid(kp, t, M, a, start, window, causal)) {
+          const double* kr = k + ((size_t)kp * KVH + h) * D;
+          dot = 0.0;
+          for (int d = 0; d < D; ++d) dot += qr[d] * kr[d];
+          dot *= scale * log2e;
+          if (dot > mx) mx = dot;
+        }
+        s[kp] = dot;
+      }
+      double sum = 0.0;
+      double* o = out + (size_t)row * D;
+      for (int d = 0; d < D; ++d) o[d] = 0.0;
+      if (mx != -INFINITY) {
+        for (int kp = 0; kp < T; ++kp) {
+          if (s[kp] == -INFINITY) continue;
+          const double p = exp2(s[kp] - mx);
+          sum += p;
+          const double* vr = v + ((size_t)kp * KVH + h) * D;
+          for (int d = 0; d < D; ++d) o[d] += p * vr[d];
+        }
+      }
+      for (int d = 0; d < D; ++d) o[d] = sum > 0 ? o[d] / sum : 0.0;
+    }
+  free(s);
+}
+
+/* The reference's int8 verify attention as the fp64 softmax attention of its int8 operands (the reference's own
+ * accuracy claim is against exactly this, benchmarks/verify_attention.txt): Q quantized per 32-dim group
+ * (orc_rec_quantize_q), K and V of position kpos and head h read from the record pages (through bt) and dequantized
+ * (q x scale) as they are used, so memory stays at the pages whatever the context. Masks and softmax as
+ * orc_verify_attention_d, term for term. */
+static const uint8_t* rec_at(const uint8_t* pages, const int32_t* bt, int KVH, int pos, int h) {
+  const int phys = bt ? bt[pos / 32] : pos / 32;
+  return pages + (size_t)phys * 32 * KVH * 264 + ((size_t)(pos % 32) * KVH + h) * 264;
+}
+
+void orc_verify_attention_rec(const uint16_t* q, const uint8_t* pages, const int32_t* bt, int M, int QH, int KVH,
+                              int a, int start, int window, int causal, double* out) {
+  const int D = 128, T = a + M, rows = M * QH, G = QH / KVH;
+  const double scale = 1.0 / sqrt((double)D), log2e = 1.4426950408889634;
+  int8_t* q8 = (int8_t*)malloc((size_t)rows * D);
+  float* qs = (float*)malloc(sizeof(float) * (size_t)rows * (D / 32));
+  double* s = (double*)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+  double qd[128];
+  orc_rec_quantize_q(q, rows, D, q8, qs);
+  for (int t = 0; t < M; ++t)
+    for (int qh = 0; qh < QH; ++qh) {
+      const int h = qh / G, row = t * QH + qh;
+      for (int d = 0; d < D; ++d) qd[d] = (double)q8[(size_t)row * D + d] * (double)qs[(size_t)row * (D / 32) + d / 32];
+      double mx = -INFINITY;
+      for (int kp = 0; kp < T; ++kp) {
+        double dot = -INFINITY;
+        if (key_valid(kp, t, M, a, start, window, causal)) {
+          const uint8_t* r = rec_at(pages, bt, KVH, kp, h);
+          float ks;
+          memcpy(&ks, r + D, 4);
+          dot = 0.0;
+          for (int d = 0; d < D; ++d) dot += qd[d] * ((double)(int8_t)r[d] * (double)ks);
+          dot *= scale * log2e;
+          if (dot > mx) mx = dot;
+        }
+        s[kp] = dot;
+      }
+      double sum = 0.0;
+      double* o = out + (size_t)row * D;
+      for (int d = 0; d < D; ++d) o[d] = 0.0;
+      if (mx != -INFINITY) {
+        for (int kp = 0; kp < T; ++kp) {
+          if (s[kp] == -INFINITY) continue;
+          const double p = exp2(s[kp] - mx);
+          sum += p;
+          const uint8_t* r = rec_at(pages, bt, KVH, kp, h);
+          float vs;
+          memcpy(&vs, r + 2 * D + 4, 4);
+          for (int d = 0; d < D; ++d) o[d] += p * ((double)(int8_t)r[D + 4 + d] * (double)vs);
+        }
+      }
+      for (int d = 0; d < D; ++d) o[d] = sum > 0 ? o[d] / sum : 0.0;
+    }
+  free(q8);
+  free(qs);
+  free(s);
+}
+
 /* ------------------------------------------------------------------ weight formats */
 
 static float round_even(float f) { return (float)nearbyint((double)f); }

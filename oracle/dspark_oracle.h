@@ -16,6 +16,9 @@
  *   accept / commit ......... invariants (0%/100% planting, offsets) + hand-worked cases
  *   int8 GEMM / crop head ... numpy fp64 matmul; quantization KATs internal/weights/quant_test.go:9-55
  *   Markov lane transpose ... reference KAT cmd/pack/main_test.go:8-28
+ *   int8 K/V records ........ quantize_pair closed forms (half-away ties, clamp, the 1e-6 floor, exact multiples),
+ *                             round-trip bound |x - q s| <= s/2, byte layout; Q group quantization vs numpy rint;
+ *                             fp64 attention of dequantized operands vs orc_verify_attention on fp16-valued input
  *   target/drafter layers ... composed of the pinned pieces above + numpy restatements of RMS norm, RoPE,
  *                             short conv (tests/test_oracle.py::test_rms_norm_rope_conv)
  */
@@ -60,6 +63,17 @@ void orc_verify_attention_mt(const uint16_t* q, const uint16_t* k, const uint16_
                              int a, int start, int window, int causal, double* out, int threads);
 void orc_verify_attention_f32_mt(const uint16_t* q, const uint16_t* k, const uint16_t* v, int M, int QH, int KVH, int D,
                                  int a, int start, int window, int causal, float* out, int threads);
+
+/* ---- int8 K/V records (kernels/ops.hip:212-251; internal/model/engine.go:30-32; dspark.hip:1020-1046)
+ * Record of (position, KV head): K int8[128] | f32 k scale | V int8[128] | f32 v scale (264 B), pages of 32 positions
+ * laid out [page][slot][KV head][record]. */
+float orc_rec_quantize(const float* x, int D, int8_t* q);
+void orc_kv_write_rec(const float* k, const float* v, int n, int KVH, int pos0, const int32_t* bt, uint8_t* pages);
+void orc_rec_quantize_q(const uint16_t* q, int rows, int D, int8_t* q8, float* qs);
+void orc_verify_attention_d(const double* q, const double* k, const double* v, int M, int QH, int KVH, int D, int a,
+                            int start, int window, int causal, double* out);
+void orc_verify_attention_rec(const uint16_t* q, const uint8_t* pages, const int32_t* bt, int M, int QH, int KVH,
+                              int a, int start, int window, int causal, double* out);
 
 /* ---- argmax key and penalised verify argmax (dspark.hip:967-971, 2222-2300; internal/sample/sample.go:59-117) */
 uint64_t orc_argmax_key(float v, uint32_t idx);

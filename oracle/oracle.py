@@ -81,6 +81,11 @@ def lib():
             "orc_conv_step": (ctypes.c_float, [ctypes.c_float, ctypes.c_float, ctypes.c_float, c_f32p, ctypes.c_int,
                                                c_f32p]),
             "orc_silu": (ctypes.c_float, [ctypes.c_float]),
+            "orc_rec_quantize": (ctypes.c_float, [c_f32p, ctypes.c_int, c_i8p]),
+            "orc_kv_write_rec": (None, [c_f32p, c_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_i32p, c_u8p]),
+            "orc_rec_quantize_q": (None, [c_u16p, ctypes.c_int, ctypes.c_int, c_i8p, c_f32p]),
+            "orc_verify_attention_d": (None, [c_f64p, c_f64p, c_f64p] + [ctypes.c_int] * 8 + [c_f64p]),
+            "orc_verify_attention_rec": (None, [c_u16p, c_u8p, c_i32p] + [ctypes.c_int] * 7 + [c_f64p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -127,6 +132,84 @@ def int8_uniform(seed, shape):
 def uniform_u32(seed, n, bound):
     out = np.empty(n, dtype=np.uint32)
     lib().orc_gen_uniform_u32(seed, n, bound, _p(out, c_u32p))
+    return out
+
+
+# ---------------------------------------------------------------- int8 K/V records
+REC_BYTES = 264
+
+
+def rec_quantize(x):
+    """quantize_pair of one 128-value row (fp32): (int8 [128], scale)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.shape, dtype=np.int8)
+    s = lib().orc_rec_quantize(_p(x, c_f32p), x.size, _p(q, c_i8p))
+    return q, np.float32(s)
+
+
+def kv_write_rec(k, v, pages, pos0=0, bt=None):
+    """k, v fp32 [n][KVH][128] -> records in `pages` (uint8 [n_pages][32][KVH][264]), in place."""
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    n, KVH, D = k.shape
+    assert D == 128 and v.shape == k.shape and pages.dtype == np.uint8 and pages.flags.c_contiguous
+    btp = None
+    if bt is not None:
+        bt = np.ascontiguousarray(bt, dtype=np.int32)
+        btp = _p(bt, c_i32p)
+    lib().orc_kv_write_rec(_p(k, c_f32p), _p(v, c_f32p), n, KVH, pos0, btp, _p(pages, c_u8p))
+    return pages
+
+
+def rec_pages(n_pages, KVH):
+    return np.zeros((n_pages, 32, KVH, REC_BYTES), dtype=np.uint8)
+
+
+def rec_read(pages, pos, h, bt=None):
+    """(k int8 [128], k scale, v int8 [128], v scale) of position pos, KV head h."""
+    phys = int(bt[pos // 32]) if bt is not None else pos // 32
+    r = pages[phys, pos % 32, h]
+    return (r[:128].view(np.int8).copy(), r[128:132].view(np.float32)[0], r[132:260].view(np.int8).copy(),
+            r[260:264].view(np.float32)[0])
+
+
+def rec_quantize_q(q):
+    """q fp16 bits [rows][D] -> (int8 [rows][D], group scales fp32 [rows][D / 32])."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    rows, D = q.shape
+    q8 = np.empty((rows, D), dtype=np.int8)
+    qs = np.empty((rows, D // 32), dtype=np.float32)
+    lib().orc_rec_quantize_q(_p(q, c_u16p), rows, D, _p(q8, c_i8p), _p(qs, c_f32p))
+    return q8, qs
+
+
+def verify_attention_d(q, k, v, a, start=0, window=0, causal=True):
+    """fp64 attention of fp64 operands: q [M][QH][D], k, v [T][KVH][D]."""
+    q = np.ascontiguousarray(q, dtype=np.float64)
+    k = np.ascontiguousarray(k, dtype=np.float64)
+    v = np.ascontiguousarray(v, dtype=np.float64)
+    M, QH, D = q.shape
+    KVH = k.shape[1]
+    assert k.shape[0] >= a + M and k.shape == v.shape
+    out = np.empty((M, QH, D), dtype=np.float64)
+    lib().orc_verify_attention_d(_p(q, c_f64p), _p(k, c_f64p), _p(v, c_f64p), M, QH, KVH, D, a, start, window,
+                                 int(causal), _p(out, c_f64p))
+    return out
+
+
+def verify_attention_rec(q, pages, a, start=0, window=0, causal=True, bt=None):
+    """q fp16 bits [M][QH][128]; pages uint8 [n][32][KVH][264]. fp64 [M][QH][128]."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    pages = np.ascontiguousarray(pages, dtype=np.uint8)
+    M, QH, D = q.shape
+    KVH = pages.shape[2]
+    btp = None
+    if bt is not None:
+        bt = np.ascontiguousarray(bt, dtype=np.int32)
+        btp = _p(bt, c_i32p)
+    out = np.empty((M, QH, D), dtype=np.float64)
+    lib().orc_verify_attention_rec(_p(q, c_u16p), _p(pages, c_u8p), btp, M, QH, KVH, a, start, window, int(causal),
+                                   _p(out, c_f64p))
     return out
 
 

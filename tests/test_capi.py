@@ -110,6 +110,43 @@ def test_bounds_are_checked_on_the_host():
     assert not h.value
 
 
+def test_record_entry_points_check_their_arguments():
+    """The int8-record path: workspace sizes of the reference geometry (one key split per workgroup over all four KV
+    heads, the fp16 path's partial layout), and refusals before any launch (D, KVH, rows, a V pool, pools of 2 GiB,
+    rows past the pool)."""
+    host = load_host()
+    lib = host.lib()
+    fake = ctypes.c_void_p(256)
+    args = host.AttnArgs()
+    args.M, args.QH, args.KVH, args.D, args.a, args.causal = 9, 16, 4, 128, 131063, 1   # 4096 pages
+    ws = lib.dspark_verify_attention_rec_workspace(ctypes.byref(args))
+    # 36 rows -> 3 row blocks of 16 per KV head, 4 heads, 256 splits of 16 pages: acc [4][S][48][128] f32 + (m, l)
+    S = 256
+    acc = 4 * S * 48 * 128 * 4
+    assert ws == acc + ((4 * S * 48 * 8 + 255) // 256) * 256, ws
+    args.M = 17    # 68 rows per KV head: more than one wave per row block can take
+    assert lib.dspark_verify_attention_rec_workspace(ctypes.byref(args)) == 0
+    args.M, args.D = 9, 64
+    assert lib.dspark_verify_attention_rec_workspace(ctypes.byref(args)) == 0
+    args.D, args.KVH, args.QH = 128, 8, 32
+    assert lib.dspark_verify_attention_rec_workspace(ctypes.byref(args)) == 0
+    args.KVH, args.QH = 4, 16
+    args.q, args.k_pages, args.v_pages, args.out = 256, 256, 256, 256   # a V pool: records carry V themselves
+    args.kv_pages = 4200
+    assert lib.dspark_verify_attention_rec(ctypes.byref(args), None) == 1001
+    args.v_pages = None
+    args.kv_pages = (1 << 31) // (32 * 4 * 264) + 1                      # pool of 2 GiB or more
+    assert lib.dspark_verify_attention_rec(ctypes.byref(args), None) == 1001
+    args.kv_pages = 100                                                   # positions past the pool, no block table
+    assert lib.dspark_verify_attention_rec(ctypes.byref(args), None) == 1001
+    args.kv_pages = 4200
+    assert lib.dspark_verify_attention_rec(ctypes.byref(args), None) == 1002   # no workspace
+    # writer: 10 pages hold positions 0..319
+    assert lib.dspark_kv_write_rec(fake, fake, 512, fake, None, 10, 4, 300, 40, None) == 1001
+    assert lib.dspark_kv_write_rec(fake, fake, 256, fake, None, 10, 4, 0, 1, None) == 1001   # row < KVH * 128
+    assert lib.dspark_kv_write_rec(None, fake, 512, fake, None, 10, 4, 0, 1, None) == 1001
+
+
 @pytest.mark.parametrize("base,pairs,D", [(1e6, 32, 128), (1e4, 64, 128), (1e6, 32, 64), (1e4, 16, 64)])
 def test_rope_table_matches_the_reference_formula(base, pairs, D):
     """The library's table (what the engine uploads) against a numpy restatement, bit for bit over 70000 positions, plus
