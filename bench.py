@@ -108,11 +108,13 @@ def cpu_baseline_c2(ctx, M, QH, KVH, D, seconds):
                     "core of the host"}
 
 
-def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None):
-    """Verify attention of L GQA layers (32 q / 8 kv heads, head_dim 64) at context ctx for M verify tokens, `sets`
-    rotating KV sets (so the Infinity Cache cannot serve a step from the previous one). A step = per layer the
-    key-split pass and the merge. Returns step time, GB/s, and the split pass's average launch time."""
-    QH, KVH, D = 32, 8, 64
+def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None, rec=False):
+    """Verify attention of L GQA layers at context ctx for M verify tokens, `sets` rotating KV sets (so the Infinity
+    Cache cannot serve a step from the previous one). A step = per layer the key-split pass and the merge. fp16 pages:
+    32 q / 8 kv heads, head_dim 64 (the configs' geometry); rec: int8 K/V records of the reference geometry (16 q / 4 kv
+    heads, head_dim 128, 264 bytes per position and KV head). Returns step time, GB/s, and the split pass's average
+    launch time."""
+    QH, KVH, D = (16, 4, 128) if rec else (32, 8, 64)
     steps = steps or args.steps
     warmup = args.warmup if warmup is None else warmup
     lib = host.lib()
@@ -126,30 +128,51 @@ def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None)
     def rnd(*shape):
         return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(torch.float16)
 
-    kv = [[(rnd(n_pages, KVH, 32, D), rnd(n_pages, KVH, D, 32)) for _ in range(L)] for _ in range(sets)]
+    def rnd32(*shape):
+        return torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+
     q = [rnd(M, QH, D) for _ in range(L)]
-    fk = [rnd(M, KVH, D) for _ in range(L)]
-    fv = [rnd(M, KVH, D) for _ in range(L)]
     out = [torch.empty((M, QH, D), dtype=torch.float16, device=dev) for _ in range(L)]
-    argv = [[host.attn_args(q[l], kv[s][l][0], kv[s][l][1], ctx, out=out[l]) for l in range(L)] for s in range(sets)]
-    need = lib.dspark_verify_attention_workspace(ctypes.byref(argv[0][0]))
+    if rec:
+        # every position's records written by the library's quantize_pair writer from N(0,1) rows
+        kv = [[host.rec_pages_alloc(n_pages, KVH) for _ in range(L)] for _ in range(sets)]
+        for s_ in range(sets):
+            for l in range(L):
+                for p0 in range(0, ctx + M, 16384):
+                    n = min(16384, ctx + M - p0)
+                    host.kv_write_rec(rnd32(n, KVH, D), rnd32(n, KVH, D), kv[s_][l], p0)
+        argv = [[host.rec_attn_args(q[l], kv[s_][l], ctx, out=out[l]) for l in range(L)] for s_ in range(sets)]
+        need = lib.dspark_verify_attention_rec_workspace(ctypes.byref(argv[0][0]))
+        f_all, f_split, f_merge = (lib.dspark_verify_attention_rec, lib.dspark_verify_attention_rec_splits,
+                                   lib.dspark_verify_attention_rec_combine)
+        layer_bytes = ctx * KVH * host.REC_BYTES
+    else:
+        kv = [[(rnd(n_pages, KVH, 32, D), rnd(n_pages, KVH, D, 32)) for _ in range(L)] for _ in range(sets)]
+        fk = [rnd(M, KVH, D) for _ in range(L)]
+        fv = [rnd(M, KVH, D) for _ in range(L)]
+        argv = [[host.attn_args(q[l], kv[s_][l][0], kv[s_][l][1], ctx, out=out[l]) for l in range(L)]
+                for s_ in range(sets)]
+        need = lib.dspark_verify_attention_workspace(ctypes.byref(argv[0][0]))
+        f_all, f_split, f_merge = (lib.dspark_verify_attention, lib.dspark_verify_attention_splits,
+                                   lib.dspark_verify_attention_combine)
+        layer_bytes = ctx * KVH * D * 2 * 2
+        # The verified block's K/V rows go into every layer's pages once (in the full step the kernel that produces
+        # them writes them); each step then re-verifies the same block.
+        for s_ in range(sets):
+            for l in range(L):
+                host.check(lib.dspark_kv_write(ctypes.c_void_p(fk[l].data_ptr()), ctypes.c_void_p(fv[l].data_ptr()),
+                                               KVH * D, ctypes.c_void_p(kv[s_][l][0].data_ptr()),
+                                               ctypes.c_void_p(kv[s_][l][1].data_ptr()), None, n_pages, KVH, D, ctx, M,
+                                               sh), "kv_write")
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
-    for s in range(sets):
+    for s_ in range(sets):
         for l in range(L):
-            argv[s][l].workspace, argv[s][l].workspace_bytes = ws.data_ptr(), ws.numel()
-    # The verified block's K/V rows go into every layer's pages once (in the full step the kernel that produces them
-    # writes them); each step then re-verifies the same block.
-    for s in range(sets):
-        for l in range(L):
-            host.check(lib.dspark_kv_write(ctypes.c_void_p(fk[l].data_ptr()), ctypes.c_void_p(fv[l].data_ptr()),
-                                           KVH * D, ctypes.c_void_p(kv[s][l][0].data_ptr()),
-                                           ctypes.c_void_p(kv[s][l][1].data_ptr()), None, n_pages, KVH, D, ctx, M, sh),
-                       "kv_write")
+            argv[s_][l].workspace, argv[s_][l].workspace_bytes = ws.data_ptr(), ws.numel()
 
     def step(i):
-        s = i % sets
+        s_ = i % sets
         for l in range(L):
-            host.check(lib.dspark_verify_attention(ctypes.byref(argv[s][l]), sh), "verify_attention")
+            host.check(f_all(ctypes.byref(argv[s_][l]), sh), "verify_attention")
 
     for i in range(warmup):
         step(i)
@@ -161,22 +184,21 @@ def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None)
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / steps
-    layer_bytes = ctx * KVH * D * 2 * 2
 
-    # Dominant kernel: the key-split pass (verify_attn_lds_kernel), which streams the K/V pages. Its average launch
-    # duration: the same launches back to back with nothing between them, HIP events recorded on the library's stream
-    # around all of them, elapsed / launches (launch gaps included, so this errs low). The merge kernel is timed the
-    # same way and reported beside it.
+    # Dominant kernel: the key-split pass, which streams the K/V pages. Its average launch duration: the same launches
+    # back to back with nothing between them, HIP events recorded on the library's stream around all of them,
+    # elapsed / launches (launch gaps included, so this errs low). The merge kernel is timed the same way and reported
+    # beside it.
     n_launch = steps * L
     t0, t1, t2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
     t0.record(stream)
     for i in range(steps):
         for l in range(L):
-            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % sets][l]), sh), "splits")
+            host.check(f_split(ctypes.byref(argv[i % sets][l]), sh), "splits")
     t1.record(stream)
     for i in range(steps):
         for l in range(L):
-            host.check(lib.dspark_verify_attention_combine(ctypes.byref(argv[i % sets][l]), sh), "combine")
+            host.check(f_merge(ctypes.byref(argv[i % sets][l]), sh), "combine")
     t2.record(stream)
     torch.cuda.synchronize()
     kern_avg = t0.elapsed_time(t1) / n_launch
@@ -187,7 +209,7 @@ def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None)
     for i in range(steps):
         for l in range(L):
             ev[j][0].record(stream)
-            host.check(lib.dspark_verify_attention_splits(ctypes.byref(argv[i % sets][l]), sh), "splits")
+            host.check(f_split(ctypes.byref(argv[i % sets][l]), sh), "splits")
             ev[j][1].record(stream)
             j += 1
     torch.cuda.synchronize()
@@ -198,6 +220,21 @@ def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None)
             "step_gbs": L * layer_bytes / (ms_per_step * 1e-3) / 1e9, "split_avg_ms": kern_avg,
             "split_gbs": layer_bytes / (kern_avg * 1e-3) / 1e9, "merge_avg_ms": combine_avg,
             "split_bracket_median_ms": split_br[len(split_br) // 2]}
+
+
+def rec_attention_fields(args, host, torch):
+    """Verify attention over the reference's int8 K/V records (reference geometry 16/4/128, its 9-token block) at 32k
+    and 128k keys: 2 layers, 2 rotating record sets."""
+    out = []
+    for ctx in (32768, 131072):
+        r = bench_attention(args, host, torch, 2, ctx, 9, 2, steps=max(4, args.steps // 2), warmup=2, rec=True)
+        out.append({"ctx": ctx, "verify_tokens": 9, "record_bytes_per_layer": r["layer_bytes"],
+                    "ms_per_layer": round(r["ms_per_step"] / 2, 5), "step_GBs": round(r["step_gbs"], 1),
+                    "step_frac": round(r["step_gbs"] / HBM_PEAK_GBS, 4),
+                    "split_avg_us": round(r["split_avg_ms"] * 1e3, 2), "split_GBs": round(r["split_gbs"], 1),
+                    "split_frac": round(r["split_gbs"] / HBM_PEAK_GBS, 4),
+                    "merge_avg_us": round(r["merge_avg_ms"] * 1e3, 2)})
+    return out
 
 
 def bench_c2(args, host, torch):
@@ -343,7 +380,19 @@ def engine_setup(host, torch, ctx, block, seed, desc=None):
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     for name in eng.names():
-        if name.startswith(("kv.", "ring.D", "conv.")):
+        if name.endswith(".rec"):
+            # int8 K/V records: codes uniform in [-127, 127], both scales 1/40 (|K|, |V| up to ~3, as N(0,1) rows give)
+            ptr_, nbytes = eng.tensor(name)
+            chunk = 264 * (1 << 18)
+            for off in range(0, nbytes, chunk):
+                n = min(chunk, nbytes - off) // 264
+                r = torch.randint(-127, 128, (n, 264), generator=g, device="cuda", dtype=torch.int32).to(torch.int8)
+                sc = torch.full((n, 1), 1.0 / 40, device="cuda", dtype=torch.float32).view(torch.int8)
+                r[:, 128:132] = sc
+                r[:, 260:264] = sc
+                host._hip().hipMemcpy(ctypes.c_void_p(ptr_ + off), ctypes.c_void_p(r.data_ptr()),
+                                      ctypes.c_size_t(264 * n), 3)
+        elif name.startswith(("kv.", "ring.D", "conv.")):
             ptr_, nbytes = eng.tensor(name)
             chunk = 64 << 20
             for off in range(0, nbytes, chunk):
@@ -417,7 +466,8 @@ def round_bytes(eng, desc, a):
     the block); one Markov table row and one cropped-head row per draft step. Returns (round bytes, target K/V bytes)."""
     w = sum(eng.tensor(n)[1] for n in eng.names() if n.endswith((".w", ".s")) and not n.startswith("markov."))
     B = desc.block
-    row = desc.kv_heads * desc.head_dim * 2 * 2  # K and V bytes per position
+    # K and V bytes per position: fp16 pages, or int8 records (264 bytes per KV head)
+    row = desc.kv_heads * (264 if desc.kv_format else desc.head_dim * 2 * 2)
     kv = 0
     for i in range(desc.n_layers):
         if desc.layer_kind[i] == 1:
@@ -536,10 +586,11 @@ def bench_engine(args, host, torch, workload):
     for k in list(cache):
         cache.pop(k)[1].close()
     model = ("reference geometry: 24 layers (13 conv k=7 / 6 full / 5 sliding-256 attention, 16/4/128), FFN 7680, "
-             "vocab 128000, 3-layer drafter; fp16 KV" if ref else "C4 geometry")
+             "vocab 128000, 3-layer drafter; the reference's int8 K/V records" if ref else "C4 geometry")
+    kv = ("int8 K/V records (codes uniform in [-127, 127], scales 1/40)" if ref else "N(0,1) fp16 KV caches")
     return {"metric": f"greedy decode tok/s (DSpark rounds, random-init model, {model})", "workload": workload,
             "rounds": rounds, "warmup": warm, "cases": out,
-            "data": "random-init weights (int8 uniform, per-row fp16 scales), N(0,1) fp16 KV caches; planted drafts "
+            "data": f"random-init weights (int8 uniform, per-row fp16 scales), {kv}; planted drafts "
                     "replay the target's own greedy chain (one-token verify rounds) with per-position probability p"}
 
 
@@ -566,9 +617,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy", "attn"])
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy", "attn", "rec"])
     ap.add_argument("--ctx", type=int, default=131072, help="attn workload: context (keys before the block)")
-    ap.add_argument("--tokens", type=int, default=33, help="attn workload: verify tokens (M)")
+    ap.add_argument("--tokens", type=int, default=0, help="attn / rec workload: verify tokens (default 33 / 9)")
     ap.add_argument("--layers", type=int, default=2, help="attn workload: layers per step")
     ap.add_argument("--c2-only", action="store_true",
                     help="default workload without the headline tiers and the C5 attention fields")
@@ -588,10 +639,13 @@ def main():
     if args.workload == "c3":
         print(json.dumps(bench_c3(args, host, torch)), flush=True)
         return
-    if args.workload == "attn":
-        # verify attention alone (the C2 kernels) at any context and block: what the C5 attention profiles run
-        r = bench_attention(args, host, torch, args.layers, args.ctx, args.tokens, 2)
-        print(json.dumps({"metric": "verify attention HBM GB/s", "workload": "attn", "ctx": args.ctx,
+    if args.workload in ("attn", "rec"):
+        # verify attention alone at any context and block: the C2 kernels (fp16 pages, 32/8/64), or the int8-record
+        # kernels (reference geometry 16/4/128); what the attention profiles run
+        rec = args.workload == "rec"
+        args.tokens = args.tokens or (9 if rec else 33)
+        r = bench_attention(args, host, torch, args.layers, args.ctx, args.tokens, 2, rec=rec)
+        print(json.dumps({"metric": "verify attention HBM GB/s", "workload": args.workload, "ctx": args.ctx,
                           "verify_tokens": args.tokens, "layers": args.layers, "steps": args.steps,
                           "ms_per_layer": round(r["ms_per_step"] / args.layers, 5),
                           "step_GBs": round(r["step_gbs"], 1), "split_avg_us": round(r["split_avg_ms"] * 1e3, 2),
@@ -619,6 +673,7 @@ def main():
                     "verify_attention.txt:54-58) / this round time; a round verifies the same tokens whatever is "
                     "accepted, so its time does not depend on the draws; tok_s is the rate of the planted draws"}
         res["c5_attention"] = c5_attention_fields(args, host, torch)
+        res["ref_int8_record_attention"] = rec_attention_fields(args, host, torch)
     if not args.no_cpu:
         sys.path.insert(0, ROOT)
         res["cpu_baseline"] = cpu_baseline_c2(32768, 16, 32, 8, 64, args.cpu_seconds)

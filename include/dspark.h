@@ -139,6 +139,9 @@ int dspark_kv_write_rec(const float* k, const float* v, int64_t row_stride, void
  * combine_phase (2132-2185). */
 size_t dspark_verify_attention_rec_workspace(const dspark_attn_args* args);
 int dspark_verify_attention_rec(const dspark_attn_args* args, dspark_stream_t stream);
+/* Its two phases called apart, as dspark_verify_attention_splits / _combine (bit-identical to the one call). */
+int dspark_verify_attention_rec_splits(const dspark_attn_args* args, dspark_stream_t stream);
+int dspark_verify_attention_rec_combine(const dspark_attn_args* args, dspark_stream_t stream);
 
 /* ---------------------------------------------------------------- verify argmax (greedy head)
  * best_keys[t] = max over r < V of key(pv, r), pv the repetition-penalised fp16-rounded logit (seen[] bitmap, plus
@@ -228,6 +231,11 @@ typedef struct dspark_model_desc {
   float rope_base_swa;
   int32_t rope_pairs_swa;
   int32_t conv_slots;      /* conv-state slots per conv layer, slot 0 the running state (engine.go:122, 138); >= 1 */
+  /* K/V format of the target's attention layers and the drafter ring: 0 fp16 pages in matrix-core order (above), 1 the
+   * reference's int8 records (DSPARK_REC_BYTES per position and KV head, quantize_pair; engine.go:30-32), which needs
+   * head_dim 128, kv_heads 4 and q_heads / kv_heads x block <= 64. Tensors "kv.L<i>.rec" / "ring.D<j>.rec" then hold
+   * the record pages instead of "kv.L<i>.k|v" / "ring.D<j>.k|v". */
+  int32_t kv_format;
 } dspark_model_desc;
 
 typedef struct dspark_engine dspark_engine;

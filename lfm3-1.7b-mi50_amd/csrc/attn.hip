@@ -600,28 +600,34 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
 #ifndef DSPARK_ATTN_COMBINE_LANES
 #define DSPARK_ATTN_COMBINE_LANES 8
 #endif
+// Up to 64 splits: COMBINE_LANES lanes of up to 8 splits each; more splits (the record kernel's, up to 256): 32 lanes of
+// up to 8 each, so every split's loads are in flight at once (batches of 64 one after the other measured 9-11 us for
+// 256 splits).
 constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 64 / COMBINE_LANES;
+constexpr int COMBINE_LANES_WIDE = 32;
 
-template <int D>
+template <int D, int LANES>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
+  constexpr int PER_LANE = 8;  // splits per lane per batch
   const int run = run_flag_load(p.st);  // tested once the partial loads are in flight
   const int hr = blockIdx.y, h = hr / p.RG, rg = hr % p.RG;
   const int R = p.R;
-  const int e = blockIdx.x * (256 / COMBINE_LANES) + (int)(threadIdx.x / COMBINE_LANES);
-  const int j = threadIdx.x % COMBINE_LANES;
-  const bool live = e < R * D / 4;
+  const int e = blockIdx.x * (256 / LANES) + (int)(threadIdx.x / LANES);
+  const int j = threadIdx.x % LANES;
+  // rows past G*M (padding of the last row block) are neither read nor stored
+  const bool live = e < R * D / 4 && rg * R + e / (D / 4) < p.G * p.M;
   const int r = live ? e / (D / 4) : 0, c4 = e % (D / 4);
   const size_t slot0 = (size_t)hr * p.S;
-  // Splits in batches of COMBINE_LANES x COMBINE_MAX_PER_LANE (one batch up to 64 splits): a lane's loads of a batch
-  // are all in flight before the first is used, and each batch folds into the lane's running (m, l, acc).
+  // Splits in batches of LANES x PER_LANE: a lane's loads of a batch are all in flight before the first is used,
+  // and each batch folds into the lane's running (m, l, acc).
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0, 0, 0, 0};
-  for (int b0 = 0; b0 < p.S; b0 += COMBINE_LANES * COMBINE_MAX_PER_LANE) {
-    f32x2 ml[COMBINE_MAX_PER_LANE];
-    f32x4 av[COMBINE_MAX_PER_LANE];
+  for (int b0 = 0; b0 < p.S; b0 += LANES * PER_LANE) {
+    f32x2 ml[PER_LANE];
+    f32x4 av[PER_LANE];
 #pragma unroll
-    for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
-      const int sp = b0 + j + COMBINE_LANES * i;
+    for (int i = 0; i < PER_LANE; ++i) {
+      const int sp = b0 + j + LANES * i;
       const bool ok = live && sp < p.S;
       ml[i] = ok ? ldg(p.part_ml + (slot0 + sp) * R + r) : f32x2{-INFINITY, 0.f};
       av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + ((slot0 + sp) * R + r) * D) + c4) : f32x4{0, 0, 0, 0};
@@ -632,14 +638,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     }
     float mb = m;
 #pragma unroll
-    for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) mb = fmaxf(mb, ml[i][0]);
+    for (int i = 0; i < PER_LANE; ++i) mb = fmaxf(mb, ml[i][0]);
     if (mb > -INFINITY) {
       const float fr = m == -INFINITY ? 0.f : fast_exp2(m - mb);  // the running state rescaled to the batch max
       l *= fr;
       acc *= fr;
       m = mb;
 #pragma unroll
-      for (int i = 0; i < COMBINE_MAX_PER_LANE; ++i) {
+      for (int i = 0; i < PER_LANE; ++i) {
         const float f = ml[i][0] == -INFINITY ? 0.f : fast_exp2(ml[i][0] - m);
         l = fmaf(f, ml[i][1], l);
         acc += f * av[i];
@@ -647,7 +653,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     }
   }
 #pragma unroll
-  for (int off = 1; off < COMBINE_LANES; off <<= 1) {
+  for (int off = 1; off < LANES; off <<= 1) {
     const float mk = __shfl_xor(m, off), lk = __shfl_xor(l, off);
     f32x4 ak;
 #pragma unroll
@@ -662,7 +668,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
   }
   if (j != 0 || !live) return;
   const int row = rg * R + r;
-  if (row >= p.G * p.M) return;
   float scale = l > 0.f ? 1.f / l : 0.f;
   const int t = row / p.G, qh = h * p.G + row % p.G;
   if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * p.QH + qh)));
@@ -931,12 +936,17 @@ int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
     if (rc) return rc;
   }
   if (phases & 2) {
-    constexpr int QPB = 256 / COMBINE_LANES;  // output quads per block
-    const dim3 grid((p.R * D / 4 + QPB - 1) / QPB, p.KVH * p.RG);
-    if (D == 64)
-      hipLaunchKernelGGL(attn_combine_kernel<64>, grid, dim3(256), 0, s, p);
+    const bool wide = p.S > COMBINE_LANES * COMBINE_MAX_PER_LANE;
+    const int qpb = 256 / (wide ? COMBINE_LANES_WIDE : COMBINE_LANES);  // output quads per block
+    const dim3 grid((p.R * D / 4 + qpb - 1) / qpb, p.KVH * p.RG);
+    if (D == 64 && !wide)
+      hipLaunchKernelGGL((attn_combine_kernel<64, COMBINE_LANES>), grid, dim3(256), 0, s, p);
+    else if (D == 64)
+      hipLaunchKernelGGL((attn_combine_kernel<64, COMBINE_LANES_WIDE>), grid, dim3(256), 0, s, p);
+    else if (!wide)
+      hipLaunchKernelGGL((attn_combine_kernel<128, COMBINE_LANES>), grid, dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL(attn_combine_kernel<128>, grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((attn_combine_kernel<128, COMBINE_LANES_WIDE>), grid, dim3(256), 0, s, p);
   }
   return (int)hipGetLastError();
 }

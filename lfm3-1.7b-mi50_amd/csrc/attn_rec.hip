@@ -9,7 +9,8 @@
 //
 // Attention numerics of the reference's int8 path (query_fresh, dspark.hip:1020-1035; attention_pass, 1215-1412):
 //   Q int8 per 32-dim group: s_g = max(amax_g / 127, 1e-20), q8 = rint(q * rcp(s_g));
-//   score (log2 units) = ks * sum_g idot_g * (s_g * log2(e) / sqrt(128)), each group's int8 dot product exact;
+//   score (log2 units) = ks * sum_g idot_g * (s_g * log2(e) / sqrt(128)), each group's int8 dot product exact
+//   (the group terms summed in order g = 0..3, where the reference sums pairs (0 + 1) + (2 + 3): an ulp of the score);
 //   p = exp2(score - m); l = sum p; P = fp16(p * vs * PSCALE); acc += P * v (int8 V, exact in fp16); o = acc / PSCALE.
 // The output is the softmax of those scores over the dequantized V, the reference's fp64 claim (accuracy against an
 // fp64 attention of the same int8 Q/K/V, benchmarks/verify_attention.txt).
@@ -49,16 +50,11 @@ static_assert(REC_PAGE % 1024 == 0, "a record page is whole 1 KB chunks");
 
 // ---------------------------------------------------------------- record writer
 // quantize_pair over one wave: lane l holds x0 = dim 2l, x1 = dim 2l + 1; stores the two int8 values at q + 2l and
-// returns the scale. Every step is one IEEE fp32 operation (no contraction), as the reference writes it.
+// returns the scale.
 __device__ __forceinline__ float rec_quantize(float x0, float x1, uint8_t* q, int lane) {
-  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const float scale = fmaxf(__fdiv_rn(amax, 127.f), 1e-6f);
+  const float scale = rec_scale(wave_max(fmaxf(fabsf(x0), fabsf(x1))));
   const float inv = __fdiv_rn(1.f, scale);
-  float a = __fmul_rn(x0, inv), b = __fmul_rn(x1, inv);
-  a = a >= 0.f ? __fadd_rn(a, 0.5f) : __fsub_rn(a, 0.5f);
-  b = b >= 0.f ? __fadd_rn(b, 0.5f) : __fsub_rn(b, 0.5f);
-  const int qa = (int)truncf(fminf(fmaxf(a, -128.f), 127.f)), qb = (int)truncf(fminf(fmaxf(b, -128.f), 127.f));
-  *reinterpret_cast<uint16_t*>(q + 2 * lane) = (uint16_t)((qa & 255) | ((qb & 255) << 8));
+  *reinterpret_cast<uint16_t*>(q + 2 * lane) = (uint16_t)((rec_code(x0, inv) & 255) | ((rec_code(x1, inv) & 255) << 8));
   return scale;
 }
 
@@ -116,39 +112,58 @@ __device__ __forceinline__ RecQ rec_quantize_q(const u32x4 (&raw)[4]) {
   return r;
 }
 
-// V of one page into the transposed fp16 copy and the page's scales: task (head hh, keys 4 kq .. + 3, dims 4 dq .. + 3)
-// reads four 4-byte pieces, transposes the 4x4 bytes and widens them (v ^ 0x80 under the exponent of 1024 is
-// 1152 + v in fp16, exact); V^T chunk c of head hh holds lane (n, g)'s keys 8 g .. + 7 of dim 16 c + n at (n + 16 g) * 16.
+// V^T copy of a page: per head 8 chunks (dims 16 c .. + 15) of 64 lane slots of 16 bytes, lane (n, g) holding keys
+// 8 g .. + 7 of dim 16 c + n, with 16 bytes of padding after every 8 slots (slot l at (l + l / 8) * 16). The PV operand
+// reads stay lane-linear (conflict-free) and the expansion's 16-byte writes fall in distinct banks.
+constexpr int VT_CHUNK = 64 * 16 + 8 * 16;  // 1152 bytes
+__device__ __forceinline__ int vt_slot(int l) { return (l + (l >> 3)) * 16; }
+
+// V of one page into the V^T copy, and the page's scales. Task (head hh, keys 8 g .. + 7, dims 4 dq .. + 3): eight
+// 4-byte reads, an 8x4 byte transpose, widening to fp16 (v ^ 0x80 under the exponent of 1024 is 1152 + v, exact) and
+// four 16-byte writes. Task bits: dq & 3, g & 1, dq >> 2, g >> 1, hh (so the 8 tasks of a write pass hit 8 bank groups).
 template <int NT>
 __device__ __forceinline__ void rec_expand(const char* page, char* vt, float* kvs) {
   const half2v bias = {(_Float16)1152.f, (_Float16)1152.f};
-  for (int task = threadIdx.x; task < REC_KVH * 8 * 32; task += NT) {
-    const int hh = task >> 8, kq = (task >> 5) & 7, dq = task & 31;
-    const char* r0 = page + ((4 * kq) * REC_KVH + hh) * REC_BYTES + REC_D + 4 + 4 * dq;
+  for (int task = threadIdx.x; task < REC_KVH * 4 * 32; task += NT) {
+    const int dq = (task & 3) | (((task >> 3) & 7) << 2), g = ((task >> 2) & 1) | (((task >> 6) & 1) << 1);
+    const int hh = task >> 7;
     constexpr int KS = REC_KVH * REC_BYTES;  // one position on
-    const uint32_t w0 = *reinterpret_cast<const uint32_t*>(r0) ^ 0x80808080u;
-    const uint32_t w1 = *reinterpret_cast<const uint32_t*>(r0 + KS) ^ 0x80808080u;
-    const uint32_t w2 = *reinterpret_cast<const uint32_t*>(r0 + 2 * KS) ^ 0x80808080u;
-    const uint32_t w3 = *reinterpret_cast<const uint32_t*>(r0 + 3 * KS) ^ 0x80808080u;
-    const uint32_t x01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u), y01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
-    const uint32_t x23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u), y23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
-    const uint32_t dims[4] = {__builtin_amdgcn_perm(x23, x01, 0x05040100u), __builtin_amdgcn_perm(x23, x01, 0x07060302u),
-                              __builtin_amdgcn_perm(y23, y01, 0x05040100u), __builtin_amdgcn_perm(y23, y01, 0x07060302u)};
+    const char* r0 = page + ((8 * g) * REC_KVH + hh) * REC_BYTES + REC_D + 4 + 4 * dq;
+    uint32_t w[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, dims[i], 0x04010400u);
-      const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, dims[i], 0x04030402u);
-      const half2v a = __builtin_bit_cast(half2v, lo) - bias, b = __builtin_bit_cast(half2v, hi) - bias;
-      const int d = 4 * dq + i;
-      char* dst = vt + (hh * 8 + (d >> 4)) * 1024 + ((d & 15) + 16 * (kq >> 1)) * 16 + (kq & 1) * 8;
-      *reinterpret_cast<u32x2*>(dst) = u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+    for (int k = 0; k < 8; ++k) w[k] = *reinterpret_cast<const uint32_t*>(r0 + k * KS) ^ 0x80808080u;
+    // dims j of keys 0-3 and 4-7: byte j of each key's word
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint32_t* v = w + 4 * half;
+      const uint32_t x01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u), y01 = __builtin_amdgcn_perm(v[1], v[0], 0x07030602u);
+      const uint32_t x23 = __builtin_amdgcn_perm(v[3], v[2], 0x05010400u), y23 = __builtin_amdgcn_perm(v[3], v[2], 0x07030602u);
+      uint32_t* d = half ? hi : lo;
+      d[0] = __builtin_amdgcn_perm(x23, x01, 0x05040100u);
+      d[1] = __builtin_amdgcn_perm(x23, x01, 0x07060302u);
+      d[2] = __builtin_amdgcn_perm(y23, y01, 0x05040100u);
+      d[3] = __builtin_amdgcn_perm(y23, y01, 0x07060302u);
+    }
+    char* base = vt + (hh * 8 + (dq >> 2)) * VT_CHUNK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half2v a = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo[j], 0x04010400u)) - bias;
+      const half2v b = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo[j], 0x04030402u)) - bias;
+      const half2v c = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, hi[j], 0x04010400u)) - bias;
+      const half2v e = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, hi[j], 0x04030402u)) - bias;
+      const int l = 4 * (dq & 3) + j + 16 * g;
+      *reinterpret_cast<u32x4*>(base + vt_slot(l)) =
+          u32x4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, c),
+                __builtin_bit_cast(uint32_t, e)};
     }
   }
   for (int e = threadIdx.x; e < REC_KVH * PAGE; e += NT) {
     const int hh = e / PAGE, key = e % PAGE;
     const char* rec = page + (key * REC_KVH + hh) * REC_BYTES;
     kvs[(hh * 2) * PAGE + key] = *reinterpret_cast<const float*>(rec + REC_D);
-    kvs[(hh * 2 + 1) * PAGE + key] = *reinterpret_cast<const float*>(rec + 2 * REC_D + 4);
+    // v scale x PSCALE (a power of two: fp16(p * (vs * PSCALE)) = fp16(fp32(p * vs) * PSCALE) exactly)
+    kvs[(hh * 2 + 1) * PAGE + key] = *reinterpret_cast<const float*>(rec + 2 * REC_D + 4) * REC_PSCALE;
   }
 }
 
@@ -159,7 +174,7 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
   constexpr int NW = REC_KVH * NRG, NT = NW * 64;
   constexpr int LPW = (REC_CHUNKS + NW - 1) / NW;  // page chunk loads per wave
   __shared__ __attribute__((aligned(16))) char ring0[REC_PAGE], ring1[REC_PAGE], ring2[REC_PAGE];
-  __shared__ __attribute__((aligned(16))) char vt[REC_KVH * 8 * 1024];
+  __shared__ __attribute__((aligned(16))) char vt[REC_KVH * 8 * VT_CHUNK];
   __shared__ __attribute__((aligned(16))) float kvs[REC_KVH * 2 * PAGE];
   __shared__ __attribute__((aligned(16))) char trash[1024];
   __shared__ int32_t sm_bt[REC_BT_MAX];
@@ -193,6 +208,7 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) qraw[qb][grp] = ldg(reinterpret_cast<const u32x4*>(qr + 32 * grp));
   }
+  __builtin_amdgcn_sched_barrier(0);  // the Q loads stay ahead of the page loads, so waiting for Q drains no page
 
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)p.kp, (short)0, (int)p.k_bytes, 0x00020000);
   // Page k of the split into `slot`: chunk c < 33 of the page goes to wave c % NW; every wave issues exactly LPW loads
@@ -264,9 +280,11 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
         const f32x4 ks = b ? ks1 : ks0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float lo = fmaf((float)ai[1][i], qv[qb].qsc[1], (float)ai[0][i] * qv[qb].qsc[0]);
-          const float hi = fmaf((float)ai[3][i], qv[qb].qsc[3], (float)ai[2][i] * qv[qb].qsc[2]);
-          sc[qb][b][i] = fmaf(lo + hi, ks[i], mneg[qb]);
+          float d = (float)ai[0][i] * qv[qb].qsc[0];
+          d = fmaf((float)ai[1][i], qv[qb].qsc[1], d);
+          d = fmaf((float)ai[2][i], qv[qb].qsc[2], d);
+          d = fmaf((float)ai[3][i], qv[qb].qsc[3], d);
+          sc[qb][b][i] = fmaf(d, ks[i], mneg[qb]);
         }
       }
     }
@@ -324,15 +342,15 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
       for (int i = 0; i < 4; ++i) {
         const float p0 = fast_exp2(sc[qb][0][i]), p1 = fast_exp2(sc[qb][1][i]);
         ps += p0 + p1;
-        pp[qb][i] = (_Float16)(__fmul_rn(p0, vs0[i]) * REC_PSCALE);
-        pp[qb][4 + i] = (_Float16)(__fmul_rn(p1, vs1[i]) * REC_PSCALE);
+        pp[qb][i] = (_Float16)__fmul_rn(p0, vs0[i]);
+        pp[qb][4 + i] = (_Float16)__fmul_rn(p1, vs1[i]);
       }
       l[qb] += ps;
     }
     // one V^T operand at a time, shared by the row blocks
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const half8 vop = *reinterpret_cast<const half8*>(vt + (h * 8 + c) * 1024 + lane * 16);
+      const half8 vop = *reinterpret_cast<const half8*>(vt + (h * 8 + c) * VT_CHUNK + vt_slot(lane));
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) o[qb][c] = mfma16x16x32(vop, pp[qb], o[qb][c]);
     }
@@ -356,6 +374,7 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
     float L = l[qb] + __shfl_xor(l[qb], 16);
     L = L + __shfl_xor(L, 32);
     if (rb >= p.nrb) break;
+    if (rb * 16 + n >= p.G * p.M) continue;  // padding rows: the merge never reads them
 #pragma unroll
     for (int c = 0; c < 8; ++c)
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[qb][c] * (1.f / REC_PSCALE)), ra,
@@ -369,7 +388,8 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
 
 // ---------------------------------------------------------------- host side
 // One wave per (KV head, 16-row block): up to 4 row blocks per head (64 rows: 16 tokens at 4 query heads per KV head;
-// the reference verifies at most 9). Two row blocks per wave would not fit the register budget without spills.
+// the reference verifies at most 9). Measured alternatives at 128k keys: two row blocks per wave in 8 waves (the 36 rows
+// of 9 tokens padded to 64) 52.0 against 45.1 us; one wave per head with all its row blocks 52.8 us.
 void attn_rec_plan(AttnParams& p, int cus) {
   const int rows = p.G * p.M;
   const int nblk = (rows + 15) / 16;
@@ -400,7 +420,7 @@ void attn_rec_plan(AttnParams& p, int cus) {
 
 int attn_rec_launch(AttnParams& p, int phases, hipStream_t s) {
   if (phases & 1) {
-    if (p.KVH != REC_KVH || p.pps > REC_BT_MAX || p.nrb < 1 || p.nrb > 4 || p.qb != 1) return DSPARK_EUNSUPPORTED;
+    if (p.KVH != REC_KVH || p.pps > REC_BT_MAX || p.nrb < 1 || p.nrb > 4 || p.qb * p.nrg < p.nrb) return DSPARK_EUNSUPPORTED;
     const dim3 grid(p.S);
     switch (p.qb * 10 + p.nrg) {
       case 11: hipLaunchKernelGGL((verify_attn_rec_kernel<1, 1>), grid, dim3(REC_KVH * 1 * 64), 0, s, p); break;

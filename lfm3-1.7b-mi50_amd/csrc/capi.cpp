@@ -14,7 +14,7 @@ using namespace dspark;
 
 namespace {
 
-constexpr int ABI_VERSION = 2;
+constexpr int ABI_VERSION = 3;
 
 // Compute units of the current device (queried once per device; 256 on MI355X).
 int device_cus() {
@@ -253,13 +253,23 @@ size_t dspark_verify_attention_rec_workspace(const dspark_attn_args* a) {
   return attn_workspace_bytes(p, 128);
 }
 
-int dspark_verify_attention_rec(const dspark_attn_args* a, dspark_stream_t stream) {
+static int verify_attention_rec_phases(const dspark_attn_args* a, int phases, dspark_stream_t stream) {
   if (!rec_args_ok(a)) return DSPARK_EINVAL;
   AttnParams p = rec_params(a);
   const size_t need = attn_workspace_bytes(p, 128);
   if (!a->workspace || a->workspace_bytes < need) return DSPARK_ENOSPACE;
   attn_bind_workspace(p, 128, a->workspace);
-  return attn_rec_launch(p, 3, S(stream));
+  return attn_rec_launch(p, phases, S(stream));
+}
+
+int dspark_verify_attention_rec(const dspark_attn_args* a, dspark_stream_t stream) {
+  return verify_attention_rec_phases(a, 3, stream);
+}
+int dspark_verify_attention_rec_splits(const dspark_attn_args* a, dspark_stream_t stream) {
+  return verify_attention_rec_phases(a, 1, stream);
+}
+int dspark_verify_attention_rec_combine(const dspark_attn_args* a, dspark_stream_t stream) {
+  return verify_attention_rec_phases(a, 2, stream);
 }
 
 int dspark_kv_write_rec(const float* k, const float* v, int64_t row_stride, void* pages, const int32_t* block_table,

@@ -57,6 +57,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// quantize_pair (kernels/ops.hip:212-224) of a record's 128 values, one IEEE fp32 operation per step: the scale from
+// the values' absolute maximum, and the int8 code of x with inv = 1 / scale.
+__device__ __forceinline__ float rec_scale(float amax) { return fmaxf(__fdiv_rn(amax, 127.f), 1e-6f); }
+__device__ __forceinline__ int rec_code(float x, float inv) {
+  float a = __fmul_rn(x, inv);
+  a = a >= 0.f ? __fadd_rn(a, 0.5f) : __fsub_rn(a, 0.5f);
+  return (int)truncf(fminf(fmaxf(a, -128.f), 127.f));
+}
+
 // Argmax key (reference dspark.hip:967-971): ordered float bits above, 0xFFFFFFFF - index below. The maximum key is the
 // largest value and, among equal values, the smallest index.
 __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {

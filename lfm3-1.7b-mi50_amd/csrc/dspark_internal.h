@@ -75,6 +75,7 @@ struct QkRopeParams {
   int gate_in_mix;
   _Float16* kp;                 // K/V page pools and block table
   _Float16* vp;
+  uint8_t* rec;                 // or (D = 128): the int8 record pool ([page][slot][KVH][264]), written instead
   const int32_t* bt;
   int pos_from_ctx, count_from_ctx;  // positions st->ctx_pos + t, tokens t < st->ctx_new (context projection)
 };

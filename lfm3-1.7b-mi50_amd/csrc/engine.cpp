@@ -45,6 +45,7 @@ struct LayerW {
   _Float16 *conv_w = nullptr, *conv_ring = nullptr;
   _Float16 *q_norm = nullptr, *k_norm = nullptr;
   _Float16 *kv_k = nullptr, *kv_v = nullptr;
+  uint8_t* kv_rec = nullptr;  // int8 record pages (kv_format 1) instead of kv_k / kv_v
   int64_t kv_pages = 0;
   const int32_t* bt = nullptr;  // drafter ring table (target layers: identity)
   int tap_slot = -1;
@@ -282,10 +283,11 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   p.st = e->ast;
   p.drafter = drafter;
   p.q = e->q16;
-  p.kp = Lw.kv_k;
+  p.kp = Lw.kv_rec ? reinterpret_cast<const _Float16*>(Lw.kv_rec) : Lw.kv_k;
   p.vp = Lw.kv_v;
   p.bt = Lw.bt;
-  p.k_bytes = p.v_bytes = (uint32_t)(Lw.kv_pages * d.kv_heads * PAGE * d.head_dim * 2);
+  p.k_bytes = p.v_bytes = (uint32_t)(Lw.kv_rec ? Lw.kv_pages * PAGE * d.kv_heads * DSPARK_REC_BYTES
+                                               : Lw.kv_pages * d.kv_heads * PAGE * d.head_dim * 2);
   p.out16 = e->y16;
   p.out_op = e->tbs;
   p.gate = gate;
@@ -303,11 +305,14 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
     p.start = std::max(0, plan_a - d.window + 1);
   }
   p.S = 0;
-  attn_plan(p, d.head_dim, e->cus);
+  if (Lw.kv_rec)
+    attn_rec_plan(p, e->cus);
+  else
+    attn_plan(p, d.head_dim, e->cus);
   if (drafter) p.window = d.draft_window;  // attn_range (device) derives start and drops the per-token window
   if (attn_workspace_bytes(p, d.head_dim) > e->ws_attn_bytes) return DSPARK_ENOSPACE;
   attn_bind_workspace(p, d.head_dim, e->ws_attn);
-  return attn_launch(p, d.head_dim, 3, s);
+  return Lw.kv_rec ? attn_rec_launch(p, 3, s) : attn_launch(p, d.head_dim, 3, s);
 }
 
 QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode) {
@@ -331,6 +336,7 @@ QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int
   p.gate_in_mix = p.gate ? 1 : 0;
   p.kp = Lw.kv_k;
   p.vp = Lw.kv_v;
+  p.rec = Lw.kv_rec;
   p.bt = Lw.bt;
   p.pos_from_ctx = ctx_mode;
   p.count_from_ctx = ctx_mode;
@@ -512,7 +518,7 @@ int64_t kv_pages_for(const dspark_model_desc& d, int max_context) {
   return (positions + PAGE - 1) / PAGE + 1;
 }
 int64_t kv_pool_bytes(const dspark_model_desc& d, int max_context) {
-  return kv_pages_for(d, max_context) * d.kv_heads * PAGE * d.head_dim * 2;
+  return kv_pages_for(d, max_context) * d.kv_heads * PAGE * (d.kv_format ? DSPARK_REC_BYTES : d.head_dim * 2);
 }
 
 bool desc_ok(const dspark_model_desc* d, int max_context) {
@@ -527,6 +533,10 @@ bool desc_ok(const dspark_model_desc* d, int max_context) {
   if (!(d->rope_base > 0.f)) return false;
   if (d->rope_base_swa > 0.f && (d->rope_pairs_swa < 0 || d->rope_pairs_swa > d->head_dim / 2)) return false;
   if (d->conv_slots < 0 || d->conv_slots > 65536) return false;
+  // int8 records: the record attention kernel's geometry (D 128, 4 KV heads, up to 64 rows per KV head)
+  if (d->kv_format < 0 || d->kv_format > 1) return false;
+  if (d->kv_format == 1 && (d->head_dim != 128 || d->kv_heads != 4 || d->q_heads / d->kv_heads * d->block > 64))
+    return false;
   if (d->draft_layers < 1 || d->block < 2 || d->block > 64 || d->max_drafts < 0 || d->max_drafts > d->block - 1) return false;
   if (d->crop_rows < 16 || d->crop_rows % 16 || d->markov_rank < 16 || d->markov_rank % 16) return false;
   if (d->crop_rows > d->vocab) return false;
@@ -621,8 +631,13 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
       W.q_norm = h16(pre + "q_norm", D);
       W.k_norm = h16(pre + "k_norm", D);
       W.kv_pages = e->kv_pages;
-      W.kv_k = h16("kv.L" + std::to_string(i) + ".k", (size_t)e->kv_pages * KVH * PAGE * D);
-      W.kv_v = h16("kv.L" + std::to_string(i) + ".v", (size_t)e->kv_pages * KVH * PAGE * D);
+      if (d.kv_format) {
+        W.kv_rec = static_cast<uint8_t*>(
+            e->alloc("kv.L" + std::to_string(i) + ".rec", (size_t)e->kv_pages * PAGE * KVH * DSPARK_REC_BYTES, &err));
+      } else {
+        W.kv_k = h16("kv.L" + std::to_string(i) + ".k", (size_t)e->kv_pages * KVH * PAGE * D);
+        W.kv_v = h16("kv.L" + std::to_string(i) + ".v", (size_t)e->kv_pages * KVH * PAGE * D);
+      }
     }
   }
   const int64_t bt_entries = (positions + PAGE - 1) / PAGE + 1;
@@ -647,8 +662,13 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     W.q_norm = h16(pre + "q_norm", D);
     W.k_norm = h16(pre + "k_norm", D);
     W.kv_pages = e->ring_pages;
-    W.kv_k = h16("ring.D" + std::to_string(j) + ".k", (size_t)e->ring_pages * KVH * PAGE * D);
-    W.kv_v = h16("ring.D" + std::to_string(j) + ".v", (size_t)e->ring_pages * KVH * PAGE * D);
+    if (d.kv_format) {
+      W.kv_rec = static_cast<uint8_t*>(
+          e->alloc("ring.D" + std::to_string(j) + ".rec", (size_t)e->ring_pages * PAGE * KVH * DSPARK_REC_BYTES, &err));
+    } else {
+      W.kv_k = h16("ring.D" + std::to_string(j) + ".k", (size_t)e->ring_pages * KVH * PAGE * D);
+      W.kv_v = h16("ring.D" + std::to_string(j) + ".v", (size_t)e->ring_pages * KVH * PAGE * D);
+    }
     W.bt = e->ring_bt;
   }
   e->draft_norm = h16("draft_norm", H);
@@ -727,7 +747,8 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
   const int G = QH / KVH;
   const size_t rows_pad = (size_t)(G * B + 16 * 8);
-  e->ws_attn_bytes = (size_t)KVH * 64 * rows_pad * (D * 4 + 8) + (size_t)KVH * 64 * 4 + 4096;
+  e->ws_attn_bytes = (size_t)KVH * (d.kv_format ? ATTN_REC_MAX_SPLITS : 64) * rows_pad * (D * 4 + 8) +
+                     (size_t)KVH * 64 * 4 + 4096;
   e->ws_attn = e->alloc("ws_attn", e->ws_attn_bytes, &err);
   e->ws_argmax_bytes = verify_argmax_ws(B, d.vocab);
   e->ws_argmax = e->alloc("ws_argmax", e->ws_argmax_bytes, &err);

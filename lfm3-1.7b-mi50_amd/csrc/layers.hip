@@ -215,6 +215,37 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
       r[e + ne / 2] = x1 * c + x0 * s;
     }
   }
+  const int kvh = hh - p.QH;
+  const float* vsrc = row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)p.KVH * D + (size_t)kvh * D;
+  if (!isq && p.rec) {
+    // int8 record of (pos, kvh) (D = 128: lanes 0..31 hold dims l, l + 32, l + 64, l + 96; lanes 32..63 repeat
+    // them): quantize_pair of K (normed, rotated, fp32) and of V (fp32), kernels/ops.hip:212-251
+    float vv[MAXE];
+    for (int e = 0; e < ne; ++e) vv[e] = vsrc[(lane & 31) + 32 * e];
+    float ak = 0.f, av = 0.f;
+    for (int e = 0; e < ne; ++e) {
+      ak = fmaxf(ak, fabsf(r[e]));
+      av = fmaxf(av, fabsf(vv[e]));
+    }
+    ak = wave_max(ak);
+    av = wave_max(av);
+    if (lane >= 32) return;
+    const int lp = pos / PAGE, slot = pos % PAGE;
+    const int phys = p.bt ? p.bt[lp] : lp;
+    uint8_t* rb = p.rec + (size_t)phys * ((size_t)PAGE * p.KVH * 264) + ((size_t)slot * p.KVH + kvh) * 264;
+    const float ks = rec_scale(ak), vs = rec_scale(av);
+    const float ki = __fdiv_rn(1.f, ks), vi = __fdiv_rn(1.f, vs);
+    for (int e = 0; e < ne; ++e) {
+      const int d = (lane & 31) + 32 * e;
+      rb[d] = (uint8_t)rec_code(r[e], ki);
+      rb[D + 4 + d] = (uint8_t)rec_code(vv[e], vi);
+    }
+    if (lane == 0) {
+      *reinterpret_cast<float*>(rb + D) = ks;
+      *reinterpret_cast<float*>(rb + 2 * D + 4) = vs;
+    }
+    return;
+  }
   if (lane >= 32) return;
   if (isq) {
     _Float16* q = p.q16 + ((size_t)t * p.QH + hh) * D;
@@ -225,8 +256,6 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
     return;
   }
   // K (normed, rotated) and V (as is) into the pages at `pos`
-  const int kvh = hh - p.QH;
-  const float* vsrc = row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)p.KVH * D + (size_t)kvh * D;
   const int lp = pos / PAGE, slot = pos % PAGE;
   const int phys = p.bt ? p.bt[lp] : lp;
   _Float16* kb = p.kp + ((size_t)phys * p.KVH + kvh) * (PAGE * D);

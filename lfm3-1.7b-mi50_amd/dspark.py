@@ -60,6 +60,8 @@ _SIGS = {
                                            ctypes.c_int32, ctypes.c_void_p]),
     "dspark_verify_attention_rec_workspace": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "dspark_verify_attention_rec": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "dspark_verify_attention_rec_splits": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "dspark_verify_attention_rec_combine": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "dspark_rope_table": (ctypes.c_int, [ctypes.c_float, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                          ctypes.c_void_p]),
     "dspark_verify_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
@@ -377,7 +379,8 @@ class ModelDesc(ctypes.Structure):
                 ("markov_rank", ctypes.c_int32), ("n_taps", ctypes.c_int32), ("tap_layer", ctypes.c_int32 * MAX_TAPS),
                 ("draft_window", ctypes.c_int32), ("ring_positions", ctypes.c_int32), ("mask_token", ctypes.c_int32),
                 ("conf_bias", ctypes.c_float), ("conf_thr", ctypes.c_float), ("eps", ctypes.c_float),
-                ("rope_base_swa", ctypes.c_float), ("rope_pairs_swa", ctypes.c_int32), ("conv_slots", ctypes.c_int32)]
+                ("rope_base_swa", ctypes.c_float), ("rope_pairs_swa", ctypes.c_int32), ("conv_slots", ctypes.c_int32),
+                ("kv_format", ctypes.c_int32)]
 
 
 class LaunchArgs(ctypes.Structure):
@@ -458,23 +461,23 @@ def c4_desc(block=16, vocab=65536):
                       conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
 
 
-def ref_desc(block=9, max_drafts=7, vocab=128000):
+def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1):
     """The reference model's geometry (internal/model/engine.go:23-40; internal/model/dspark.go:22-41;
     cmd/pack/main.go:193, 329): 24 target layers in the reference order (13 gated short-conv k=7, 6 full and 5
     sliding-window-256 GQA attention layers, 16/4/128), hidden 2048, gated FFN 7680, vocab 128000; 3 attention-only
     drafter layers (FFN 7680) over 9-token blocks, 16384-row cropped head, Markov rank 256, taps {2, 6, 12, 18, 23},
     drafter window 2048, ring 4096. max_drafts follows the reference policy (7, or 3 from position 57344,
     generate.go:136). RoPE per layer kind as the reference builds it (engine.go:333-338): full attention and the
-    drafter at base 1e6 with 32 rotating pairs, sliding layers at base 1e4 with 64. Storage formats stay this build's:
-    fp16 KV pages (the reference keeps int8 K/V records, half the KV bytes) and int8 weights with per-row fp16
-    scales."""
+    drafter at base 1e6 with 32 rotating pairs, sliding layers at base 1e4 with 64. K/V in the reference's int8
+    records (264 bytes per position and KV head, quantize_pair; engine.go:30-32, ops.hip:212-251) unless
+    kv_format=0 (fp16 pages); int8 weights with per-row fp16 scales."""
     kinds = [0, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0]
     return model_desc(hidden=2048, ffn=7680, vocab=vocab, n_layers=24, layer_kind=kinds, q_heads=16, kv_heads=4,
                       head_dim=128, conv_kernel=7, window=256, rope_base=1e6, rope_pairs=32, rope_base_swa=1e4,
                       rope_pairs_swa=64, draft_layers=3,
                       draft_ffn=7680, block=block, max_drafts=max_drafts, crop_rows=16384, markov_rank=256, n_taps=5,
                       tap_layer=[2, 6, 12, 18, 23], draft_window=2048, ring_positions=4096, mask_token=vocab - 1,
-                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
+                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5, kv_format=kv_format)
 
 
 class Engine:

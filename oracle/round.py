@@ -94,6 +94,33 @@ def attn_fp16(q16, K, V, a, M, start, window, causal):
     return orc.verify_attention(to16(q16), to16(K[:T]), to16(V[:T]), a, start, window, causal)
 
 
+def attn_rec(q16, K, V, a, M, start, window, causal):
+    """The int8-record attention (dspark.hip:1020-1035, 1215-1412): q (fp16-valued) quantized per 32-dim group, K/V
+    [T][KVH][D] already the dequantized record values (kv_store), fp64 softmax of those operands."""
+    QH, D = q16.shape[1], q16.shape[2]
+    q8, qs = orc.rec_quantize_q(np.asarray(q16, np.float64).astype(np.float16).view(np.uint16).reshape(-1, D))
+    qd = (q8.astype(np.float64).reshape(-1, D // 32, 32) * qs.astype(np.float64)[:, :, None]).reshape(M, QH, D)
+    T = a + M
+    return orc.verify_attention_d(qd, K[:T], V[:T], a, start, window, causal)
+
+
+def kv_store(d, K, V, pos, h, k, v):
+    """K/V of (pos, KV head h) into the logical cache: fp16 values, or (kv_format 1) the dequantized quantize_pair
+    record of the fp32 values (kernels/ops.hip:212-224)."""
+    if getattr(d, "kv_format", 0):
+        kq, ks = orc.rec_quantize(np.asarray(k, np.float64).astype(np.float32))
+        vq, vs = orc.rec_quantize(np.asarray(v, np.float64).astype(np.float32))
+        K[pos, h] = kq.astype(np.float64) * float(ks)
+        V[pos, h] = vq.astype(np.float64) * float(vs)
+    else:
+        K[pos, h] = f16(k)
+        V[pos, h] = f16(v)
+
+
+def attention(d, q16, K, V, a, M, start, window, causal):
+    return (attn_rec if getattr(d, "kv_format", 0) else attn_fp16)(q16, K, V, a, M, start, window, causal)
+
+
 def context_projection(W, C, st, rope):
     """The round's context projection (sec 0): the taps of the last round's committed positions ctx_pos ..
     ctx_pos + ctx_new - 1 (C.taps, the residual stream after each tapped layer) into the drafter rings."""
@@ -142,8 +169,8 @@ def project_rows(W, C, x, pos0, rope):
             row = kv[t, j * 2 * KVH * D:(j + 1) * 2 * KVH * D]
             for h in range(KVH):
                 k = norm_head(row[h * D:(h + 1) * D], kn, d.eps)
-                K[pos, h] = f16(rope_rows(k, pos, rope, d.rope_pairs))
-                V[pos, h] = f16(row[KVH * D + h * D:KVH * D + (h + 1) * D])
+                kv_store(d, K, V, pos, h, rope_rows(k, pos, rope, d.rope_pairs),
+                         row[KVH * D + h * D:KVH * D + (h + 1) * D])
 
 
 def drafter_block(W, C, st, rope):
@@ -170,11 +197,11 @@ def drafter_block(W, C, st, rope):
                 q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, rope, d.rope_pairs))
             for hh in range(KVH):
                 o = QH * D + hh * D
-                K[pos, hh] = f16(rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs))
-                o = QH * D + KVH * D + hh * D
-                V[pos, hh] = f16(mix[t, o:o + D])
+                ov = QH * D + KVH * D + hh * D
+                kv_store(d, K, V, pos, hh, rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs),
+                         mix[t, ov:ov + D])
         start = max(st["ctx_lo"], a - d.draft_window)
-        o = attn_fp16(q16, K, V, a, B, start, 0, False)
+        o = attention(d, q16, K, V, a, B, start, 0, False)
         y = f16(o.reshape(B, QH * D))
         ow, os_ = W.gemm_w(pre + "out", H, H)
         vout = gemm(y, ow, os_)
@@ -271,12 +298,12 @@ def verify(W, C, st, tokens, rope, rope_swa=None):
                     q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, table, rot))
                 for hh in range(KVH):
                     o = QH * D + hh * D
-                    K[pos, hh] = f16(rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, table, rot))
-                    o = QH * D + KVH * D + hh * D
-                    V[pos, hh] = f16(mix[t, o:o + D])
+                    ov = QH * D + KVH * D + hh * D
+                    kv_store(d, K, V, pos, hh, rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, table, rot),
+                             mix[t, ov:ov + D])
             window = d.window if kind == 2 else 0
             start = max(0, a - window + 1) if window else 0
-            o = attn_fp16(q16, K, V, a, B, start, window, True)
+            o = attention(d, q16, K, V, a, B, start, window, True)
             gate = mix[:, (QH + 2 * KVH) * D:(QH + 2 * KVH) * D + QH].astype(np.float32).astype(np.float64)
             y = f16((o * (1.0 / (1.0 + np.exp(-gate)))[:, :, None]).reshape(B, QH * D))
         ow, os_ = W.gemm_w(pre + "out", H, H)
