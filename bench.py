@@ -586,11 +586,13 @@ def bench_engine(args, host, torch, workload):
     for k in list(cache):
         cache.pop(k)[1].close()
     model = ("reference geometry: 24 layers (13 conv k=7 / 6 full / 5 sliding-256 attention, 16/4/128), FFN 7680, "
-             "vocab 128000, 3-layer drafter; the reference's int8 K/V records" if ref else "C4 geometry")
+             "vocab 128000, 3-layer drafter; the reference's int8 K/V records and per-128-column weight scales" if ref
+             else "C4 geometry")
     kv = ("int8 K/V records (codes uniform in [-127, 127], scales 1/40)" if ref else "N(0,1) fp16 KV caches")
+    scales = "per-128-column fp16 scales" if ref else "per-row fp16 scales"
     return {"metric": f"greedy decode tok/s (DSpark rounds, random-init model, {model})", "workload": workload,
             "rounds": rounds, "warmup": warm, "cases": out,
-            "data": f"random-init weights (int8 uniform, per-row fp16 scales), {kv}; planted drafts "
+            "data": f"random-init weights (int8 uniform, {scales}), {kv}; planted drafts "
                     "replay the target's own greedy chain (one-token verify rounds) with per-position probability p"}
 
 

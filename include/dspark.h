@@ -180,6 +180,18 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
                    int32_t epilogue, float* y_f32, void* y_f16, void* workspace, size_t workspace_bytes,
                    dspark_stream_t stream);
 size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K); /* counters + split-K partials (0: no split) */
+/* dspark_gemm_i8 with the reference's per-128-column weight scales (weights.Pack, internal/weights/quant.go:66-104):
+ * y[t][r] = sum_g gscale[g][r] * sum_{k in group g} x[t][k] * q[r][k], groups of 128 columns, gscale fp16 [K/128][N]
+ * (group-major: dspark_g128_scales converts the packer's [row][quarter][i] layout), weights biased int8 [N][K] as
+ * above, fp16 x. M <= 16 (the reference verifies 9 tokens), K % 128 == 0; same epilogues; no workspace. Each 64-column
+ * chunk's products are scaled in fp32 by its group's scale and added in chunk order. The reference's default build
+ * also quantizes x to int8 per 16 columns (LFM3_X8, dspark.hip:25-27, 802-823); x stays fp16 here, as in the
+ * reference's LFM3_F16 build. Replaces gemv_phase / unit_dot_r over packed weights (dspark.hip:541-716). */
+int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* gscale, int32_t N,
+                        int32_t epilogue, float* y_f32, void* y_f16, dspark_stream_t stream);
+/* Host helper: the packer's scale rows ([N][SRow] fp16, SRow = 16 for K = 2048 and 64 otherwise, entry (quarter, i) =
+ * group 4 i + quarter at quarter * SRow / 4 + i; quant.go:13-29, 66-104) -> gscale [K/128][N]. No device memory. */
+int dspark_g128_scales(const uint16_t* packed, int32_t N, int32_t K, uint16_t* out);
 
 /* ---------------------------------------------------------------- cropped head + row argmax
  * y[t][r] = sum_k x[t][k] * W[r][k] (fp16 W [N][K], fp16 x [M][K], fp32 accumulation), and best_keys[t] = max key(y, r)
@@ -236,6 +248,10 @@ typedef struct dspark_model_desc {
    * head_dim 128, kv_heads 4 and q_heads / kv_heads x block <= 64. Tensors "kv.L<i>.rec" / "ring.D<j>.rec" then hold
    * the record pages instead of "kv.L<i>.k|v" / "ring.D<j>.k|v". */
   int32_t kv_format;
+  /* Scales of the int8 weights ("<name>.s"): 0 one fp16 scale per output row ([N]); 1 the reference's per-128-column
+   * group scales (weights.Pack, internal/weights/quant.go:66-104) as fp16 [K/128][N] (dspark_g128_scales converts the
+   * packer's layout), which needs block <= 16. */
+  int32_t weight_format;
 } dspark_model_desc;
 
 typedef struct dspark_engine dspark_engine;

@@ -339,6 +339,41 @@ int dspark_gemm_i8(const void* x, int32_t M, int32_t K, const uint8_t* w, const 
   return gemm_launch(p, true, S(stream));
 }
 
+int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* gscale, int32_t N,
+                        int32_t epilogue, float* y_f32, void* y_f16, dspark_stream_t stream) {
+  if (!x || !w || !gscale || M < 1 || M > 16 || N < 16 || N % 16 || K < 128 || K % 128) return DSPARK_EINVAL;
+  if (epilogue < 0 || epilogue > 2) return DSPARK_EINVAL;
+  if (epilogue == 0 && !y_f32 && !y_f16) return DSPARK_EINVAL;
+  if (epilogue != 0 && !y_f16) return DSPARK_EINVAL;
+  GemmParams p = {};
+  p.x = static_cast<const _Float16*>(x);
+  p.w = w;
+  p.gscale = static_cast<const _Float16*>(gscale);
+  p.y32 = epilogue == 0 ? y_f32 : nullptr;
+  p.y16 = static_cast<_Float16*>(y_f16);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.epilogue = epilogue;
+  GemmPlan pl;
+  gemm_plan(M, N, K, true, false, &pl, 0, false, 1, true);
+  p.ksplit = pl.ksplit;
+  p.wpg = pl.wpg;
+  p.cpb = pl.cpb;
+  p.kw = pl.kw;
+  p.xd = pl.xd;
+  return gemm_launch(p, true, S(stream));
+}
+
+int dspark_g128_scales(const uint16_t* packed, int32_t N, int32_t K, uint16_t* out) {
+  if (!packed || !out || N < 1 || K < 128 || K % 128) return DSPARK_EINVAL;
+  const int groups = K / 128, srow = (K / 512 == 4) ? 16 : 64, sq = srow / 4;
+  if ((groups + 3) / 4 > sq) return DSPARK_EINVAL;  // more groups than the packed row holds
+  for (int r = 0; r < N; ++r)
+    for (int g = 0; g < groups; ++g) out[(size_t)g * N + r] = packed[(size_t)r * srow + (g % 4) * sq + g / 4];
+  return 0;
+}
+
 size_t dspark_head_argmax_workspace(int32_t M, int32_t N) {
   if (M < 1 || M > 64 || N < 16 || N % 16) return 0;
   return (size_t)M * (N / 16) * sizeof(uint64_t);

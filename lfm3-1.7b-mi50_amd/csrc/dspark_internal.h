@@ -179,6 +179,8 @@ struct GemmParams {
   const _Float16* x;        // [M][K]
   const void* w;            // [N][K] biased int8 or fp16
   const _Float16* scale;    // [N] or nullptr
+  const _Float16* gscale;   // or [K / 128][N]: one fp16 scale per (128-column group, row), the reference's per-128
+                            // format (internal/weights/quant.go:66-104); K-sliced plans with one token block only
   float* y32;               // [M][N]
   _Float16* y16;            // [M][N] ([M][N/2] for the gated epilogue)
   float* part;              // split-K partials [ksplit][M][N]
@@ -212,7 +214,7 @@ struct GemmPlan {
 // xop: X comes in operand order (GemmParams::xop); max_bands > 1: the caller adds up to that many output bands
 // (GemmParams::bands).
 void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req = 0, bool xop = false,
-               int max_bands = 1);
+               int max_bands = 1, bool gs = false);
 // Split-K workspace: GEMM_COUNTER_BYTES of arrival counters (one u32 per row group, at the same offset for every shape),
 // then the partials. Zero-filled once; every call leaves its counters at zero.
 constexpr int GEMM_COUNTER_SLOTS = 8192;

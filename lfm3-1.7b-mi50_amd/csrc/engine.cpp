@@ -215,7 +215,9 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.st = e->ast;
   p.x = x;
   p.w = w;
-  p.scale = s;
+  const bool gs = e->d.weight_format == 1;  // per-128-column group scales [K/128][N]
+  p.scale = gs ? nullptr : s;
+  p.gscale = gs ? s : nullptr;
   p.y32 = epilogue == 0 ? y32 : nullptr;
   p.y16 = y16;
   p.M = M;
@@ -234,7 +236,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
     wpg_req = 3;
   }
   GemmPlan pl;
-  gemm_plan(M, N, K, true, true, &pl, wpg_req, xop, bands ? *bands : 1);
+  gemm_plan(M, N, K, true, true, &pl, wpg_req, xop, bands ? *bands : 1, gs);
   if (bands) *bands = pl.bands;
   p.bands = pl.bands;
   p.ksplit = pl.ksplit;
@@ -535,6 +537,9 @@ bool desc_ok(const dspark_model_desc* d, int max_context) {
   if (d->conv_slots < 0 || d->conv_slots > 65536) return false;
   // int8 records: the record attention kernel's geometry (D 128, 4 KV heads, up to 64 rows per KV head)
   if (d->kv_format < 0 || d->kv_format > 1) return false;
+  // group scales: the K-sliced kernel with one token block, whole 128-column groups
+  if (d->weight_format < 0 || d->weight_format > 1) return false;
+  if (d->weight_format == 1 && (d->block > 16 || d->hidden % 128 || d->ffn % 128 || d->draft_ffn % 128)) return false;
   if (d->kv_format == 1 && (d->head_dim != 128 || d->kv_heads != 4 || d->q_heads / d->kv_heads * d->block > 64))
     return false;
   if (d->draft_layers < 1 || d->block < 2 || d->block > 64 || d->max_drafts < 0 || d->max_drafts > d->block - 1) return false;
@@ -576,6 +581,8 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   }
   int err = 0;
   auto h16 = [&](const std::string& n, size_t count) { return static_cast<_Float16*>(e->alloc(n, count * 2, &err)); };
+  // scales of an int8 [N][K] weight: [N] per row, or [K/128][N] per 128-column group (weight_format 1)
+  auto sc = [&](const std::string& n, int N, int K) { return h16(n, d.weight_format ? (size_t)(K / 128) * N : (size_t)N); };
   // an int8 GEMM weight [N][K] and its tile-major copy
   auto u8 = [&](const std::string& n, int N, int K) {
     uint8_t* w = static_cast<uint8_t*>(e->alloc(n, (size_t)N * K, &err));
@@ -593,7 +600,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->embed = h16("embed", (size_t)d.vocab * H);
   e->final_norm = h16("final_norm", H);
   e->head_w = u8("head.w", d.vocab, H);
-  e->head_s = h16("head.s", d.vocab);
+  e->head_s = sc("head.s", d.vocab, H);
   int tap_slot[DSPARK_MAX_LAYERS];
   for (int i = 0; i < DSPARK_MAX_LAYERS; ++i) tap_slot[i] = -1;
   for (int i = 0; i < d.n_taps; ++i) tap_slot[d.tap_layer[i]] = i;
@@ -609,14 +616,14 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     W.post_ffn_norm = h16(pre + "post_ffn_norm", H);
     W.mix_rows = W.kind == 0 ? 3 * H : align16(QH * D + 2 * KVH * D + QH);
     W.mix_w = u8(pre + "mix.w", W.mix_rows, H);
-    W.mix_s = h16(pre + "mix.s", W.mix_rows);
+    W.mix_s = sc(pre + "mix.s", W.mix_rows, H);
     W.out_w = u8(pre + "out.w", H, H);
-    W.out_s = h16(pre + "out.s", H);
+    W.out_s = sc(pre + "out.s", H, H);
     W.ffn = d.ffn;
     W.w13_w = u8(pre + "w13.w", 2 * d.ffn, H);
-    W.w13_s = h16(pre + "w13.s", 2 * d.ffn);
+    W.w13_s = sc(pre + "w13.s", 2 * d.ffn, H);
     W.w2_w = u8(pre + "w2.w", H, d.ffn);
-    W.w2_s = h16(pre + "w2.s", H);
+    W.w2_s = sc(pre + "w2.s", H, d.ffn);
     if (W.kind == 0) {
       W.conv_w = h16(pre + "conv.w", (size_t)H * d.conv_kernel);
       W.conv_ring = h16("conv.L" + std::to_string(i), (size_t)CONV_RING * H);
@@ -651,14 +658,14 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     W.ffn_norm = h16(pre + "ffn_norm", H);
     W.mix_rows = align16(QH * D + 2 * KVH * D);
     W.mix_w = u8(pre + "mix.w", W.mix_rows, H);
-    W.mix_s = h16(pre + "mix.s", W.mix_rows);
+    W.mix_s = sc(pre + "mix.s", W.mix_rows, H);
     W.out_w = u8(pre + "out.w", H, H);
-    W.out_s = h16(pre + "out.s", H);
+    W.out_s = sc(pre + "out.s", H, H);
     W.ffn = d.draft_ffn;
     W.w13_w = u8(pre + "w13.w", 2 * d.draft_ffn, H);
-    W.w13_s = h16(pre + "w13.s", 2 * d.draft_ffn);
+    W.w13_s = sc(pre + "w13.s", 2 * d.draft_ffn, H);
     W.w2_w = u8(pre + "w2.w", H, d.draft_ffn);
-    W.w2_s = h16(pre + "w2.s", H);
+    W.w2_s = sc(pre + "w2.s", H, d.draft_ffn);
     W.q_norm = h16(pre + "q_norm", D);
     W.k_norm = h16(pre + "k_norm", D);
     W.kv_pages = e->ring_pages;
@@ -674,7 +681,7 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->draft_norm = h16("draft_norm", H);
   e->crop_n = align16(d.crop_rows + 1);
   e->crop_w = u8("crop.w", e->crop_n, H);
-  e->crop_s = h16("crop.s", e->crop_n);
+  e->crop_s = sc("crop.s", e->crop_n, H);
   e->crop_ids = static_cast<int32_t*>(e->alloc("crop_ids", (size_t)d.crop_rows * 4, &err));
   e->w2q = static_cast<int8_t*>(e->alloc("markov.w2q", (size_t)d.crop_rows * d.markov_rank, &err));
   e->w2s = static_cast<float*>(e->alloc("markov.w2s", (size_t)d.crop_rows * 4, &err));
@@ -688,11 +695,11 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   }
   e->tap_norms = h16("tap_norms", (size_t)d.n_taps * H);
   e->fc_w = u8("fc.w", H, d.n_taps * H);
-  e->fc_s = h16("fc.s", H);
+  e->fc_s = sc("fc.s", H, d.n_taps * H);
   e->hidden_norm = h16("hidden_norm", H);
   const int ckv_rows = d.draft_layers * 2 * KVH * D;
   e->ckv_w = u8("ckv.w", ckv_rows, H);
-  e->ckv_s = h16("ckv.s", ckv_rows);
+  e->ckv_s = sc("ckv.s", ckv_rows, H);
   e->rope = h16("rope", (size_t)(positions + 1) * D);
   const bool own_swa = d.rope_base_swa > 0.f;
   e->rope_swa = own_swa ? h16("rope_swa", (size_t)(positions + 1) * D) : e->rope;

@@ -414,8 +414,12 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 // weights held in registers (up to 4 token blocks); XD = true (TB = 1) has every wave load its own range of X straight
 // into B operands. Ranges longer than CPW chunks go in batches of CPW. Chunk order inside a range, then range order,
 // fixes the summation order, so results do not depend on timing.
-template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024>
+// GS (one token block, X per wave): weights with per-128-column group scales (p.gscale [K/128][N]): each 64-column
+// chunk's products go to a fresh accumulator that is scaled by its group's scales of the lane's 4 rows and added in chunk
+// order (the reference applies the scale per group as well, dspark.hip:553-580).
+template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
+  static_assert(!GS || (XD && TB == 1 && I8), "group scales: one token block, X per wave, int8 weights");
   // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
   // anything is stored), so its latency overlaps theirs; a stopped round writes nothing.
   const int run = run_flag_load(p.st);
@@ -481,11 +485,13 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     // compiler's wait for the previous iteration's loads would also hold the first batch back behind the flag load.
     auto batch = [&](int cb) {
       u32x4 xb[CPW][2];
+      u32x2 gsr[GS ? CPW : 1];  // group scales of chunk cb + i for rows row0 + 4 g .. + 3 (4 halves)
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = min(cb + i, c1 - 1);
         xb[i][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs));
         xb[i][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + xhs));
+        if constexpr (GS) gsr[i] = ldg(reinterpret_cast<const u32x2*>(p.gscale + (size_t)(c >> 1) * p.N + row0 + 4 * g));
       }
       load(w, cb);
 #pragma unroll
@@ -493,8 +499,16 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
         if (cb + i < c1) {
           half8 a[2];
           weights(w[i], a);
-          acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
-          acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
+          if constexpr (GS) {
+            f32x4 t = mfma16x16x32(a[0], as_half8(xb[i][0]), f32x4{0, 0, 0, 0});
+            t = mfma16x16x32(a[1], as_half8(xb[i][1]), t);
+            const half4 sc = __builtin_bit_cast(half4, gsr[i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[0][j] = fmaf(t[j], (float)sc[j], acc[0][j]);
+          } else {
+            acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
+            acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
+          }
         }
       }
     };
@@ -724,6 +738,10 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const size_t lds = gemm_sliced_lds_bytes(p, I8);
   const int cpk = ((p.K / 64 + p.bands - 1) / p.bands + p.kw - 1) / p.kw;  // chunks per range (of the band's)
   if constexpr (I8) {
+    if (TB == 1 && gemm_sliced_xd(p, I8) && p.gscale) {  // gemm_launch checked block.x <= 512
+      hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true>), grid, block, lds, s, p);
+      return;
+    }
     if (TB == 1 && gemm_sliced_xd(p, I8)) {
       if (block.x <= 512)  // up to 8 waves: twice the registers per wave (no spills with the first batch peeled)
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512>), grid, block, lds, s, p);
@@ -791,14 +809,15 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // of at most 128 KB when all of them do not fit (ranges of at most 8 chunks): 33 tokens, C5 round 2.19 -> 1.95 ms
 // against the split-K kernel (2.02 with 64 KB passes of one token block). Returns false when no sliced plan fits (the
 // split-K plan is used).
-static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, int max_bands, GemmPlan* pl) {
+static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, int max_bands, GemmPlan* pl,
+                             bool gs = false) {
   const int strips = N / 16, chunks = K / 64;
-  if (!DSPARK_GEMM_SLICED || tb > 4) return false;
+  if ((!DSPARK_GEMM_SLICED && !gs) || tb > 4) return false;
   int S, KW, bands = 1;
   if (wpg_req > 0) {
     S = wpg_req;
-    KW = 16 / S;
-  } else if (i8 && strips <= 512 && (xop || K <= 4096)) {
+    KW = (gs ? 8 : 16) / S;  // group scales: at most 8 waves (the 1024-thread variant would spill)
+  } else if (i8 && ((strips <= 512 && (xop || K <= 4096)) || gs)) {  // group scales: always one strip per workgroup
     S = 1;
     // fewer than 256 strips: K in bands over more workgroups when the caller adds the bands (at least 8 chunks each)
     while (bands * 2 <= max_bands && strips * bands * 2 <= 256 && chunks / (bands * 2) >= 8) bands *= 2;
@@ -824,9 +843,9 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
   return true;
 }
 
-void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req, bool xop, int max_bands) {
+void gemm_plan(int M, int N, int K, bool i8, bool split, GemmPlan* pl, int wpg_req, bool xop, int max_bands, bool gs) {
   const int strips = N / 16, chunks = K / 64, tb = (M + 15) / 16;
-  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, xop, max_bands, pl)) return;
+  if (gemm_plan_sliced(N, K, tb, i8, wpg_req, xop, max_bands, pl, gs)) return;
   pl->kw = 0;
   pl->bands = 1;
   const int wpg = wpg_req > 0 ? wpg_req : (strips >= 8 * 512 ? 8 : std::min(4, std::max(1, strips)));
@@ -866,6 +885,9 @@ float* gemm_ws_partials(void* ws) { return reinterpret_cast<float*>(static_cast<
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
   if ((p.xop && p.xop < (p.M + 15) / 16) || (p.yop && p.yop < (p.M + 15) / 16)) return DSPARK_EINVAL;
+  // group scales: the K-sliced kernel with X per wave (one token block), whole 128-column groups, no row scales
+  if (p.gscale && (!i8 || p.kw <= 0 || !gemm_sliced_xd(p, i8) || p.K % 128 || p.scale || p.wpg * p.kw > 8))
+    return DSPARK_EINVAL;
   if (p.kw > 0) {
     // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
     const int tb = (p.M + 15) / 16;

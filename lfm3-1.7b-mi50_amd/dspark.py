@@ -74,6 +74,10 @@ _SIGS = {
     "dspark_gemm_i8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                       ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "dspark_gemm_i8_g128": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p]),
+    "dspark_g128_scales": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_head_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
     "dspark_head_argmax_f16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                               ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -350,6 +354,29 @@ def gemm_i8(x, w_biased, scale, epilogue=0, y_f32=None, y_f16=None, workspace=No
     return y_f32 if epilogue == 0 and y_f32 is not None else y_f16
 
 
+def gemm_i8_g128(x, w_biased, gscale, epilogue=0, y_f32=None, y_f16=None, stream=None):
+    """x fp16 [M][K] (M <= 16); w uint8 [N][K] biased; gscale fp16 [K/128][N] (per-128-column group scales)."""
+    torch = _torch()
+    M, K = x.shape
+    N = w_biased.shape[0]
+    if epilogue == 0 and y_f32 is None and y_f16 is None:
+        y_f32 = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    rc = lib().dspark_gemm_i8_g128(ptr(x), M, K, ptr(w_biased), ptr(gscale), N, epilogue, ptr(y_f32), ptr(y_f16),
+                                   stream_handle(stream))
+    check(rc, "dspark_gemm_i8_g128")
+    return y_f32, y_f16
+
+
+def g128_scales(packed, N, K):
+    """The packer's scale rows (uint16 [N][SRow]) -> group-major [K/128][N] (host numpy)."""
+    import numpy as np
+    packed = np.ascontiguousarray(packed, dtype=np.uint16)
+    out = np.empty((K // 128, N), dtype=np.uint16)
+    check(lib().dspark_g128_scales(packed.ctypes.data_as(ctypes.c_void_p), N, K, out.ctypes.data_as(ctypes.c_void_p)),
+          "dspark_g128_scales")
+    return out
+
+
 def head_argmax(x, w, y_f32=None, best=None, workspace=None, stream=None):
     torch = _torch()
     M, K = x.shape
@@ -380,7 +407,7 @@ class ModelDesc(ctypes.Structure):
                 ("draft_window", ctypes.c_int32), ("ring_positions", ctypes.c_int32), ("mask_token", ctypes.c_int32),
                 ("conf_bias", ctypes.c_float), ("conf_thr", ctypes.c_float), ("eps", ctypes.c_float),
                 ("rope_base_swa", ctypes.c_float), ("rope_pairs_swa", ctypes.c_int32), ("conv_slots", ctypes.c_int32),
-                ("kv_format", ctypes.c_int32)]
+                ("kv_format", ctypes.c_int32), ("weight_format", ctypes.c_int32)]
 
 
 class LaunchArgs(ctypes.Structure):
@@ -461,7 +488,7 @@ def c4_desc(block=16, vocab=65536):
                       conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
 
 
-def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1):
+def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1, weight_format=1):
     """The reference model's geometry (internal/model/engine.go:23-40; internal/model/dspark.go:22-41;
     cmd/pack/main.go:193, 329): 24 target layers in the reference order (13 gated short-conv k=7, 6 full and 5
     sliding-window-256 GQA attention layers, 16/4/128), hidden 2048, gated FFN 7680, vocab 128000; 3 attention-only
@@ -470,14 +497,15 @@ def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1):
     generate.go:136). RoPE per layer kind as the reference builds it (engine.go:333-338): full attention and the
     drafter at base 1e6 with 32 rotating pairs, sliding layers at base 1e4 with 64. K/V in the reference's int8
     records (264 bytes per position and KV head, quantize_pair; engine.go:30-32, ops.hip:212-251) unless
-    kv_format=0 (fp16 pages); int8 weights with per-row fp16 scales."""
+    kv_format=0 (fp16 pages); int8 weights with the reference's per-128-column fp16 scales (weights.Pack,
+    quant.go:66-104) unless weight_format=0 (one scale per row)."""
     kinds = [0, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0]
     return model_desc(hidden=2048, ffn=7680, vocab=vocab, n_layers=24, layer_kind=kinds, q_heads=16, kv_heads=4,
                       head_dim=128, conv_kernel=7, window=256, rope_base=1e6, rope_pairs=32, rope_base_swa=1e4,
                       rope_pairs_swa=64, draft_layers=3,
                       draft_ffn=7680, block=block, max_drafts=max_drafts, crop_rows=16384, markov_rank=256, n_taps=5,
                       tap_layer=[2, 6, 12, 18, 23], draft_window=2048, ring_positions=4096, mask_token=vocab - 1,
-                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5, kv_format=kv_format)
+                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5, kv_format=kv_format, weight_format=weight_format)
 
 
 class Engine:

@@ -691,6 +691,24 @@ void orc_gemm_i8(const uint16_t* x, const uint8_t* w, int biased, const uint16_t
   free(xf);
 }
 
+/* Per-128-column group scales (weights.Pack, internal/weights/quant.go:66-104; applied per group as gemv_phase does,
+ * dspark.hip:553-580): y[t][r] = sum_g gs[g][r] * sum_{k in g} q[r][k] x[t][k], gs fp16 [K/128][N], fp64. */
+void orc_gemm_g128(const uint16_t* x, const uint8_t* w, const uint16_t* gs, int M, int N, int K, double* y) {
+  const int G = K / 128;
+  for (int r = 0; r < N; ++r) {
+    const uint8_t* wr = w + (size_t)r * K;
+    for (int t = 0; t < M; ++t) {
+      double acc = 0.0;
+      for (int g = 0; g < G; ++g) {
+        double part = 0.0;
+        for (int k = 128 * g; k < 128 * g + 128; ++k) part += (double)((int)wr[k] - 128) * h2d(x[(size_t)t * K + k]);
+        acc += part * h2d(gs[(size_t)g * N + r]);
+      }
+      y[(size_t)t * N + r] = acc;
+    }
+  }
+}
+
 void orc_gemm_f16(const uint16_t* x, const uint16_t* w, int M, int N, int K, double* y) {
   double* xf = (double*)malloc(sizeof(double) * (size_t)M * K);
   double* wf = (double*)malloc(sizeof(double) * (size_t)K);

@@ -108,6 +108,7 @@ void orc_transpose_lanes(const uint8_t* src, uint8_t* dst, int64_t n);          
 /* ---- verify GEMMs (dspark.hip:541-716 restated for per-output-channel scales) */
 /* y[t][r] = scale[r] * sum_k x[t][k] * q[r][k]; w signed int8 [N][K] or biased (q+128) when biased != 0. */
 void orc_gemm_i8(const uint16_t* x, const uint8_t* w, int biased, const uint16_t* scale, int M, int N, int K, double* y);
+void orc_gemm_g128(const uint16_t* x, const uint8_t* w, const uint16_t* gs, int M, int N, int K, double* y);
 void orc_gemm_f16(const uint16_t* x, const uint16_t* w, int M, int N, int K, double* y);
 /* First-max row argmax of y [M][N] (fp32 keys, ties -> smallest index). */
 void orc_row_argmax(const float* y, int M, int N, int32_t* idx);

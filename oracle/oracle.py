@@ -74,6 +74,7 @@ def lib():
             "orc_transpose_lanes": (None, [c_u8p, c_u8p, ctypes.c_int64]),
             "orc_gemm_i8": (None, [c_u16p, c_u8p, ctypes.c_int, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    c_f64p]),
+            "orc_gemm_g128": (None, [c_u16p, c_u8p, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_f64p]),
             "orc_gemm_f16": (None, [c_u16p, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_f64p]),
             "orc_row_argmax": (None, [c_f32p, ctypes.c_int, ctypes.c_int, c_i32p]),
             "orc_rms_norm": (None, [c_f32p, c_u16p, ctypes.c_int, ctypes.c_float, c_f32p]),
@@ -369,6 +370,18 @@ def gemm_i8(x_f16, w, scale_f16, biased=False):
     N = w.shape[0]
     y = np.empty((M, N))
     lib().orc_gemm_i8(_p(x, c_u16p), _p(w, c_u8p), int(biased), _p(s, c_u16p), M, N, K, _p(y, c_f64p))
+    return y
+
+
+def gemm_g128(x_f16, w_biased, gs_f16):
+    """x fp16 bits [M][K]; w biased uint8 [N][K]; gs fp16 bits [K/128][N] -> fp64 [M][N]."""
+    x = np.ascontiguousarray(x_f16, dtype=np.uint16)
+    w = np.ascontiguousarray(w_biased, dtype=np.uint8)
+    gs = np.ascontiguousarray(gs_f16, dtype=np.uint16)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=np.float64)
+    lib().orc_gemm_g128(_p(x, c_u16p), _p(w, c_u8p), _p(gs, c_u16p), M, N, K, _p(y, c_f64p))
     return y
 
 

@@ -37,13 +37,24 @@ class Weights:
         return a.reshape(shape) if shape else a
 
     def gemm_w(self, name, rows, cols):
+        """(q [rows][cols], scales): per-row scales [rows], or (weight_format 1) per-128-column group scales
+        [cols / 128][rows] from the tensor's [cols / 128][N] layout (N its allocated rows)."""
         w = (self.t[name + ".w"][:rows * cols].astype(np.int16) - 128).reshape(rows, cols).astype(np.float64)
-        s = h2f(self.t[name + ".s"][:rows])
+        if getattr(self.d, "weight_format", 0):
+            raw = self.t[name + ".s"]
+            n_alloc = raw.size // (cols // 128)
+            s = h2f(raw).reshape(cols // 128, n_alloc)[:, :rows]
+        else:
+            s = h2f(self.t[name + ".s"][:rows])
         return w, s
 
 
 def gemm(x16, w, s):
-    """y = (x @ q^T) * scale (per output row), fp64; x already fp16-valued."""
+    """y = (x @ q^T) * scale (per output row), or with per-128-column group scales s [K/128][N] the sum over groups of
+    each group's products times its scale (gemv_phase, dspark.hip:553-580); fp64; x already fp16-valued."""
+    if s.ndim == 2:
+        return sum((x16[:, 128 * g:128 * g + 128] @ w[:, 128 * g:128 * g + 128].T) * s[g][None, :]
+                   for g in range(s.shape[0]))
     return (x16 @ w.T) * s[None, :]
 
 

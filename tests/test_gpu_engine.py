@@ -49,9 +49,10 @@ MID = dict(hidden=1024, ffn=4096, vocab=4096, n_layers=4, layer_kind=[0, 1, 0, 2
 # token blocks), three token blocks (K split across workgroups, the last split running the fused conv epilogue).
 MID24 = dict(MID, block=24, max_drafts=12)
 MID33 = dict(MID, block=33, max_drafts=16)
-# The reference's K/V format: int8 records (quantize_pair, 264 bytes per position and KV head) for the target's attention
-# layers and the drafter ring, in the reference's attention geometry 16/4/128 (hidden 2048) with small FFNs.
-REF_REC = dict(REF_SMALL, hidden=2048, q_heads=16, kv_heads=4, ffn=1024, draft_ffn=1024, kv_format=1)
+# The reference's storage formats: int8 K/V records (quantize_pair, 264 bytes per position and KV head) for the target's
+# attention layers and the drafter ring, and int8 weights with per-128-column group scales (weights.Pack), in the
+# reference's attention geometry 16/4/128 (hidden 2048) with small FFNs.
+REF_REC = dict(REF_SMALL, hidden=2048, q_heads=16, kv_heads=4, ffn=1024, draft_ffn=1024, kv_format=1, weight_format=1)
 REL = 1e-3  # the bar of every value comparison in the round parity test (see the module docstring)
 REL_REC = 5e-3  # the same bar with int8 K/V records
 GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE, "mid": MID,
@@ -82,7 +83,9 @@ def make_weights(eng, desc, seed, stop_half=False):
             a = rng.integers(1, 256, nb, dtype=np.uint8)
         elif n.endswith(".s"):
             rows = nb // 2
-            K = sizes[n[:-2] + ".w"] // rows
+            # per-row scales: K = weight bytes / rows; per-128-column group scales ([K/128][N] entries): scaled for
+            # K = hidden, whatever the tensor's K
+            K = desc.hidden if desc.weight_format else sizes[n[:-2] + ".w"] // rows
             a = (rng.uniform(0.75, 1.25, rows) / (73.3 * np.sqrt(K))).astype(np.float16).view(np.uint16)
         elif n == "embed":
             a = rng.standard_normal(nb // 2).astype(np.float16).view(np.uint16)
