@@ -85,6 +85,9 @@ _SIGS = {
 }
 
 
+ABI_VERSION = 3  # dspark_abi_version() of the library these signatures describe
+
+
 def lib():
     """Load libdspark_amd.so; raises if it has not been built (no fallback path exists)."""
     global _lib
@@ -96,6 +99,9 @@ def lib():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+        if L.dspark_abi_version() != ABI_VERSION:
+            raise DsparkError(f"{LIB_PATH} has ABI {L.dspark_abi_version()}, this module binds {ABI_VERSION}: "
+                              "rebuild it")
         _lib = L
     return _lib
 
