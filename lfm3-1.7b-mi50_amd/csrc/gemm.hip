@@ -414,12 +414,38 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 // weights held in registers (up to 4 token blocks); XD = true (TB = 1) has every wave load its own range of X straight
 // into B operands. Ranges longer than CPW chunks go in batches of CPW. Chunk order inside a range, then range order,
 // fixes the summation order, so results do not depend on timing.
-// GS (one token block, X per wave): weights with per-128-column group scales (p.gscale [K/128][N]): each 64-column
-// chunk's products go to a fresh accumulator that is scaled by its group's scales of the lane's 4 rows and added in chunk
-// order (the reference applies the scale per group as well, dspark.hip:553-580).
+// GS (one token block, int8 weights): per-128-column group scales (p.gscale [K/128][N]): the products of a group's two
+// 64-column chunks go to a fresh accumulator that is scaled by the group's scales of the lane's 4 rows and added in group
+// order (the reference applies the scale per group as well, dspark.hip:553-580). Every range and band starts on an
+// even chunk (gemm_launch checks), so a batch's chunk pairs (cb + 2 j, cb + 2 j + 1) are whole groups, the second one
+// absent only at the end of a range.
+template <int CPW>
+__device__ __forceinline__ void gscale_load(const GemmParams& p, u32x2 (&gsr)[CPW / 2], int cb, int c1, int r4) {
+#pragma unroll
+  for (int j = 0; j < CPW / 2; ++j) {
+    const int c = min(cb + 2 * j, c1 - 1);
+    gsr[j] = ldg(reinterpret_cast<const u32x2*>(p.gscale + (size_t)(c >> 1) * p.N + r4));
+  }
+}
+
+// prod(i, t): t plus the products of chunk cb + i
+template <int CPW, typename F>
+__device__ __forceinline__ void gscale_products(f32x4& acc, const u32x2 (&gsr)[CPW / 2], int cb, int c1, F prod) {
+#pragma unroll
+  for (int j = 0; j < CPW / 2; ++j) {
+    if (cb + 2 * j < c1) {
+      f32x4 t = prod(2 * j, f32x4{0, 0, 0, 0});
+      if (cb + 2 * j + 1 < c1) t = prod(2 * j + 1, t);
+      const half4 sc = __builtin_bit_cast(half4, gsr[j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(t[r], (float)sc[r], acc[r]);
+    }
+  }
+}
+
 template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
-  static_assert(!GS || (XD && TB == 1 && I8), "group scales: one token block, X per wave, int8 weights");
+  static_assert(!GS || (TB == 1 && I8 && CPW % 2 == 0), "group scales: one token block, int8 weights, whole groups");
   // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
   // anything is stored), so its latency overlaps theirs; a stopped round writes nothing.
   const int run = run_flag_load(p.st);
@@ -485,27 +511,28 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     // compiler's wait for the previous iteration's loads would also hold the first batch back behind the flag load.
     auto batch = [&](int cb) {
       u32x4 xb[CPW][2];
-      u32x2 gsr[GS ? CPW : 1];  // group scales of chunk cb + i for rows row0 + 4 g .. + 3 (4 halves)
+      u32x2 gsr[GS ? CPW / 2 : 1];
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = min(cb + i, c1 - 1);
         xb[i][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs));
         xb[i][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + xhs));
-        if constexpr (GS) gsr[i] = ldg(reinterpret_cast<const u32x2*>(p.gscale + (size_t)(c >> 1) * p.N + row0 + 4 * g));
       }
+      if constexpr (GS) gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
       load(w, cb);
-#pragma unroll
-      for (int i = 0; i < CPW; ++i) {
-        if (cb + i < c1) {
+      if constexpr (GS) {
+        gscale_products<CPW>(acc[0], gsr, cb, c1, [&](int i, f32x4 t) {
           half8 a[2];
           weights(w[i], a);
-          if constexpr (GS) {
-            f32x4 t = mfma16x16x32(a[0], as_half8(xb[i][0]), f32x4{0, 0, 0, 0});
-            t = mfma16x16x32(a[1], as_half8(xb[i][1]), t);
-            const half4 sc = __builtin_bit_cast(half4, gsr[i]);
+          t = mfma16x16x32(a[0], as_half8(xb[i][0]), t);
+          return mfma16x16x32(a[1], as_half8(xb[i][1]), t);
+        });
+      } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[0][j] = fmaf(t[j], (float)sc[j], acc[0][j]);
-          } else {
+        for (int i = 0; i < CPW; ++i) {
+          if (cb + i < c1) {
+            half8 a[2];
+            weights(w[i], a);
             acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
             acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
           }
@@ -542,11 +569,27 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
         }
       }
     };
+    u32x2 gsr[GS ? CPW / 2 : 1];
+    if constexpr (GS) gscale_load<CPW>(p, gsr, c0, c1, row0 + 4 * g);  // older than X: covered by the wait below
     stage(0, min(tbp, TB));
     load(w, c0);
     __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPW * WV));
     __builtin_amdgcn_s_barrier();
-    if (all || CPW > 8) {  // (16-chunk batches: the plan never takes passes)
+    if constexpr (GS) {  // one token block, X^T of the band in LDS at once (gemm_launch checked)
+      for (int cb = c0; cb < c1; cb += CPW) {
+        if (cb != c0) {
+          gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
+          load(w, cb);
+        }
+        gscale_products<CPW>(acc[0], gsr, cb, c1, [&](int i, f32x4 t) {
+          half8 a[2];
+          weights(w[i], a);
+          const u32x4* xb = xs + ((size_t)(cb + i - b0) * 2) * 64;
+          t = mfma16x16x32(a[0], as_half8(xb[lane]), t);
+          return mfma16x16x32(a[1], as_half8(xb[64 + lane]), t);
+        });
+      }
+    } else if (all || CPW > 8) {  // (16-chunk batches: the plan never takes passes)
       for (int cb = c0; cb < c1; cb += CPW) {
         if (cb != c0) load(w, cb);
 #pragma unroll
@@ -737,11 +780,18 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const dim3 grid(groups * p.bands), block(64 * p.wpg * p.kw);
   const size_t lds = gemm_sliced_lds_bytes(p, I8);
   const int cpk = ((p.K / 64 + p.bands - 1) / p.bands + p.kw - 1) / p.kw;  // chunks per range (of the band's)
-  if constexpr (I8) {
-    if (TB == 1 && gemm_sliced_xd(p, I8) && p.gscale) {  // gemm_launch checked block.x <= 512
-      hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true>), grid, block, lds, s, p);
+  if constexpr (I8 && TB == 1) {
+    if (p.gscale) {  // group scales: X per wave, or X^T of the band in LDS at once (gemm_launch checked)
+      if (gemm_sliced_xd(p, I8)) {
+        hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true>), grid, block, lds, s, p);
+      } else {
+        allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true>, lds);
+        hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true>), grid, block, lds, s, p);
+      }
       return;
     }
+  }
+  if constexpr (I8) {
     if (TB == 1 && gemm_sliced_xd(p, I8)) {
       if (block.x <= 512)  // up to 8 waves: twice the registers per wave (no spills with the first batch peeled)
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512>), grid, block, lds, s, p);
@@ -807,8 +857,11 @@ static void launch_gemm(const GemmParams& p, hipStream_t s) {
 // 9.6 against 10.3 us through LDS; equal at 3104 and 6144 rows, slower for S = 5 and 16), else staged in LDS once (at
 // most 64 KB). Two to four token blocks (X through LDS) take the same groups, X^T in passes of two or one token blocks
 // of at most 128 KB when all of them do not fit (ranges of at most 8 chunks): 33 tokens, C5 round 2.19 -> 1.95 ms
-// against the split-K kernel (2.02 with 64 KB passes of one token block). Returns false when no sliced plan fits (the
-// split-K plan is used).
+// against the split-K kernel (2.02 with 64 KB passes of one token block). Group scales (9 tokens, operand-order X) take
+// the same plans, with even chunk counts per band and range, and X through LDS where X per wave would need more than 8
+// waves: 128000 x 2048 50.0 us (47.6 with row scales; 63.3 with one strip and 4 ranges per workgroup), 15360 x 2048
+// 10.2 (9.6), 2048 x 7680 in 2 bands 7.3 (7.0), 3072 x 2048 5.0 (5.0). Returns false when no sliced plan fits (the
+// split-K plan is used; never with group scales).
 static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xop, int max_bands, GemmPlan* pl,
                              bool gs = false) {
   const int strips = N / 16, chunks = K / 64;
@@ -816,8 +869,8 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
   int S, KW, bands = 1;
   if (wpg_req > 0) {
     S = wpg_req;
-    KW = (gs ? 8 : 16) / S;  // group scales: at most 8 waves (the 1024-thread variant would spill)
-  } else if (i8 && ((strips <= 512 && (xop || K <= 4096)) || gs)) {  // group scales: always one strip per workgroup
+    KW = 16 / S;
+  } else if (i8 && strips <= 512 && (xop || K <= 4096)) {
     S = 1;
     // fewer than 256 strips: K in bands over more workgroups when the caller adds the bands (at least 8 chunks each)
     while (bands * 2 <= max_bands && strips * bands * 2 <= 256 && chunks / (bands * 2) >= 8) bands *= 2;
@@ -828,7 +881,26 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
   }
-  const bool xd = i8 && tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S));
+  bool xd = i8 && tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S));
+  if (gs) {
+    // group scales: every band and range starts on an even chunk (whole 128-column groups); X^T of a band through LDS
+    // only when it fits at once, else one strip per workgroup with X per wave
+    while (bands > 1 && ((chunks + bands - 1) / bands) % 2) bands /= 2;
+    const int gbc = (chunks + bands - 1) / bands;
+    const bool fits = (size_t)gbc * 2048 <= GEMM_X_LDS;
+    if (xd && S * KW > 8) {  // the X-per-wave kernel with group scales takes at most 8 waves (16 would spill)
+      if (fits)
+        xd = false;
+      else
+        KW = std::max(1, 8 / S);
+    }
+    if (!xd && !fits) {
+      S = 1;
+      KW = std::min(8, std::max(4, (gbc + 7) / 8));
+      xd = true;
+    }
+    while (KW > 1 && ((gbc + KW - 1) / KW) % 2) --KW;
+  }
   // X^T through LDS: all token blocks at once when they fit 64 KB, else one token block per pass, each pass's X^T
   // within 64 KB and each range within one 8-chunk batch (its weights stay in registers)
   const int bc = (chunks + bands - 1) / bands, cpk = (bc + KW - 1) / std::max(1, KW);
@@ -885,9 +957,15 @@ float* gemm_ws_partials(void* ws) { return reinterpret_cast<float*>(static_cast<
 
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
   if ((p.xop && p.xop < (p.M + 15) / 16) || (p.yop && p.yop < (p.M + 15) / 16)) return DSPARK_EINVAL;
-  // group scales: the K-sliced kernel with X per wave (one token block), whole 128-column groups, no row scales
-  if (p.gscale && (!i8 || p.kw <= 0 || !gemm_sliced_xd(p, i8) || p.K % 128 || p.scale || p.wpg * p.kw > 8))
-    return DSPARK_EINVAL;
+  // group scales: the K-sliced kernel, one token block, whole 128-column groups in every band and range, X per wave or
+  // the band's X^T in LDS at once, no row scales
+  if (p.gscale) {
+    if (!i8 || p.kw <= 0 || p.M > 16 || p.K % 128 || p.scale) return DSPARK_EINVAL;
+    const int bands = std::max(1, p.bands), bc = (p.K / 64 + bands - 1) / bands, cpk = (bc + p.kw - 1) / p.kw;
+    if ((bands > 1 && bc % 2) || cpk % 2 || (!gemm_sliced_xd(p, i8) && (size_t)bc * 2048 > GEMM_X_LDS) ||
+        (gemm_sliced_xd(p, i8) && p.wpg * p.kw > 8))
+      return DSPARK_EINVAL;
+  }
   if (p.kw > 0) {
     // K-sliced: whole K in one workgroup of wpg x kw <= 16 waves; X^T in LDS (<= 64 KB) unless one strip per group
     const int tb = (p.M + 15) / 16;
