@@ -12,9 +12,12 @@ Prints one JSON line (the driver's contract) with a `roofline` object for the do
 `verify_attn_lds_kernel`) timed with HIP events on the library's stream, and a `cpu_baseline` object (the C oracle's
 fp32 restatement timed on a bounded sample of the same workload, on all CPUs of the job's share and on one). The same
 line carries the metric's other half, `headline_tok_s` (greedy decode tok/s of full DSpark rounds at 1k / 32k / 128k
-context, beside the reference's published MI50 numbers), and `c5_attention` (verify attention at 131072 keys for 33 and
-16 verify tokens). `--c2-only` skips those two; `--workload` selects the other configs (c3, c4, c5, tiers, ref), or
-verify attention alone at any context and block (`attn`, `--ctx`, `--tokens`).
+context, beside the reference's published MI50 numbers, on the C4 geometry) and `headline_ref_tok_s` (the same on the
+reference model's geometry, draft policy and storage formats), `c5_attention` (verify attention at 131072 keys for 33 and
+16 verify tokens) and `ref_int8_record_attention` (verify attention over the reference's int8 K/V records, its
+geometry and 9-token block, at 32768 and 131072 keys). `--c2-only` skips those; `--workload` selects the other configs
+(c3, c4, c5, tiers, ref with `--ref-formats`), or verify attention alone at any context and block (`attn` over fp16
+pages, `rec` over int8 records; `--ctx`, `--tokens`).
 """
 import argparse
 import ctypes
@@ -549,7 +552,8 @@ def bench_engine(args, host, torch, workload):
         if key not in cache:
             for k in list(cache):
                 cache.pop(k)[1].close()
-            desc_ = host.ref_desc(block=block, max_drafts=max_drafts) if ref else None
+            fmt = 1 if args.ref_formats == "reference" else 0
+            desc_ = host.ref_desc(block=block, max_drafts=max_drafts, kv_format=fmt, weight_format=fmt) if ref else None
             cache[key] = engine_setup(host, torch, ctx, block, 20261201 + ctx + block, desc_)
         desc, eng = cache[key]
         a0, anchor = ctx, 17
@@ -585,11 +589,13 @@ def bench_engine(args, host, torch, workload):
         print(json.dumps(rec), file=sys.stderr, flush=True)
     for k in list(cache):
         cache.pop(k)[1].close()
+    recf = ref and args.ref_formats == "reference"
     model = ("reference geometry: 24 layers (13 conv k=7 / 6 full / 5 sliding-256 attention, 16/4/128), FFN 7680, "
-             "vocab 128000, 3-layer drafter; the reference's int8 K/V records and per-128-column weight scales" if ref
+             "vocab 128000, 3-layer drafter; " + ("the reference's int8 K/V records and per-128-column weight scales"
+                                                  if recf else "fp16 K/V pages and per-row weight scales") if ref
              else "C4 geometry")
-    kv = ("int8 K/V records (codes uniform in [-127, 127], scales 1/40)" if ref else "N(0,1) fp16 KV caches")
-    scales = "per-128-column fp16 scales" if ref else "per-row fp16 scales"
+    kv = ("int8 K/V records (codes uniform in [-127, 127], scales 1/40)" if recf else "N(0,1) fp16 KV caches")
+    scales = "per-128-column fp16 scales" if recf else "per-row fp16 scales"
     return {"metric": f"greedy decode tok/s (DSpark rounds, random-init model, {model})", "workload": workload,
             "rounds": rounds, "warmup": warm, "cases": out,
             "data": f"random-init weights (int8 uniform, {scales}), {kv}; planted drafts "
@@ -620,11 +626,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy", "attn", "rec"])
+    ap.add_argument("--ref-formats", default="reference", choices=["reference", "fp16"],
+                    help="ref workload: the reference's storage formats (int8 K/V records, per-128-column weight "
+                         "scales) or fp16 K/V pages with per-row scales")
     ap.add_argument("--ctx", type=int, default=131072, help="attn workload: context (keys before the block)")
     ap.add_argument("--tokens", type=int, default=0, help="attn / rec workload: verify tokens (default 33 / 9)")
     ap.add_argument("--layers", type=int, default=2, help="attn workload: layers per step")
     ap.add_argument("--c2-only", action="store_true",
-                    help="default workload without the headline tiers and the C5 attention fields")
+                    help="default workload without the headline tiers and the C5 and int8-record attention fields")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -674,6 +683,16 @@ def main():
             "note": "tok_s_at_mi50_tau = the MI50's measured committed tokens per round (benchmarks/"
                     "verify_attention.txt:54-58) / this round time; a round verifies the same tokens whatever is "
                     "accepted, so its time does not depend on the draws; tok_s is the rate of the planted draws"}
+        # The same tiers on the reference model's geometry, draft policy and storage formats (int8 K/V records,
+        # per-128-column weight scales): the configuration the MI50 numbers were measured on.
+        rargs = argparse.Namespace(**vars(targs))
+        rargs.ref_formats = "reference"
+        rtiers = bench_engine(rargs, host, torch, "ref")
+        res["headline_ref_tok_s"] = {
+            "model": rtiers["metric"], "rounds": targs.steps, "warmup": targs.warmup,
+            "tiers": [{k: c[k] for k in ("ctx", "max_drafts", "ms_per_round", "tokens_per_round", "tok_s",
+                                         "tok_s_at_mi50_tau", "mi50_tok_s", "vs_mi50", "planted_tau_expected")}
+                      for c in rtiers["cases"]]}
         res["c5_attention"] = c5_attention_fields(args, host, torch)
         res["ref_int8_record_attention"] = rec_attention_fields(args, host, torch)
     if not args.no_cpu:

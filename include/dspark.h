@@ -183,8 +183,8 @@ size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K); /* counters + 
 /* dspark_gemm_i8 with the reference's per-128-column weight scales (weights.Pack, internal/weights/quant.go:66-104):
  * y[t][r] = sum_g gscale[g][r] * sum_{k in group g} x[t][k] * q[r][k], groups of 128 columns, gscale fp16 [K/128][N]
  * (group-major: dspark_g128_scales converts the packer's [row][quarter][i] layout), weights biased int8 [N][K] as
- * above, fp16 x. M <= 16 (the reference verifies 9 tokens), K % 128 == 0; same epilogues; no workspace. Each 64-column
- * chunk's products are scaled in fp32 by its group's scale and added in chunk order. The reference's default build
+ * above, fp16 x. M <= 16 (the reference verifies 9 tokens), K % 128 == 0; same epilogues; no workspace. Each
+ * 128-column group's products are scaled in fp32 by the group's scale and added in group order. The reference's build
  * also quantizes x to int8 per 16 columns (LFM3_X8, dspark.hip:25-27, 802-823); x stays fp16 here, as in the
  * reference's LFM3_F16 build. Replaces gemv_phase / unit_dot_r over packed weights (dspark.hip:541-716). */
 int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* gscale, int32_t N,
