@@ -308,17 +308,18 @@ __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
       }
   }
   __syncthreads();
-  const size_t slot = ((size_t)h * p.RG + rg) * p.S + split;
-  f32x4* dst = reinterpret_cast<f32x4*>(p.part_acc + slot * R * D);
+  // row-major partials: row r of this split at ((hr R + r) S + split)
+  const size_t row0 = ((size_t)h * p.RG + rg) * R * p.S + split;
+  f32x4* dst = reinterpret_cast<f32x4*>(p.part_acc) + row0 * (D / 4);
   for (int e = threadIdx.x; e < R * D / 4; e += 256) {
     const int r = e / (D / 4), c4 = e % (D / 4);
-    dst[e] = sm_o[0][r][c4] + sm_o[1][r][c4];
+    dst[(size_t)r * p.S * (D / 4) + c4] = sm_o[0][r][c4] + sm_o[1][r][c4];
   }
   for (int r = threadIdx.x; r < R; r += 256) {
     const float mx = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
     const float L = (fast_exp2(sm_m[1][r] - mx) * sm_l[1][r] + fast_exp2(sm_m[0][r] - mx) * sm_l[0][r]) +
                     (fast_exp2(sm_m[3][r] - mx) * sm_l[3][r] + fast_exp2(sm_m[2][r] - mx) * sm_l[2][r]);
-    p.part_ml[slot * R + r] = f32x2{L > 0.f ? mx : -INFINITY, L};
+    p.part_ml[row0 + (size_t)r * p.S] = f32x2{L > 0.f ? mx : -INFINITY, L};
   }
 }
 
@@ -566,98 +567,86 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   if (pl != 0) return;
   // The split's partial, stored device-coherent (SC1: written through to memory, so the end of the kernel has no
   // dirty L2 lines to write back; measured 0.4-0.6 us less per C2 layer than default stores).
-  const size_t slot = (size_t)h * p.S + split;
-  const __amdgpu_buffer_rsrc_t ra =
-      __builtin_amdgcn_make_buffer_rsrc(p.part_acc + slot * R * D, (short)0, R * D * (int)sizeof(float), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rm =
-      __builtin_amdgcn_make_buffer_rsrc(p.part_ml + slot * R, (short)0, R * (int)sizeof(f32x2), 0x00020000);
+  // row-major partials ([head][row][split][D]; the head's region is R x S rows of D floats)
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      p.part_acc + (size_t)h * R * p.S * D, (short)0, R * p.S * D * (int)sizeof(float), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(p.part_ml + (size_t)h * R * p.S, (short)0,
+                                                                      R * p.S * (int)sizeof(f32x2), 0x00020000);
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int rb = rg * QB + qb;
     if (rb >= NRB) break;  // padding row blocks of the last group
+    const int ri = (rb * 16 + n) * p.S + split;
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc)
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, rs.o[qb][cc]), ra,
-                                             (uint32_t)(((rb * 16 + n) * D + 16 * cc + 4 * g) * sizeof(float)), 0,
+                                             (uint32_t)((ri * D + 16 * cc + 4 * g) * sizeof(float)), 0,
                                              ATTN_CPOL_COHERENT);
     if (g == 0) {
       const float L = rs.ls[qb][0];
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{L > 0.f ? rs.m[qb] : -INFINITY, L}), rm,
-                                            (uint32_t)((rb * 16 + n) * sizeof(f32x2)), 0, ATTN_CPOL_COHERENT);
+                                            (uint32_t)(ri * sizeof(f32x2)), 0, ATTN_CPOL_COHERENT);
     }
   }
 }
 #undef DSPARK_LDSP
 
 // ---------------------------------------------------------------- merge of the split partials
-// COMBINE_LANES lanes per output quad (row r, dims 4 c4 .. + 3): lane j takes splits j, j + COMBINE_LANES, ... with
-// all its loads in flight and merges them as a log-sum-exp (m = max, l = sum f_s l_s, acc = sum f_s acc_s,
-// f_s = exp2(m_s - m)); the lanes then merge pairwise in a fixed tree (lanes 1, 2, 4 apart), so outputs are
-// bit-identical run to run. o = acc / l (0 when nothing was visible), times the optional sigmoid gate, stored fp16
-// and/or fp32. blockIdx.y = KV head x row group. Eight lanes of at most 8 splits each measured 3.6-3.9 us per C2 merge
-// against 4.4 us for four lanes of 16. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60
-// workgroups' key ranges).
-#ifndef DSPARK_ATTN_COMBINE_LANES
-#define DSPARK_ATTN_COMBINE_LANES 8
-#endif
-// Up to 64 splits: COMBINE_LANES lanes of up to 8 splits each; more splits (the record kernel's, up to 256): 32 lanes of
-// up to 8 each, so every split's loads are in flight at once (batches of 64 one after the other measured 9-11 us for
-// 256 splits).
-constexpr int COMBINE_LANES = DSPARK_ATTN_COMBINE_LANES, COMBINE_MAX_PER_LANE = 64 / COMBINE_LANES;
-constexpr int COMBINE_LANES_WIDE = 32;
-
-template <int D, int LANES>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
-  constexpr int PER_LANE = 8;  // splits per lane per batch
+// The partials are row-major ([KV head x row group][row][split][D]), so one workgroup merges one output row: thread
+// (j, q) takes dims 4 q .. 4 q + 3 of splits j, j + SL, ... with batches of 8 loads in flight (one load of a wave covers
+// 64 / (D / 4) whole splits of the row, contiguous), and merges them as a log-sum-exp (m = max, l = sum f_s l_s,
+// acc = sum f_s acc_s, f_s = exp2(m_s - m)); the split lanes of a wave then merge pairwise in a fixed xor tree and the
+// waves in wave order through LDS, so outputs are bit-identical run to run. o = acc / l (0 when nothing was visible),
+// times the optional sigmoid gate, stored fp16 and/or fp32. blockIdx = (row, KV head x row group); rows past G M (padding
+// of the last row block, never stored by the split kernels) are skipped. Measured on MI355X, graph-replayed with the
+// partials in HBM: 256 splits at D 128 6.8 us (18.7 with the split-major layout and 32 lanes per output quad, whose
+// every load touched 32 cache lines), 64 splits 3.6 (4.9), C2's 24 splits at D 64 3.4 (3.5); 16 split lanes beyond 96
+// splits, 8 below. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
+template <int D, int SL>
+__global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) {
+  constexpr int Q = D / 4, NT = SL * Q, W = NT / 64, PER = 8;
+  static_assert(NT % 64 == 0 && 64 % Q == 0, "whole waves of whole rows");
+  __shared__ f32x4 s_acc[W > 1 ? W - 1 : 1][Q];
+  __shared__ f32x2 s_ml[W > 1 ? W - 1 : 1][Q];
+  const int hr = blockIdx.y, h = hr / p.RG, rg = hr % p.RG, r = blockIdx.x;
+  const int row = rg * p.R + r;
+  if (row >= p.G * p.M) return;  // the same for the whole workgroup
   const int run = run_flag_load(p.st);  // tested once the partial loads are in flight
-  const int hr = blockIdx.y, h = hr / p.RG, rg = hr % p.RG;
-  const int R = p.R;
-  const int e = blockIdx.x * (256 / LANES) + (int)(threadIdx.x / LANES);
-  const int j = threadIdx.x % LANES;
-  // rows past G*M (padding of the last row block) are neither read nor stored
-  const bool live = e < R * D / 4 && rg * R + e / (D / 4) < p.G * p.M;
-  const int r = live ? e / (D / 4) : 0, c4 = e % (D / 4);
-  const size_t slot0 = (size_t)hr * p.S;
-  // Splits in batches of LANES x PER_LANE: a lane's loads of a batch are all in flight before the first is used,
-  // and each batch folds into the lane's running (m, l, acc).
+  const int q = threadIdx.x % Q, j = threadIdx.x / Q;
+  const size_t base = ((size_t)hr * p.R + r) * p.S;
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0, 0, 0, 0};
-  for (int b0 = 0; b0 < p.S; b0 += LANES * PER_LANE) {
-    f32x2 ml[PER_LANE];
-    f32x4 av[PER_LANE];
+  for (int b0 = 0; b0 < p.S; b0 += SL * PER) {
+    f32x2 ml[PER];
+    f32x4 av[PER];
 #pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) {
-      const int sp = b0 + j + LANES * i;
-      const bool ok = live && sp < p.S;
-      ml[i] = ok ? ldg(p.part_ml + (slot0 + sp) * R + r) : f32x2{-INFINITY, 0.f};
-      av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + ((slot0 + sp) * R + r) * D) + c4) : f32x4{0, 0, 0, 0};
+    for (int i = 0; i < PER; ++i) {
+      const int sp = b0 + j + SL * i;
+      const bool ok = sp < p.S;
+      ml[i] = ok ? ldg(p.part_ml + base + sp) : f32x2{-INFINITY, 0.f};
+      av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + (base + sp) * D) + q) : f32x4{0, 0, 0, 0};
     }
-    if (!run_flag_set(run)) {  // a stopped round writes nothing
+    if (!run_flag_set(run)) {  // a stopped round writes nothing (the same for the whole workgroup)
       __builtin_amdgcn_s_waitcnt(0);
       return;
     }
     float mb = m;
 #pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) mb = fmaxf(mb, ml[i][0]);
+    for (int i = 0; i < PER; ++i) mb = fmaxf(mb, ml[i][0]);
     if (mb > -INFINITY) {
       const float fr = m == -INFINITY ? 0.f : fast_exp2(m - mb);  // the running state rescaled to the batch max
       l *= fr;
       acc *= fr;
       m = mb;
 #pragma unroll
-      for (int i = 0; i < PER_LANE; ++i) {
+      for (int i = 0; i < PER; ++i) {
         const float f = ml[i][0] == -INFINITY ? 0.f : fast_exp2(ml[i][0] - m);
         l = fmaf(f, ml[i][1], l);
         acc += f * av[i];
       }
     }
   }
-#pragma unroll
-  for (int off = 1; off < LANES; off <<= 1) {
-    const float mk = __shfl_xor(m, off), lk = __shfl_xor(l, off);
-    f32x4 ak;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ak[i] = __shfl_xor(acc[i], off);
+  auto fold = [&](float mk, float lk, f32x4 ak) {
     const float mx = fmaxf(m, mk);
     if (mx > -INFINITY) {
       const float fa = m == -INFINITY ? 0.f : fast_exp2(m - mx), fb = mk == -INFINITY ? 0.f : fast_exp2(mk - mx);
@@ -665,19 +654,38 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
       acc = acc * fa + ak * fb;
       m = mx;
     }
+  };
+#pragma unroll
+  for (int off = Q; off < 64; off <<= 1) {
+    f32x4 ak;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ak[i] = __shfl_xor(acc[i], off);
+    fold(__shfl_xor(m, off), __shfl_xor(l, off), ak);
   }
-  if (j != 0 || !live) return;
-  const int row = rg * R + r;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if constexpr (W > 1) {
+    if (wave > 0 && lane < Q) {
+      s_acc[wave - 1][q] = acc;
+      s_ml[wave - 1][q] = f32x2{m, l};
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w = 0; w < W - 1; ++w) {
+      const f32x2 mlw = s_ml[w][q];
+      fold(mlw[0], mlw[1], s_acc[w][q]);
+    }
+  }
+  if (lane >= Q) return;
   float scale = l > 0.f ? 1.f / l : 0.f;
   const int t = row / p.G, qh = h * p.G + row % p.G;
   if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * p.QH + qh)));
   acc *= scale;
-  const size_t idx = ((size_t)t * p.QH + qh) * D + 4 * c4;
+  const size_t idx = ((size_t)t * p.QH + qh) * D + 4 * q;
   if (p.out16) {
     half4 hv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) hv[i] = (_Float16)acc[i];
-    *reinterpret_cast<half4*>(p.out16 + (p.out_op ? xop_elem(t, qh * D + 4 * c4, p.out_op) : idx)) = hv;
+    *reinterpret_cast<half4*>(p.out16 + (p.out_op ? xop_elem(t, qh * D + 4 * q, p.out_op) : idx)) = hv;
   }
   if (p.out32) *reinterpret_cast<f32x4*>(p.out32 + idx) = acc;
 }
@@ -936,17 +944,16 @@ int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
     if (rc) return rc;
   }
   if (phases & 2) {
-    const bool wide = p.S > COMBINE_LANES * COMBINE_MAX_PER_LANE;
-    const int qpb = 256 / (wide ? COMBINE_LANES_WIDE : COMBINE_LANES);  // output quads per block
-    const dim3 grid((p.R * D / 4 + qpb - 1) / qpb, p.KVH * p.RG);
+    const bool wide = p.S > 96;  // 16 split lanes per row, else 8
+    const dim3 grid(p.R, p.KVH * p.RG);
     if (D == 64 && !wide)
-      hipLaunchKernelGGL((attn_combine_kernel<64, COMBINE_LANES>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((attn_combine_kernel<64, 8>), grid, dim3(8 * 16), 0, s, p);
     else if (D == 64)
-      hipLaunchKernelGGL((attn_combine_kernel<64, COMBINE_LANES_WIDE>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((attn_combine_kernel<64, 16>), grid, dim3(16 * 16), 0, s, p);
     else if (!wide)
-      hipLaunchKernelGGL((attn_combine_kernel<128, COMBINE_LANES>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((attn_combine_kernel<128, 8>), grid, dim3(8 * 32), 0, s, p);
     else
-      hipLaunchKernelGGL((attn_combine_kernel<128, COMBINE_LANES_WIDE>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((attn_combine_kernel<128, 16>), grid, dim3(16 * 32), 0, s, p);
   }
   return (int)hipGetLastError();
 }

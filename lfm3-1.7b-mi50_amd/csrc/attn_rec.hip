@@ -363,11 +363,11 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // partials of this split: rows of KV head h, (max, sum) and acc / PSCALE
-  const size_t slot = (size_t)h * p.S + split;
-  const __amdgpu_buffer_rsrc_t ra =
-      __builtin_amdgcn_make_buffer_rsrc(p.part_acc + slot * R * REC_D, (short)0, R * REC_D * (int)sizeof(float), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rm =
-      __builtin_amdgcn_make_buffer_rsrc(p.part_ml + slot * R, (short)0, R * (int)sizeof(f32x2), 0x00020000);
+  // row-major partials ([head][row][split][D]; the head's region is R x S rows of D floats)
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      p.part_acc + (size_t)h * R * p.S * REC_D, (short)0, R * p.S * REC_D * (int)sizeof(float), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(p.part_ml + (size_t)h * R * p.S, (short)0,
+                                                                      R * p.S * (int)sizeof(f32x2), 0x00020000);
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int rb = rg * QB + qb;
@@ -375,13 +375,14 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
     L = L + __shfl_xor(L, 32);
     if (rb >= p.nrb) break;
     if (rb * 16 + n >= p.G * p.M) continue;  // padding rows: the merge never reads them
+    const int ri = (rb * 16 + n) * p.S + split;
 #pragma unroll
     for (int c = 0; c < 8; ++c)
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[qb][c] * (1.f / REC_PSCALE)), ra,
-                                             (uint32_t)(((rb * 16 + n) * REC_D + 16 * c + 4 * g) * sizeof(float)), 0, 16);
+                                             (uint32_t)((ri * REC_D + 16 * c + 4 * g) * sizeof(float)), 0, 16);
     if (g == 0)
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{L > 0.f ? m[qb] : -INFINITY, L}), rm,
-                                            (uint32_t)((rb * 16 + n) * sizeof(f32x2)), 0, 16);
+                                            (uint32_t)(ri * sizeof(f32x2)), 0, 16);
   }
 }
 #undef DSPARK_LDSP

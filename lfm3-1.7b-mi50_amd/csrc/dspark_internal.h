@@ -22,8 +22,8 @@ struct AttnParams {
   const _Float16* vp;
   const int32_t* bt;
   uint32_t k_bytes, v_bytes;  // page pool sizes (range of the buffer loads; < 2 GiB)
-  float* part_acc;   // [KVH][RG][S][R][D]
-  f32x2_t* part_ml;  // [KVH][RG][S][R] (max, sum); max = -inf when the split saw no key of the row
+  float* part_acc;   // [KVH][RG][R][S][D] (row-major: one row's splits contiguous for the merge)
+  f32x2_t* part_ml;  // [KVH][RG][R][S] (max, sum); max = -inf when the split saw no key of the row
   _Float16* out16;            // [M][QH][D], or operand order (xop_elem, column qh D + d) when out_op > 0
   float* out32;
   const float* gate;
