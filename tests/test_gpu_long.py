@@ -4,7 +4,9 @@
   tokens, against the fp64 C oracle at 2e-3 max-abs (the oracle's threaded form, which gives its single-threaded bits);
 * full DSpark rounds on random-init models of the C4 geometry (16 layers: 10 gated short-conv k=3 + 6 GQA 32/8/64,
   hidden 2048, FFN 8192, vocab 65536, 4-layer drafter): block 33 at context 131072 (C5) with drafts planted at 0 %,
-  50 % and 100 % acceptance -- a rollback in every round of the first two -- and block 16 at context 32768 (C4). The
+  50 % and 100 % acceptance -- a rollback in every round of the first two -- and block 16 at context 32768 (C4); and the
+  reference model's geometry on the reference's storage formats (int8 K/V records, per-128-column weight scales) at
+  context 131072 with its 9-token block and 3 drafts. The
   property checked at these sizes is the one a speculative round must keep whatever is drafted: the committed tokens
   are exactly the target's greedy chain (one-token verify rounds), each round commits its accepted prefix plus the
   target's token, and the State's position and counters follow.
@@ -105,25 +107,34 @@ def planted_rounds(torch, host, eng, a0, anchor, rounds, p, seed):
     return commits
 
 
-@pytest.mark.parametrize("case", ["c5", "c4"])
+@pytest.mark.parametrize("case", ["c5", "c4", "ref"])
 def test_planted_rounds_full_geometry(dev, case):
+    """c5 / c4: the C4-geometry model; ref: the reference model's geometry (24 layers, 16/4/128, FFN 7680, vocab
+    128000, 3-layer drafter, 3 drafts from position 57344) on the reference's storage formats (int8 K/V records,
+    per-128-column weight scales) at context 131072, which runs the record attention at 4096 pages and the group-scale
+    GEMMs at their widest plans (the 128000-row head through LDS, w2 in bands)."""
     torch = dev
     host = load_host()
     bench = bench_module()
+    desc_ = None
     if case == "c5":
         ctx, block, rates = 131072, 33, (1.0, 0.5, 0.0)
+    elif case == "ref":
+        ctx, block, rates = 131072, 9, (1.0, 0.5, 0.0)
+        desc_ = host.ref_desc(block=9, max_drafts=3)
     else:
         ctx, block, rates = 32768, 16, (0.7,)
     print(f"case planted rounds {case}: ctx {ctx} block {block}", flush=True)
-    desc, eng = bench.engine_setup(host, torch, ctx, block, 20261201 + ctx + block)
+    desc, eng = bench.engine_setup(host, torch, ctx, block, 20261201 + ctx + block, desc_)
     assert eng.max_context > 131072 or case == "c4"
+    nd = eng.desc.max_drafts
     for i, p in enumerate(rates):
         commits = planted_rounds(torch, host, eng, ctx, 17, 4, p, 7 + i)
         print(f"p={p}: commits per round {commits}", flush=True)
         if p == 0.0:
             assert commits == [1] * 4
         if p == 1.0:
-            assert commits == [block] * 4
+            assert commits == [nd + 1] * 4
         if 0 < p < 1:
-            assert any(k < block for k in commits)  # rollback happened
+            assert any(k < nd + 1 for k in commits)  # rollback happened
     eng.close()
