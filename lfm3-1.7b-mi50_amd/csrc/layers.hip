@@ -173,8 +173,9 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   const int t = task / heads, hh = task % heads;
   const bool isq = hh < p.QH;
   if (isq && !p.q16) return;
-  // The State's run flag, position base and token count are loaded by vector loads together with the row (tested
-  // and used once they are all in flight) instead of scalar loads waited for before the row is requested.
+  // Two rounds of loads: first the row, V, the norm weights and the State words (run flag, position base, token count;
+  // vector loads, tested and used once everything is in flight), then the RoPE row and the block-table entry of the
+  // position. (Loaded where they are used, they had formed a chain of five dependent load latencies.)
   const int run = run_flag_load(p.st);
   const int base_v = state_word_load(p.st, p.pos_from_ctx ? (int)offsetof(dspark_state, ctx_pos)
                                                            : (int)offsetof(dspark_state, a));
@@ -183,11 +184,18 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   const float* row = p.mix + (size_t)t * p.row;
   const float* src = isq ? row + (size_t)hh * D : row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)(hh - p.QH) * D;
   const _Float16* nw = isq ? p.q_norm : p.k_norm;
+  const int kvh = hh - p.QH;
+  const float* vsrc = row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)p.KVH * D + (size_t)kvh * D;
   // lane l holds dims l and l + 32 (D = 64) or l, l+32, l+64, l+96 (D = 128): pairs (i, i + D/2) share a lane
   constexpr int MAXE = 4;
   const int ne = D / 32;  // 2 or 4
-  float v[MAXE];
-  for (int e = 0; e < ne; ++e) v[e] = src[(lane & 31) + 32 * e];
+  float v[MAXE], vv[MAXE], wn[MAXE];
+  for (int e = 0; e < ne; ++e) {
+    const int d = (lane & 31) + 32 * e;
+    v[e] = src[d];
+    wn[e] = (float)nw[d];
+    vv[e] = isq ? 0.f : vsrc[d];
+  }
   if (!run_flag_set(run)) {  // a stopped round writes nothing
     __builtin_amdgcn_s_waitcnt(0);
     return;
@@ -195,33 +203,37 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   const int count = __builtin_amdgcn_readfirstlane(count_v);
   if (t >= count) return;
   const int pos = __builtin_amdgcn_readfirstlane(base_v) + t;
+  // RoPE: pair (i, i + half) for i < rot, cos/sin from the table row of `pos` (cos | sin, D halves)
+  const _Float16* rt = p.rope + (size_t)pos * D;
+  float cs[MAXE / 2], sn[MAXE / 2];
+  for (int e = 0; e < ne / 2; ++e) {
+    const int i = (lane & 31) + 32 * e;  // i < half
+    cs[e] = (float)rt[i];
+    sn[e] = (float)rt[half + i];
+  }
+  const int lp = pos / PAGE, slot = pos % PAGE;
+  const int phys = isq ? 0 : (p.bt ? p.bt[lp] : lp);
   float ss = 0.f;
   for (int e = 0; e < ne; ++e) ss += v[e] * v[e];
   // lanes 32..63 duplicate lanes 0..31; sum over the first 32 lanes
   ss = (lane < 32) ? ss : 0.f;
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / D + p.eps);
-  for (int e = 0; e < ne; ++e) v[e] = v[e] * inv * (float)nw[(lane & 31) + 32 * e];
-  // RoPE: pair (i, i + half) for i < rot, cos/sin from the table row of `pos` (cos | sin, D halves)
-  const _Float16* rt = p.rope + (size_t)pos * D;
+  for (int e = 0; e < ne; ++e) v[e] = v[e] * inv * wn[e];
   float r[MAXE];
   for (int e = 0; e < ne; ++e) r[e] = v[e];
   for (int e = 0; e < ne / 2; ++e) {
     const int i = (lane & 31) + 32 * e;  // i < half
     if (i < p.rot) {
-      const float c = (float)rt[i], s = (float)rt[half + i];
+      const float c = cs[e], s = sn[e];
       const float x0 = v[e], x1 = v[e + ne / 2];
       r[e] = x0 * c - x1 * s;
       r[e + ne / 2] = x1 * c + x0 * s;
     }
   }
-  const int kvh = hh - p.QH;
-  const float* vsrc = row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)p.KVH * D + (size_t)kvh * D;
   if (!isq && p.rec) {
     // int8 record of (pos, kvh) (D = 128: lanes 0..31 hold dims l, l + 32, l + 64, l + 96; lanes 32..63 repeat
     // them): quantize_pair of K (normed, rotated, fp32) and of V (fp32), kernels/ops.hip:212-251
-    float vv[MAXE];
-    for (int e = 0; e < ne; ++e) vv[e] = vsrc[(lane & 31) + 32 * e];
     float ak = 0.f, av = 0.f;
     for (int e = 0; e < ne; ++e) {
       ak = fmaxf(ak, fabsf(r[e]));
@@ -230,8 +242,6 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
     ak = wave_max(ak);
     av = wave_max(av);
     if (lane >= 32) return;
-    const int lp = pos / PAGE, slot = pos % PAGE;
-    const int phys = p.bt ? p.bt[lp] : lp;
     uint8_t* rb = p.rec + (size_t)phys * ((size_t)PAGE * p.KVH * 264) + ((size_t)slot * p.KVH + kvh) * 264;
     const float ks = rec_scale(ak), vs = rec_scale(av);
     const float ki = __fdiv_rn(1.f, ks), vi = __fdiv_rn(1.f, vs);
@@ -256,14 +266,12 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
     return;
   }
   // K (normed, rotated) and V (as is) into the pages at `pos`
-  const int lp = pos / PAGE, slot = pos % PAGE;
-  const int phys = p.bt ? p.bt[lp] : lp;
   _Float16* kb = p.kp + ((size_t)phys * p.KVH + kvh) * (PAGE * D);
   _Float16* vb = p.vp + ((size_t)phys * p.KVH + kvh) * (D * PAGE);
   for (int e = 0; e < ne; ++e) {
     const int d = (lane & 31) + 32 * e;
     kb[k_page_elem(slot, d, D)] = (_Float16)r[e];
-    vb[v_page_elem(slot, d)] = (_Float16)vsrc[d];
+    vb[v_page_elem(slot, d)] = (_Float16)vv[e];
   }
 }
 
