@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256) void markov_table_kernel(const int8_t* w1q, co
 // loads in flight, then a workgroup argmax.
 constexpr int CHAIN_THREADS = 1024, CHAIN_ROWS = 16, CHAIN_MAX_N = CHAIN_THREADS * CHAIN_ROWS;
 __global__ __launch_bounds__(1024) void markov_chain_kernel(MarkovParams p) {
-  __shared__ uint64_t red[CHAIN_THREADS / 64];
+  __shared__ uint64_t red[2][CHAIN_THREADS / 64];  // double-buffered by step parity: one barrier per step
   dspark_state* st = p.st;
   if (stopped(st)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -457,21 +457,33 @@ __global__ __launch_bounds__(1024) void markov_chain_kernel(MarkovParams p) {
   int M = st->M;  // nonzero when step 0's confidence test stopped drafting
   uint64_t key = 0;
   if (M == 0 && cap >= 1) key = __hip_atomic_load(p.best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // A step's base row and confidence word do not depend on the previous step's argmax: each is loaded one step ahead
+  // (with the current step's table row), so only the table row's latency lies on the chain.
+  f32x4 bv[CHAIN_ROWS / 4];
+  float bconf = 0.f;
+  auto base_row = [&](int j, f32x4 (&b)[CHAIN_ROWS / 4], float& c) {
+    const float* brow = p.base + (size_t)j * p.stride;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < CHAIN_ROWS / 4; ++i) b[i] = ldg(reinterpret_cast<const f32x4*>(brow + r0) + i);
+    }
+    c = ldg(brow + N);
+  };
+  if (M == 0 && cap >= 2) base_row(1, bv, bconf);
   for (int j = 1; j < cap && M == 0; ++j) {
     const uint32_t ci = 0xffffffffu - (uint32_t)key;
-    const float* brow = p.base + (size_t)j * p.stride;
-    f32x4 tv[CHAIN_ROWS / 4], bv[CHAIN_ROWS / 4];
+    f32x4 tv[CHAIN_ROWS / 4];
     if (live) {
       const f32x4* trow = reinterpret_cast<const f32x4*>(p.table + (size_t)ci * N + r0);
 #pragma unroll
-      for (int i = 0; i < CHAIN_ROWS / 4; ++i) {
-        tv[i] = ldg(trow + i);
-        bv[i] = ldg(reinterpret_cast<const f32x4*>(brow + r0) + i);
-      }
+      for (int i = 0; i < CHAIN_ROWS / 4; ++i) tv[i] = ldg(trow + i);
     }
     const int prev = ldg(p.crop_ids + ci);
     const float s1 = ldg(p.s1c + ci);
-    const float conf = ldg(brow + N) + ldg(p.c2c + ci) + p.conf_bias;
+    const float conf = bconf + ldg(p.c2c + ci) + p.conf_bias;
+    f32x4 bn[CHAIN_ROWS / 4];
+    float bnconf = 0.f;
+    base_row(min(j + 1, cap - 1), bn, bnconf);  // the last step reloads its own row (unused)
     if (!(conf >= p.conf_thr)) {
       if (tid == 0) {
         st->tokens[j] = prev;
@@ -492,13 +504,16 @@ __global__ __launch_bounds__(1024) void markov_chain_kernel(MarkovParams p) {
         }
     }
     best = wave_max_u64(best);
-    if (lane == 0) red[wave] = best;
+    // red[j & 1] was last read in step j - 2, before every thread passed step j - 1's barrier
+    if (lane == 0) red[j & 1][wave] = best;
     __syncthreads();
-    key = red[0];
+    key = red[j & 1][0];
 #pragma unroll
-    for (int w = 1; w < CHAIN_THREADS / 64; ++w) key = red[w] > key ? red[w] : key;
-    __syncthreads();  // red is rewritten by the next step
+    for (int w = 1; w < CHAIN_THREADS / 64; ++w) key = red[j & 1][w] > key ? red[j & 1][w] : key;
     if (tid == 0) p.best[j] = key;
+#pragma unroll
+    for (int i = 0; i < CHAIN_ROWS / 4; ++i) bv[i] = bn[i];
+    bconf = bnconf;
   }
   if (tid != 0) return;
   st->tokens[0] = st->anchor;
