@@ -600,8 +600,9 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
 // times the optional sigmoid gate, stored fp16 and/or fp32. blockIdx = (row, KV head x row group); rows past G M (padding
 // of the last row block, never stored by the split kernels) are skipped. Measured on MI355X, graph-replayed with the
 // partials in HBM: 256 splits at D 128 6.8 us (18.7 with the split-major layout and 32 lanes per output quad, whose
-// every load touched 32 cache lines), 64 splits 3.6 (4.9), C2's 24 splits at D 64 3.4 (3.5); 16 split lanes beyond 96
-// splits, 8 below. Reference combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
+// every load touched 32 cache lines), 64 splits 3.6 (4.9), C2's 24 splits at D 64 2.9 with 4 split lanes, one wave
+// per row (3.6; 3.3 with 8 lanes); 16 split lanes beyond 96 splits, 8 below (4 at D = 64 up to 32 splits). Reference
+// combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
 template <int D, int SL>
 __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) {
   constexpr int Q = D / 4, NT = SL * Q, W = NT / 64, PER = 8;
@@ -944,9 +945,11 @@ int attn_launch(AttnParams& p, int D, int phases, hipStream_t s) {
     if (rc) return rc;
   }
   if (phases & 2) {
-    const bool wide = p.S > 96;  // 16 split lanes per row, else 8
+    const bool wide = p.S > 96;  // 16 split lanes per row, else 8 (4 at D = 64 up to 32 splits: one wave per row)
     const dim3 grid(p.R, p.KVH * p.RG);
-    if (D == 64 && !wide)
+    if (D == 64 && p.S <= 32)
+      hipLaunchKernelGGL((attn_combine_kernel<64, 4>), grid, dim3(4 * 16), 0, s, p);
+    else if (D == 64 && !wide)
       hipLaunchKernelGGL((attn_combine_kernel<64, 8>), grid, dim3(8 * 16), 0, s, p);
     else if (D == 64)
       hipLaunchKernelGGL((attn_combine_kernel<64, 16>), grid, dim3(16 * 16), 0, s, p);
