@@ -412,7 +412,11 @@ void attn_rec_plan(AttnParams& p, int cus) {
   p.R = 16 * nblk;
   p.OCC = 1;
   int S = p.S;
-  if (S <= 0) S = std::min(cus, (p.npages + 1) / 2);  // one workgroup per CU (the LDS ring), two pages or more each
+  // One workgroup per CU (the LDS ring). A split costs ~8 us before its first page and ~1.9 us per page, so up to 96
+  // pages every page gets its own split (the merge keeps its 8-lane form); beyond, two pages or more per split (4096
+  // keys: 129 one-page splits took 16.8 us per layer with the merge, 65 two-page splits 16.2; 1024 keys 12.9 against
+  // 14.8; reference-geometry rounds 1.448 -> 1.428 ms at 1k).
+  if (S <= 0) S = p.npages <= 96 ? p.npages : std::min(cus, (p.npages + 1) / 2);
   S = std::max(S, (p.npages + REC_BT_MAX - 1) / REC_BT_MAX);
   S = std::max(1, std::min(S, std::min(ATTN_REC_MAX_SPLITS, p.npages)));
   p.pps = (p.npages + S - 1) / S;
