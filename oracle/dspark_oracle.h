@@ -19,6 +19,10 @@
  *   int8 K/V records ........ quantize_pair closed forms (half-away ties, clamp, the 1e-6 floor, exact multiples),
  *                             round-trip bound |x - q s| <= s/2, byte layout; Q group quantization vs numpy rint;
  *                             fp64 attention of dequantized operands vs orc_verify_attention on fp16-valued input
+ *   per-128-column GEMM ..... numpy fp64 sum over groups; equal group scales reduce to the per-row GEMM; one group's
+ *                             scales zeroed removes exactly its product (tests/test_oracle_g128.py)
+ *   weights.Pack restated ... packed then reconstructed within half a code step per weight of the fp16 matrix product;
+ *                             scale slots against the packer's index rule (tests/test_oracle_g128.py)
  *   target/drafter layers ... composed of the pinned pieces above + numpy restatements of RMS norm, RoPE,
  *                             short conv (tests/test_oracle.py::test_rms_norm_rope_conv)
  */
