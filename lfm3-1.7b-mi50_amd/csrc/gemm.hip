@@ -877,6 +877,17 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
     const int bc = chunks / bands;
     // ranges of at most 8 chunks: one batch per wave (row-major X with one token block: four ranges)
     KW = xop || tb > 1 ? std::min(8, std::max(4, (bc + 7) / 8)) : 4;
+    if (tb > 1 && !gs) {
+      // X^T of 2-4 token blocks staged per workgroup outweighs one strip's weights: two strips per workgroup when
+      // that still leaves 128 or more workgroups, else shorter ranges (33 tokens: 6144 x 2048 21.1 -> 11.4 us,
+      // 3104 x 2048 11.3 -> 10.1 us)
+      if (strips >= 256 && bands == 1) {
+        S = 2;
+        KW = 4;
+      } else {
+        KW = std::max(KW, std::min(8, bc / 4));
+      }
+    }
   } else {
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
