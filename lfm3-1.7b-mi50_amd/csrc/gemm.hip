@@ -509,14 +509,18 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     const size_t xcs = p.xop ? (size_t)p.xop * 1024 : 64, xhs = p.xop ? 512 : 8;  // halves per chunk, per half
     // One batch: its X and weight loads, then its products. The first batch is outside the loop: at a loop head the
     // compiler's wait for the previous iteration's loads would also hold the first batch back behind the flag load.
+    // Token block tb of chunk c (operand order, TB > 1 needs it): the next 1 KB block pair, tb * 1024 halves on.
     auto batch = [&](int cb) {
-      u32x4 xb[CPW][2];
+      u32x4 xb[CPW][TB][2];
       u32x2 gsr[GS ? CPW / 2 : 1];
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = min(cb + i, c1 - 1);
-        xb[i][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs));
-        xb[i][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + xhs));
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          xb[i][tb][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024));
+          xb[i][tb][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024 + xhs));
+        }
       }
       if constexpr (GS) gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
       load(w, cb);
@@ -524,8 +528,8 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
         gscale_products<CPW>(acc[0], gsr, cb, c1, [&](int i, f32x4 t) {
           half8 a[2];
           weights(w[i], a);
-          t = mfma16x16x32(a[0], as_half8(xb[i][0]), t);
-          return mfma16x16x32(a[1], as_half8(xb[i][1]), t);
+          t = mfma16x16x32(a[0], as_half8(xb[i][0][0]), t);
+          return mfma16x16x32(a[1], as_half8(xb[i][0][1]), t);
         });
       } else {
 #pragma unroll
@@ -533,8 +537,11 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
           if (cb + i < c1) {
             half8 a[2];
             weights(w[i], a);
-            acc[0] = mfma16x16x32(a[0], as_half8(xb[i][0]), acc[0]);
-            acc[0] = mfma16x16x32(a[1], as_half8(xb[i][1]), acc[0]);
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+              acc[tb] = mfma16x16x32(a[0], as_half8(xb[i][tb][0]), acc[tb]);
+              acc[tb] = mfma16x16x32(a[1], as_half8(xb[i][tb][1]), acc[tb]);
+            }
           }
         }
       }
@@ -753,7 +760,11 @@ static void launch_gemm_tb(const GemmParams& p, dim3 grid, dim3 block, size_t ld
 }
 
 // K-sliced launches where every wave loads its own range of X (the plan's choice; int8, one token block).
-static bool gemm_sliced_xd(const GemmParams& p, bool i8) { return i8 && p.xd && p.M <= 16; }
+// X loaded per wave straight into B operands: one token block (row-major or operand-order X), or 2-4 token blocks in
+// operand order within 8 waves
+static bool gemm_sliced_xd(const GemmParams& p, bool i8) {
+  return i8 && p.xd && (p.M <= 16 || (p.xop && p.M <= 64 && p.wpg * p.kw <= 8 && !p.gscale));
+}
 
 // LDS of a K-sliced launch: X^T (unless each wave loads its own), the range sums, the fused epilogue's tile.
 static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
@@ -788,6 +799,12 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
         allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true>, lds);
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true>), grid, block, lds, s, p);
       }
+      return;
+    }
+  }
+  if constexpr (I8 && TB > 1) {
+    if (gemm_sliced_xd(p, I8)) {  // X per wave for 2-4 token blocks (operand order): 4-chunk batches, <= 8 waves
+      hipLaunchKernelGGL((gemm_sliced_kernel<TB, I8, 4, true, 512>), grid, block, lds, s, p);
       return;
     }
   }
@@ -867,6 +884,7 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
   const int strips = N / 16, chunks = K / 64;
   if ((!DSPARK_GEMM_SLICED && !gs) || tb > 4) return false;
   int S, KW, bands = 1;
+  bool xdm = false;  // X per wave for 2-4 token blocks (operand-order X)
   if (wpg_req > 0) {
     S = wpg_req;
     KW = 16 / S;
@@ -878,21 +896,27 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
     // ranges of at most 8 chunks: one batch per wave (row-major X with one token block: four ranges)
     KW = xop || tb > 1 ? std::min(8, std::max(4, (bc + 7) / 8)) : 4;
     if (tb > 1 && !gs) {
-      // X^T of 2-4 token blocks staged per workgroup outweighs one strip's weights: two strips per workgroup when
-      // that still leaves 128 or more workgroups, else shorter ranges (33 tokens: 6144 x 2048 21.1 -> 11.4 us,
-      // 3104 x 2048 11.3 -> 10.1 us)
+      // 2-4 token blocks: two strips per workgroup when that still leaves 128 or more workgroups, else shorter
+      // ranges; with operand-order X every wave loads its own X (33 tokens: 6144 x 2048 21.1 us with one strip and X^T
+      // staged in LDS -> 11.4 with two strips -> 9.8 with X per wave; 3104 x 2048 11.3 -> 7.3; 2048 x 8192 in two
+      // bands 16.7 -> 11.1; 2048 x 2048 in two bands 7.3 -> 5.5)
       if (strips >= 256 && bands == 1) {
         S = 2;
         KW = 4;
       } else {
         KW = std::max(KW, std::min(8, bc / 4));
       }
+      xdm = xop;
     }
   } else {
     S = std::min(16, std::max(4, (strips + 255) / 256));
     KW = std::max(1, 16 / S);
+    if (tb >= 3 && xop && !gs && S == 4) {  // 33 tokens, 16384 x 2048: 16.4 -> 15.2 us (17 tokens: staged X^T is better)
+      KW = 2;
+      xdm = true;
+    }
   }
-  bool xd = i8 && tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S));
+  bool xd = i8 && ((tb == 1 && (S == 1 || (xop && S <= DSPARK_GEMM_XD_MAX_S))) || xdm);
   if (gs) {
     // group scales: every band and range starts on an even chunk (whole 128-column groups); X^T of a band through LDS
     // only when it fits at once, else one strip per workgroup with X per wave
