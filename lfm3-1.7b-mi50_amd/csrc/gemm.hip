@@ -900,7 +900,7 @@ static bool gemm_plan_sliced(int N, int K, int tb, bool i8, int wpg_req, bool xo
       // ranges; with operand-order X every wave loads its own X (33 tokens: 6144 x 2048 21.1 us with one strip and X^T
       // staged in LDS -> 11.4 with two strips -> 9.8 with X per wave; 3104 x 2048 11.3 -> 7.3; 2048 x 8192 in two
       // bands 16.7 -> 11.1; 2048 x 2048 in two bands 7.3 -> 5.5)
-      if (strips >= 256 && bands == 1) {
+      if (strips > 256 && bands == 1) {  // (256 strips: one per workgroup, 4096 x 2048 7.5 us against 9.5 with two)
         S = 2;
         KW = 4;
       } else {
