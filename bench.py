@@ -542,7 +542,8 @@ def bench_engine(args, host, torch, workload):
     elif workload == "c5":
         cases = [(131072, 33, 0.0), (131072, 33, 0.5), (131072, 33, 1.0)]
     else:  # tiers / ref: the reference's verify block (MT = 9) at the MI50's measured committed tokens per round
-        cases = [(c, 9, ("tau", MI50_TAU[c])) for c in (1024, 32768, 131072)]
+        tiers = [int(c) for c in args.tiers.split(",")] if getattr(args, "tiers", "") else (1024, 32768, 131072)
+        cases = [(c, 9, ("tau", MI50_TAU[c])) for c in tiers]
     rounds, warm = args.steps, args.warmup
     cache = {}
     for ctx, block, plant in cases:
@@ -629,6 +630,8 @@ def main():
     ap.add_argument("--ref-formats", default="reference", choices=["reference", "fp16"],
                     help="ref workload: the reference's storage formats (int8 K/V records, per-128-column weight "
                          "scales) or fp16 K/V pages with per-row scales")
+    ap.add_argument("--tiers", default="", help="tiers / ref workloads: comma-separated contexts out of 1024, 32768, "
+                                                  "131072 (default all three)")
     ap.add_argument("--ctx", type=int, default=131072, help="attn workload: context (keys before the block)")
     ap.add_argument("--tokens", type=int, default=0, help="attn / rec workload: verify tokens (default 33 / 9)")
     ap.add_argument("--layers", type=int, default=2, help="attn workload: layers per step")
