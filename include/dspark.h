@@ -57,8 +57,9 @@ typedef struct dspark_state {
 
 /* ---------------------------------------------------------------- verify attention
  * One layer's verify attention for M tokens at positions a..a+M-1 whose K/V are already in the pages (dspark_kv_write):
- * token t sees key position kpos iff kpos >= start, kpos <= (causal ? a + t : a + M - 1) and, for window > 0,
- * kpos > a + t - window. GQA: query head qh reads KV head qh / (QH / KVH). Output o = softmax(q k^T / sqrt(D)) v,
+ * token t sees a context key kpos < a iff kpos >= start and, for window > 0, kpos > a + t - window, and the block's
+ * key a + j iff j <= t (causal) or j < M (not causal): start and window bound the context keys only
+ * (dspark.hip:1308-1312, 2006-2012). GQA: query head qh reads KV head qh / (QH / KVH). Output o = softmax(q k^T / sqrt(D)) v,
  * optionally times sigmoid(gate[t][qh]), stored as fp16 (out) and/or fp32 (out_f32).
  * Replaces verify_attention_paged / attention_v2 / attention_v3 / attention_pass + combine_phase
  * (dspark.hip:1070-1412, 1488-2130, 2132-2185; dispatch 2519-2556). */

@@ -120,10 +120,10 @@ __device__ __forceinline__ void page_prep(const AttnParams& p, int lpage, int ro
   if (base < p.full_lo || base + PAGE - 1 > p.full_hi) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      // Visible keys of the lane's row (token t = row / G; padding rows act as the last token): the window bounds the
-      // context keys only (dspark.hip:1308-1312, 2006-2012), the block's own keys are visible up to t whatever it is.
+      // Visible keys of the lane's row (token t = row / G; padding rows act as the last token): start and the window
+      // bound the context keys only (dspark.hip:1308-1312, 2006-2012), the block's own keys are visible up to t.
       const int t = min((row0 + 16 * qb + (lane & 15)) / p.G, p.M - 1);
-      const int lo = max(p.start, p.window > 0 ? min(p.a, p.a + t - p.window + 1) : 0);
+      const int lo = min(p.a, max(p.start, p.window > 0 ? p.a + t - p.window + 1 : 0));
       const int hi = p.causal ? p.a + t : p.a + p.M - 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -813,7 +813,7 @@ static bool lds_shape(int D, int nblk, int* qb, int* nrg, int* pl, int* ppl, int
 void attn_plan(AttnParams& p, int D, int cus) {
   const int rows = p.G * p.M;
   const int nblk = (rows + 15) / 16;
-  const int lo0 = std::max(p.start, p.window > 0 ? p.a - p.window + 1 : 0);
+  const int lo0 = std::min(p.a, std::max(p.start, p.window > 0 ? p.a - p.window + 1 : 0));  // the block's keys from a
   const int lo_last = std::max(p.start, p.window > 0 ? p.a + p.M - 1 - p.window + 1 : 0);
   const int hi_last = p.a + p.M - 1;
   p.full_lo = lo_last;

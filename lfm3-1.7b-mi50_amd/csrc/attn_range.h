@@ -18,7 +18,7 @@ __device__ inline void attn_range(AttnParams& p) {
   } else if (p.window > 0) {
     p.start = max(0, a - p.window + 1);
   }
-  const int lo0 = max(p.start, p.window > 0 ? a - p.window + 1 : 0);
+  const int lo0 = min(a, max(p.start, p.window > 0 ? a - p.window + 1 : 0));  // the block's keys from a
   const int lo_last = max(p.start, p.window > 0 ? a + p.M - p.window : 0);
   const int hi_last = a + p.M - 1;
   p.full_lo = lo_last;

@@ -294,8 +294,8 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         const int t = min(((rg * QB + qb) * 16 + n) / p.G, p.M - 1);
-        // the window bounds the context keys only (dspark.hip:1308-1312, 2006-2012)
-        const int lo = max(p.start, p.window > 0 ? min(p.a, p.a + t - p.window + 1) : 0);
+        // start and the window bound the context keys only (dspark.hip:1308-1312, 2006-2012)
+        const int lo = min(p.a, max(p.start, p.window > 0 ? p.a + t - p.window + 1 : 0));
         const int hi = p.causal ? p.a + t : p.a + p.M - 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
 void attn_rec_plan(AttnParams& p, int cus) {
   const int rows = p.G * p.M;
   const int nblk = (rows + 15) / 16;
-  const int lo0 = std::max(p.start, p.window > 0 ? p.a - p.window + 1 : 0);
+  const int lo0 = std::min(p.a, std::max(p.start, p.window > 0 ? p.a - p.window + 1 : 0));  // the block's keys from a
   const int lo_last = std::max(p.start, p.window > 0 ? p.a + p.M - 1 - p.window + 1 : 0);
   const int hi_last = p.a + p.M - 1;
   p.full_lo = lo_last;

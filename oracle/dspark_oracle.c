@@ -114,8 +114,7 @@ void orc_gen_uniform_u32(uint64_t seed, int64_t n, uint32_t bound, uint32_t* out
  * context keys need start <= kpos < a and (window == 0 || kpos > qpos - window); fresh keys j < M need
  * j <= t when causal (target layers) and nothing else (drafter block keys, causal = false). */
 static int key_valid(int kpos, int t, int M, int a, int start, int window, int causal) {
-  if (kpos < start) return 0;
-  if (kpos < a) return window == 0 || kpos > a + t - window;
+  if (kpos < a) return kpos >= start && (window == 0 || kpos > a + t - window);
   const int j = kpos - a;
   if (j >= M) return 0;
   return causal ? j <= t : 1;

@@ -82,6 +82,8 @@ def run_case(torch, orc, host, M, QH, KVH, D, a, start=0, window=0, causal=True,
     (64, 16, 4, 64, 300, 0, 0, True, True),       # the same with 4 KV heads, permuted block table
     (64, 16, 4, 64, 300, 261, 40, True, False),   # sliding window shorter than the block (later rows see block keys only)
     (33, 32, 8, 64, 2048, 2017, 32, True, False), # the same at 33 tokens, window of one page
+    (16, 32, 8, 64, 300, 305, 0, True, False),    # start inside the block: it bounds context keys only
+    (9, 16, 4, 128, 300, 304, 0, False, True),    # the same, bidirectional, permuted block table
     (33, 16, 4, 128, 1700, 0, 0, True, True),     # reference geometry, 9 row blocks: one page per step, Q apart
     (24, 16, 4, 128, 900, 0, 0, True, False),     # reference geometry, 6 row blocks
 ])

@@ -164,7 +164,9 @@ def test_transpose_lanes_kat(orc):
 
 # ---------------------------------------------------------------- verify attention
 def _np_attention(q, k, v, a, start, window, causal):
-    """Independent numpy fp64 statement: full softmax with an explicit mask matrix."""
+    """Independent numpy fp64 statement: full softmax with an explicit mask matrix. Context keys (kpos < a) need
+    kpos >= start and the window, block keys j = kpos - a only j <= t (causal) or j < M: start and window bound the
+    context keys alone (dspark.hip:1311-1312, 2006-2012)."""
     qf = q.view(np.float16).astype(np.float64)
     kf = k.view(np.float16).astype(np.float64)
     vf = v.view(np.float16).astype(np.float64)
@@ -175,8 +177,8 @@ def _np_attention(q, k, v, a, start, window, causal):
     out = np.zeros((M, QH, D))
     kpos = np.arange(T)
     for t in range(M):
-        valid = kpos >= start
         ctx = kpos < a
+        valid = ~ctx | (kpos >= start)
         if window:
             valid &= ~ctx | (kpos > a + t - window)
         j = kpos - a
@@ -199,6 +201,9 @@ def _np_attention(q, k, v, a, start, window, causal):
     (9, 16, 4, 128, 50, 10, 0, False),     # drafter: ring range, bidirectional block
     (1, 8, 8, 64, 0, 0, 0, True),          # empty cache: the token attends only to itself
     (16, 32, 8, 64, 33, 0, 0, True),
+    (9, 16, 4, 128, 50, 53, 0, True),      # start inside the block: no context keys, the block's keys all kept
+    (9, 16, 4, 128, 50, 56, 0, False),     # the same, bidirectional
+    (16, 16, 4, 64, 100, 90, 8, True),     # window shorter than the block: later rows see block keys only
 ])
 def test_attention_matches_numpy(orc, M, QH, KVH, D, a, start, window, causal):
     q = orc.normal_f16(11, (M, QH, D))
