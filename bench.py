@@ -227,10 +227,11 @@ def bench_attention(args, host, torch, L, ctx, M, sets, steps=None, warmup=None,
 
 def rec_attention_fields(args, host, torch):
     """Verify attention over the reference's int8 K/V records (reference geometry 16/4/128, its 9-token block) at 32k
-    and 128k keys: 2 layers, 2 rotating record sets."""
+    and 128k keys: 2 layers; 8 rotating record sets at 32k (16 x 34.6 MB) and 2 at 128k (4 x 138 MB), so a layer's
+    records come back after more than the 256 MB Infinity Cache has been read."""
     out = []
-    for ctx in (32768, 131072):
-        r = bench_attention(args, host, torch, 2, ctx, 9, 2, steps=max(4, args.steps // 2), warmup=2, rec=True)
+    for ctx, sets in ((32768, 8), (131072, 2)):
+        r = bench_attention(args, host, torch, 2, ctx, 9, sets, steps=max(8, args.steps // 2), warmup=2, rec=True)
         out.append({"ctx": ctx, "verify_tokens": 9, "record_bytes_per_layer": r["layer_bytes"],
                     "ms_per_layer": round(r["ms_per_step"] / 2, 5), "step_GBs": round(r["step_gbs"], 1),
                     "step_frac": round(r["step_gbs"] / HBM_PEAK_GBS, 4),
@@ -297,10 +298,10 @@ MI50_TAU = {1024: 3.47, 32768: 3.30, 131072: 2.27}         # benchmarks/verify_a
 
 def bench_c3(args, host, torch):
     """int8-weight FFN 2048 -> 8192 (SiLU) -> 2048 for M = 16 tokens with one fp16 scale per output
-    row, then the 2048 x 16384 fp16 cropped-head projection with its row argmax. Three weight sets rotate (3 x 100.7 MB
+    row, then the 2048 x 16384 fp16 cropped-head projection with its row argmax. Four weight sets rotate (a set returns after 3 x 100.7 MB
     > the 256 MB Infinity Cache)."""
     M, H, I, N = 16, 2048, 8192, 16384
-    SETS = 3
+    SETS = 4
     dev = "cuda"
     stream = torch.cuda.current_stream()
     g = torch.Generator(device=dev)
@@ -361,7 +362,7 @@ def bench_c3(args, host, torch):
         "metric": "C3 int8 FFN + crop head: weight GB/s and MFMA utilisation", "value": round(gbs, 1), "unit": "GB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t_step, 5),
         "higher_is_better": True, "dtype": "int8 weights, fp16 MFMA, fp32 accumulation",
-        "data": "synthetic: int8 uniform [-127, 127] weights, fp16 N(0,1) activations, 3 rotating weight sets",
+        "data": "synthetic: int8 uniform [-127, 127] weights, fp16 N(0,1) activations, 4 rotating weight sets",
         "config": {"workload": "C3 (BASELINE configs[2]): M=16, FFN 2048->8192 (SiLU epilogue)->2048 int8 with per-row "
                                "fp16 scales, then 2048x16384 fp16 crop head + row argmax",
                    "algorithmic_bytes_per_step": total_bytes, "flops_per_step": flops_ffn + flops_crop},
@@ -521,6 +522,79 @@ def plant_drafts(eng, chain, a0, p, seed, vocab):
     eng.upload("plant", buf)
 
 
+def conv_snapshot(eng):
+    import numpy as np
+    return {nm: eng.download(nm, np.uint16) for nm in eng.names() if nm.startswith("conv.L")}
+
+
+def conv_restore(eng, rings):
+    for nm, buf in rings.items():
+        eng.upload(nm, buf)
+
+
+def planted_pass(eng, torch, a0, anchor, n_rounds, rings0):
+    """Untimed: n_rounds planted rounds from a0 (conv rings as at a0); returns the tokens they emitted."""
+    import numpy as np
+    conv_restore(eng, rings0)
+    engine_state(eng, a0, anchor)
+    for _ in range(n_rounds):
+        eng.round(-1, a0)
+    torch.cuda.synchronize()
+    return eng.download("out_tokens", np.int32)[:eng.state().count].copy()
+
+
+def settle_chain(eng, host, torch, desc, a0, anchor, need, p, n_rounds, rings0, tries=6):
+    """The greedy chain the planted drafts replay, checked against what planted rounds actually emit.
+
+    Planted rounds emit the target's own greedy continuation under their own arithmetic (accepted drafts equal the
+    target's tokens, the bonus is the target's token). The chain comes from one-token rounds, and where a verify pass
+    of M rows resolves a near tie differently (the attention's key splits follow a and M, so the fp32 sums differ in
+    order), the emitted tokens leave the chain at some index and every later planted draft is wrong. So: plant, run
+    the pass, and where it left the chain take its tokens, extend them by one-token rounds from where the pass
+    stopped, plant again; until a pass emits the chain itself. The timed rounds repeat the last pass exactly (every
+    reduction has a fixed order), so their acceptance follows the planted draws. Returns (chain, re-plants)."""
+    import numpy as np
+    chain = greedy_chain(eng, host, torch, a0, anchor, need)
+    fixes = 0
+    for _ in range(tries):
+        plant_drafts(eng, chain, a0, p, 7, desc.vocab)
+        out = planted_pass(eng, torch, a0, anchor, n_rounds, rings0)
+        n = len(out)
+        if np.array_equal(out, chain[:n]):
+            break
+        fixes += 1
+        ext = greedy_chain(eng, host, torch, a0 + n, int(out[-1]), max(1, need - n))
+        chain = np.concatenate([out, ext]).astype(np.int32)
+    conv_restore(eng, rings0)
+    return chain, fixes
+
+
+def run_launches(eng, torch, a0, anchor, rings0, n_warm, n_timed):
+    """The drop-in path: draftLaunch's loop (internal/model/generate.go:133-162) over dspark_engine_launch, each launch
+    from the State the last one left to the next 32-position boundary (32 rounds at most), planted drafts. Host wall
+    clock around the timed launches (each launch returns when its State is back on the host)."""
+    conv_restore(eng, rings0)
+    torch.cuda.synchronize()
+    kw = dict(a=a0, anchor=anchor, ctx_new=1, ctx_pos=a0 - 1, miss=0, skip=0)
+    lo = max(0, a0 - 2048)
+    tok = rounds = enq = 0
+    t0 = None
+    for i in range(n_warm + n_timed):
+        if i == n_warm:
+            t0 = time.perf_counter()
+        _, res = eng.launch(kw["a"], kw["anchor"], budget=512, rounds=32, ctx_new=kw["ctx_new"],
+                            ctx_pos=kw["ctx_pos"], ctx_lo=lo, force_m=-1, miss=kw["miss"], skip=kw["skip"])
+        st = res.state
+        kw = dict(a=st.a, anchor=st.anchor, ctx_new=st.ctx_new, ctx_pos=st.ctx_pos, miss=st.miss, skip=st.skip)
+        if i >= n_warm:
+            tok += res.count
+            rounds += res.rounds
+            enq += res.rounds_enqueued
+    wall = time.perf_counter() - t0
+    return {"launches": n_timed, "rounds": rounds, "rounds_enqueued": enq, "tokens": tok,
+            "ms_per_round": wall * 1e3 / rounds, "tokens_per_round": tok / rounds, "tok_s": tok / wall}
+
+
 def p_for_tau(tau, drafts):
     """Per-position planting probability whose expected committed tokens per round is tau (truncated geometric)."""
     lo, hi = 0.0, 1.0
@@ -566,13 +640,23 @@ def bench_engine(args, host, torch, workload):
             rec["accepted_histogram"] = dict(sorted(collections.Counter(accs).items()))
         else:
             p = plant if not isinstance(plant, tuple) else p_for_tau(plant[1], desc.max_drafts)
-            need = (warm + rounds + 1) * block + 2
-            chain = greedy_chain(eng, host, torch, a0, anchor, need)
-            plant_drafts(eng, chain, a0, p, 7, desc.vocab)
+            n_launch = (1, 4) if isinstance(plant, tuple) else (0, 0)  # the tiers also time the drop-in launch path
+            need = max((warm + rounds + 1) * block + 2, (sum(n_launch) + 1) * 32 + 2 * block)
+            rings0 = conv_snapshot(eng)
+            chain, fixes = settle_chain(eng, host, torch, desc, a0, anchor, need, p, warm + rounds, rings0)
             ms, committed, accs, st = run_rounds(eng, torch, -1, a0, anchor, warm, rounds)
             rec["planted_p"] = round(p, 4)
             rec["planted_tau_expected"] = round(1 + sum(p ** k for k in range(1, desc.max_drafts + 1)), 3)
             rec["max_drafts"] = desc.max_drafts
+            rec["replants"] = fixes
+            if n_launch[1]:
+                lr = run_launches(eng, torch, a0, anchor, rings0, *n_launch)
+                rec["launch"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in lr.items()}
+                rec["launch_tok_s"] = round(lr["tok_s"], 1)
+                # the drop-in path against the round rate: time per round (launch boundaries, host round trips and
+                # the rounds a launch enqueues included) and tok/s at the same committed tokens per round
+                rec["launch_round_time_ratio"] = round(ms / lr["ms_per_round"], 4)
+                rec["launch_tok_s_at_mi50_tau"] = round(plant[1] / (lr["ms_per_round"] * 1e-3), 1)
         rec["phase_us"] = phase_times(eng, host, torch, 0 if plant is None else -1, a0, anchor)
         rec.update({"ms_per_round": round(ms, 4), "tokens_per_round": round(committed, 3),
                     "tok_s": round(committed / (ms * 1e-3), 1)})
@@ -682,10 +766,14 @@ def main():
                      "weights; 4-layer drafter), random-init, block 9 (the reference's verify block)",
             "rounds": targs.steps, "warmup": targs.warmup,
             "tiers": [{k: c[k] for k in ("ctx", "ms_per_round", "tokens_per_round", "tok_s", "tok_s_at_mi50_tau",
-                                         "mi50_tok_s", "vs_mi50", "planted_tau_expected")} for c in tiers["cases"]],
+                                         "mi50_tok_s", "vs_mi50", "planted_tau_expected", "replants", "launch_tok_s",
+                                         "launch_tok_s_at_mi50_tau", "launch_round_time_ratio", "launch")}
+                      for c in tiers["cases"]],
             "note": "tok_s_at_mi50_tau = the MI50's measured committed tokens per round (benchmarks/"
                     "verify_attention.txt:54-58) / this round time; a round verifies the same tokens whatever is "
-                    "accepted, so its time does not depend on the draws; tok_s is the rate of the planted draws"}
+                    "accepted, so its time does not depend on the draws; tok_s is the rate of the planted draws; "
+                    "launch_* time the drop-in path (dspark_engine_launch, draftLaunch's loop: one launch per "
+                    "32-position block, State read back by the host after each) on the same planted chain"}
         # The same tiers on the reference model's geometry, draft policy and storage formats (int8 K/V records,
         # per-128-column weight scales): the configuration the MI50 numbers were measured on.
         rargs = argparse.Namespace(**vars(targs))
@@ -694,7 +782,9 @@ def main():
         res["headline_ref_tok_s"] = {
             "model": rtiers["metric"], "rounds": targs.steps, "warmup": targs.warmup,
             "tiers": [{k: c[k] for k in ("ctx", "max_drafts", "ms_per_round", "tokens_per_round", "tok_s",
-                                         "tok_s_at_mi50_tau", "mi50_tok_s", "vs_mi50", "planted_tau_expected")}
+                                         "tok_s_at_mi50_tau", "mi50_tok_s", "vs_mi50", "planted_tau_expected",
+                                         "replants", "launch_tok_s", "launch_tok_s_at_mi50_tau",
+                                         "launch_round_time_ratio", "launch")}
                       for c in rtiers["cases"]]}
         res["c5_attention"] = c5_attention_fields(args, host, torch)
         res["ref_int8_record_attention"] = rec_attention_fields(args, host, torch)

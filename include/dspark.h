@@ -185,14 +185,17 @@ size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K); /* counters + 
  * y[t][r] = sum_g gscale[g][r] * sum_{k in group g} x[t][k] * q[r][k], groups of 128 columns, gscale fp16 [K/128][N]
  * (group-major: dspark_g128_scales converts the packer's [row][quarter][i] layout), weights biased int8 [N][K] as
  * above, fp16 x. M <= 16 (the reference verifies 9 tokens), K % 128 == 0; same epilogues; no workspace. Each
- * 128-column group's products are scaled in fp32 by the group's scale and added in group order. The reference's build
- * also quantizes x to int8 per 16 columns (LFM3_X8, dspark.hip:25-27, 802-823); x stays fp16 here, as in the
- * reference's LFM3_F16 build. Replaces gemv_phase / unit_dot_r over packed weights (dspark.hip:541-716). */
+ * 128-column group's products are scaled in fp32 by the group's scale and added in group order. x stays fp16 here,
+ * as in the reference's LFM3_F16 build; the reference's default build (LFM3_X8, dspark.hip:24-26, 802-823, which
+ * kernels/build.sh uses) quantizes x to int8 per 16 columns first. Replaces gemv_phase / unit_dot_r over packed
+ * weights (dspark.hip:541-716). */
 int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* gscale, int32_t N,
                         int32_t epilogue, float* y_f32, void* y_f16, dspark_stream_t stream);
 /* Host helper: the packer's scale rows ([N][SRow] fp16, SRow = 16 for K = 2048 and 64 otherwise, entry (quarter, i) =
  * group 4 i + quarter at quarter * SRow / 4 + i; quant.go:13-29, 66-104) -> gscale [K/128][N]. No device memory. */
 int dspark_g128_scales(const uint16_t* packed, int32_t N, int32_t K, uint16_t* out);
+/* K must be a multiple of 512: weights.Pack stores group g's scale only while g / 4 < K / 512 (quant.go:96-99), so
+ * another K leaves trailing groups with no stored scale (DSPARK_EINVAL). */
 
 /* ---------------------------------------------------------------- cropped head + row argmax
  * y[t][r] = sum_k x[t][k] * W[r][k] (fp16 W [N][K], fp16 x [M][K], fp32 accumulation), and best_keys[t] = max key(y, r)
@@ -286,8 +289,9 @@ const char* dspark_engine_tensor_name(dspark_engine* e, int32_t i);
  * reads its own packed weights directly (dspark.go:635-659) and takes the Markov dots at every step (markov_phase,
  * dspark.hip:2322-2366). */
 int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream);
-/* Enqueue one round on `stream`. force_m > 0 skips the drafter and verifies tokens[0..force_m) of the State as they
- * are (the reference's force_m debug mode, dspark.hip:147, 2442-2451). force_m = -1 runs the drafter, then replaces
+/* Enqueue one round on `stream`. The verify pass is 1 + max_drafts rows wide (at least force_m). force_m > 0 skips
+ * the drafter and verifies tokens[0..force_m) of the State as they are (the reference's force_m debug mode,
+ * dspark.hip:147, 2442-2451). force_m = -1 runs the drafter, then replaces
  * its drafts by the engine tensor "plant" (int32 by position: draft j of a round at anchor position a is plant[a + j])
  * -- benchmarks of a set acceptance rate on random-init models; this mode has no counterpart in the reference. The first call for a (force_m, plan) records
  * the round as a HIP graph; later calls replay it. `plan_a` is the position the attention plan is tuned for (any
@@ -320,6 +324,15 @@ int dspark_engine_conv_copy(dspark_engine* e, int32_t src, int32_t dst, dspark_s
  * a, anchor, limit, budget, eos, stop_at, ctx_*, miss, skip, ckpt_slot are set from the arguments as
  * internal/model/dspark.go:543-566 does: stop_at = min(next multiple of 32 after a, max_context), limit =
  * min(stop_at + block, max_context)), then copy the State and the emitted tokens back. Synchronous on `stream`.
+ * Rounds run until the State stops (run == 0, dspark.hip:2438-2440) or `rounds` have run: the host keeps on the
+ * stream only rounds that the books of the last finished round prove necessary (each round mirrors its books into
+ * host memory, which the calling thread polls while later rounds run, as the reference's host spins on its mailbox),
+ * so a launch enqueues no round that would find run == 0 (an eos can leave the rounds already in flight idle).
+ * Each round verifies 1 + the launch's draft cap tokens (the reference verifies 1 + drafts, dspark.hip:2657): a
+ * 3-draft launch verifies 4. The first `skip` rounds are skip rounds (dspark.hip:2441-2451): the context projection,
+ * then the anchor alone verified without drafting, State.skip decremented; skip_after stays 0 (draftLaunch never
+ * sets it), so no round starts skipping again. After the launch, rounds outside a launch (dspark_engine_round) use
+ * the model's max_drafts and the penalty of the last dspark_engine_init_seen again.
  * With conv_slot >= 0 the launch first loads the conv history of positions a - (conv_kernel - 1) .. a - 1 from that
  * conv-state slot into the engine's position ring, and at its end writes the running state (the history before the
  * final a) back to the slot and, when ckpt_slot >= 0 and the launch reached stop_at, the history before stop_at to
@@ -348,6 +361,7 @@ typedef struct dspark_launch_result {
   int32_t boundary;        /* the block boundary the launch ran to */
   int32_t ckpt_written;    /* 1: the launch reached the boundary and ckpt_slot holds the conv state there */
   dspark_state state;      /* State after the launch (ctx_new, ctx_pos, miss, skip carry to the next launch) */
+  int32_t rounds_enqueued; /* rounds the launch put on the stream (equals rounds unless an eos stopped it early) */
 } dspark_launch_result;
 
 int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* args, int32_t* out_tokens, int32_t max_out,

@@ -875,7 +875,8 @@ void attn_plan(AttnParams& p, int D, int cus) {
   finish(S);
 }
 
-// Workspace: partial accumulators [KVH][RG][S][R][D] f32, then (max, sum) pairs [KVH][RG][S][R].
+// Workspace: partial accumulators [KVH][RG][R][S][D] f32 (row-major: one row's splits contiguous), then (max, sum)
+// pairs [KVH][RG][R][S].
 static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 size_t attn_workspace_bytes(const AttnParams& p, int D) {

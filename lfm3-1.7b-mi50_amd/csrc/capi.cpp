@@ -14,7 +14,7 @@ using namespace dspark;
 
 namespace {
 
-constexpr int ABI_VERSION = 3;
+constexpr int ABI_VERSION = 4;
 
 // Compute units of the current device (queried once per device; 256 on MI355X).
 int device_cus() {
@@ -65,7 +65,6 @@ bool attn_args_ok(const dspark_attn_args* a) {
   if (a->KVH < 1 || a->QH < a->KVH || a->QH % a->KVH != 0) return false;
   if (a->M < 1 || a->M > DSPARK_MT_MAX) return false;
   if (a->a < 0 || a->start < 0 || a->window < 0) return false;
-  if (a->start > a->a + a->M - 1) return false;
   if (a->splits < 0) return false;
   if (a->kv_pages < 1 || a->kv_pages * a->KVH * DSPARK_PAGE_TOKENS * a->D * 2 >= (int64_t)1 << 31) return false;
   if (!a->block_table && a->kv_pages < (a->a + a->M + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS) return false;
@@ -211,7 +210,7 @@ static bool rec_args_ok(const dspark_attn_args* a) {
   if (!a->out && !a->out_f32) return false;
   if (a->D != 128 || a->KVH != 4 || a->QH < a->KVH || a->QH % a->KVH != 0) return false;
   if (a->M < 1 || a->M > DSPARK_MT_MAX || (int64_t)a->QH / a->KVH * a->M > 4 * 16) return false;
-  if (a->a < 0 || a->start < 0 || a->window < 0 || a->start > a->a + a->M - 1) return false;
+  if (a->a < 0 || a->start < 0 || a->window < 0) return false;
   if (a->splits < 0) return false;
   if (a->kv_pages < 1 || a->kv_pages * DSPARK_PAGE_TOKENS * a->KVH * DSPARK_REC_BYTES >= (int64_t)1 << 31) return false;
   if (!a->block_table && a->kv_pages < (a->a + a->M + DSPARK_PAGE_TOKENS - 1) / DSPARK_PAGE_TOKENS) return false;
@@ -366,7 +365,9 @@ int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, c
 }
 
 int dspark_g128_scales(const uint16_t* packed, int32_t N, int32_t K, uint16_t* out) {
-  if (!packed || !out || N < 1 || K < 128 || K % 128) return DSPARK_EINVAL;
+  // weights.Pack stores group g's scale only while g / 4 < groups / 4 (quant.go:96-99): K % 512 != 0 leaves trailing
+  // groups without a stored scale, so such a K has no packed layout to convert
+  if (!packed || !out || N < 1 || K < 512 || K % 512) return DSPARK_EINVAL;
   const int groups = K / 128, srow = (K / 512 == 4) ? 16 : 64, sq = srow / 4;
   if ((groups + 3) / 4 > sq) return DSPARK_EINVAL;  // more groups than the packed row holds
   for (int r = 0; r < N; ++r)

@@ -238,7 +238,11 @@ int verify_argmax_chunks(int V);
 int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip_now, int32_t* out_tokens, int out_cap,
                          uint32_t* seen, hipStream_t s);
 // The verify argmax's partial keys folded into best[M] (as fold_keys would), then accept + commit of State->M tokens.
+// skip_now: the round is a skip round (State.skip is decremented instead of the miss count kept). mirror (optional):
+// host memory that receives the State's run, a, count, rounds_left, skip, miss, accepted, verified after the books
+// (words 1-8) between two copies of rounds_done (word 15 first, word 0 last).
 int accept_commit_fold_launch(dspark_state* st, const uint64_t* part, int nchunks, int M, uint64_t* best,
-                              int32_t* out_tokens, int out_cap, uint32_t* seen, hipStream_t s);
+                              int32_t* out_tokens, int out_cap, uint32_t* seen, int skip_now, int32_t* mirror,
+                              hipStream_t s);
 
 }  // namespace dspark

@@ -13,6 +13,7 @@
 //   commit     acceptance + books; K/V of the accepted positions are already in the pages          (2848-2913)
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -124,8 +125,13 @@ struct dspark_engine {
   int cus = 256;
   dspark_state host_st;  // launch-time uploads stay alive until the stream has consumed them
   float host_lp[4] = {1.f, 1.f, 0.f, 0.f};
-  // recorded rounds: key (force_m, plan bucket) -> graph
-  std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  float seen_rep = 1.f;  // the penalty of the last dspark_engine_init_seen (what rounds outside a launch use)
+  float host_lp_idle[4] = {1.f, 1.f, 0.f, 0.f};  // the values restored at the end of a launch
+  // host memory the commit kernel mirrors the State's books into after every round (accept_commit_fold_launch), read
+  // by the launch loop while later rounds run
+  int32_t* mirror = nullptr;
+  // recorded rounds: key (force_m, tracing, verify width, skip, plan bucket) -> graph
+  std::map<std::vector<int>, hipGraphExec_t> graphs;
   // phase tracing: marks [2 + 2 DSPARK_TRACE_MAX_MARKS] u64 (count, round | active, then (phase, clock) pairs)
   uint64_t* trace = nullptr;
   bool trace_on = false;
@@ -134,6 +140,7 @@ struct dspark_engine {
   ~dspark_engine() {
     for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
     for (void* p : allocs) (void)hipFree(p);
+    if (mirror) (void)hipHostFree(mirror);
   }
 
   void* alloc(const std::string& name, size_t bytes, int* err) {
@@ -257,15 +264,15 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   return gemm_launch(p, true, st);
 }
 
-// Residual + RMS norm of the B block rows.
-int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, const _Float16* post_w,
+// Residual + RMS norm of M block rows (the bands of v are [M][H] each, as the GEMM of M rows wrote them).
+int resnorm(dspark_engine* e, int M, const float* h_old, const float* v, int bands, const _Float16* post_w,
             const _Float16* norm_w, int sandwich, float* dst, float* tap, hipStream_t s) {
   ResNormParams p = {};
   p.st = e->ast;
   p.h_old = h_old;
   p.v = v;
   p.bands = bands;
-  p.v_band_stride = (size_t)e->B * e->d.hidden;
+  p.v_band_stride = (size_t)M * e->d.hidden;
   p.post_w = post_w;
   p.norm_w = norm_w;
   p.sandwich = sandwich;
@@ -276,10 +283,10 @@ int resnorm(dspark_engine* e, const float* h_old, const float* v, int bands, con
   p.x_row = e->d.hidden;
   p.H = e->d.hidden;
   p.xop = e->tbs;
-  return resnorm_launch(p, e->B, 1, s);
+  return resnorm_launch(p, M, 1, s);
 }
 
-int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const float* gate, hipStream_t s) {
+int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const float* gate, int M, hipStream_t s) {
   const dspark_model_desc& d = e->d;
   AttnParams p = {};
   p.st = e->ast;
@@ -293,7 +300,7 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   p.out16 = e->y16;
   p.out_op = e->tbs;
   p.gate = gate;
-  p.M = e->B;
+  p.M = M;
   p.QH = d.q_heads;
   p.KVH = d.kv_heads;
   p.G = d.q_heads / d.kv_heads;
@@ -317,13 +324,14 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   return Lw.kv_rec ? attn_rec_launch(p, 3, s) : attn_launch(p, d.head_dim, 3, s);
 }
 
-QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode) {
+QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int row, bool with_q, bool ctx_mode,
+                       int M) {
   const dspark_model_desc& d = e->d;
   QkRopeParams p = {};
   p.st = e->ast;
   p.mix = mix;
   p.row = row;
-  p.M = e->B;
+  p.M = M;
   p.QH = d.q_heads;
   p.KVH = d.kv_heads;
   p.D = d.head_dim;
@@ -348,19 +356,19 @@ QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int
 // The attention mix GEMM, then the q/k norm + RoPE + K/V page write (qkrope). A fused epilogue needs one head per
 // workgroup: 49 workgroups for the C4 mix (10.6 us against 5.1 + 4.7 unfused) and 25 for the reference geometry's
 // 128-dim heads (14.5 us), so the two kernels are faster (measured on MI355X).
-int gemm_mix_qk(dspark_engine* e, const LayerW& W, hipStream_t s) {
-  int rc = gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s);
-  return rc ? rc : qkrope_launch(qk_params(e, W, e->mix, W.mix_rows, true, false), s);
+int gemm_mix_qk(dspark_engine* e, const LayerW& W, int M, hipStream_t s) {
+  int rc = gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s);
+  return rc ? rc : qkrope_launch(qk_params(e, W, e->mix, W.mix_rows, true, false, M), s);
 }
 
 // The conv mix GEMM with the gated short conv fused into its epilogue (16 channels per group); output y16.
-int gemm_mix_conv(dspark_engine* e, const LayerW& W, hipStream_t s) {
+int gemm_mix_conv(dspark_engine* e, const LayerW& W, int M, hipStream_t s) {
   GemmParams f = {};
   f.fuse = GEMM_FUSE_CONV;
   f.conv_w = W.conv_w;
   f.conv_ring = W.conv_ring;
   f.conv_k = e->d.conv_kernel;
-  return gemm(e, e->x16, e->B, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
+  return gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
 }
 
 // Output bands the round's norm kernels add (the w2, out and fc GEMMs may split K over that many workgroups).
@@ -387,23 +395,25 @@ int enqueue_context(dspark_engine* e, const _Float16* x_fc, bool x_op, hipStream
   const int B = e->B, H = d.hidden;
   int nb = ENGINE_BANDS;
   CK(gemm(e, x_fc, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s, nullptr, &nb, x_op));
-  CK(resnorm(e, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
+  CK(resnorm(e, B, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
   const int kvrow = 2 * d.kv_heads * d.head_dim;
   CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
   for (int j0 = 0; j0 < d.draft_layers; j0 += QKROPE_BATCH) {  // one launch for up to 8 drafter layers
     QkRopeBatch b = {};
     b.n = std::min(QKROPE_BATCH, d.draft_layers - j0);
     for (int j = 0; j < b.n; ++j)
-      b.l[j] = qk_params(e, e->DL[j0 + j], e->ckvout + (size_t)(j0 + j) * kvrow, d.draft_layers * kvrow, false, true);
+      b.l[j] = qk_params(e, e->DL[j0 + j], e->ckvout + (size_t)(j0 + j) * kvrow, d.draft_layers * kvrow, false, true, B);
     CK(qkrope_batch_launch(b, s));
   }
   return 0;
 }
 
-// The round's launch sequence (see the file header).
-int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
+// The round's launch sequence (see the file header). mv: verify width, the token rows of the verify pass (the
+// round's drafts are capped below it, so 1 + drafts <= mv; the drafter block stays B wide). skip: a skip round
+// (dspark.hip:2441-2451): the context projection, then the anchor alone verified (no drafter), State.skip decremented.
+int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, hipStream_t s) {
   const dspark_model_desc& d = e->d;
-  const int B = e->B, H = d.hidden;
+  const int B = e->B, H = d.hidden, MV = mv;
   uint64_t* vbest = e->keys;
   uint64_t* mbest = e->keys + B;
   e->ast = e->st;
@@ -430,25 +440,29 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     }
     CK(enqueue_context(e, e->x16, true, s));
     CK(mark(e, DSPARK_TRACE_CONTEXT, s));
+  }
+  if (skip) {
+    CK(force_m_launch(e->st, 1, s));
+  } else if (force_m <= 0) {
     // ---- drafter block
     CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
     int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
     for (int j = 0; j < d.draft_layers; ++j) {
       const LayerW& W = e->DL[j];
-      CK(resnorm(e, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
+      CK(resnorm(e, B, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
-      CK(gemm_mix_qk(e, W, s));
-      CK(attention(e, W, 1, plan_a, nullptr, s));
+      CK(gemm_mix_qk(e, W, B, s));
+      CK(attention(e, W, 1, plan_a, nullptr, B, s));
       int ob = ENGINE_BANDS;
       CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
-      CK(resnorm(e, e->h[cur], e->vout, ob, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
+      CK(resnorm(e, B, e->h[cur], e->vout, ob, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
       w2b = ENGINE_BANDS;
       CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
     }
     CK(mark(e, DSPARK_TRACE_DRAFTER, s));
-    CK(resnorm(e, e->h[cur], e->w2out, w2b, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
+    CK(resnorm(e, B, e->h[cur], e->w2out, w2b, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
     CK(gemm(e, e->x16, B, H, e->crop_w, e->crop_s, e->crop_n, 0, e->base, nullptr, s));
     CK(mark(e, DSPARK_TRACE_CROP_HEAD, s));
     MarkovParams mp = {};
@@ -476,41 +490,41 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, hipStream_t s) {
     if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, reinterpret_cast<const int32_t*>(e->rep + 2), s));
     CK(mark(e, DSPARK_TRACE_MARKOV, s));
   }
-  // ---- verify
-  CK(embed_launch(e->embed, e->st, 0, 0, B, H, d.vocab, e->h[0], s));
+  // ---- verify (MV rows; rows past the State's M are computed and never committed)
+  CK(embed_launch(e->embed, e->st, 0, 0, MV, H, d.vocab, e->h[0], s));
   int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
   for (int i = 0; i < d.n_layers; ++i) {
     const LayerW& W = e->L[i];
     const LayerW* P = i ? &e->L[i - 1] : nullptr;
     float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
-    CK(resnorm(e, e->h[cur], i ? e->w2out : nullptr, w2b, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
+    CK(resnorm(e, MV, e->h[cur], i ? e->w2out : nullptr, w2b, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
                e->h[cur ^ 1], tap, s));
     cur ^= 1;
     if (W.kind == 0) {
-      CK(gemm_mix_conv(e, W, s));
+      CK(gemm_mix_conv(e, W, MV, s));
     } else {
-      CK(gemm_mix_qk(e, W, s));
-      CK(attention(e, W, 0, plan_a, e->gate, s));
+      CK(gemm_mix_qk(e, W, MV, s));
+      CK(attention(e, W, 0, plan_a, e->gate, MV, s));
     }
     int ob = ENGINE_BANDS;
-    CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
-    CK(resnorm(e, e->h[cur], e->vout, ob, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
+    CK(gemm(e, e->y16, MV, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
+    CK(resnorm(e, MV, e->h[cur], e->vout, ob, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
     cur ^= 1;
-    CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
+    CK(gemm(e, e->x16, MV, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
     w2b = ENGINE_BANDS;
-    CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
+    CK(gemm(e, e->a16, MV, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
     CK(mark(e, DSPARK_TRACE_VERIFY_LAYER + i, s));
   }
   {
     const LayerW& P = e->L[d.n_layers - 1];
     float* tap = P.tap_slot >= 0 ? e->taps + (size_t)P.tap_slot * B * H : nullptr;
-    CK(resnorm(e, e->h[cur], e->w2out, w2b, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
+    CK(resnorm(e, MV, e->h[cur], e->w2out, w2b, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
   }
-  CK(gemm(e, e->x16, B, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
+  CK(gemm(e, e->x16, MV, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
   CK(mark(e, DSPARK_TRACE_LM_HEAD, s));
-  CK(verify_argmax_launch(e->logits, 0, B, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep, false));
-  CK(accept_commit_fold_launch(e->st, static_cast<const uint64_t*>(e->ws_argmax), verify_argmax_chunks(d.vocab), B, vbest,
-                               e->out_tokens, e->max_context + 2 * B, e->seen, s));
+  CK(verify_argmax_launch(e->logits, 0, MV, d.vocab, e->seen, e->st, 1.f, 1.f, vbest, e->ws_argmax, s, e->rep, false));
+  CK(accept_commit_fold_launch(e->st, static_cast<const uint64_t*>(e->ws_argmax), verify_argmax_chunks(d.vocab), MV,
+                               vbest, e->out_tokens, e->max_context + 2 * B, e->seen, skip ? 1 : 0, e->mirror, s));
   CK(mark(e, DSPARK_TRACE_COMMIT, s));
   return 0;
 }
@@ -721,6 +735,11 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->out_tokens = static_cast<int32_t*>(e->alloc("out_tokens", (size_t)(max_context + 2 * B) * 4, &err));
   e->plant = static_cast<int32_t*>(e->alloc("plant", (size_t)(positions + B + 1) * 4, &err));
   e->rep = static_cast<float*>(e->alloc("rep", 16, &err));
+  if (!err && hipHostMalloc((void**)&e->mirror, 16 * sizeof(int32_t), hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
+    e->mirror = nullptr;
+    err = DSPARK_ENOSPACE;
+  }
+  if (e->mirror) std::memset(e->mirror, 0, 16 * sizeof(int32_t));
   e->trace = static_cast<uint64_t*>(e->alloc("trace", (size_t)(2 + 2 * DSPARK_TRACE_MAX_MARKS) * 8, &err));
   e->x_cols = std::max(std::max(H, d.n_taps * H), std::max(d.ffn, d.draft_ffn));
   e->mix_cols = std::max(std::max(3 * H, align16(QH * D + 2 * KVH * D + QH)), ckv_rows);
@@ -746,9 +765,11 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   const int Ks[] = {H, d.n_taps * H, d.ffn, d.draft_ffn};
   const int Ns[] = {H,        3 * H,    2 * d.ffn, 2 * d.draft_ffn, d.vocab, e->crop_n, ckv_rows,
                     align16(QH * D + 2 * KVH * D + QH), QH * D + 2 * KVH * D};
-  for (int K : Ks)
-    for (int N : Ns)
-      for (int wpg_req : {0, 3}) gws = std::max(gws, gemm_ws_bytes(B, N, K, wpg_req, true));
+  // every verify width 1 .. B (a round's verify pass is sized to its draft cap)
+  for (int m = 1; m <= B; ++m)
+    for (int K : Ks)
+      for (int N : Ns)
+        for (int wpg_req : {0, 3}) gws = std::max(gws, gemm_ws_bytes(m, N, K, wpg_req, true));
   gws = std::max(gws, gemm_ws_bytes(B, H, d.n_taps * H, 0, false));  // the prompt projection's fc (row-major taps)
   e->ws_gemm_bytes = gws + 256;
   e->ws_gemm = e->alloc("ws_gemm", e->ws_gemm_bytes, &err);
@@ -900,30 +921,27 @@ int prepare(dspark_engine* e, hipStream_t s, bool all) {
 }
 }  // namespace
 
-int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream) {
-  if (!e) return DSPARK_EINVAL;
-  return prepare(e, reinterpret_cast<hipStream_t>(stream), true);
-}
-
-int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream) {
-  if (!e || force_m < -1 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+namespace {
+// One round at verify width mv (skip: a skip round), recorded as a HIP graph the first time its key is met, then
+// replayed on s.
+int round_enqueue(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, hipStream_t s) {
+  if (mv < 1 || mv > e->B || (force_m > 0 && !skip && mv < force_m)) return DSPARK_EINVAL;
   if (e->mtab_dirty || e->tiles_dirty) {
     const int rc = prepare(e, s, false);
     if (rc) return rc;
   }
   const int bucket = plan_a / ROUND_PLAN_BUCKET;
-  const auto key = std::make_pair((int)force_m + (e->trace_on ? 1000 : 0), bucket);
+  const std::vector<int> key = {force_m, e->trace_on ? 1 : 0, mv, skip ? 1 : 0, bucket};
   auto it = e->graphs.find(key);
   if (it == e->graphs.end()) {
-    // Record the round on a private stream (capture needs a non-default stream), then replay it on `stream`.
+    // Record the round on a private stream (capture needs a non-default stream), then replay it on `s`.
     hipStream_t cap;
     if (hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return DSPARK_ENOSPACE;
     hipGraph_t g = nullptr;
     int rc = (int)hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal);
     if (!rc) {
       const int plan = bucket * ROUND_PLAN_BUCKET + ROUND_PLAN_BUCKET / 2;
-      rc = enqueue_round(e, force_m, plan, cap);
+      rc = enqueue_round(e, force_m, plan, mv, skip, cap);
       const int rc2 = (int)hipStreamEndCapture(cap, &g);
       if (!rc) rc = rc2;
     }
@@ -936,6 +954,19 @@ int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspar
   }
   return (int)hipGraphLaunch(it->second, s);
 }
+}  // namespace
+
+int dspark_engine_prepare(dspark_engine* e, dspark_stream_t stream) {
+  if (!e) return DSPARK_EINVAL;
+  return prepare(e, reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int dspark_engine_round(dspark_engine* e, int32_t force_m, int32_t plan_a, dspark_stream_t stream) {
+  if (!e || force_m < -1 || force_m > e->B || plan_a < 0) return DSPARK_EINVAL;
+  // outside a launch the device's draft cap is the model's: drafts <= max_drafts, so 1 + max_drafts verify rows
+  const int mv = std::max(force_m, 1 + e->d.max_drafts);
+  return round_enqueue(e, force_m, plan_a, mv, false, reinterpret_cast<hipStream_t>(stream));
+}
 
 int dspark_engine_init_seen(dspark_engine* e, const int32_t* tokens, int32_t n, float rep, dspark_stream_t stream) {
   if (!e || n < 0 || (n > 0 && !tokens)) return DSPARK_EINVAL;
@@ -947,6 +978,7 @@ int dspark_engine_init_seen(dspark_engine* e, const int32_t* tokens, int32_t n, 
     if (t >= 0 && t < V) e->host_seen[t >> 5] |= 1u << (t & 31);
   }
   if (rep == 0.f) rep = 1.f;
+  e->seen_rep = rep;
   e->host_lp[0] = rep;
   e->host_lp[1] = 1.f / rep;
   if (hipMemcpyAsync(e->seen, e->host_seen.data(), e->host_seen.size() * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
@@ -1041,7 +1073,7 @@ int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t*
   if (a->conv_slot < -1 || a->conv_slot >= e->conv.slots || a->ckpt_slot < -1 || a->ckpt_slot >= e->conv.slots)
     return DSPARK_EINVAL;
   if (a->ckpt_slot >= 0 && a->conv_slot < 0) return DSPARK_EINVAL;  // a checkpoint needs the conv state's slots
-  if (a->ctx_new < 0 || a->ctx_new > e->B || a->ctx_lo < 0) return DSPARK_EINVAL;
+  if (a->ctx_new < 0 || a->ctx_new > e->B || a->ctx_lo < 0 || a->skip < 0) return DSPARK_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int block_tokens = 32;  // the prefix cache's block (internal/model/engine.go:30)
   const int stop = std::min((a->a / block_tokens + 1) * block_tokens, e->max_context);
@@ -1076,8 +1108,78 @@ int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t*
     return DSPARK_EINVAL;
   int rc = 0;
   if (a->conv_slot >= 0) rc = conv_load_launch(e->conv, e->st, a->conv_slot, s);
-  for (int r = 0; r < a->rounds && !rc; ++r) rc = dspark_engine_round(e, a->force_m, a->a, stream);
+  // Rounds until the State stops (dspark.hip:2438-2440), without enqueueing rounds that would find run == 0: the host
+  // keeps in flight only rounds the last round it has seen proves necessary (each commits at most mv tokens, a skip
+  // round exactly one), reading the books each round mirrors into host memory while the next rounds run.
+  // Verify width: the launch's draft cap (the reference verifies 1 + drafts, dspark.hip:2657); skip rounds verify the
+  // anchor alone (dspark.hip:2441-2444); force_m rounds verify force_m tokens.
+  const int mv = a->force_m > 0 ? std::max(a->force_m, 1 + md) : 1 + md;
+  const int m_max = a->force_m > 0 ? a->force_m : mv;
+  const int skip0 = a->skip;  // skip rounds come first (State.skip_after is 0: no round sets skip again)
+  // rounds enqueued before this call (dspark_engine_round) mirror their own books: let them finish first
+  if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = DSPARK_EINVAL;
+  volatile int32_t* mir = e->mirror;
+  for (int i = 0; i < 16; ++i) mir[i] = -1;
+  int done = 0, enq = 0;  // rounds completed (seen in the mirror) and enqueued
+  int cur_a = st.a, cur_count = 0, cur_run = 1;
+  auto needed = [&]() {  // rounds the books of the last round seen prove necessary from there
+    if (!cur_run) return 0;
+    int left = std::max(1, std::min(stop - cur_a, st.budget - cur_count));
+    int need = 0;
+    const int sk = std::max(0, skip0 - done);  // skip rounds still ahead commit one token each
+    const int k1 = std::min(sk, left);
+    need += k1;
+    left -= k1;
+    if (left > 0) need += (left + m_max - 1) / m_max;
+    return std::min(need, a->rounds - done);
+  };
+  while (!rc) {
+    const int need = needed();
+    while (!rc && enq - done < need) {
+      rc = round_enqueue(e, a->force_m, a->a, enq < skip0 ? 1 : mv, enq < skip0, s);
+      ++enq;
+    }
+    if (rc || enq == done) break;  // nothing in flight: the State has stopped (or every round has run)
+    // Wait for the next round's books in the mirror. The stream going idle without them means the rounds in flight
+    // stopped without a commit (round_begin's bounds check, a full output buffer): the launch is over.
+    const int want = done + 1;  // the State starts with rounds_done = 0
+    bool got = false, idle = false;
+    for (long spin = 0;; ++spin) {
+      const int end = mir[0];
+      if (end >= want) {
+        std::atomic_thread_fence(std::memory_order_acquire);
+        const int run = mir[1], a_now = mir[2], count = mir[3];
+        std::atomic_thread_fence(std::memory_order_acquire);
+        if (mir[15] == end) {  // one round's values (the next commit had not begun rewriting them)
+          done = end;
+          cur_run = run;
+          cur_a = a_now;
+          cur_count = count;
+          got = true;
+          break;
+        }
+        continue;
+      }
+      if (idle) break;  // the mirror was read once more after the stream went idle
+      if ((spin & 1023) == 1023) {
+        const hipError_t q = hipStreamQuery(s);
+        if (q == hipSuccess) {
+          idle = true;
+        } else if (q != hipErrorNotReady) {
+          rc = (int)q;
+          break;
+        }
+      }
+    }
+    if (!got) break;
+  }
   if (!rc && a->conv_slot >= 0) rc = conv_store_launch(e->conv, e->st, a->conv_slot, s);
+  // rounds outside a launch use the model's draft cap and the request's penalty again
+  e->host_lp_idle[0] = e->seen_rep;
+  e->host_lp_idle[1] = 1.f / e->seen_rep;
+  std::memcpy(&e->host_lp_idle[2], &e->d.max_drafts, 4);
+  if (hipMemcpyAsync(e->rep, e->host_lp_idle, sizeof(e->host_lp_idle), hipMemcpyHostToDevice, s) != hipSuccess && !rc)
+    rc = DSPARK_EINVAL;
   if (rc) {
     (void)hipStreamSynchronize(s);  // the host copies above stay in use until the stream has consumed them
     return rc;
@@ -1098,6 +1200,7 @@ int dspark_engine_launch(dspark_engine* e, const dspark_launch_args* a, int32_t*
   res->verified = res->state.verified;
   res->boundary = stop;
   res->ckpt_written = (a->ckpt_slot >= 0 && res->state.a >= stop) ? 1 : 0;
+  res->rounds_enqueued = enq;
   return 0;
 }
 

@@ -130,9 +130,13 @@ __device__ __forceinline__ int key_token(uint64_t k) { return (int)(0xffffffffu 
 
 // part (optional): the verify argmax's partial keys [mfold][nchunks], folded here into best[t] first (every thread
 // loads its share at once; u64 max in LDS, order-free) instead of by a separate fold_keys launch.
+// mirror (optional): host memory the launch loop polls; after the books, words 1.. get the State's run, a, count,
+// rounds_left, skip, miss, accepted, verified, and words 0 (last, release) and 15 (first) the State's rounds_done, so
+// a reader that finds word 15 == word 0 has read one round's values (system-scope stores: visible to the host).
 __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uint64_t* best, int m, int skip_now,
                                                            int32_t* out_tokens, int out_cap, uint32_t* seen,
-                                                           const uint64_t* part, int nchunks, int mfold) {
+                                                           const uint64_t* part, int nchunks, int mfold,
+                                                           int32_t* mirror) {
   if (st->run == 0) return;
   if (part) {
     __shared__ unsigned long long sb[64];
@@ -201,6 +205,15 @@ __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uin
   st->rounds_done += 1;
   st->rounds_left -= 1;
   st->run = (!stop && st->rounds_left > 0 && st->a < st->stop_at && count < st->budget) ? 1 : 0;
+  if (mirror) {
+    const int seq = st->rounds_done;
+    const int words[8] = {st->run, st->a, st->count, st->rounds_left, st->skip, st->miss, st->accepted, st->verified};
+    __hip_atomic_store(mirror + 15, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __atomic_thread_fence(__ATOMIC_RELEASE);  // word 15 before the values
+#pragma unroll
+    for (int i = 0; i < 8; ++i) __hip_atomic_store(mirror + 1 + i, words[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(mirror, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 size_t verify_argmax_ws(int M, int V) {
@@ -234,17 +247,18 @@ int accept_commit_launch(dspark_state* st, const uint64_t* best, int m, int skip
                          uint32_t* seen, hipStream_t s) {
   // best is only read when no partial keys are given
   hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, const_cast<uint64_t*>(best), m, skip_now,
-                     out_tokens, out_cap, seen, (const uint64_t*)nullptr, 0, 0);
+                     out_tokens, out_cap, seen, (const uint64_t*)nullptr, 0, 0, (int32_t*)nullptr);
   return (int)hipGetLastError();
 }
 
 int verify_argmax_chunks(int V) { return (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
 
 int accept_commit_fold_launch(dspark_state* st, const uint64_t* part, int nchunks, int M, uint64_t* best,
-                              int32_t* out_tokens, int out_cap, uint32_t* seen, hipStream_t s) {
+                              int32_t* out_tokens, int out_cap, uint32_t* seen, int skip_now, int32_t* mirror,
+                              hipStream_t s) {
   if (M < 1 || M > 64 || nchunks < 1) return DSPARK_EINVAL;
-  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, 0, 0, out_tokens, out_cap, seen, part,
-                     nchunks, M);
+  hipLaunchKernelGGL(accept_commit_kernel, dim3(1), dim3(64), 0, s, st, best, 0, skip_now, out_tokens, out_cap, seen,
+                     part, nchunks, M, mirror);
   return (int)hipGetLastError();
 }
 

@@ -85,7 +85,7 @@ _SIGS = {
 }
 
 
-ABI_VERSION = 3  # dspark_abi_version() of the library these signatures describe
+ABI_VERSION = 4  # dspark_abi_version() of the library these signatures describe
 
 
 def lib():
@@ -427,7 +427,7 @@ class LaunchArgs(ctypes.Structure):
 class LaunchResult(ctypes.Structure):
     _fields_ = [("count", ctypes.c_int32), ("rounds", ctypes.c_int32), ("accepted", ctypes.c_int32),
                 ("verified", ctypes.c_int32), ("boundary", ctypes.c_int32), ("ckpt_written", ctypes.c_int32),
-                ("state", State)]
+                ("state", State), ("rounds_enqueued", ctypes.c_int32)]
 
 
 _SIGS.update({

@@ -258,13 +258,15 @@ def markov(W, st, base):
 
 
 def verify(W, C, st, tokens, rope, rope_swa=None):
-    """Logits [B][V] (fp64) of the verify pass over the B block tokens; updates K/V caches, conv rings and taps.
-    Sliding layers (kind 2) rotate with rope_swa and d.rope_pairs_swa when the description gives them their own table
-    (rope_base_swa > 0; internal/model/engine.go:333-338), else with `rope` and d.rope_pairs."""
+    """Logits [m][V] (fp64) of the verify pass over the first m = min(len(tokens), block) tokens (the reference
+    verifies m = 1 + drafts, dspark.hip:2657); updates K/V caches, conv rings and taps. Sliding layers (kind 2)
+    rotate with rope_swa and d.rope_pairs_swa when the description gives them their own table (rope_base_swa > 0;
+    internal/model/engine.go:333-338), else with `rope` and d.rope_pairs."""
     d = W.d
     H, B, QH, KVH, D, I = d.hidden, d.block, d.q_heads, d.kv_heads, d.head_dim, d.ffn
     emb = W.f16("embed", (d.vocab, H))
     toks = [t if 0 <= t < d.vocab else 0 for t in tokens[:B]]
+    B = len(toks)
     h = emb[toks]
     a = st["a"]
     v_prev = None

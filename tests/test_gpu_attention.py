@@ -84,6 +84,8 @@ def run_case(torch, orc, host, M, QH, KVH, D, a, start=0, window=0, causal=True,
     (33, 32, 8, 64, 2048, 2017, 32, True, False), # the same at 33 tokens, window of one page
     (16, 32, 8, 64, 300, 305, 0, True, False),    # start inside the block: it bounds context keys only
     (9, 16, 4, 128, 300, 304, 0, False, True),    # the same, bidirectional, permuted block table
+    (16, 32, 8, 64, 300, 900, 0, True, False),    # start past the block's last position: no context key, block keys kept
+    (9, 16, 4, 128, 300, 5000, 0, False, True),   # the same, bidirectional, permuted block table
     (33, 16, 4, 128, 1700, 0, 0, True, True),     # reference geometry, 9 row blocks: one page per step, Q apart
     (24, 16, 4, 128, 900, 0, 0, True, False),     # reference geometry, 6 row blocks
 ])

@@ -109,6 +109,8 @@ def run_case(torch, orc, host, M, a, start=0, window=0, causal=True, paged=False
     (16, 1000, 993, 8, True, False),    # sliding window shorter than the block: later rows see block keys only
     (9, 1000, 1004, 0, True, False),    # start inside the block: it bounds context keys only
     (9, 1000, 1003, 0, False, True),    # the same, bidirectional, paged
+    (9, 1000, 4000, 0, True, False),    # start past the block's last position: no context key, block keys kept
+    (16, 300, 1200, 0, False, True),    # the same, bidirectional, paged
 ])
 def test_verify_attention_rec_matches_oracle(dev, orc, M, a, start, window, causal, paged):
     run_case(dev, orc, load_host(), M, a, start, window, causal, paged)

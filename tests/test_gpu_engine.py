@@ -47,9 +47,10 @@ MID = dict(hidden=1024, ffn=4096, vocab=4096, n_layers=4, layer_kind=[0, 1, 0, 2
            ring_positions=256, mask_token=4095, conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
 # MID with 24- and 33-token blocks: two token blocks (K-sliced GEMMs with X^T in LDS, the fused conv epilogue over two
 # token blocks), three token blocks (K split across workgroups, the last split running the fused conv epilogue).
-MID24 = dict(MID, block=24, max_drafts=12)
-MID33 = dict(MID, block=33, max_drafts=16)
-MID64 = dict(MID, block=64, max_drafts=32)  # four token blocks: the GEMMs' X per wave for 4 blocks, 16 attention row blocks
+# (max_drafts = block - 1: a round verifies 1 + max_drafts rows, so the verify pass is the whole block)
+MID24 = dict(MID, block=24, max_drafts=23)
+MID33 = dict(MID, block=33, max_drafts=32)
+MID64 = dict(MID, block=64, max_drafts=63)  # four token blocks: the GEMMs' X per wave for 4 blocks, 16 attention row blocks
 # The reference's storage formats: int8 K/V records (quantize_pair, 264 bytes per position and KV head) for the target's
 # attention layers and the drafter ring, and int8 weights with per-128-column group scales (weights.Pack), in the
 # reference's attention geometry 16/4/128 (hidden 2048) with small FFNs.
@@ -216,10 +217,11 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
     eng.round(0, a)
     torch.cuda.synchronize()
     B, V, N = desc.block, desc.vocab, desc.crop_rows
+    MV = min(B, 1 + desc.max_drafts)  # the verify pass's rows (drafts never exceed max_drafts)
     st = eng.state()
     base_gpu = eng.download("base", np.float32)[:B * ((N + 1 + 15) // 16 * 16)].reshape(B, -1)
-    logits_gpu = eng.download("logits", np.float32, (B, V))
-    keys_gpu = eng.download("keys", np.uint64, (2 * B,))[:B]
+    logits_gpu = eng.download("logits", np.float32)[:MV * V].reshape(MV, V)
+    keys_gpu = eng.download("keys", np.uint64, (2 * B,))[:MV]
     # RoPE tables: the oracle uses its own (engine.go:428-461 restated in numpy); the engine's must be the same bits
     D = desc.head_dim
     rope_u16 = eng.download("rope", np.uint16).reshape(-1, D)
@@ -285,18 +287,18 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
         assert M == st.M and toks == gpu_toks
 
     # verify over the tokens the GPU verified
-    verified = gpu_toks + list(st.tokens)[st.M:B]  # positions past M hold what the State held (verified, unused)
-    logits = rnd.verify(W, C, dict(st0, tokens=verified), verified[:B], rope, rope_swa)
+    verified = gpu_toks + list(st.tokens)[st.M:MV]  # positions past M hold what the State held (verified, unused)
+    logits = rnd.verify(W, C, dict(st0, tokens=verified), verified[:MV], rope, rope_swa)
     lscale = np.max(np.abs(logits))
     lerr = np.max(np.abs(logits_gpu - logits))
     print(f"logits max-abs {lerr:.3e} (scale {lscale:.2f})", flush=True)
     assert lerr <= rel * lscale
     # argmax keys on the GPU's logits are bit-exact with the oracle's key rule
     seen = eng.download("seen", np.uint32)
-    want_keys = orc.verify_argmax(logits_gpu.astype(np.float32), seen, np.array(verified[:B], np.int32))
+    want_keys = orc.verify_argmax(logits_gpu.astype(np.float32), seen, np.array(verified[:MV], np.int32))
     assert np.array_equal(keys_gpu, want_keys)
     # and agree with the oracle's own logits up to near ties
-    ok = orc.keys_to_tokens(orc.verify_argmax(logits.astype(np.float32), seen, np.array(verified[:B], np.int32)))
+    ok = orc.keys_to_tokens(orc.verify_argmax(logits.astype(np.float32), seen, np.array(verified[:MV], np.int32)))
     for t in range(st.M):
         g = int(orc.keys_to_tokens(keys_gpu[t:t + 1])[0])
         assert near_tie_ok(logits[t], g, int(ok[t])), (t, g, ok[t])

@@ -81,18 +81,20 @@ def oracle_books(orc, host, eng, chain, planted, args):
     st = orc.new_state(a=args["a"], anchor=args["anchor"], count=0, rounds_left=args["rounds"], limit=limit,
                        budget=min(args["budget"], 512), eos=args["eos"], ctx_new=args["ctx_new"],
                        ctx_pos=args["ctx_pos"], ctx_lo=args["ctx_lo"], run=1, force_m=args["force_m"],
-                       miss=args.get("miss", 0),
+                       miss=args.get("miss", 0), skip=args.get("skip", 0),
                        skip_rounds=1, stop_at=stop, ckpt_slot=args.get("ckpt_slot", -1), tokens=[args["anchor"]])
     out = np.zeros(4096, np.int32)
     seen = np.zeros((eng.desc.vocab + 31) // 32, np.uint32)
     while st.run:
         a = st.a
-        cap = max(min(min(md, B - 1), min(st.limit - a, st.budget - st.count) - 1), 0)
+        skip_now = st.skip
+        # a skip round verifies the anchor alone (dspark.hip:2441-2444); otherwise the draft cap of dspark.hip:2640
+        cap = 0 if skip_now > 0 else max(min(min(md, B - 1), min(st.limit - a, st.budget - st.count) - 1), 0)
         tokens = [st.anchor] + [int(planted[a + j - A0 - 1]) for j in range(1, cap + 1)]
         for j, t in enumerate(tokens):
             st.tokens[j] = t
         best = np.array([chain[a + t - A0] for t in range(cap + 1)], np.int32)
-        orc.accept_commit(st, best, cap + 1, out, seen)
+        orc.accept_commit(st, best, cap + 1, out, seen, skip_now=1 if skip_now > 0 else 0)
     return st, out[:st.count].copy(), stop
 
 
@@ -105,6 +107,8 @@ LAUNCH_CASES = {
     "draft_cap": (dict(max_drafts=3), (6,)),
     "rounds": (dict(rounds=2), (4,)),
     "miss_carried": (dict(miss=2), (0, 1, 8)),
+    "skip": (dict(skip=2), (5,)),  # two skip rounds (the anchor alone), then drafted rounds
+    "skip_cap": (dict(skip=1, max_drafts=3), (7,)),
 }
 
 
@@ -139,6 +143,16 @@ def test_launch_matches_rounds_and_oracle_books(dev, orc, name):
     for f in host.STATE_FIELDS:
         if f != "M":
             assert getattr(res.state, f) == getattr(want_st, f), (f, getattr(res.state, f), getattr(want_st, f))
+    # no round was put on the stream that found the State stopped (an eos stop may leave rounds in flight idle)
+    if args["eos"] < 0:
+        assert res.rounds_enqueued == res.rounds, (res.rounds_enqueued, res.rounds)
+    else:
+        assert res.rounds <= res.rounds_enqueued <= args["rounds"]
+    if "max_drafts" in extra or "skip" in extra:
+        # bare rounds verify 1 + the model's max_drafts and skip nothing: the launch's own cap and skip rounds have
+        # no one-by-one counterpart (test_launch_cap_and_penalty_do_not_stick covers rounds after such a launch)
+        eng.close()
+        return
 
     # the same rounds enqueued one by one from the State the launch sets
     for nm, buf in rings.items():
@@ -155,6 +169,38 @@ def test_launch_matches_rounds_and_oracle_books(dev, orc, name):
     for f in host.STATE_FIELDS:
         assert getattr(st, f) == getattr(res.state, f), f
     assert eng.download("out_tokens", np.int32)[:st.count].tolist() == toks
+    eng.close()
+
+
+def test_launch_cap_and_penalty_do_not_stick(dev, orc):
+    """A launch's draft cap and penalty are its own: after a 3-draft launch with rep 1.3, a bare planted round drafts
+    up to the model's max_drafts again (verifies 1 + 7 tokens) and commits the unpenalised greedy chain."""
+    torch = dev
+    host = load_host()
+    desc = host.model_desc(**GEOMETRIES["small"])
+    eng = host.Engine(desc, 512)
+    make_weights(eng, desc, 43)
+    setup_caches(eng, host, desc, A0, CTX_LO, 143)
+    print("case launch cap/rep reset", flush=True)
+    chain = greedy_chain(eng, torch, 24)
+    plant(eng, chain, (), desc.vocab)
+    rings = conv_rings(eng)
+    eng.init_seen([])
+    _, res = eng.launch(A0, ANCHOR, rep=1.3, max_drafts=3, ctx_new=1, ctx_pos=A0 - 1, ctx_lo=CTX_LO, force_m=-1)
+    torch.cuda.synchronize()
+    assert res.verified <= 4 * res.rounds  # the launch verified at most 1 + 3 tokens a round
+    for nm, buf in rings.items():
+        eng.upload(nm, buf)
+    eng.init_seen([])
+    eng.set_state(a=A0, anchor=ANCHOR, count=0, rounds_left=1, limit=eng.max_context, budget=1 << 20, eos=-1,
+                  ctx_new=1, ctx_pos=A0 - 1, ctx_lo=CTX_LO, run=1, skip_rounds=1, stop_at=eng.max_context,
+                  ckpt_slot=-1, tokens=[ANCHOR])
+    eng.round(-1, A0)
+    torch.cuda.synchronize()
+    st = eng.state()
+    assert st.verified == 1 + desc.max_drafts, st.verified
+    assert st.count == 1 + desc.max_drafts  # every planted draft of the unpenalised chain accepted
+    assert eng.download("out_tokens", np.int32)[:st.count].tolist() == chain[:st.count].tolist()
     eng.close()
 
 

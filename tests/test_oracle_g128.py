@@ -59,3 +59,27 @@ def test_packed_weights_reproduce_the_matrix(K):
     step = np.repeat(orc.f16_to_f32(gs).astype(np.float64), 128, axis=0)  # [K][N] code step of each weight
     bound = np.abs(xf) @ (0.5 * step) + 1e-9
     assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("K", [128, 384, 640, 7552])
+def test_converter_refuses_unpacked_groups(K):
+    """weights.Pack stores group g's scale only while g / 4 < groups / 4 (quant.go:96-99): a K that is not a multiple
+    of 512 leaves trailing groups without a stored scale, so the converter refuses it instead of reading padding."""
+    host = load_host()
+    srow = 16 if K // 512 == 4 else 64
+    packed = np.ones((4, srow), dtype=np.uint16)
+    with pytest.raises(host.DsparkError):
+        host.g128_scales(packed, 4, K)
+
+
+def test_converter_against_the_packers_layout_at_1024():
+    """K = 1024 (8 groups, SRow 64): every group's scale comes from the slot the packer wrote, none from padding."""
+    host = load_host()
+    rng = np.random.default_rng(1024)
+    N, K = 16, 1024
+    wf = orc.f32_to_f16((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+    _, packed = orc.pack_g128(wf, N, K)
+    packed = packed.reshape(N, 64)
+    gs = host.g128_scales(packed, N, K)
+    amax = np.abs(orc.f16_to_f32(wf).astype(np.float32)).reshape(N, K // 128, 128).max(axis=2)
+    assert np.array_equal(gs.T, orc.f32_to_f16(np.maximum(amax, 1e-8) / 127))
