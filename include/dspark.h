@@ -388,6 +388,16 @@ enum {
 int dspark_engine_trace(dspark_engine* e, int32_t enable, dspark_stream_t stream);
 int dspark_engine_trace_read(dspark_engine* e, uint64_t* out, int32_t cap, int32_t* n);
 
+/* Layer-boundary dumps (a debug aid, as the reference's raw dbg_logits dump, dspark.hip:186, 2285). With dumps on,
+ * every round records, before each drafter layer j and before the draft norm, and before each target layer i and
+ * before the final norm, the residual stream h and the value the next norm adds to it (the previous layer's FFN
+ * output, its K bands summed in band order; zeros before the first layer) into the tensor "debug_layers":
+ * fp32 [draft_layers + 1 + n_layers + 1][2][block][hidden], slot j (drafter j, block rows), slot draft_layers (before
+ * the draft norm), slot draft_layers + 1 + i (target layer i, the verify rows), slot draft_layers + 1 + n_layers
+ * (before the final norm); [0] = h, [1] = the added value. Rounds with dumps on are recorded as their own graphs and
+ * run one small kernel more per layer. */
+int dspark_engine_debug_layers(dspark_engine* e, int32_t enable);
+
 /* token id of an argmax key */
 static inline int32_t dspark_key_token(uint64_t key) { return (int32_t)(0xFFFFFFFFu - (uint32_t)key); }
 

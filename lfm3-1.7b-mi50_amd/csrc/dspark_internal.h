@@ -116,6 +116,9 @@ int markov_table_launch(const int8_t* w1q, const float* w1s, const float* c2, co
 int round_begin_launch(struct ::dspark_state* st, uint64_t* keys, int nkeys, uint32_t* seen, int block, int max_pos,
                        int vocab, int out_cap, hipStream_t s);
 int force_m_launch(struct ::dspark_state* st, int m, hipStream_t s);
+// Layer-boundary dump of a debug round: h [rows][H] and the band sum of v ([bands][rows][H], band stride rows x H)
+// into dst[0] and dst[1] (each block x H floats).
+int layer_dump_launch(float* dst, const float* h, const float* v, int bands, int rows, int H, int block, hipStream_t s);
 // Phase trace mark: buf = [count, round << 1 | active, (phase | round << 32, clock) ...]; `begin` marks open a round
 // (counted only when the State runs), later marks of an inactive round record nothing.
 int trace_mark_launch(uint64_t* buf, const struct ::dspark_state* st, int phase, int begin, int max_marks, hipStream_t s);

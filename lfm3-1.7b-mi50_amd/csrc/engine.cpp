@@ -135,6 +135,9 @@ struct dspark_engine {
   // phase tracing: marks [2 + 2 DSPARK_TRACE_MAX_MARKS] u64 (count, round | active, then (phase, clock) pairs)
   uint64_t* trace = nullptr;
   bool trace_on = false;
+  // layer-boundary dumps of debug rounds: [draft_layers + 1 + n_layers + 1][2][B][H] fp32 (dspark_engine_debug_layers)
+  float* dump = nullptr;
+  bool dump_on = false;
   std::vector<void*> allocs;
 
   ~dspark_engine() {
@@ -380,6 +383,13 @@ constexpr int ENGINE_BANDS = 2;
     if (_rc) return _rc;     \
   } while (0)
 
+// A layer-boundary dump (debug rounds only) into slot `slot`: the residual h and the summed bands of v.
+int dump(dspark_engine* e, int slot, const float* h, const float* v, int bands, int rows, hipStream_t s) {
+  if (!e->dump_on) return 0;
+  const size_t per = (size_t)2 * e->B * e->d.hidden;
+  return layer_dump_launch(e->dump + slot * per, h, v, bands, rows, e->d.hidden, e->B, s);
+}
+
 // A trace mark after a phase (tracing rounds only): one thread stores (phase | round << 32, clock).
 int mark(dspark_engine* e, int phase, hipStream_t s) {
   if (!e->trace_on) return 0;
@@ -449,6 +459,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
     int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
     for (int j = 0; j < d.draft_layers; ++j) {
       const LayerW& W = e->DL[j];
+      CK(dump(e, j, e->h[cur], j ? e->w2out : nullptr, w2b, B, s));
       CK(resnorm(e, B, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm_mix_qk(e, W, B, s));
@@ -462,6 +473,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
     }
     CK(mark(e, DSPARK_TRACE_DRAFTER, s));
+    CK(dump(e, d.draft_layers, e->h[cur], e->w2out, w2b, B, s));
     CK(resnorm(e, B, e->h[cur], e->w2out, w2b, nullptr, e->draft_norm, 0, nullptr, nullptr, s));
     CK(gemm(e, e->x16, B, H, e->crop_w, e->crop_s, e->crop_n, 0, e->base, nullptr, s));
     CK(mark(e, DSPARK_TRACE_CROP_HEAD, s));
@@ -497,6 +509,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
     const LayerW& W = e->L[i];
     const LayerW* P = i ? &e->L[i - 1] : nullptr;
     float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
+    CK(dump(e, d.draft_layers + 1 + i, e->h[cur], i ? e->w2out : nullptr, w2b, MV, s));
     CK(resnorm(e, MV, e->h[cur], i ? e->w2out : nullptr, w2b, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
                e->h[cur ^ 1], tap, s));
     cur ^= 1;
@@ -518,6 +531,7 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
   {
     const LayerW& P = e->L[d.n_layers - 1];
     float* tap = P.tap_slot >= 0 ? e->taps + (size_t)P.tap_slot * B * H : nullptr;
+    CK(dump(e, d.draft_layers + 1 + d.n_layers, e->h[cur], e->w2out, w2b, MV, s));
     CK(resnorm(e, MV, e->h[cur], e->w2out, w2b, P.post_ffn_norm, e->final_norm, 1, nullptr, tap, s));
   }
   CK(gemm(e, e->x16, MV, H, e->head_w, e->head_s, d.vocab, 0, e->logits, nullptr, s));
@@ -741,6 +755,8 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   }
   if (e->mirror) std::memset(e->mirror, 0, 16 * sizeof(int32_t));
   e->trace = static_cast<uint64_t*>(e->alloc("trace", (size_t)(2 + 2 * DSPARK_TRACE_MAX_MARKS) * 8, &err));
+  e->dump = static_cast<float*>(
+      e->alloc("debug_layers", (size_t)(d.draft_layers + d.n_layers + 2) * 2 * B * H * sizeof(float), &err));
   e->x_cols = std::max(std::max(H, d.n_taps * H), std::max(d.ffn, d.draft_ffn));
   e->mix_cols = std::max(std::max(3 * H, align16(QH * D + 2 * KVH * D + QH)), ckv_rows);
   e->h[0] = static_cast<float*>(e->alloc("h0", (size_t)B * H * 4, &err));
@@ -931,7 +947,7 @@ int round_enqueue(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
     if (rc) return rc;
   }
   const int bucket = plan_a / ROUND_PLAN_BUCKET;
-  const std::vector<int> key = {force_m, e->trace_on ? 1 : 0, mv, skip ? 1 : 0, bucket};
+  const std::vector<int> key = {force_m, (e->trace_on ? 1 : 0) | (e->dump_on ? 2 : 0), mv, skip ? 1 : 0, bucket};
   auto it = e->graphs.find(key);
   if (it == e->graphs.end()) {
     // Record the round on a private stream (capture needs a non-default stream), then replay it on `s`.
@@ -1046,6 +1062,12 @@ int dspark_engine_trace(dspark_engine* e, int32_t enable, dspark_stream_t stream
   if (!e->trace_on) return 0;
   // a fresh trace: count and round counter to zero (outside any graph)
   return (int)hipMemsetAsync(e->trace, 0, 16, reinterpret_cast<hipStream_t>(stream));
+}
+
+int dspark_engine_debug_layers(dspark_engine* e, int32_t enable) {
+  if (!e) return DSPARK_EINVAL;
+  e->dump_on = enable != 0;
+  return 0;
 }
 
 int dspark_engine_trace_read(dspark_engine* e, uint64_t* out, int32_t cap, int32_t* n) {

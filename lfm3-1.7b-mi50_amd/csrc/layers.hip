@@ -668,4 +668,26 @@ int force_m_launch(dspark_state* st, int m, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+// Layer-boundary dump (debug rounds): dst[0][t][c] = h[t][c], dst[1][t][c] = the sum of the `bands` inputs v in band
+// order (the value the next norm kernel adds; 0 without bands), for t < rows.
+__global__ void layer_dump_kernel(float* dst, const float* h, const float* v, int bands, size_t band_stride, int rows,
+                                  int H, size_t half) {
+  const size_t n = (size_t)rows * H;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    dst[i] = h[i];
+    float acc = 0.f;
+    for (int b = 0; b < bands; ++b) acc += v[b * band_stride + i];
+    dst[half + i] = acc;
+  }
+}
+
+int layer_dump_launch(float* dst, const float* h, const float* v, int bands, int rows, int H, int block,
+                      hipStream_t s) {
+  const size_t n = (size_t)rows * H;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(layer_dump_kernel, dim3(blocks), dim3(256), 0, s, dst, h, v, v ? bands : 0, n, rows, H,
+                     (size_t)block * H);
+  return (int)hipGetLastError();
+}
+
 }  // namespace dspark

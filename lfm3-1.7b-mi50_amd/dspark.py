@@ -438,6 +438,7 @@ _SIGS.update({
                                             ctypes.POINTER(ctypes.c_size_t)]),
     "dspark_engine_tensor_count": (ctypes.c_int, [ctypes.c_void_p]),
     "dspark_engine_tensor_name": (ctypes.c_char_p, [ctypes.c_void_p, ctypes.c_int32]),
+    "dspark_engine_debug_layers": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
     "dspark_engine_prepare": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "dspark_engine_round": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_engine_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(LaunchArgs), ctypes.c_void_p, ctypes.c_int32,
@@ -584,6 +585,10 @@ class Engine:
     def project_prompt(self, first, end, stream=None):
         check(lib().dspark_engine_project_prompt(self.h, first, end, stream_handle(stream)),
               "dspark_engine_project_prompt")
+
+    def debug_layers(self, enable=True):
+        """Layer-boundary dumps into the tensor "debug_layers" (dspark_engine_debug_layers)."""
+        check(lib().dspark_engine_debug_layers(self.h, int(enable)), "dspark_engine_debug_layers")
 
     def trace(self, enable=True, stream=None):
         """Phase tracing on (a fresh trace) or off for the rounds enqueued after this call."""

@@ -98,14 +98,17 @@ class Caches:
         self.taps = None  # [n_taps][B][H]
 
 
-def attn_fp16(q16, K, V, a, M, start, window, causal):
-    """fp64 verify attention via liborc (q [M][QH][D], K/V [T][KVH][D], all fp16-valued)."""
+def attn_fp16(q16, K, V, a, M, start, window, causal, threads=1):
+    """fp64 verify attention via liborc (q [M][QH][D], K/V [T][KVH][D], all fp16-valued); threads > 1: the threaded
+    form of the same arithmetic."""
     to16 = lambda x: np.ascontiguousarray(np.asarray(x, np.float64).astype(np.float16).view(np.uint16))
     T = a + M
+    if threads > 1:
+        return orc.verify_attention_mt(to16(q16), to16(K[:T]), to16(V[:T]), a, start, window, causal, threads)
     return orc.verify_attention(to16(q16), to16(K[:T]), to16(V[:T]), a, start, window, causal)
 
 
-def attn_rec(q16, K, V, a, M, start, window, causal):
+def attn_rec(q16, K, V, a, M, start, window, causal, threads=1):
     """The int8-record attention (dspark.hip:1020-1035, 1215-1412): q (fp16-valued) quantized per 32-dim group, K/V
     [T][KVH][D] already the dequantized record values (kv_store), fp64 softmax of those operands."""
     QH, D = q16.shape[1], q16.shape[2]
@@ -128,8 +131,8 @@ def kv_store(d, K, V, pos, h, k, v):
         V[pos, h] = f16(v)
 
 
-def attention(d, q16, K, V, a, M, start, window, causal):
-    return (attn_rec if getattr(d, "kv_format", 0) else attn_fp16)(q16, K, V, a, M, start, window, causal)
+def attention(d, q16, K, V, a, M, start, window, causal, threads=1):
+    return (attn_rec if getattr(d, "kv_format", 0) else attn_fp16)(q16, K, V, a, M, start, window, causal, threads)
 
 
 def context_projection(W, C, st, rope):
@@ -184,48 +187,63 @@ def project_rows(W, C, x, pos0, rope):
                          row[KVH * D + h * D:KVH * D + (h + 1) * D])
 
 
+def drafter_layer(W, C, j, h, v_prev, a, ctx_lo, rope):
+    """Drafter layer j over the block rows of the residual h (v_prev: the previous layer's FFN output, None for the
+    first): kind 3, no sandwich post-norms, no gate, attention to the ring context [max(ctx_lo, a - window), a) and the
+    whole block (dspark.hip:2706-2780, 2531). Stores the block's K/V in ring j. Returns (h, v) for the next layer."""
+    d = W.d
+    H, QH, KVH, D = d.hidden, d.q_heads, d.kv_heads, d.head_dim
+    B = h.shape[0]
+    pre = f"D{j}."
+    h, x = resnorm(h, v_prev, None, W.f16(pre + "op_norm"), 0, d.eps)
+    rows = QH * D + 2 * KVH * D
+    mw, ms = W.gemm_w(pre + "mix", rows, H)
+    mix = gemm(x, mw, ms)
+    qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
+    K, V = C.ring[j]
+    q16 = np.zeros((B, QH, D))
+    for t in range(B):
+        pos = a + t
+        for qh in range(QH):
+            q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, rope, d.rope_pairs))
+        for hh in range(KVH):
+            o = QH * D + hh * D
+            ov = QH * D + KVH * D + hh * D
+            kv_store(d, K, V, pos, hh, rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs),
+                     mix[t, ov:ov + D])
+    start = max(ctx_lo, a - d.draft_window)
+    o = attention(d, q16, K, V, a, B, start, 0, False)
+    y = f16(o.reshape(B, QH * D))
+    ow, os_ = W.gemm_w(pre + "out", H, H)
+    vout = gemm(y, ow, os_)
+    h, x = resnorm(h, vout, None, W.f16(pre + "ffn_norm"), 0, d.eps)
+    ww, ws = W.gemm_w(pre + "w13", 2 * d.draft_ffn, H)
+    gu = gemm(x, ww, ws)
+    g, u = gu[:, 0::2], gu[:, 1::2]
+    act = f16(g / (1.0 + np.exp(-g)) * u)
+    w2, s2 = W.gemm_w(pre + "w2", H, d.draft_ffn)
+    return h, gemm(act, w2, s2)
+
+
+def crop_head(W, h, v_prev):
+    """Draft norm + cropped head (dspark.hip:2564-2587): base [B][crop_rows + 1] (fp64)."""
+    d = W.d
+    _, x = resnorm(h, v_prev, None, W.f16("draft_norm"), 0, d.eps)
+    cw, cs = W.gemm_w("crop", d.crop_rows + 1, d.hidden)
+    return gemm(x, cw, cs)
+
+
 def drafter_block(W, C, st, rope):
     """Returns base [B][crop_rows + 1] (fp64): the cropped head over the drafter block."""
     d = W.d
-    H, B, QH, KVH, D = d.hidden, d.block, d.q_heads, d.kv_heads, d.head_dim
+    H, B = d.hidden, d.block
     emb = W.f16("embed", (d.vocab, H))
     toks = [st["anchor"]] + [d.mask_token] * (B - 1)
     h = emb[toks]
-    a = st["a"]
     v_prev = None
     for j in range(d.draft_layers):
-        pre = f"D{j}."
-        h, x = resnorm(h, v_prev, None, W.f16(pre + "op_norm"), 0, d.eps)
-        rows = QH * D + 2 * KVH * D
-        mw, ms = W.gemm_w(pre + "mix", rows, H)
-        mix = gemm(x, mw, ms)
-        qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
-        K, V = C.ring[j]
-        q16 = np.zeros((B, QH, D))
-        for t in range(B):
-            pos = a + t
-            for qh in range(QH):
-                q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, rope, d.rope_pairs))
-            for hh in range(KVH):
-                o = QH * D + hh * D
-                ov = QH * D + KVH * D + hh * D
-                kv_store(d, K, V, pos, hh, rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, rope, d.rope_pairs),
-                         mix[t, ov:ov + D])
-        start = max(st["ctx_lo"], a - d.draft_window)
-        o = attention(d, q16, K, V, a, B, start, 0, False)
-        y = f16(o.reshape(B, QH * D))
-        ow, os_ = W.gemm_w(pre + "out", H, H)
-        vout = gemm(y, ow, os_)
-        h, x = resnorm(h, vout, None, W.f16(pre + "ffn_norm"), 0, d.eps)
-        ww, ws = W.gemm_w(pre + "w13", 2 * d.draft_ffn, H)
-        gu = gemm(x, ww, ws)
-        g, u = gu[:, 0::2], gu[:, 1::2]
-        act = f16(g / (1.0 + np.exp(-g)) * u)
-        w2, s2 = W.gemm_w(pre + "w2", H, d.draft_ffn)
-        v_prev = gemm(act, w2, s2)
-    h, x = resnorm(h, v_prev, None, W.f16("draft_norm"), 0, d.eps)
-    cw, cs = W.gemm_w("crop", d.crop_rows + 1, H)
-    return gemm(x, cw, cs)
+        h, v_prev = drafter_layer(W, C, j, h, v_prev, st["a"], st["ctx_lo"], rope)
+    return crop_head(W, h, v_prev)
 
 
 def markov(W, st, base):
@@ -257,13 +275,101 @@ def markov(W, st, base):
     return toks, len(toks), zs
 
 
+def verify_layer(W, C, i, h, v_prev, a, rope, rope_swa=None, threads=1):
+    """Target layer i over the verify rows of the residual h (v_prev: the previous layer's FFN output, None for layer
+    0): sandwich norm, conv (conv_wave) or attention (query_fresh, verify attention, gated combine), out GEMM, sandwich
+    norm, gated FFN (dspark.hip:2519-2846). Updates layer i's K/V cache or conv ring at positions a .. a + rows - 1.
+    Returns (h after the first norm's add -- the tap of layer i - 1 --, h, v) with (h, v) the next layer's input."""
+    d = W.d
+    H, QH, KVH, D, I = d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.ffn
+    B = h.shape[0]
+    pre = f"L{i}."
+    post = W.f16(f"L{i - 1}.post_ffn_norm") if i else None
+    h, x = resnorm(h, v_prev, post, W.f16(pre + "op_norm"), 1, d.eps)
+    h_in = h
+    kind = d.layer_kind[i]
+    if kind == 0:
+        mw, ms = W.gemm_w(pre + "mix", 3 * H, H)
+        mix = gemm(x, mw, ms)
+        cw = W.f16(pre + "conv.w", (H, d.conv_kernel))
+        ring = C.conv[i]
+        Kc = d.conv_kernel
+        y = np.zeros((B, H))
+        for t in range(B):
+            Bv, Cv, Xv = mix[t, 0::3], mix[t, 1::3], mix[t, 2::3]
+            bx = f16(Bv * Xv)
+            conv = cw[:, Kc - 1] * bx
+            for k in range(Kc - 1):
+                conv = conv + cw[:, k] * ring[a + t - (Kc - 1) + k]
+            ring[a + t] = bx
+            y[t] = f16(Cv * conv)
+    else:
+        rows = QH * D + 2 * KVH * D + QH
+        rows16 = (rows + 15) // 16 * 16
+        mw, ms = W.gemm_w(pre + "mix", rows16, H)
+        mix = gemm(x, mw, ms)
+        qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
+        K, V = C.kv[i]
+        own = kind == 2 and getattr(d, "rope_base_swa", 0) > 0
+        table = rope_swa if own else rope
+        rot = d.rope_pairs_swa if own else d.rope_pairs
+        q16 = np.zeros((B, QH, D))
+        for t in range(B):
+            pos = a + t
+            for qh in range(QH):
+                q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, table, rot))
+            for hh in range(KVH):
+                o = QH * D + hh * D
+                ov = QH * D + KVH * D + hh * D
+                kv_store(d, K, V, pos, hh, rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, table, rot),
+                         mix[t, ov:ov + D])
+        window = d.window if kind == 2 else 0
+        start = max(0, a - window + 1) if window else 0
+        o = attention(d, q16, K, V, a, B, start, window, True, threads)
+        gate = mix[:, (QH + 2 * KVH) * D:(QH + 2 * KVH) * D + QH].astype(np.float32).astype(np.float64)
+        y = f16((o * (1.0 / (1.0 + np.exp(-gate)))[:, :, None]).reshape(B, QH * D))
+    ow, os_ = W.gemm_w(pre + "out", H, H)
+    vout = gemm(y, ow, os_)
+    h, x = resnorm(h, vout, W.f16(pre + "post_op_norm"), W.f16(pre + "ffn_norm"), 1, d.eps)
+    ww, ws = W.gemm_w(pre + "w13", 2 * I, H)
+    gu = gemm(x, ww, ws)
+    g, u = gu[:, 0::2], gu[:, 1::2]
+    act = f16(g / (1.0 + np.exp(-g)) * u)
+    w2, s2 = W.gemm_w(pre + "w2", H, I)
+    return h_in, h, gemm(act, w2, s2)
+
+
+def final_x(W, h, v_prev):
+    """The final norm of the verify pass: (h, x fp16-valued), x the LM head's input."""
+    d = W.d
+    return resnorm(h, v_prev, W.f16(f"L{d.n_layers - 1}.post_ffn_norm"), W.f16("final_norm"), 1, d.eps)
+
+
+def lm_head(W, x, row_chunk=16384):
+    """Logits [rows][V] (fp64) of the int8 LM head for fp16-valued x (head_run, dspark.hip:2219-2318), by row chunks
+    of the head (its fp64 copy would be 8 bytes per weight)."""
+    d = W.d
+    H, V = d.hidden, d.vocab
+    out = np.zeros((x.shape[0], V))
+    for r0 in range(0, V, row_chunk):
+        r1 = min(V, r0 + row_chunk)
+        w = (W.t["head.w"][r0 * H:r1 * H].astype(np.int16) - 128).reshape(r1 - r0, H).astype(np.float64)
+        if getattr(d, "weight_format", 0):
+            raw = W.t["head.s"]
+            s = h2f(raw).reshape(H // 128, raw.size // (H // 128))[:, r0:r1]
+        else:
+            s = h2f(W.t["head.s"][r0:r1])
+        out[:, r0:r1] = gemm(x, w, s)
+    return out
+
+
 def verify(W, C, st, tokens, rope, rope_swa=None):
     """Logits [m][V] (fp64) of the verify pass over the first m = min(len(tokens), block) tokens (the reference
     verifies m = 1 + drafts, dspark.hip:2657); updates K/V caches, conv rings and taps. Sliding layers (kind 2)
     rotate with rope_swa and d.rope_pairs_swa when the description gives them their own table (rope_base_swa > 0;
     internal/model/engine.go:333-338), else with `rope` and d.rope_pairs."""
     d = W.d
-    H, B, QH, KVH, D, I = d.hidden, d.block, d.q_heads, d.kv_heads, d.head_dim, d.ffn
+    H, B = d.hidden, d.block
     emb = W.f16("embed", (d.vocab, H))
     toks = [t if 0 <= t < d.vocab else 0 for t in tokens[:B]]
     B = len(toks)
@@ -273,63 +379,11 @@ def verify(W, C, st, tokens, rope, rope_swa=None):
     taps = np.zeros((d.n_taps, B, H))
     tap_of = {l: i for i, l in enumerate(d.tap_layer[:d.n_taps])}
     for i in range(d.n_layers):
-        pre = f"L{i}."
-        post = W.f16(f"L{i - 1}.post_ffn_norm") if i else None
-        h, x = resnorm(h, v_prev, post, W.f16(pre + "op_norm"), 1, d.eps)
+        h_in, h, v_prev = verify_layer(W, C, i, h, v_prev, a, rope, rope_swa)
         if i and (i - 1) in tap_of:
-            taps[tap_of[i - 1]] = h
-        kind = d.layer_kind[i]
-        if kind == 0:
-            mw, ms = W.gemm_w(pre + "mix", 3 * H, H)
-            mix = gemm(x, mw, ms)
-            cw = W.f16(pre + "conv.w", (H, d.conv_kernel))
-            ring = C.conv[i]
-            Kc = d.conv_kernel
-            y = np.zeros((B, H))
-            for t in range(B):
-                Bv, Cv, Xv = mix[t, 0::3], mix[t, 1::3], mix[t, 2::3]
-                bx = f16(Bv * Xv)
-                conv = cw[:, Kc - 1] * bx
-                for k in range(Kc - 1):
-                    conv = conv + cw[:, k] * ring[a + t - (Kc - 1) + k]
-                ring[a + t] = bx
-                y[t] = f16(Cv * conv)
-        else:
-            rows = QH * D + 2 * KVH * D + QH
-            rows16 = (rows + 15) // 16 * 16
-            mw, ms = W.gemm_w(pre + "mix", rows16, H)
-            mix = gemm(x, mw, ms)
-            qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
-            K, V = C.kv[i]
-            own = kind == 2 and getattr(d, "rope_base_swa", 0) > 0
-            table = rope_swa if own else rope
-            rot = d.rope_pairs_swa if own else d.rope_pairs
-            q16 = np.zeros((B, QH, D))
-            for t in range(B):
-                pos = a + t
-                for qh in range(QH):
-                    q16[t, qh] = f16(rope_rows(norm_head(mix[t, qh * D:(qh + 1) * D], qn, d.eps), pos, table, rot))
-                for hh in range(KVH):
-                    o = QH * D + hh * D
-                    ov = QH * D + KVH * D + hh * D
-                    kv_store(d, K, V, pos, hh, rope_rows(norm_head(mix[t, o:o + D], kn, d.eps), pos, table, rot),
-                             mix[t, ov:ov + D])
-            window = d.window if kind == 2 else 0
-            start = max(0, a - window + 1) if window else 0
-            o = attention(d, q16, K, V, a, B, start, window, True)
-            gate = mix[:, (QH + 2 * KVH) * D:(QH + 2 * KVH) * D + QH].astype(np.float32).astype(np.float64)
-            y = f16((o * (1.0 / (1.0 + np.exp(-gate)))[:, :, None]).reshape(B, QH * D))
-        ow, os_ = W.gemm_w(pre + "out", H, H)
-        vout = gemm(y, ow, os_)
-        h, x = resnorm(h, vout, W.f16(pre + "post_op_norm"), W.f16(pre + "ffn_norm"), 1, d.eps)
-        ww, ws = W.gemm_w(pre + "w13", 2 * I, H)
-        gu = gemm(x, ww, ws)
-        g, u = gu[:, 0::2], gu[:, 1::2]
-        act = f16(g / (1.0 + np.exp(-g)) * u)
-        w2, s2 = W.gemm_w(pre + "w2", H, I)
-        v_prev = gemm(act, w2, s2)
+            taps[tap_of[i - 1]] = h_in
     last = d.n_layers - 1
-    h, x = resnorm(h, v_prev, W.f16(f"L{last}.post_ffn_norm"), W.f16("final_norm"), 1, d.eps)
+    h, x = final_x(W, h, v_prev)
     if last in tap_of:
         taps[tap_of[last]] = h
     C.taps = taps

@@ -78,7 +78,7 @@ def make_weights(eng, desc, seed, stop_half=False):
                                                            "h0", "h1", "x16", "mix", "q16", "gate", "y16", "vout", "a16",
                                                            "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys",
                                                            "ws_", "rope", "ring_table", "tap_x", "plant", "conv_state",
-                                                           "trace"))]
+                                                           "trace", "debug_layers"))]
     for n in weight_names:
         nb = sizes[n]
         if n.endswith(".w") and not n.endswith("conv.w"):
