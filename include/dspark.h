@@ -191,6 +191,16 @@ size_t dspark_gemm_i8_workspace(int32_t M, int32_t N, int32_t K); /* counters + 
  * weights (dspark.hip:541-716). */
 int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, const void* gscale, int32_t N,
                         int32_t epilogue, float* y_f32, void* y_f16, dspark_stream_t stream);
+/* dspark_gemm_i8_g128 with the reference's default activation format (LFM3_X8, kernels/dspark.hip:24-26): x as int8
+ * with one fp32 scale per 16 columns. y[t][r] = sum over 16-column pieces p of fp32(gscale[p / 8][r] * s[t][p]) *
+ * (sum_{k in p} q[r][k] * c[t][k]), the integer dots exact (unit_dot_r, dspark.hip:541-566). xscale NULL: x is fp16
+ * [M][K] and is quantized per piece as it is loaded, s = max(max|x| / 127, 1e-20), c = rint(x * rcp(s)) (x_fill,
+ * 883-904; rcp is the hardware reciprocal, as in the reference); xscale given: x holds the codes c as integer-valued
+ * fp16 [M][K] and xscale the scales fp32 [M][K / 16] (the norm's output, norm_compute 802-823). Same shapes, epilogues
+ * and no workspace as dspark_gemm_i8_g128. */
+int dspark_gemm_i8_g128_x8(const void* x, const float* xscale, int32_t M, int32_t K, const uint8_t* w,
+                           const void* gscale, int32_t N, int32_t epilogue, float* y_f32, void* y_f16,
+                           dspark_stream_t stream);
 /* Host helper: the packer's scale rows ([N][SRow] fp16, SRow = 16 for K = 2048 and 64 otherwise, entry (quarter, i) =
  * group 4 i + quarter at quarter * SRow / 4 + i; quant.go:13-29, 66-104) -> gscale [K/128][N]. No device memory. */
 int dspark_g128_scales(const uint16_t* packed, int32_t N, int32_t K, uint16_t* out);
@@ -256,6 +266,11 @@ typedef struct dspark_model_desc {
    * group scales (weights.Pack, internal/weights/quant.go:66-104) as fp16 [K/128][N] (dspark_g128_scales converts the
    * packer's layout), which needs block <= 16. */
   int32_t weight_format;
+  /* Activations of the int8 GEMMs: 0 fp16; 1 the reference's default build (LFM3_X8, kernels/dspark.hip:24-26):
+   * every GEMM input quantized to int8 with one fp32 scale per 16 columns -- by the norm kernel from its fp32 output
+   * (norm_compute, 802-823), as it is loaded from fp16 sources (x_fill, 883-904) -- and multiplied int8 by int8
+   * (unit_dot_r, 541-566). Needs weight_format 1. */
+  int32_t x_format;
 } dspark_model_desc;
 
 typedef struct dspark_engine dspark_engine;

@@ -14,7 +14,7 @@ using namespace dspark;
 
 namespace {
 
-constexpr int ABI_VERSION = 4;
+constexpr int ABI_VERSION = 5;
 
 // Compute units of the current device (queried once per device; 256 on MI355X).
 int device_cus() {
@@ -354,6 +354,36 @@ int dspark_gemm_i8_g128(const void* x, int32_t M, int32_t K, const uint8_t* w, c
   p.N = N;
   p.K = K;
   p.epilogue = epilogue;
+  GemmPlan pl;
+  gemm_plan(M, N, K, true, false, &pl, 0, false, 1, true);
+  p.ksplit = pl.ksplit;
+  p.wpg = pl.wpg;
+  p.cpb = pl.cpb;
+  p.kw = pl.kw;
+  p.xd = pl.xd;
+  return gemm_launch(p, true, S(stream));
+}
+
+int dspark_gemm_i8_g128_x8(const void* x, const float* xscale, int32_t M, int32_t K, const uint8_t* w,
+                           const void* gscale, int32_t N, int32_t epilogue, float* y_f32, void* y_f16,
+                           dspark_stream_t stream) {
+  if (!x || !w || !gscale || M < 1 || M > 16 || N < 16 || N % 16 || K < 128 || K % 128) return DSPARK_EINVAL;
+  if (epilogue < 0 || epilogue > 2) return DSPARK_EINVAL;
+  if (epilogue == 0 && !y_f32 && !y_f16) return DSPARK_EINVAL;
+  if (epilogue != 0 && !y_f16) return DSPARK_EINVAL;
+  GemmParams p = {};
+  p.x = static_cast<const _Float16*>(x);
+  p.w = w;
+  p.gscale = static_cast<const _Float16*>(gscale);
+  p.y32 = epilogue == 0 ? y_f32 : nullptr;
+  p.y16 = static_cast<_Float16*>(y_f16);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.epilogue = epilogue;
+  p.x8 = xscale ? 2 : 1;
+  p.xsc = xscale;
+  p.xsc_row = K / 16;
   GemmPlan pl;
   gemm_plan(M, N, K, true, false, &pl, 0, false, 1, true);
   p.ksplit = pl.ksplit;

@@ -59,6 +59,10 @@ struct ResNormParams {
   int x_row;
   int H;
   int xop;                      // > 0: x16 in the verify GEMM's X operand order with xop token blocks
+  // LFM3_X8: x16 receives int8 codes (integer-valued halves) and xsc their fp32 scales, one per 16 columns, piece
+  // c / 16 of token t at t xsc_row + c / 16 (c the x column); nullptr: fp16 x
+  float* xsc;
+  int xsc_row;
 };
 
 struct QkRopeParams {
@@ -204,6 +208,11 @@ struct GemmParams {
   //   GEMM_FUSE_CONV: each group is 16 channels [B, C, X] of the conv mix (48 rows): gated short conv, y16 [M][N/3]
   //     and the conv history ring at st->a + t (conv_wave)
   int fuse;
+  // LFM3_X8 (with gscale only): 1 x is fp16, quantized per 16-column piece as it is loaded; 2 x holds int8 codes as
+  // integer-valued halves and xsc their fp32 scales, [token][xsc_row] with piece k / 16 of token t at t xsc_row + k / 16
+  int x8;
+  const float* xsc;
+  int xsc_row;
   const _Float16* conv_w;   // [N/3][conv_k]
   _Float16* conv_ring;      // [CONV_RING][N/3]
   int conv_k;

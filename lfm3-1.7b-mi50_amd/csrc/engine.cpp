@@ -113,6 +113,7 @@ struct dspark_engine {
   float *h[2] = {nullptr, nullptr}, *mix = nullptr, *vout = nullptr, *w2out = nullptr, *ctxv = nullptr, *ckvout = nullptr,
         *taps = nullptr, *logits = nullptr, *base = nullptr, *gate = nullptr;
   _Float16 *x16 = nullptr, *q16 = nullptr, *y16 = nullptr, *a16 = nullptr;
+  float* xsc = nullptr;  // x_format 1: the int8 codes' scales of the norm outputs in x16, [16 tbs][x_cols / 16]
   uint64_t* keys = nullptr;  // [B] verify best, then [B] Markov best
   void* ws_attn = nullptr;
   size_t ws_attn_bytes = 0;
@@ -236,6 +237,12 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.epilogue = epilogue;
   p.xop = xop ? e->tbs : 0;  // every GEMM of the round reads x16, y16 or a16
   p.yop = e->tbs;
+  if (e->d.x_format == 1) {
+    // int8 x: x16 holds the norm kernel's codes and scales; other inputs (fp16) are quantized as they are loaded
+    p.x8 = (x == e->x16 && xop) ? 2 : 1;
+    p.xsc = e->xsc;
+    p.xsc_row = e->x_cols / 16;
+  }
   int wpg_req = 0;
   if (fuse) {
     p.fuse = fuse->fuse;
@@ -286,6 +293,8 @@ int resnorm(dspark_engine* e, int M, const float* h_old, const float* v, int ban
   p.x_row = e->d.hidden;
   p.H = e->d.hidden;
   p.xop = e->tbs;
+  p.xsc = e->xsc;
+  p.xsc_row = e->x_cols / 16;
   return resnorm_launch(p, M, 1, s);
 }
 
@@ -446,6 +455,8 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       p.x_group_stride = H;
       p.H = H;
       p.xop = e->tbs;
+      p.xsc = e->xsc;
+      p.xsc_row = e->x_cols / 16;
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
     CK(enqueue_context(e, e->x16, true, s));
@@ -568,6 +579,8 @@ bool desc_ok(const dspark_model_desc* d, int max_context) {
   // group scales: the K-sliced kernel with one token block, whole 128-column groups
   if (d->weight_format < 0 || d->weight_format > 1) return false;
   if (d->weight_format == 1 && (d->block > 16 || d->hidden % 128 || d->ffn % 128 || d->draft_ffn % 128)) return false;
+  // int8 x (LFM3_X8): with group scales only
+  if (d->x_format < 0 || d->x_format > 1 || (d->x_format == 1 && d->weight_format != 1)) return false;
   if (d->kv_format == 1 && (d->head_dim != 128 || d->kv_heads != 4 || d->q_heads / d->kv_heads * d->block > 64))
     return false;
   if (d->draft_layers < 1 || d->block < 2 || d->block > 64 || d->max_drafts < 0 || d->max_drafts > d->block - 1) return false;
@@ -763,6 +776,8 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->h[1] = static_cast<float*>(e->alloc("h1", (size_t)B * H * 4, &err));
   e->tbs = (B + 15) / 16;
   e->x16 = h16("x16", (size_t)16 * e->tbs * e->x_cols);
+  if (d.x_format == 1)
+    e->xsc = static_cast<float*>(e->alloc("x_scales", (size_t)16 * e->tbs * (e->x_cols / 16) * sizeof(float), &err));
   e->mix = static_cast<float*>(e->alloc("mix", (size_t)B * e->mix_cols * 4, &err));
   e->q16 = h16("q16", (size_t)B * QH * D);
   e->gate = static_cast<float*>(e->alloc("gate", (size_t)B * QH * 4, &err));

@@ -443,9 +443,61 @@ __device__ __forceinline__ void gscale_products(f32x4& acc, const u32x2 (&gsr)[C
   }
 }
 
-template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false>
+// LFM3_X8 (the reference's default build, dspark.hip:24-26; unit_dot_r 541-566): the GEMM input as int8 codes with one
+// fp32 scale per 16-column piece. Lane (g, n) holds token n's piece g of a 64-column chunk (x0: columns 16 g .. + 7,
+// x1: 16 g + 8 .. + 15), so a piece never leaves its lane. p.x8 = 1: x is fp16 and the lane quantizes its piece as
+// x_fill does (883-904): s = max(max|x| / 127, 1e-20), codes rint(x * rcp(s)); p.x8 = 2: x already holds the codes
+// (integer-valued halves, written by the norm kernel) and p.xsc the scales [token][K / 16].
+__device__ __forceinline__ float x8_quantize(u32x4& x0, u32x4& x1) {
+  half8 h0 = as_half8(x0), h1 = as_half8(x1);
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fmaxf(fabsf((float)h0[j]), fabsf((float)h1[j])));
+  const float sc = fmaxf(__fdiv_rn(m, 127.f), 1e-20f);
+  const float inv = __builtin_amdgcn_rcpf(sc);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    h0[j] = (_Float16)rintf((float)h0[j] * inv);
+    h1[j] = (_Float16)rintf((float)h1[j] * inv);
+  }
+  __builtin_memcpy(&x0, &h0, 16);
+  __builtin_memcpy(&x1, &h1, 16);
+  return sc;
+}
+
+// One chunk's products under LFM3_X8: for each piece g' the integer dot of the strip's rows with token n's codes of
+// the piece (two MFMAs with every lane group but g' zeroed in B; exact in fp32, |dot| <= 16 * 127 * 127), then
+// acc[r] += dot * fp32(ws[r] * xs4[g']) as unit_dot_r scales a piece (ws: the lane's 4 rows' scales of the chunk's
+// 128-column group, xs4: token n's 4 piece scales of the chunk).
+__device__ __forceinline__ void x8_products(f32x4& acc, const half8 (&a)[2], u32x4 x0, u32x4 x1, f32x4 xs4, half4 ws,
+                                            int g) {
+  const u32x4 zero = {0, 0, 0, 0};
+  const f32x4 z4 = {0, 0, 0, 0};
+#pragma unroll
+  for (int gp = 0; gp < 4; ++gp) {
+    const bool on = g == gp;
+    f32x4 t = mfma16x16x32(a[0], as_half8(on ? x0 : zero), z4);
+    t = mfma16x16x32(a[1], as_half8(on ? x1 : zero), t);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = fmaf((float)ws[r] * xs4[gp], t[r], acc[r]);
+  }
+}
+
+// Token n's 4 piece scales of chunk c: loaded (p.x8 == 2) or, after x8_quantize, gathered from the lanes (g', n).
+__device__ __forceinline__ f32x4 x8_scales_load(const GemmParams& p, int n, int c) {
+  return ldg(reinterpret_cast<const f32x4*>(p.xsc + (size_t)min(n, p.M - 1) * p.xsc_row + 4 * c));
+}
+__device__ __forceinline__ f32x4 x8_scales_gather(float sc, int n) {
+  f32x4 v;
+#pragma unroll
+  for (int gp = 0; gp < 4; ++gp) v[gp] = __shfl(sc, 16 * gp + n);
+  return v;
+}
+
+template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, bool X8 = false>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   static_assert(!GS || (TB == 1 && I8 && CPW % 2 == 0), "group scales: one token block, int8 weights, whole groups");
+  static_assert(!X8 || GS, "int8 x goes with group scales");
   // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
   // anything is stored), so its latency overlaps theirs; a stopped round writes nothing.
   const int run = run_flag_load(p.st);
@@ -513,6 +565,7 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     auto batch = [&](int cb) {
       u32x4 xb[CPW][TB][2];
       u32x2 gsr[GS ? CPW / 2 : 1];
+      f32x4 xsl[X8 ? CPW : 1];
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = min(cb + i, c1 - 1);
@@ -521,10 +574,24 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
           xb[i][tb][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024));
           xb[i][tb][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024 + xhs));
         }
+        if constexpr (X8) {
+          if (p.x8 == 2) xsl[i] = x8_scales_load(p, n, c);
+        }
       }
       if constexpr (GS) gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
       load(w, cb);
-      if constexpr (GS) {
+      if constexpr (X8) {
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+          if (cb + i < c1) {
+            half8 a[2];
+            weights(w[i], a);
+            u32x4 x0 = xb[i][0][0], x1 = xb[i][0][1];
+            const f32x4 xs4 = p.x8 == 2 ? xsl[i] : x8_scales_gather(x8_quantize(x0, x1), n);
+            x8_products(acc[0], a, x0, x1, xs4, __builtin_bit_cast(half4, gsr[i >> 1]), g);
+          }
+        }
+      } else if constexpr (GS) {
         gscale_products<CPW>(acc[0], gsr, cb, c1, [&](int i, f32x4 t) {
           half8 a[2];
           weights(w[i], a);
@@ -577,12 +644,52 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
       }
     };
     u32x2 gsr[GS ? CPW / 2 : 1];
+    // LFM3_X8 codes from the norm (p.x8 == 2): the band's piece scales go to LDS after its X^T, [chunk][token] x 16 B
+    // (token t's 4 pieces of the chunk), by the same kind of loads (issued before the weights, so the counted wait
+    // below covers them)
+    const f32x4* xsc_lds = reinterpret_cast<const f32x4*>(xs + (size_t)(b1 - b0) * 2 * 64);
+    if constexpr (X8) {
+      if (p.x8 == 2) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)p.xsc, (short)0, (int)((size_t)p.M * p.xsc_row * 4), 0x00020000);
+        const int bcs = b1 - b0;
+        for (int r = wave_u; r < (bcs + 3) / 4; r += nw) {
+          const int j = b0 + 4 * r + g;  // lane (g, n): token n's scales of chunk j
+          if (n < p.M && j < b1)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(xs + (size_t)bcs * 2 * 64 + (size_t)r * 64), 16,
+                (uint32_t)(((size_t)n * p.xsc_row + 4 * j) * 4), 0, 0, 0);
+        }
+      }
+    }
     if constexpr (GS) gscale_load<CPW>(p, gsr, c0, c1, row0 + 4 * g);  // older than X: covered by the wait below
     stage(0, min(tbp, TB));
     load(w, c0);
     __builtin_amdgcn_s_waitcnt(GEMM_VMCNT(CPW * WV));
     __builtin_amdgcn_s_barrier();
-    if constexpr (GS) {  // one token block, X^T of the band in LDS at once (gemm_launch checked)
+    if constexpr (X8) {  // one token block, X^T of the band in LDS at once, as below
+      for (int cb = c0; cb < c1; cb += CPW) {
+        if (cb != c0) {
+          gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
+          load(w, cb);
+        }
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+          if (cb + i < c1) {
+            half8 a[2];
+            weights(w[i], a);
+            const u32x4* xb = xs + ((size_t)(cb + i - b0) * 2) * 64;
+            u32x4 x0 = xb[lane], x1 = xb[64 + lane];
+            // chunk j's scales of token n sit at 16 (j - b0) + n... in 4-chunk rows of 64 lanes: row (j - b0) / 4,
+            // lane 16 ((j - b0) % 4) + n
+            const int jr = cb + i - b0;
+            const f32x4 xs4 = p.x8 == 2 ? xsc_lds[(jr >> 2) * 64 + 16 * (jr & 3) + n]
+                                        : x8_scales_gather(x8_quantize(x0, x1), n);
+            x8_products(acc[0], a, x0, x1, xs4, __builtin_bit_cast(half4, gsr[i >> 1]), g);
+          }
+        }
+      }
+    } else if constexpr (GS) {  // one token block, X^T of the band in LDS at once (gemm_launch checked)
       for (int cb = c0; cb < c1; cb += CPW) {
         if (cb != c0) {
           gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
@@ -771,7 +878,8 @@ static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
   const int tb = (p.M + 15) / 16;
   const int bands = std::max(1, p.bands);
   const int bc = (p.K / 64 + bands - 1) / bands;  // X^T of the token blocks of one pass (all of them when they fit)
-  const size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)gemm_pass_tbs(tb, bc) * bc * 2048;
+  size_t x = gemm_sliced_xd(p, i8) ? 0 : (size_t)gemm_pass_tbs(tb, bc) * bc * 2048;
+  if (x && p.x8 == 2) x += (size_t)(bc + 3) / 4 * 1024;  // the band's int8-x piece scales after X^T
   const size_t red = (size_t)(p.kw - 1) * p.wpg * tb * 1024;
   const size_t tile = p.fuse ? (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float) : 0;
   return std::max(x, std::max(red, tile));
@@ -793,6 +901,15 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const int cpk = ((p.K / 64 + p.bands - 1) / p.bands + p.kw - 1) / p.kw;  // chunks per range (of the band's)
   if constexpr (I8 && TB == 1) {
     if (p.gscale) {  // group scales: X per wave, or X^T of the band in LDS at once (gemm_launch checked)
+      if (p.x8) {  // int8 x (LFM3_X8)
+        if (gemm_sliced_xd(p, I8)) {
+          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, true>), grid, block, lds, s, p);
+        } else {
+          allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, true>, lds);
+          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, true>), grid, block, lds, s, p);
+        }
+        return;
+      }
       if (gemm_sliced_xd(p, I8)) {
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true>), grid, block, lds, s, p);
       } else {
@@ -994,6 +1111,7 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
   if ((p.xop && p.xop < (p.M + 15) / 16) || (p.yop && p.yop < (p.M + 15) / 16)) return DSPARK_EINVAL;
   // group scales: the K-sliced kernel, one token block, whole 128-column groups in every band and range, X per wave or
   // the band's X^T in LDS at once, no row scales
+  if (p.x8 && (!p.gscale || p.x8 > 2 || (p.x8 == 2 && (!p.xsc || p.xsc_row < p.K / 16)))) return DSPARK_EINVAL;
   if (p.gscale) {
     if (!i8 || p.kw <= 0 || p.M > 16 || p.K % 128 || p.scale) return DSPARK_EINVAL;
     const int bands = std::max(1, p.bands), bc = (p.K / 64 + bands - 1) / bands, cpk = (bc + p.kw - 1) / p.kw;

@@ -146,16 +146,33 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const int i = 1024 * k + 4 * (int)threadIdx.x;
+    float xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xf[j] = hv[k][j] * inv * (float)wn[k][j];
+    half4 x;
+    float xsc = 0.f;
+    if (p.xsc) {
+      // LFM3_X8 (norm_compute, dspark.hip:802-823): the fp32 value as int8 codes with one scale per 16 columns, the 4
+      // threads of a quad holding a piece (columns past H are zero, whole pieces: H % 16 == 0)
+      float m = fmaxf(fmaxf(fabsf(xf[0]), fabsf(xf[1])), fmaxf(fabsf(xf[2]), fabsf(xf[3])));
+      m = fmaxf(m, __shfl_xor(m, 1));
+      m = fmaxf(m, __shfl_xor(m, 2));
+      xsc = fmaxf(__fdiv_rn(m, 127.f), 1e-20f);
+      const float r = __builtin_amdgcn_rcpf(xsc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = (_Float16)rintf(xf[j] * r);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = (_Float16)xf[j];
+    }
     if (ok[k]) {
       const size_t o = (size_t)gi * p.group_stride + (size_t)t * H + i;
       if (p.dst) *reinterpret_cast<f32x4*>(p.dst + o) = hv[k];
       if (p.tap) *reinterpret_cast<f32x4*>(p.tap + (size_t)t * H + i) = hv[k];
-      half4 x;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = (_Float16)(hv[k][j] * inv * (float)wn[k][j]);
-      const size_t xo = p.xop ? xop_elem(t, gi * (int)p.x_group_stride + i, p.xop)
-                              : (size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i;
+      const int xcol = gi * (int)p.x_group_stride + i;
+      const size_t xo = p.xop ? xop_elem(t, xcol, p.xop) : (size_t)gi * p.x_group_stride + (size_t)t * p.x_row + i;
       *reinterpret_cast<half4*>(p.x16 + xo) = x;
+      if (p.xsc && (threadIdx.x & 3) == 0) p.xsc[(size_t)t * p.xsc_row + xcol / 16] = xsc;
     }
   }
 }

@@ -77,6 +77,9 @@ _SIGS = {
     "dspark_gemm_i8_g128": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                            ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                                            ctypes.c_void_p, ctypes.c_void_p]),
+    "dspark_gemm_i8_g128_x8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "dspark_g128_scales": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "dspark_head_argmax_workspace": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32]),
     "dspark_head_argmax_f16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
@@ -85,7 +88,7 @@ _SIGS = {
 }
 
 
-ABI_VERSION = 4  # dspark_abi_version() of the library these signatures describe
+ABI_VERSION = 5  # dspark_abi_version() of the library these signatures describe
 
 
 def lib():
@@ -373,6 +376,20 @@ def gemm_i8_g128(x, w_biased, gscale, epilogue=0, y_f32=None, y_f16=None, stream
     return y_f32, y_f16
 
 
+def gemm_i8_g128_x8(x, w_biased, gscale, xscale=None, epilogue=0, y_f32=None, y_f16=None, stream=None):
+    """The LFM3_X8 form of gemm_i8_g128: x fp16 [M][K] quantized per 16 columns on load (xscale None), or x the int8
+    codes as integer-valued fp16 with xscale fp32 [M][K/16]."""
+    torch = _torch()
+    M, K = x.shape
+    N = w_biased.shape[0]
+    if epilogue == 0 and y_f32 is None and y_f16 is None:
+        y_f32 = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    rc = lib().dspark_gemm_i8_g128_x8(ptr(x), ptr(xscale), M, K, ptr(w_biased), ptr(gscale), N, epilogue, ptr(y_f32),
+                                      ptr(y_f16), stream_handle(stream))
+    check(rc, "dspark_gemm_i8_g128_x8")
+    return y_f32, y_f16
+
+
 def g128_scales(packed, N, K):
     """The packer's scale rows (uint16 [N][SRow]) -> group-major [K/128][N] (host numpy)."""
     import numpy as np
@@ -413,7 +430,7 @@ class ModelDesc(ctypes.Structure):
                 ("draft_window", ctypes.c_int32), ("ring_positions", ctypes.c_int32), ("mask_token", ctypes.c_int32),
                 ("conf_bias", ctypes.c_float), ("conf_thr", ctypes.c_float), ("eps", ctypes.c_float),
                 ("rope_base_swa", ctypes.c_float), ("rope_pairs_swa", ctypes.c_int32), ("conv_slots", ctypes.c_int32),
-                ("kv_format", ctypes.c_int32), ("weight_format", ctypes.c_int32)]
+                ("kv_format", ctypes.c_int32), ("weight_format", ctypes.c_int32), ("x_format", ctypes.c_int32)]
 
 
 class LaunchArgs(ctypes.Structure):
@@ -495,7 +512,7 @@ def c4_desc(block=16, vocab=65536):
                       conf_bias=3.0, conf_thr=-0.4, eps=1e-5)
 
 
-def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1, weight_format=1):
+def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1, weight_format=1, x_format=0):
     """The reference model's geometry (internal/model/engine.go:23-40; internal/model/dspark.go:22-41;
     cmd/pack/main.go:193, 329): 24 target layers in the reference order (13 gated short-conv k=7, 6 full and 5
     sliding-window-256 GQA attention layers, 16/4/128), hidden 2048, gated FFN 7680, vocab 128000; 3 attention-only
@@ -505,14 +522,16 @@ def ref_desc(block=9, max_drafts=7, vocab=128000, kv_format=1, weight_format=1):
     drafter at base 1e6 with 32 rotating pairs, sliding layers at base 1e4 with 64. K/V in the reference's int8
     records (264 bytes per position and KV head, quantize_pair; engine.go:30-32, ops.hip:212-251) unless
     kv_format=0 (fp16 pages); int8 weights with the reference's per-128-column fp16 scales (weights.Pack,
-    quant.go:66-104) unless weight_format=0 (one scale per row)."""
+    quant.go:66-104) unless weight_format=0 (one scale per row). x_format=1: the GEMM inputs as int8 per 16 columns, the
+    reference's default build (LFM3_X8, kernels/dspark.hip:24-26); needs weight_format=1."""
     kinds = [0, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0, 2, 0, 1, 0]
     return model_desc(hidden=2048, ffn=7680, vocab=vocab, n_layers=24, layer_kind=kinds, q_heads=16, kv_heads=4,
                       head_dim=128, conv_kernel=7, window=256, rope_base=1e6, rope_pairs=32, rope_base_swa=1e4,
                       rope_pairs_swa=64, draft_layers=3,
                       draft_ffn=7680, block=block, max_drafts=max_drafts, crop_rows=16384, markov_rank=256, n_taps=5,
                       tap_layer=[2, 6, 12, 18, 23], draft_window=2048, ring_positions=4096, mask_token=vocab - 1,
-                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5, kv_format=kv_format, weight_format=weight_format)
+                      conf_bias=3.0, conf_thr=-0.4, eps=1e-5, kv_format=kv_format, weight_format=weight_format,
+                      x_format=x_format)
 
 
 class Engine:

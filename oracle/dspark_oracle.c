@@ -708,6 +708,38 @@ void orc_gemm_g128(const uint16_t* x, const uint8_t* w, const uint16_t* gs, int 
   }
 }
 
+/* LFM3_X8's activation format: per 16 values one fp32 scale, int8 codes (norm_compute, kernels/dspark.hip:802-823;
+ * x_fill, 883-904). */
+void orc_quantize_x16(const float* x, int64_t n, int8_t* q, float* s) {
+  for (int64_t p = 0; p < n / 16; ++p) {
+    float m = 0.f;
+    for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(x[16 * p + j]));
+    const float sc = fmaxf(m / 127.f, 1e-20f);
+    const float inv = 1.f / sc;
+    s[p] = sc;
+    for (int j = 0; j < 16; ++j) q[16 * p + j] = (int8_t)(int)rintf(x[16 * p + j] * inv);
+  }
+}
+
+/* unit_dot_r under LFM3_X8 (kernels/dspark.hip:541-566): per 16-column piece the exact integer dot of the biased
+ * weights (q + 128, XOR 0x80 = q) with the int8 codes, times fp32(group scale * piece scale). */
+void orc_gemm_x8(const int8_t* q, const float* s, const uint8_t* w, const uint16_t* gs, int M, int N, int K, double* y) {
+  const int P = K / 16;
+  for (int r = 0; r < N; ++r) {
+    const uint8_t* wr = w + (size_t)r * K;
+    for (int t = 0; t < M; ++t) {
+      double acc = 0.0;
+      for (int p = 0; p < P; ++p) {
+        int32_t d = 0;
+        for (int k = 16 * p; k < 16 * p + 16; ++k) d += ((int)wr[k] - 128) * (int)q[(size_t)t * K + k];
+        const float f = orc_f16_to_f32(gs[(size_t)(p / 8) * N + r]) * s[(size_t)t * P + p];
+        acc += (double)f * (double)d;
+      }
+      y[(size_t)t * N + r] = acc;
+    }
+  }
+}
+
 void orc_gemm_f16(const uint16_t* x, const uint16_t* w, int M, int N, int K, double* y) {
   double* xf = (double*)malloc(sizeof(double) * (size_t)M * K);
   double* wf = (double*)malloc(sizeof(double) * (size_t)K);

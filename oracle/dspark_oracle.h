@@ -23,6 +23,10 @@
  *                             scales zeroed removes exactly its product (tests/test_oracle_g128.py)
  *   weights.Pack restated ... packed then reconstructed within half a code step per weight of the fp16 matrix product;
  *                             scale slots against the packer's index rule (tests/test_oracle_g128.py)
+ *   int8 x (LFM3_X8) ........ closed forms: integer pieces with max 127 give scale 1 and the codes themselves, the
+ *                             round-trip bound |x - q s| <= s/2, the all-zero piece at the 1e-20 floor, the +-127 code
+ *                             at each piece's max; the x8 GEMM equals the group GEMM on codes times the piece scales
+ *                             (fp64 numpy) and reduces to it at unit scales (tests/test_oracle_x8.py)
  *   target/drafter layers ... composed of the pinned pieces above + numpy restatements of RMS norm, RoPE,
  *                             short conv (tests/test_oracle.py::test_rms_norm_rope_conv)
  */
@@ -113,6 +117,12 @@ void orc_transpose_lanes(const uint8_t* src, uint8_t* dst, int64_t n);          
 /* y[t][r] = scale[r] * sum_k x[t][k] * q[r][k]; w signed int8 [N][K] or biased (q+128) when biased != 0. */
 void orc_gemm_i8(const uint16_t* x, const uint8_t* w, int biased, const uint16_t* scale, int M, int N, int K, double* y);
 void orc_gemm_g128(const uint16_t* x, const uint8_t* w, const uint16_t* gs, int M, int N, int K, double* y);
+/* LFM3_X8 (kernels/dspark.hip:24-26): GEMV inputs as int8 with one fp32 scale per 16 columns. quantize: per piece of
+ * 16 values s = max(max|x| / 127, 1e-20) (fp32 division), q = rint(x * (1 / s)) (norm_compute 802-823, x_fill
+ * 883-904; the reference takes 1 / s with the hardware reciprocal, here IEEE fp32). gemm: y[t][r] = sum over pieces p
+ * of fp32(gs[p / 8][r] * s[t][p]) * (integer dot of the piece), summed in fp64 (unit_dot_r 541-566). */
+void orc_quantize_x16(const float* x, int64_t n, int8_t* q, float* s);
+void orc_gemm_x8(const int8_t* q, const float* s, const uint8_t* w, const uint16_t* gs, int M, int N, int K, double* y);
 void orc_gemm_f16(const uint16_t* x, const uint16_t* w, int M, int N, int K, double* y);
 /* First-max row argmax of y [M][N] (fp32 keys, ties -> smallest index). */
 void orc_row_argmax(const float* y, int M, int N, int32_t* idx);

@@ -75,6 +75,8 @@ def lib():
             "orc_gemm_i8": (None, [c_u16p, c_u8p, ctypes.c_int, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    c_f64p]),
             "orc_gemm_g128": (None, [c_u16p, c_u8p, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_f64p]),
+            "orc_quantize_x16": (None, [c_f32p, ctypes.c_int64, c_i8p, c_f32p]),
+            "orc_gemm_x8": (None, [c_i8p, c_f32p, c_u8p, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_f64p]),
             "orc_gemm_f16": (None, [c_u16p, c_u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_f64p]),
             "orc_row_argmax": (None, [c_f32p, ctypes.c_int, ctypes.c_int, c_i32p]),
             "orc_rms_norm": (None, [c_f32p, c_u16p, ctypes.c_int, ctypes.c_float, c_f32p]),
@@ -382,6 +384,28 @@ def gemm_g128(x_f16, w_biased, gs_f16):
     N = w.shape[0]
     y = np.empty((M, N), dtype=np.float64)
     lib().orc_gemm_g128(_p(x, c_u16p), _p(w, c_u8p), _p(gs, c_u16p), M, N, K, _p(y, c_f64p))
+    return y
+
+
+def quantize_x16(x):
+    """LFM3_X8's per-16-value int8 quantization of fp32 x [..., K] -> (int8 codes, fp32 scales [..., K / 16])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.shape, dtype=np.int8)
+    s = np.empty(x.shape[:-1] + (x.shape[-1] // 16,), dtype=np.float32)
+    lib().orc_quantize_x16(_p(x, c_f32p), x.size, _p(q, c_i8p), _p(s, c_f32p))
+    return q, s
+
+
+def gemm_x8(q, s, w_biased, gs_f16):
+    """int8 codes [M][K] + piece scales [M][K / 16] times biased int8 weights [N][K] with group scales [K/128][N]."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    w = np.ascontiguousarray(w_biased, dtype=np.uint8)
+    gs = np.ascontiguousarray(gs_f16, dtype=np.uint16)
+    M, K = q.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=np.float64)
+    lib().orc_gemm_x8(_p(q, c_i8p), _p(s, c_f32p), _p(w, c_u8p), _p(gs, c_u16p), M, N, K, _p(y, c_f64p))
     return y
 
 

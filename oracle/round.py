@@ -31,6 +31,25 @@ class Weights:
     def __init__(self, desc, tensors):
         self.d = desc
         self.t = tensors
+        # LFM3_X8 (kernels/dspark.hip:24-26): every int8 GEMM's input quantized per 16 columns (x_format 1)
+        self.x8 = getattr(desc, "x_format", 0) == 1
+
+    def mm(self, x, w, s):
+        """The int8 GEMM of the model's activation format: fp16-valued x (gemm), or under LFM3_X8 x (fp32-valued from
+        a norm, fp16-valued otherwise) quantized per 16 columns and multiplied as unit_dot_r does (dspark.hip:541-566):
+        per piece the exact integer dot times fp32(group scale * piece scale), summed in fp64."""
+        if not self.x8:
+            return gemm(x, w, s)
+        assert s.ndim == 2, "LFM3_X8 goes with per-128-column weight scales"
+        q, sc = orc.quantize_x16(np.asarray(x, np.float64).astype(np.float32))
+        M, K = q.shape
+        P = K // 16
+        qp = q.astype(np.float64).reshape(M, P, 16).transpose(1, 0, 2)        # [P][M][16]
+        wp = w.reshape(w.shape[0], P, 16).transpose(1, 2, 0)                  # [P][16][N]
+        d = np.matmul(qp, wp)                                                 # [P][M][N] exact integers
+        f = (np.repeat(s, 8, axis=0)[:, None, :].astype(np.float32) *
+             sc.T[:, :, None]).astype(np.float32).astype(np.float64)          # [P][M][N] fp32(gs * s_p)
+        return (f * d).sum(axis=0)
 
     def f16(self, name, shape=None):
         a = h2f(self.t[name])
@@ -58,8 +77,9 @@ def gemm(x16, w, s):
     return (x16 @ w.T) * s[None, :]
 
 
-def resnorm(h_old, v, post_w, norm_w, sandwich, eps):
-    """norm_compute (dspark.hip:722-843) for a block of rows: returns (h_new, x fp16-valued)."""
+def resnorm(h_old, v, post_w, norm_w, sandwich, eps, x8=False):
+    """norm_compute (dspark.hip:722-843) for a block of rows: returns (h_new, x fp16-valued), or with x8 (LFM3_X8,
+    dspark.hip:802-823: the norm quantizes its fp32 value) x fp32-valued."""
     H = norm_w.shape[0]
     h = np.zeros_like(v if v is not None else h_old) if h_old is None else h_old.copy()
     if v is not None:
@@ -67,7 +87,8 @@ def resnorm(h_old, v, post_w, norm_w, sandwich, eps):
         pw = post_w if post_w is not None else 1.0
         h = h + (v * a) * pw
     inv = 1.0 / np.sqrt((h * h).sum(1, keepdims=True) / H + eps)
-    return h, f16(h * inv * norm_w[None, :])
+    x = h * inv * norm_w[None, :]
+    return h, (x.astype(np.float32).astype(np.float64) if x8 else f16(x))
 
 
 def rope_rows(x, pos, table, rot):
@@ -144,7 +165,7 @@ def context_projection(W, C, st, rope):
     if n_new <= 0:
         return
     tn = W.f16("tap_norms", (d.n_taps, H))
-    xs = [resnorm(C.taps[b][:B], None, None, tn[b], 0, d.eps)[1] for b in range(d.n_taps)]
+    xs = [resnorm(C.taps[b][:B], None, None, tn[b], 0, d.eps, W.x8)[1] for b in range(d.n_taps)]
     project_rows(W, C, np.concatenate(xs, axis=1)[:n_new], pos0, rope)
 
 
@@ -169,12 +190,12 @@ def project_rows(W, C, x, pos0, rope):
     H = d.hidden
     n_new = x.shape[0]
     fw, fs = W.gemm_w("fc", H, d.n_taps * H)
-    c = gemm(x, fw, fs)
-    _, x2 = resnorm(None, c, None, W.f16("hidden_norm"), 0, d.eps)
+    c = W.mm(x, fw, fs)
+    _, x2 = resnorm(None, c, None, W.f16("hidden_norm"), 0, d.eps, W.x8)
     KVH, D = d.kv_heads, d.head_dim
     rows = d.draft_layers * 2 * KVH * D
     cw, cs = W.gemm_w("ckv", rows, H)
-    kv = gemm(x2, cw, cs)
+    kv = W.mm(x2, cw, cs)
     for j in range(d.draft_layers):
         kn = W.f16(f"D{j}.k_norm")
         K, V = C.ring[j]
@@ -195,10 +216,10 @@ def drafter_layer(W, C, j, h, v_prev, a, ctx_lo, rope):
     H, QH, KVH, D = d.hidden, d.q_heads, d.kv_heads, d.head_dim
     B = h.shape[0]
     pre = f"D{j}."
-    h, x = resnorm(h, v_prev, None, W.f16(pre + "op_norm"), 0, d.eps)
+    h, x = resnorm(h, v_prev, None, W.f16(pre + "op_norm"), 0, d.eps, W.x8)
     rows = QH * D + 2 * KVH * D
     mw, ms = W.gemm_w(pre + "mix", rows, H)
-    mix = gemm(x, mw, ms)
+    mix = W.mm(x, mw, ms)
     qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
     K, V = C.ring[j]
     q16 = np.zeros((B, QH, D))
@@ -215,22 +236,22 @@ def drafter_layer(W, C, j, h, v_prev, a, ctx_lo, rope):
     o = attention(d, q16, K, V, a, B, start, 0, False)
     y = f16(o.reshape(B, QH * D))
     ow, os_ = W.gemm_w(pre + "out", H, H)
-    vout = gemm(y, ow, os_)
-    h, x = resnorm(h, vout, None, W.f16(pre + "ffn_norm"), 0, d.eps)
+    vout = W.mm(y, ow, os_)
+    h, x = resnorm(h, vout, None, W.f16(pre + "ffn_norm"), 0, d.eps, W.x8)
     ww, ws = W.gemm_w(pre + "w13", 2 * d.draft_ffn, H)
-    gu = gemm(x, ww, ws)
+    gu = W.mm(x, ww, ws)
     g, u = gu[:, 0::2], gu[:, 1::2]
     act = f16(g / (1.0 + np.exp(-g)) * u)
     w2, s2 = W.gemm_w(pre + "w2", H, d.draft_ffn)
-    return h, gemm(act, w2, s2)
+    return h, W.mm(act, w2, s2)
 
 
 def crop_head(W, h, v_prev):
     """Draft norm + cropped head (dspark.hip:2564-2587): base [B][crop_rows + 1] (fp64)."""
     d = W.d
-    _, x = resnorm(h, v_prev, None, W.f16("draft_norm"), 0, d.eps)
+    _, x = resnorm(h, v_prev, None, W.f16("draft_norm"), 0, d.eps, W.x8)
     cw, cs = W.gemm_w("crop", d.crop_rows + 1, d.hidden)
-    return gemm(x, cw, cs)
+    return W.mm(x, cw, cs)
 
 
 def drafter_block(W, C, st, rope):
@@ -285,12 +306,12 @@ def verify_layer(W, C, i, h, v_prev, a, rope, rope_swa=None, threads=1):
     B = h.shape[0]
     pre = f"L{i}."
     post = W.f16(f"L{i - 1}.post_ffn_norm") if i else None
-    h, x = resnorm(h, v_prev, post, W.f16(pre + "op_norm"), 1, d.eps)
+    h, x = resnorm(h, v_prev, post, W.f16(pre + "op_norm"), 1, d.eps, W.x8)
     h_in = h
     kind = d.layer_kind[i]
     if kind == 0:
         mw, ms = W.gemm_w(pre + "mix", 3 * H, H)
-        mix = gemm(x, mw, ms)
+        mix = W.mm(x, mw, ms)
         cw = W.f16(pre + "conv.w", (H, d.conv_kernel))
         ring = C.conv[i]
         Kc = d.conv_kernel
@@ -307,7 +328,7 @@ def verify_layer(W, C, i, h, v_prev, a, rope, rope_swa=None, threads=1):
         rows = QH * D + 2 * KVH * D + QH
         rows16 = (rows + 15) // 16 * 16
         mw, ms = W.gemm_w(pre + "mix", rows16, H)
-        mix = gemm(x, mw, ms)
+        mix = W.mm(x, mw, ms)
         qn, kn = W.f16(pre + "q_norm"), W.f16(pre + "k_norm")
         K, V = C.kv[i]
         own = kind == 2 and getattr(d, "rope_base_swa", 0) > 0
@@ -329,37 +350,44 @@ def verify_layer(W, C, i, h, v_prev, a, rope, rope_swa=None, threads=1):
         gate = mix[:, (QH + 2 * KVH) * D:(QH + 2 * KVH) * D + QH].astype(np.float32).astype(np.float64)
         y = f16((o * (1.0 / (1.0 + np.exp(-gate)))[:, :, None]).reshape(B, QH * D))
     ow, os_ = W.gemm_w(pre + "out", H, H)
-    vout = gemm(y, ow, os_)
-    h, x = resnorm(h, vout, W.f16(pre + "post_op_norm"), W.f16(pre + "ffn_norm"), 1, d.eps)
+    vout = W.mm(y, ow, os_)
+    h, x = resnorm(h, vout, W.f16(pre + "post_op_norm"), W.f16(pre + "ffn_norm"), 1, d.eps, W.x8)
     ww, ws = W.gemm_w(pre + "w13", 2 * I, H)
-    gu = gemm(x, ww, ws)
+    gu = W.mm(x, ww, ws)
     g, u = gu[:, 0::2], gu[:, 1::2]
     act = f16(g / (1.0 + np.exp(-g)) * u)
     w2, s2 = W.gemm_w(pre + "w2", H, I)
-    return h_in, h, gemm(act, w2, s2)
+    return h_in, h, W.mm(act, w2, s2)
 
 
 def final_x(W, h, v_prev):
-    """The final norm of the verify pass: (h, x fp16-valued), x the LM head's input."""
+    """The final norm of the verify pass: (h, x), x the LM head's input (fp16-valued, or fp32-valued under
+    LFM3_X8)."""
     d = W.d
-    return resnorm(h, v_prev, W.f16(f"L{d.n_layers - 1}.post_ffn_norm"), W.f16("final_norm"), 1, d.eps)
+    return resnorm(h, v_prev, W.f16(f"L{d.n_layers - 1}.post_ffn_norm"), W.f16("final_norm"), 1, d.eps, W.x8)
 
 
-def lm_head(W, x, row_chunk=16384):
-    """Logits [rows][V] (fp64) of the int8 LM head for fp16-valued x (head_run, dspark.hip:2219-2318), by row chunks
-    of the head (its fp64 copy would be 8 bytes per weight)."""
+def lm_head(W, x, row_chunk=16384, xs=None):
+    """Logits [rows][V] (fp64) of the int8 LM head (head_run, dspark.hip:2219-2318) for x (as W.mm takes it), or for
+    int8 codes x with their piece scales xs (LFM3_X8 input already quantized), by row chunks of the head (its fp64
+    copy would be 8 bytes per weight)."""
     d = W.d
     H, V = d.hidden, d.vocab
     out = np.zeros((x.shape[0], V))
     for r0 in range(0, V, row_chunk):
         r1 = min(V, r0 + row_chunk)
-        w = (W.t["head.w"][r0 * H:r1 * H].astype(np.int16) - 128).reshape(r1 - r0, H).astype(np.float64)
         if getattr(d, "weight_format", 0):
             raw = W.t["head.s"]
-            s = h2f(raw).reshape(H // 128, raw.size // (H // 128))[:, r0:r1]
+            sraw = raw.reshape(H // 128, raw.size // (H // 128))[:, r0:r1]
+            s = h2f(sraw)
         else:
             s = h2f(W.t["head.s"][r0:r1])
-        out[:, r0:r1] = gemm(x, w, s)
+        if xs is not None:
+            wb = W.t["head.w"][r0 * H:r1 * H].reshape(r1 - r0, H)
+            out[:, r0:r1] = orc.gemm_x8(np.asarray(x).astype(np.int8), xs, wb, np.ascontiguousarray(sraw))
+            continue
+        w = (W.t["head.w"][r0 * H:r1 * H].astype(np.int16) - 128).reshape(r1 - r0, H).astype(np.float64)
+        out[:, r0:r1] = W.mm(x, w, s)
     return out
 
 
@@ -388,7 +416,7 @@ def verify(W, C, st, tokens, rope, rope_swa=None):
         taps[tap_of[last]] = h
     C.taps = taps
     hw, hs = W.gemm_w("head", d.vocab, H)
-    return gemm(x, hw, hs)
+    return W.mm(x, hw, hs)
 
 
 def conv_state(C, layer, pos, km1, H):

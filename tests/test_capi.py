@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_size_queries_and_state_layout():
     host = load_host()
     lib = host.lib()
-    assert lib.dspark_abi_version() == 4
+    assert lib.dspark_abi_version() == 5
     assert lib.dspark_page_tokens() == 32
     assert lib.dspark_max_tokens() == 64
     # 22 scalars (dspark.hip:134-157, dspark.go:52-77 sTokens == 22) then tokens[64]

@@ -55,10 +55,18 @@ MID64 = dict(MID, block=64, max_drafts=63)  # four token blocks: the GEMMs' X pe
 # attention layers and the drafter ring, and int8 weights with per-128-column group scales (weights.Pack), in the
 # reference's attention geometry 16/4/128 (hidden 2048) with small FFNs.
 REF_REC = dict(REF_SMALL, hidden=2048, q_heads=16, kv_heads=4, ffn=1024, draft_ffn=1024, kv_format=1, weight_format=1)
+# The same with the reference's default activation format: every GEMM input as int8 per 16 columns (LFM3_X8)
+REF_X8 = dict(REF_REC, x_format=1)
 REL = 1e-3  # the bar of every value comparison in the round parity test (see the module docstring)
 REL_REC = 5e-3  # the same bar with int8 K/V records
+# The bar with int8 x (LFM3_X8): an input that GPU and oracle hold one fp16 step or one fp32 rounding apart takes codes
+# one step apart (1/127 of its 16-column piece's range) when it sits near a code midpoint, about 50 times the fp16
+# step; carried through every layer of the round (measured: cropped head 1.1e-2 x scale). Layer by layer, from the
+# GPU's own inputs, tests/test_gpu_fullsize.py holds int8 x to 2e-2 per layer output.
+REL_X8 = 2.5e-2
 GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE, "mid": MID,
-              "mid24": MID24, "mid33": MID33, "mid64": MID64, "ref_rec": REF_REC, "small_ctxlo": SMALL}
+              "mid24": MID24, "mid33": MID33, "mid64": MID64, "ref_rec": REF_REC, "small_ctxlo": SMALL,
+              "ref_x8": REF_X8}
 STOP_ANCHOR = 17
 
 
@@ -78,7 +86,7 @@ def make_weights(eng, desc, seed, stop_half=False):
                                                            "h0", "h1", "x16", "mix", "q16", "gate", "y16", "vout", "a16",
                                                            "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys",
                                                            "ws_", "rope", "ring_table", "tap_x", "plant", "conv_state",
-                                                           "trace", "debug_layers"))]
+                                                           "trace", "debug_layers", "x_scales"))]
     for n in weight_names:
         nb = sizes[n]
         if n.endswith(".w") and not n.endswith("conv.w"):
@@ -195,7 +203,7 @@ def near_tie_ok(values, got, want, rel=1e-3):
 @pytest.mark.parametrize("geom,seed", [("small", 11), ("small", 12), ("ref_small", 13), ("small_stop", 14),
                                        ("small_stop", 15), ("small_stop", 16), ("small_wide", 17), ("mid", 18),
                                        ("mid", 19), ("mid24", 20), ("mid33", 27), ("mid64", 30), ("ref_rec", 28),
-                                       ("small_ctxlo", 31)])
+                                       ("small_ctxlo", 31), ("ref_x8", 32)])
 def test_engine_round_matches_oracle(dev, orc, geom, seed):
     torch = dev
     host = load_host()
@@ -270,7 +278,7 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
     scale = np.max(np.abs(base[:, :N + 1]))
     err = np.max(np.abs(base_gpu[:, :N + 1] - base[:, :N + 1]))
     print(f"base max-abs {err:.3e} (scale {scale:.2f})", flush=True)
-    rel = REL_REC if desc.kv_format == 1 else REL
+    rel = REL_X8 if desc.x_format == 1 else (REL_REC if desc.kv_format == 1 else REL)
     assert err <= rel * scale
 
     # Markov drafts from the GPU's own base: exact up to near ties
@@ -301,7 +309,7 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
     ok = orc.keys_to_tokens(orc.verify_argmax(logits.astype(np.float32), seen, np.array(verified[:MV], np.int32)))
     for t in range(st.M):
         g = int(orc.keys_to_tokens(keys_gpu[t:t + 1])[0])
-        assert near_tie_ok(logits[t], g, int(ok[t])), (t, g, ok[t])
+        assert near_tie_ok(logits[t], g, int(ok[t]), max(1e-3, rel)), (t, g, ok[t])
     # commit books: the oracle's accept_commit on the same keys
     ost = orc.new_state(**dict(st0, tokens=verified[:st.M]))
     out = np.zeros(1024, np.int32)
@@ -329,7 +337,7 @@ def _greedy_chain(eng, torch, st0, n):
 
 @pytest.mark.parametrize("geom,seed,wrong", [("small", 21, ()), ("small", 22, (3, 10, 11, 20)), ("ref_small", 23, ()),
                                              ("ref_small", 24, (0, 5, 13, 14)), ("mid", 25, (2, 9)),
-                                             ("ref_rec", 29, (4, 12))])
+                                             ("ref_rec", 29, (4, 12)), ("ref_x8", 33, (3, 9))])
 def test_planted_rounds_commit_the_greedy_chain(dev, geom, seed, wrong):
     """Speculative rounds commit exactly the target's greedy chain, whatever the drafts: with drafts planted from the
     chain (force_m = -1), every round commits its drafts' accepted prefix plus the target's own next token. All
