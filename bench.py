@@ -532,18 +532,23 @@ def conv_restore(eng, rings):
         eng.upload(nm, buf)
 
 
-def planted_pass(eng, torch, a0, anchor, n_rounds, rings0):
-    """Untimed: n_rounds planted rounds from a0 (conv rings as at a0); returns the tokens they emitted."""
+def planted_pass(eng, torch, a0, anchor, n_rounds, rings0, cover=0):
+    """Untimed: n_rounds planted rounds from a0 (conv rings as at a0), then more until `cover` tokens are out; returns
+    the tokens they emitted."""
     import numpy as np
     conv_restore(eng, rings0)
     engine_state(eng, a0, anchor)
     for _ in range(n_rounds):
         eng.round(-1, a0)
     torch.cuda.synchronize()
+    while eng.state().count < cover:
+        for _ in range(8):
+            eng.round(-1, a0)
+        torch.cuda.synchronize()
     return eng.download("out_tokens", np.int32)[:eng.state().count].copy()
 
 
-def settle_chain(eng, host, torch, desc, a0, anchor, need, p, n_rounds, rings0, tries=6):
+def settle_chain(eng, host, torch, desc, a0, anchor, need, p, n_rounds, rings0, cover=0, tries=8):
     """The greedy chain the planted drafts replay, checked against what planted rounds actually emit.
 
     Planted rounds emit the target's own greedy continuation under their own arithmetic (accepted drafts equal the
@@ -552,13 +557,15 @@ def settle_chain(eng, host, torch, desc, a0, anchor, need, p, n_rounds, rings0, 
     order), the emitted tokens leave the chain at some index and every later planted draft is wrong. So: plant, run
     the pass, and where it left the chain take its tokens, extend them by one-token rounds from where the pass
     stopped, plant again; until a pass emits the chain itself. The timed rounds repeat the last pass exactly (every
-    reduction has a fixed order), so their acceptance follows the planted draws. Returns (chain, re-plants)."""
+    reduction has a fixed order), so their acceptance follows the planted draws; the pass runs on until `cover` tokens
+    are out, so the launch path's rounds (the same rounds from the same start) are covered too. Returns (chain,
+    re-plants)."""
     import numpy as np
     chain = greedy_chain(eng, host, torch, a0, anchor, need)
     fixes = 0
     for _ in range(tries):
         plant_drafts(eng, chain, a0, p, 7, desc.vocab)
-        out = planted_pass(eng, torch, a0, anchor, n_rounds, rings0)
+        out = planted_pass(eng, torch, a0, anchor, n_rounds, rings0, cover)
         n = len(out)
         if np.array_equal(out, chain[:n]):
             break
@@ -627,8 +634,10 @@ def bench_engine(args, host, torch, workload):
         if key not in cache:
             for k in list(cache):
                 cache.pop(k)[1].close()
-            fmt = 1 if args.ref_formats == "reference" else 0
-            desc_ = host.ref_desc(block=block, max_drafts=max_drafts, kv_format=fmt, weight_format=fmt) if ref else None
+            fmt = 0 if args.ref_formats == "fp16" else 1
+            x8 = 1 if args.ref_formats == "reference" else 0
+            desc_ = (host.ref_desc(block=block, max_drafts=max_drafts, kv_format=fmt, weight_format=fmt, x_format=x8)
+                     if ref else None)
             cache[key] = engine_setup(host, torch, ctx, block, 20261201 + ctx + block, desc_)
         desc, eng = cache[key]
         a0, anchor = ctx, 17
@@ -641,9 +650,10 @@ def bench_engine(args, host, torch, workload):
         else:
             p = plant if not isinstance(plant, tuple) else p_for_tau(plant[1], desc.max_drafts)
             n_launch = (1, 4) if isinstance(plant, tuple) else (0, 0)  # the tiers also time the drop-in launch path
-            need = max((warm + rounds + 1) * block + 2, (sum(n_launch) + 1) * 32 + 2 * block)
+            cover = (sum(n_launch) + 1) * 32 + block  # positions the launches reach
+            need = max((warm + rounds + 1) * block + 2, cover + 8 * block + 2)
             rings0 = conv_snapshot(eng)
-            chain, fixes = settle_chain(eng, host, torch, desc, a0, anchor, need, p, warm + rounds, rings0)
+            chain, fixes = settle_chain(eng, host, torch, desc, a0, anchor, need, p, warm + rounds, rings0, cover)
             ms, committed, accs, st = run_rounds(eng, torch, -1, a0, anchor, warm, rounds)
             rec["planted_p"] = round(p, 4)
             rec["planted_tau_expected"] = round(1 + sum(p ** k for k in range(1, desc.max_drafts + 1)), 3)
@@ -674,9 +684,11 @@ def bench_engine(args, host, torch, workload):
         print(json.dumps(rec), file=sys.stderr, flush=True)
     for k in list(cache):
         cache.pop(k)[1].close()
-    recf = ref and args.ref_formats == "reference"
+    recf = ref and args.ref_formats != "fp16"
+    xf = ("int8 GEMM inputs per 16 columns (LFM3_X8, the reference's default build)" if args.ref_formats == "reference"
+          else "fp16 GEMM inputs (the reference's LFM3_F16 build)")
     model = ("reference geometry: 24 layers (13 conv k=7 / 6 full / 5 sliding-256 attention, 16/4/128), FFN 7680, "
-             "vocab 128000, 3-layer drafter; " + ("the reference's int8 K/V records and per-128-column weight scales"
+             "vocab 128000, 3-layer drafter; " + (f"the reference's int8 K/V records and per-128-column weight scales, {xf}"
                                                   if recf else "fp16 K/V pages and per-row weight scales") if ref
              else "C4 geometry")
     kv = ("int8 K/V records (codes uniform in [-127, 127], scales 1/40)" if recf else "N(0,1) fp16 KV caches")
@@ -711,9 +723,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5", "tiers", "ref", "copy", "attn", "rec"])
-    ap.add_argument("--ref-formats", default="reference", choices=["reference", "fp16"],
-                    help="ref workload: the reference's storage formats (int8 K/V records, per-128-column weight "
-                         "scales) or fp16 K/V pages with per-row scales")
+    ap.add_argument("--ref-formats", default="reference", choices=["reference", "reference-f16x", "fp16"],
+                    help="ref workload: the reference's default build (int8 K/V records, per-128-column weight "
+                         "scales, int8 GEMM inputs per 16 columns), the same with fp16 GEMM inputs (its LFM3_F16 "
+                         "build), or fp16 K/V pages with per-row scales")
     ap.add_argument("--tiers", default="", help="tiers / ref workloads: comma-separated contexts out of 1024, 32768, "
                                                   "131072 (default all three)")
     ap.add_argument("--ctx", type=int, default=131072, help="attn workload: context (keys before the block)")
@@ -774,8 +787,8 @@ def main():
                     "accepted, so its time does not depend on the draws; tok_s is the rate of the planted draws; "
                     "launch_* time the drop-in path (dspark_engine_launch, draftLaunch's loop: one launch per "
                     "32-position block, State read back by the host after each) on the same planted chain"}
-        # The same tiers on the reference model's geometry, draft policy and storage formats (int8 K/V records,
-        # per-128-column weight scales): the configuration the MI50 numbers were measured on.
+        # The same tiers on the reference model's geometry, draft policy and default build (int8 K/V records,
+        # per-128-column weight scales, int8 GEMM inputs): the configuration the MI50 numbers were measured on.
         rargs = argparse.Namespace(**vars(targs))
         rargs.ref_formats = "reference"
         rtiers = bench_engine(rargs, host, torch, "ref")
@@ -786,6 +799,16 @@ def main():
                                          "replants", "launch_tok_s", "launch_tok_s_at_mi50_tau",
                                          "launch_round_time_ratio", "launch")}
                       for c in rtiers["cases"]]}
+        # The same on the reference's LFM3_F16 build (fp16 GEMM inputs): on MI355X the int8-x products (one masked
+        # MFMA pair and a scaled add per 16-column piece) lengthen the latency-bound GEMMs
+        fargs = argparse.Namespace(**vars(targs))
+        fargs.ref_formats = "reference-f16x"
+        ftiers = bench_engine(fargs, host, torch, "ref")
+        res["headline_ref_f16x_tok_s"] = {
+            "model": ftiers["metric"], "rounds": targs.steps, "warmup": targs.warmup,
+            "tiers": [{k: c[k] for k in ("ctx", "max_drafts", "ms_per_round", "tokens_per_round", "tok_s",
+                                         "tok_s_at_mi50_tau", "vs_mi50", "launch_tok_s", "launch_round_time_ratio")}
+                      for c in ftiers["cases"]]}
         res["c5_attention"] = c5_attention_fields(args, host, torch)
         res["ref_int8_record_attention"] = rec_attention_fields(args, host, torch)
     if not args.no_cpu:
