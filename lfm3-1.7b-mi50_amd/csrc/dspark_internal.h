@@ -237,8 +237,9 @@ int gemm_groups(const GemmPlan& pl, int N);                  // row groups (<= G
 uint32_t* gemm_ws_counters(void* ws);
 float* gemm_ws_partials(void* ws);
 int gemm_launch(GemmParams& p, bool i8, hipStream_t s);
-// Tile-major copy of an int8 weight [N][K] (the layout GemmParams::tiled reads), N % 16 == 0, K % 64 == 0.
-int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s);
+// Tile-major copy of an int8 weight [N][K] (the layout GemmParams::tiled reads), N % 16 == 0, K % 64 == 0; x8: the
+// order of the int8-x products (LFM3_X8), piece-major within a lane's 16 bytes.
+int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s, int x8 = 0);
 
 size_t verify_argmax_ws(int M, int V);
 

@@ -938,7 +938,7 @@ namespace {
 int prepare(dspark_engine* e, hipStream_t s, bool all) {
   for (auto& t : e->tiles) {
     if (!t.dirty && !all) continue;
-    const int rc = gemm_tile_launch(t.src, t.dst, t.N, t.K, s);
+    const int rc = gemm_tile_launch(t.src, t.dst, t.N, t.K, s, e->d.x_format == 1 ? 1 : 0);
     if (rc) return rc;
     t.dirty = false;
   }

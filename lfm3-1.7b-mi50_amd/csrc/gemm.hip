@@ -444,57 +444,99 @@ __device__ __forceinline__ void gscale_products(f32x4& acc, const u32x2 (&gsr)[C
 }
 
 // LFM3_X8 (the reference's default build, dspark.hip:24-26; unit_dot_r 541-566): the GEMM input as int8 codes with one
-// fp32 scale per 16-column piece. Lane (g, n) holds token n's piece g of a 64-column chunk (x0: columns 16 g .. + 7,
-// x1: 16 g + 8 .. + 15), so a piece never leaves its lane. p.x8 = 1: x is fp16 and the lane quantizes its piece as
-// x_fill does (883-904): s = max(max|x| / 127, 1e-20), codes rint(x * rcp(s)); p.x8 = 2: x already holds the codes
-// (integer-valued halves, written by the norm kernel) and p.xsc the scales [token][K / 16].
-__device__ __forceinline__ float x8_quantize(u32x4& x0, u32x4& x1) {
-  half8 h0 = as_half8(x0), h1 = as_half8(x1);
-  float m = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) m = fmaxf(m, fmaxf(fabsf((float)h0[j]), fabsf((float)h1[j])));
-  const float sc = fmaxf(__fdiv_rn(m, 127.f), 1e-20f);
-  const float inv = __builtin_amdgcn_rcpf(sc);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    h0[j] = (_Float16)rintf((float)h0[j] * inv);
-    h1[j] = (_Float16)rintf((float)h1[j] * inv);
+// fp32 scale per 16-column piece, multiplied piece by piece. On v_mfma_f32_16x16x16_f16 (K = 16) one product is one
+// piece: lane (g, n) gives row n's / token n's columns 16 p + 4 g .. + 3 of piece p. The weight tiles of an int8-x
+// engine are laid out for it (gemm_tile_kernel, x8: byte b of lane (g, n) is column 16 (b / 4) + 4 g + b % 4 of the
+// 64-column chunk, so a[p / 2] halves 4 (p % 2) .. + 3 are piece p's four weights); row-major weights (the C ABI) are
+// gathered in the same order. Codes are integer-valued halves, so each product is the piece's exact integer dot
+// (|dot| <= 16 * 127 * 127 < 2^24). p.x8 = 1: x is fp16 and each piece is quantized by the four lanes that hold it, as
+// x_fill does (883-904): s = max(max|x| / 127, 1e-20), codes rint(x * rcp(s)); p.x8 = 2: x holds the codes (the norm
+// kernel's output) and p.xsc the scales [token][K / 16].
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 mfma16x16x16(half4v a, half4v b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Token n's 4 halves of piece p of chunk c (lane (g, n)): operand-order x at p.x (xop), or row-major.
+struct X8Src {
+  const _Float16* base;  // this lane's first 4 halves of chunk 0, piece 0
+  size_t cstride, pstride;
+};
+__device__ __forceinline__ X8Src x8_src(const GemmParams& p, int g, int n) {
+  if (p.xop) {
+    // xop_elem(n, 64 c + 16 p + 4 g + j) = (((c tbs) 2 + g / 2) 64 + 16 p + n) 8 + 4 (g % 2) + j
+    return X8Src{p.x + ((size_t)(g >> 1) * 64 + n) * 8 + 4 * (g & 1), (size_t)p.xop * 1024, 128};
   }
-  __builtin_memcpy(&x0, &h0, 16);
-  __builtin_memcpy(&x1, &h1, 16);
+  return X8Src{p.x + (size_t)min(n, p.M - 1) * p.K + 4 * g, 64, 16};
+}
+
+// Per-half max of two packed pairs of fp16 magnitudes: for non-negative halves the order of the bit patterns as
+// unsigned integers is the order of the values.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pmax_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+// Max over the lanes n, n + 16, n + 32, n + 48 of a packed pair, by the two VALU half-wave swaps (no LDS-unit shuffle).
+__device__ __forceinline__ uint32_t pmax_u16_lanes(uint32_t v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  v = pmax_u16(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return pmax_u16(b[0], b[1]);
+}
+
+// p.x8 == 1: quantize the lane's 4 pieces (each piece's 16 values sit in the lanes (g', n), g' = 0..3); returns the
+// piece scales and turns xq into codes. max|x| is taken on the fp16 bit patterns, two pieces per packed word. m / 127
+// is the IEEE quotient: q0 = m * fl(1/127) corrected by one residual step, fl(q0 + fma(-q0, 127, m) * fl(1/127)),
+// equals fl(m / 127) for every finite fp16 m (checked exhaustively over all 31743 positive values).
+__device__ __forceinline__ f32x4 x8_quantize(u32x2 (&xq)[4]) {
+  uint32_t pm[4];
+#pragma unroll
+  for (int pc = 0; pc < 4; ++pc) pm[pc] = pmax_u16(xq[pc][0] & 0x7fff7fffu, xq[pc][1] & 0x7fff7fffu);
+  uint32_t m2[2];  // pieces 2 k (low half) and 2 k + 1 (high half)
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    m2[k] = pmax_u16_lanes(pmax_u16(__builtin_amdgcn_perm(pm[2 * k + 1], pm[2 * k], 0x05040100u),
+                                    __builtin_amdgcn_perm(pm[2 * k + 1], pm[2 * k], 0x07060302u)));
+  f32x4 sc;
+  const float r127 = 1.f / 127.f;
+#pragma unroll
+  for (int pc = 0; pc < 4; ++pc) {
+    half4v h = __builtin_bit_cast(half4v, xq[pc]);
+    const float m = (float)__builtin_bit_cast(_Float16, (uint16_t)(m2[pc >> 1] >> (16 * (pc & 1))));
+    const float q0 = m * r127;
+    const float s = fmaxf(fmaf(fmaf(-q0, 127.f, m), r127, q0), 1e-20f);
+    const float inv = __builtin_amdgcn_rcpf(s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = (_Float16)rintf((float)h[j] * inv);
+    xq[pc] = __builtin_bit_cast(u32x2, h);
+    sc[pc] = s;
+  }
   return sc;
 }
 
-// One chunk's products under LFM3_X8: for each piece g' the integer dot of the strip's rows with token n's codes of
-// the piece (two MFMAs with every lane group but g' zeroed in B; exact in fp32, |dot| <= 16 * 127 * 127), then
-// acc[r] += dot * fp32(ws[r] * xs4[g']) as unit_dot_r scales a piece (ws: the lane's 4 rows' scales of the chunk's
-// 128-column group, xs4: token n's 4 piece scales of the chunk).
-__device__ __forceinline__ void x8_products(f32x4& acc, const half8 (&a)[2], u32x4 x0, u32x4 x1, f32x4 xs4, half4 ws,
-                                            int g) {
-  const u32x4 zero = {0, 0, 0, 0};
+// One chunk under LFM3_X8: accg[r] += dot_p[r] * xs[p] over its 4 pieces (accg: the 128-column group's sum, scaled by
+// the lane's 4 rows' group scales once the group is done -- the reference scales each piece by fp32(ws * xs), one
+// rounding apart).
+__device__ __forceinline__ void x8_chunk(f32x4& accg, const half8 (&a)[2], const u32x2 (&xq)[4], f32x4 xs4) {
   const f32x4 z4 = {0, 0, 0, 0};
 #pragma unroll
-  for (int gp = 0; gp < 4; ++gp) {
-    const bool on = g == gp;
-    f32x4 t = mfma16x16x32(a[0], as_half8(on ? x0 : zero), z4);
-    t = mfma16x16x32(a[1], as_half8(on ? x1 : zero), t);
+  for (int pc = 0; pc < 4; ++pc) {
+    const half8 ah = a[pc >> 1];
+    const half4v ap = (pc & 1) ? half4v{ah[4], ah[5], ah[6], ah[7]} : half4v{ah[0], ah[1], ah[2], ah[3]};
+    const f32x4 t = mfma16x16x16(ap, __builtin_bit_cast(half4v, xq[pc]), z4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = fmaf((float)ws[r] * xs4[gp], t[r], acc[r]);
+    for (int r = 0; r < 4; ++r) accg[r] = fmaf(t[r], xs4[pc], accg[r]);
   }
 }
 
-// Token n's 4 piece scales of chunk c: loaded (p.x8 == 2) or, after x8_quantize, gathered from the lanes (g', n).
+// Token n's 4 piece scales of chunk c (p.x8 == 2).
 __device__ __forceinline__ f32x4 x8_scales_load(const GemmParams& p, int n, int c) {
   return ldg(reinterpret_cast<const f32x4*>(p.xsc + (size_t)min(n, p.M - 1) * p.xsc_row + 4 * c));
 }
-__device__ __forceinline__ f32x4 x8_scales_gather(float sc, int n) {
-  f32x4 v;
-#pragma unroll
-  for (int gp = 0; gp < 4; ++gp) v[gp] = __shfl(sc, 16 * gp + n);
-  return v;
-}
 
-template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, bool X8 = false>
+// X8: 0 fp16 x; 1 int8 x quantized as it is loaded (p.x8 == 1); 2 int8 codes + scales given (p.x8 == 2).
+template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, int X8 = 0>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   static_assert(!GS || (TB == 1 && I8 && CPW % 2 == 0), "group scales: one token block, int8 weights, whole groups");
   static_assert(!X8 || GS, "int8 x goes with group scales");
@@ -534,7 +576,12 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
       const int c = min(cb + i, max(c1, 1) - 1);
-      if (I8) {
+      if (X8 && !tiled) {
+        // row-major weights in the int8-x tile order: byte b = column 16 (b / 4) + 4 g + b % 4 of the chunk
+        const uint8_t* rp = reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K + (size_t)c * 64 + 4 * g;
+        w[i][0] = u32x4{ldg_nt(reinterpret_cast<const uint32_t*>(rp)), ldg_nt(reinterpret_cast<const uint32_t*>(rp + 16)),
+                        ldg_nt(reinterpret_cast<const uint32_t*>(rp + 32)), ldg_nt(reinterpret_cast<const uint32_t*>(rp + 48))};
+      } else if (I8) {
         w[i][0] = ldg_nt(reinterpret_cast<const u32x4*>(wrow + (size_t)c * cstride));
       } else {
         const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + 2 * c * 64 + 16 * g);
@@ -563,32 +610,45 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     // compiler's wait for the previous iteration's loads would also hold the first batch back behind the flag load.
     // Token block tb of chunk c (operand order, TB > 1 needs it): the next 1 KB block pair, tb * 1024 halves on.
     auto batch = [&](int cb) {
-      u32x4 xb[CPW][TB][2];
+      u32x4 xb[X8 ? 1 : CPW][TB][2];
+      u32x2 xq[X8 ? CPW : 1][4];
       u32x2 gsr[GS ? CPW / 2 : 1];
       f32x4 xsl[X8 ? CPW : 1];
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = min(cb + i, c1 - 1);
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-          xb[i][tb][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024));
-          xb[i][tb][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024 + xhs));
-        }
         if constexpr (X8) {
-          if (p.x8 == 2) xsl[i] = x8_scales_load(p, n, c);
+          const X8Src xsrc = x8_src(p, g, n);
+#pragma unroll
+          for (int pc = 0; pc < 4; ++pc)
+            xq[i][pc] = ldg(reinterpret_cast<const u32x2*>(xsrc.base + (size_t)c * xsrc.cstride + pc * xsrc.pstride));
+          if (X8 == 2) xsl[i] = x8_scales_load(p, n, c);
+        } else {
+#pragma unroll
+          for (int tb = 0; tb < TB; ++tb) {
+            xb[i][tb][0] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024));
+            xb[i][tb][1] = ldg(reinterpret_cast<const u32x4*>(xb0 + (size_t)c * xcs + tb * 1024 + xhs));
+          }
         }
       }
       if constexpr (GS) gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
       load(w, cb);
       if constexpr (X8) {
+        f32x4 accg = f32x4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
           if (cb + i < c1) {
             half8 a[2];
             weights(w[i], a);
-            u32x4 x0 = xb[i][0][0], x1 = xb[i][0][1];
-            const f32x4 xs4 = p.x8 == 2 ? xsl[i] : x8_scales_gather(x8_quantize(x0, x1), n);
-            x8_products(acc[0], a, x0, x1, xs4, __builtin_bit_cast(half4, gsr[i >> 1]), g);
+            const f32x4 xs4 = X8 == 2 ? xsl[i] : x8_quantize(xq[i]);
+            x8_chunk(accg, a, xq[i], xs4);
+          }
+          // a 128-column group ends after its second chunk (or the range's last): scale it by the rows' group scales
+          if ((i & 1) && cb + i - 1 < c1) {
+            const half4 ws = __builtin_bit_cast(half4, gsr[i >> 1]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[0][r] = fmaf(accg[r], (float)ws[r], acc[0][r]);
+            accg = f32x4{0, 0, 0, 0};
           }
         }
       } else if constexpr (GS) {
@@ -648,8 +708,8 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     // (token t's 4 pieces of the chunk), by the same kind of loads (issued before the weights, so the counted wait
     // below covers them)
     const f32x4* xsc_lds = reinterpret_cast<const f32x4*>(xs + (size_t)(b1 - b0) * 2 * 64);
-    if constexpr (X8) {
-      if (p.x8 == 2) {
+    if constexpr (X8 == 2) {
+      {
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)p.xsc, (short)0, (int)((size_t)p.M * p.xsc_row * 4), 0x00020000);
         const int bcs = b1 - b0;
@@ -673,19 +733,29 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
           gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
           load(w, cb);
         }
+        f32x4 accg = f32x4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
           if (cb + i < c1) {
             half8 a[2];
             weights(w[i], a);
-            const u32x4* xb = xs + ((size_t)(cb + i - b0) * 2) * 64;
-            u32x4 x0 = xb[lane], x1 = xb[64 + lane];
-            // chunk j's scales of token n sit at 16 (j - b0) + n... in 4-chunk rows of 64 lanes: row (j - b0) / 4,
-            // lane 16 ((j - b0) % 4) + n
+            // X^T in operand order: piece p's columns 4 g .. + 3 of token n are half g / 2 of lane 16 p + n's slot,
+            // halves 4 (g % 2) .. + 3
+            const char* xb = reinterpret_cast<const char*>(xs + ((size_t)(cb + i - b0) * 2) * 64);
+            u32x2 xq[4];
+#pragma unroll
+            for (int pc = 0; pc < 4; ++pc)
+              xq[pc] = *reinterpret_cast<const u32x2*>(xb + (((g >> 1) * 64 + 16 * pc + n) * 16 + 8 * (g & 1)));
+            // chunk j's scales of token n: 4-chunk rows of 64 lanes, row (j - b0) / 4, lane 16 ((j - b0) % 4) + n
             const int jr = cb + i - b0;
-            const f32x4 xs4 = p.x8 == 2 ? xsc_lds[(jr >> 2) * 64 + 16 * (jr & 3) + n]
-                                        : x8_scales_gather(x8_quantize(x0, x1), n);
-            x8_products(acc[0], a, x0, x1, xs4, __builtin_bit_cast(half4, gsr[i >> 1]), g);
+            const f32x4 xs4 = X8 == 2 ? xsc_lds[(jr >> 2) * 64 + 16 * (jr & 3) + n] : x8_quantize(xq);
+            x8_chunk(accg, a, xq, xs4);
+          }
+          if ((i & 1) && cb + i - 1 < c1) {
+            const half4 ws = __builtin_bit_cast(half4, gsr[i >> 1]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[0][r] = fmaf(accg[r], (float)ws[r], acc[0][r]);
+            accg = f32x4{0, 0, 0, 0};
           }
         }
       }
@@ -826,7 +896,9 @@ __global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int 
 
 // Tile-major copy of an int8 weight [N][K]: tile (strip, chunk) = 1 KB with row n, bytes 16 g .. 16 g + 15 of the
 // chunk at 16 (n + 16 g), i.e. lane l's operand at 16 l, so a wave's weight load is one contiguous 1 KB.
-__global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t* src, uint8_t* dst, int N, int K) {
+// x8: the int8-x order (byte b of lane (g, n) = column 16 (b / 4) + 4 g + b % 4 of the chunk: piece-major, for the
+// K = 16 products of gemm_sliced_kernel's X8 path); else lane (g, n) holds columns 16 g .. + 15.
+__global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t* src, uint8_t* dst, int N, int K, int x8) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece of the destination
   if (i >= (size_t)N * K / 16) return;
   const int l = (int)(i % 64), n = l % 16, g = l / 16;
@@ -834,15 +906,22 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t* src, uint
   const int chunks = K / 64;
   const size_t strip = tile / chunks;
   const int c = (int)(tile % chunks);
-  *reinterpret_cast<u32x4*>(dst + 16 * i) =
-      ldg(reinterpret_cast<const u32x4*>(src + (strip * 16 + n) * (size_t)K + c * 64 + 16 * g));
+  const uint8_t* row = src + (strip * 16 + n) * (size_t)K + c * 64;
+  u32x4 v;
+  if (x8) {
+#pragma unroll
+    for (int pc = 0; pc < 4; ++pc) v[pc] = ldg(reinterpret_cast<const uint32_t*>(row + 16 * pc + 4 * g));
+  } else {
+    v = ldg(reinterpret_cast<const u32x4*>(row + 16 * g));
+  }
+  *reinterpret_cast<u32x4*>(dst + 16 * i) = v;
 }
 
-int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s) {
+int gemm_tile_launch(const void* src, void* dst, int N, int K, hipStream_t s, int x8) {
   if (N < 16 || N % 16 || K < 64 || K % 64) return DSPARK_EINVAL;
   const size_t pieces = (size_t)N * K / 16;
   hipLaunchKernelGGL(gemm_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), N, K);
+                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), N, K, x8);
   return (int)hipGetLastError();
 }
 
@@ -901,12 +980,21 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const int cpk = ((p.K / 64 + p.bands - 1) / p.bands + p.kw - 1) / p.kw;  // chunks per range (of the band's)
   if constexpr (I8 && TB == 1) {
     if (p.gscale) {  // group scales: X per wave, or X^T of the band in LDS at once (gemm_launch checked)
-      if (p.x8) {  // int8 x (LFM3_X8)
+      if (p.x8 == 1) {  // int8 x (LFM3_X8), quantized as it is loaded
         if (gemm_sliced_xd(p, I8)) {
-          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, true>), grid, block, lds, s, p);
+          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, 1>), grid, block, lds, s, p);
         } else {
-          allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, true>, lds);
-          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, true>), grid, block, lds, s, p);
+          allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, 1>, lds);
+          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, 1>), grid, block, lds, s, p);
+        }
+        return;
+      }
+      if (p.x8 == 2) {  // int8 codes + scales from the norm kernel
+        if (gemm_sliced_xd(p, I8)) {
+          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, 2>), grid, block, lds, s, p);
+        } else {
+          allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, 2>, lds);
+          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, 2>), grid, block, lds, s, p);
         }
         return;
       }
