@@ -681,12 +681,27 @@ __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) 
   float scale = l > 0.f ? 1.f / l : 0.f;
   const int t = row / p.G, qh = h * p.G + row % p.G;
   if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * p.QH + qh)));
-  acc *= scale;
+  {
+#pragma clang fp contract(off)  // the fp16 output is the fp32 output rounded (no product fused into the conversion)
+    acc *= scale;
+  }
   const size_t idx = ((size_t)t * p.QH + qh) * D + 4 * q;
   if (p.out16) {
     half4 hv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) hv[i] = (_Float16)acc[i];
+    if (p.out_sc) {
+      // LFM3_X8 output: a 16-dim piece is a quad of lanes (q = 4 k .. 4 k + 3; Q is a multiple of 4 and every lane
+      // below Q is live)
+      uint32_t mb = max(max(x8_mag_bits(hv[0]), x8_mag_bits(hv[1])), max(x8_mag_bits(hv[2]), x8_mag_bits(hv[3])));
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1));
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2));
+      const float sc = x8_piece_scale(x8_mag_value(mb));
+      const float inv = __builtin_amdgcn_rcpf(sc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hv[i] = x8_code(hv[i], inv);
+      if ((q & 3) == 0) p.out_sc[(size_t)t * p.out_sc_row + (qh * D + 4 * q) / 16] = sc;
+    }
     *reinterpret_cast<half4*>(p.out16 + (p.out_op ? xop_elem(t, qh * D + 4 * q, p.out_op) : idx)) = hv;
   }
   if (p.out32) *reinterpret_cast<f32x4*>(p.out32 + idx) = acc;

@@ -26,6 +26,10 @@ struct AttnParams {
   f32x2_t* part_ml;  // [KVH][RG][R][S] (max, sum); max = -inf when the split saw no key of the row
   _Float16* out16;            // [M][QH][D], or operand order (xop_elem, column qh D + d) when out_op > 0
   float* out32;
+  // LFM3_X8: out16 receives the int8 codes of the fp16 outputs (integer-valued halves: what the next GEMM would make of
+  // them as it loads them) and out_sc their scales, piece c / 16 of output column c = qh D + d at t out_sc_row + c / 16
+  float* out_sc;
+  int out_sc_row;
   const float* gate;
   int out_op;                 // > 0: out16 in the verify GEMM's X operand order with out_op token blocks
   int M, QH, KVH, G;
@@ -181,6 +185,37 @@ __device__ __forceinline__ int state_word_load(const dspark_state* st, int off) 
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
+// fp16 of the exact product a b, rounded once (what fp16(a b) computed in float64 gives): the fp32 product rounded to
+// odd -- the nearest-even product moved one step toward the exact one when it is inexact and even (the residual from
+// an fma) -- then rounded to nearest-even fp16; rounding to odd at 24 bits before rounding at 11 is exact rounding.
+// Written out so that every epilogue rounds the same way, whether or not the compiler would fuse the product into
+// the conversion.
+__device__ __forceinline__ _Float16 f16_product(float a, float b) {
+  const float p = a * b;
+  const float e = fmaf(a, b, -p);
+  uint32_t u = __builtin_bit_cast(uint32_t, p);
+  if ((e > 0.f || e < 0.f) && !(u & 1u) && (p > 0.f || p < 0.f)) u += (e > 0.f) == (p > 0.f) ? 1u : 0xffffffffu;
+  return (_Float16)__builtin_bit_cast(float, u);
+}
+
+// ---------------------------------------------------------------- LFM3_X8 pieces of fp16 values
+// The scale of a 16-value piece whose largest magnitude is the finite fp16 value m (x_fill, kernels/dspark.hip:883-904):
+// max(m / 127, 1e-20), with m / 127 taken as q0 = fl(m r), r = fl(1 / 127), corrected by one residual step,
+// fl(q0 + fl(m - q0 127) r) -- equal to the IEEE quotient for every finite fp16 m.
+__device__ __forceinline__ float x8_piece_scale(float m) {
+  const float r127 = 1.f / 127.f;
+  const float q0 = m * r127;
+  return fmaxf(fmaf(fmaf(-q0, 127.f, m), r127, q0), 1e-20f);
+}
+// |h| of an fp16 value as its bit pattern (for non-negative halves the unsigned order of the patterns is the order of
+// the values, so maxima can be taken on integers).
+__device__ __forceinline__ uint32_t x8_mag_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h) & 0x7fffu; }
+__device__ __forceinline__ float x8_mag_value(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+// x's code at inv = rcp(its piece's scale): rint(x * inv), an integer in [-127, 127], as a half.
+__device__ __forceinline__ _Float16 x8_code(_Float16 x, float inv) { return (_Float16)rintf((float)x * inv); }
+
 struct GemmParams {
   const struct ::dspark_state* st;  // when set, a stopped round (run == 0) skips the launch's work
   const _Float16* x;        // [M][K]
@@ -213,6 +248,11 @@ struct GemmParams {
   int x8;
   const float* xsc;
   int xsc_row;
+  // LFM3_X8 output (gated epilogue 1 of a K-sliced plan with an even number of strips per workgroup and one band, or
+  // GEMM_FUSE_CONV; group scales only): y16 receives the int8 codes of the fp16 outputs and ysc their scales,
+  // [token][ysc_row] with output column c's piece at t ysc_row + c / 16 (the next GEMM reads them with x8 = 2)
+  float* ysc;
+  int ysc_row;
   const _Float16* conv_w;   // [N/3][conv_k]
   _Float16* conv_ring;      // [CONV_RING][N/3]
   int conv_k;

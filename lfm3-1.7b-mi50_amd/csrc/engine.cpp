@@ -16,6 +16,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -114,6 +115,12 @@ struct dspark_engine {
         *taps = nullptr, *logits = nullptr, *base = nullptr, *gate = nullptr;
   _Float16 *x16 = nullptr, *q16 = nullptr, *y16 = nullptr, *a16 = nullptr;
   float* xsc = nullptr;  // x_format 1: the int8 codes' scales of the norm outputs in x16, [16 tbs][x_cols / 16]
+  // x_format 1: the scales of the codes the attention merge, the conv epilogue and the gated epilogue write into y16
+  // or a16 (each read by the next GEMM before the other is written), [16 tbs][y_cols / 16]
+  float* ysc = nullptr;
+  // whether those producers write codes (else the out and w2 GEMMs quantize y16 / a16 as they load them: the same codes
+  // and scales, so bit-identical rounds; DSPARK_X8_PRODUCER_CODES=0 at engine creation selects that form)
+  bool y_codes = false;
   uint64_t* keys = nullptr;  // [B] verify best, then [B] Markov best
   void* ws_attn = nullptr;
   size_t ws_attn_bytes = 0;
@@ -121,7 +128,7 @@ struct dspark_engine {
   size_t ws_gemm_bytes = 0;
   void* ws_argmax = nullptr;
   size_t ws_argmax_bytes = 0;
-  int x_cols = 0, mix_cols = 0, crop_n = 0;
+  int x_cols = 0, y_cols = 0, mix_cols = 0, crop_n = 0;
   int tbs = 1;  // 16-token blocks of the round: x16, y16 and a16 hold 16 tbs token rows in the GEMMs' X operand order
   int cus = 256;
   dspark_state host_st;  // launch-time uploads stay alive until the stream has consumed them
@@ -219,9 +226,13 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
 // `bands` (optional): in, the most output bands the caller adds (y32 holds that many [M][N] blocks); out, the bands
 // the plan wrote.
 // `xop` false: x is row-major [M][K] (prompt projection) instead of the round's operand order.
+// int8 x (x_format 1): x16 holds the norm kernel's codes (scales in xsc); `x_codes`: x (y16 or a16) holds the codes a
+// producer wrote (scales in ysc); any other x is fp16, quantized as it is loaded. `y_codes` (optional): in, whether
+// the fp16 output y16 should be written as codes + ysc scales; out, whether it was (the gated epilogue needs strip
+// pairs inside a workgroup, the conv epilogue always can).
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
          float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr, int* bands = nullptr,
-         bool xop = true) {
+         bool xop = true, bool x_codes = false, bool* y_codes = nullptr) {
   GemmParams p = {};
   p.st = e->ast;
   p.x = x;
@@ -238,10 +249,10 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.xop = xop ? e->tbs : 0;  // every GEMM of the round reads x16, y16 or a16
   p.yop = e->tbs;
   if (e->d.x_format == 1) {
-    // int8 x: x16 holds the norm kernel's codes and scales; other inputs (fp16) are quantized as they are loaded
-    p.x8 = (x == e->x16 && xop) ? 2 : 1;
-    p.xsc = e->xsc;
-    p.xsc_row = e->x_cols / 16;
+    const bool norm_codes = x == e->x16 && xop;
+    p.x8 = norm_codes || x_codes ? 2 : 1;
+    p.xsc = x_codes && !norm_codes ? e->ysc : e->xsc;
+    p.xsc_row = x_codes && !norm_codes ? e->y_cols / 16 : e->x_cols / 16;
   }
   int wpg_req = 0;
   if (fuse) {
@@ -255,6 +266,16 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   GemmPlan pl;
   gemm_plan(M, N, K, true, true, &pl, wpg_req, xop, bands ? *bands : 1, gs);
   if (bands) *bands = pl.bands;
+  if (y_codes) {
+    const bool can = e->y_codes && y16 &&
+                     (fuse ? fuse->fuse == GEMM_FUSE_CONV
+                           : epilogue == 1 && pl.kw > 0 && pl.wpg % 2 == 0 && pl.bands == 1 && N % 32 == 0);
+    *y_codes = *y_codes && can;
+    if (*y_codes) {
+      p.ysc = e->ysc;
+      p.ysc_row = e->y_cols / 16;
+    }
+  }
   p.bands = pl.bands;
   p.ksplit = pl.ksplit;
   p.wpg = pl.wpg;
@@ -311,6 +332,10 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
                                                : Lw.kv_pages * d.kv_heads * PAGE * d.head_dim * 2);
   p.out16 = e->y16;
   p.out_op = e->tbs;
+  if (e->y_codes) {  // int8 x: the merge writes codes + scales for the out projection
+    p.out_sc = e->ysc;
+    p.out_sc_row = e->y_cols / 16;
+  }
   p.gate = gate;
   p.M = M;
   p.QH = d.q_heads;
@@ -380,7 +405,9 @@ int gemm_mix_conv(dspark_engine* e, const LayerW& W, int M, hipStream_t s) {
   f.conv_w = W.conv_w;
   f.conv_ring = W.conv_ring;
   f.conv_k = e->d.conv_kernel;
-  return gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f);
+  bool codes = e->y_codes;  // int8 x: codes + scales for the out projection
+  return gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f, nullptr, true, false,
+              &codes);
 }
 
 // Output bands the round's norm kernels add (the w2, out and fc GEMMs may split K over that many workgroups).
@@ -433,6 +460,7 @@ int enqueue_context(dspark_engine* e, const _Float16* x_fc, bool x_op, hipStream
 int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, hipStream_t s) {
   const dspark_model_desc& d = e->d;
   const int B = e->B, H = d.hidden, MV = mv;
+  const bool x8 = e->y_codes;  // the attention merge and the conv epilogue write y16 as int8 codes + scales
   uint64_t* vbest = e->keys;
   uint64_t* mbest = e->keys + B;
   e->ast = e->st;
@@ -476,12 +504,14 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       CK(gemm_mix_qk(e, W, B, s));
       CK(attention(e, W, 1, plan_a, nullptr, B, s));
       int ob = ENGINE_BANDS;
-      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
+      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, x8));
       CK(resnorm(e, B, e->h[cur], e->vout, ob, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
-      CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
+      bool acodes = x8;
+      CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, nullptr, nullptr, true, false,
+              &acodes));
       w2b = ENGINE_BANDS;
-      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
+      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b, true, acodes));
     }
     CK(mark(e, DSPARK_TRACE_DRAFTER, s));
     CK(dump(e, d.draft_layers, e->h[cur], e->w2out, w2b, B, s));
@@ -531,12 +561,14 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       CK(attention(e, W, 0, plan_a, e->gate, MV, s));
     }
     int ob = ENGINE_BANDS;
-    CK(gemm(e, e->y16, MV, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob));
+    CK(gemm(e, e->y16, MV, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, x8));
     CK(resnorm(e, MV, e->h[cur], e->vout, ob, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
     cur ^= 1;
-    CK(gemm(e, e->x16, MV, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s));
+    bool acodes = x8;
+    CK(gemm(e, e->x16, MV, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, nullptr, nullptr, true, false,
+            &acodes));
     w2b = ENGINE_BANDS;
-    CK(gemm(e, e->a16, MV, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b));
+    CK(gemm(e, e->a16, MV, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b, true, acodes));
     CK(mark(e, DSPARK_TRACE_VERIFY_LAYER + i, s));
   }
   {
@@ -776,8 +808,15 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->h[1] = static_cast<float*>(e->alloc("h1", (size_t)B * H * 4, &err));
   e->tbs = (B + 15) / 16;
   e->x16 = h16("x16", (size_t)16 * e->tbs * e->x_cols);
-  if (d.x_format == 1)
+  e->y_cols = std::max(H, std::max(d.ffn, d.draft_ffn));
+  {
+    const char* v = std::getenv("DSPARK_X8_PRODUCER_CODES");
+    e->y_codes = d.x_format == 1 && !(v && v[0] == '0');
+  }
+  if (d.x_format == 1) {
     e->xsc = static_cast<float*>(e->alloc("x_scales", (size_t)16 * e->tbs * (e->x_cols / 16) * sizeof(float), &err));
+    e->ysc = static_cast<float*>(e->alloc("y_scales", (size_t)16 * e->tbs * (e->y_cols / 16) * sizeof(float), &err));
+  }
   e->mix = static_cast<float*>(e->alloc("mix", (size_t)B * e->mix_cols * 4, &err));
   e->q16 = h16("q16", (size_t)B * QH * D);
   e->gate = static_cast<float*>(e->alloc("gate", (size_t)B * QH * 4, &err));

@@ -43,8 +43,8 @@ __device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0,
   if (p.epilogue == 1) {
     // rows (2i, 2i+1) = (gate, up): h[t][r/2 + i] = fp16(silu(gate) * up); r/2 is even, so the pair is contiguous
     _Float16* y = p.y16 + (p.yop ? xop_elem(t, r / 2, p.yop) : (size_t)t * (p.N / 2) + r / 2);
-    y[0] = (_Float16)(silu_f(v[0]) * v[1]);
-    y[1] = (_Float16)(silu_f(v[2]) * v[3]);
+    y[0] = f16_product(silu_f(v[0]), v[1]);
+    y[1] = f16_product(silu_f(v[2]), v[3]);
     return;
   }
   if (p.y32) *reinterpret_cast<f32x4*>(p.y32 + (size_t)t * p.N + r) = v;
@@ -93,7 +93,7 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
         const int tt = t - (K - 1) + k;
         if (tt >= 0) {
           const float* m = tile + tt * RS + 3 * cl;
-          bx[k] = (float)(_Float16)(m[0] * m[2]);
+          bx[k] = (float)f16_product(m[0], m[2]);
           if (k == K - 1) {
             C = m[1];
             bx_t = bx[k];
@@ -111,7 +111,18 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
     for (int k = 0; k < KMAX; ++k)
       if (k < K - 1) conv = fmaf(w[k], bx[k], conv);
     p.conv_ring[(size_t)((a + t) & (CONV_RING - 1)) * H + c] = (_Float16)bx_t;
-    p.y16[p.yop ? xop_elem(t, c, p.yop) : (size_t)t * H + c] = (_Float16)(C * conv);
+    _Float16 y = f16_product(C, conv);
+    if (p.ysc) {
+      // LFM3_X8 output: the group's 16 channels are one piece, held by 16 aligned lanes (nch == 16, the workgroup a
+      // multiple of 16 threads: the host checked), all live or all skipped together
+      uint32_t mb = x8_mag_bits(y);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o));
+      const float sc = x8_piece_scale(x8_mag_value(mb));
+      y = x8_code(y, __builtin_amdgcn_rcpf(sc));
+      if (cl == 0) p.ysc[(size_t)t * p.ysc_row + c / 16] = sc;
+    }
+    p.y16[p.yop ? xop_elem(t, c, p.yop) : (size_t)t * H + c] = y;
   }
 }
 
@@ -486,9 +497,7 @@ __device__ __forceinline__ uint32_t pmax_u16_lanes(uint32_t v) {
 }
 
 // p.x8 == 1: quantize the lane's 4 pieces (each piece's 16 values sit in the lanes (g', n), g' = 0..3); returns the
-// piece scales and turns xq into codes. max|x| is taken on the fp16 bit patterns, two pieces per packed word. m / 127
-// is the IEEE quotient: q0 = m * fl(1/127) corrected by one residual step, fl(q0 + fma(-q0, 127, m) * fl(1/127)),
-// equals fl(m / 127) for every finite fp16 m (checked exhaustively over all 31743 positive values).
+// piece scales and turns xq into codes. max|x| is taken on the fp16 bit patterns, two pieces per packed word.
 __device__ __forceinline__ f32x4 x8_quantize(u32x2 (&xq)[4]) {
   uint32_t pm[4];
 #pragma unroll
@@ -499,13 +508,10 @@ __device__ __forceinline__ f32x4 x8_quantize(u32x2 (&xq)[4]) {
     m2[k] = pmax_u16_lanes(pmax_u16(__builtin_amdgcn_perm(pm[2 * k + 1], pm[2 * k], 0x05040100u),
                                     __builtin_amdgcn_perm(pm[2 * k + 1], pm[2 * k], 0x07060302u)));
   f32x4 sc;
-  const float r127 = 1.f / 127.f;
 #pragma unroll
   for (int pc = 0; pc < 4; ++pc) {
     half4v h = __builtin_bit_cast(half4v, xq[pc]);
-    const float m = (float)__builtin_bit_cast(_Float16, (uint16_t)(m2[pc >> 1] >> (16 * (pc & 1))));
-    const float q0 = m * r127;
-    const float s = fmaxf(fmaf(fmaf(-q0, 127.f, m), r127, q0), 1e-20f);
+    const float s = x8_piece_scale(x8_mag_value((m2[pc >> 1] >> (16 * (pc & 1))) & 0xffffu));
     const float inv = __builtin_amdgcn_rcpf(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) h[j] = (_Float16)rintf((float)h[j] * inv);
@@ -528,6 +534,30 @@ __device__ __forceinline__ void x8_chunk(f32x4& accg, const half8 (&a)[2], const
 #pragma unroll
     for (int r = 0; r < 4; ++r) accg[r] = fmaf(t[r], xs4[pc], accg[r]);
   }
+}
+
+// The gated epilogue (1) with LFM3_X8 output: h = fp16(silu(gate) up) as int8 codes + piece scales. Strip 2 i + e of
+// the workgroup's strips holds output columns 16 i + 8 e .. + 7 (its rows are 8 (gate, up) pairs), so piece i is
+// strips 2 i and 2 i + 1: each wave takes its 8 columns' max|h| per token, the pair meets in LDS, and each wave then
+// stores its codes (strip 2 i also the scale). Every wave of the workgroup calls this (both barriers); `holder`: the
+// wave holds strip `strip`'s finished sums (range 0, a live strip). ex: 16 S words of LDS no wave still reads.
+__device__ __forceinline__ void gemm_gated_x8_out(const GemmParams& p, f32x4 v, int strip, int s, bool holder, int lane,
+                                                  uint32_t* ex) {
+  const int n = lane & 15, g = lane >> 4;
+  const _Float16 y0 = f16_product(silu_f(v[0]), v[1]), y1 = f16_product(silu_f(v[2]), v[3]);  // gemm_store's values
+  const uint32_t mb = pmax_u16_lanes(max(x8_mag_bits(y0), x8_mag_bits(y1)));  // lanes (g', n): token n's 8 columns
+  __syncthreads();  // every wave is done with the LDS it used before
+  if (holder && g == 0) ex[16 * s + n] = mb;
+  __syncthreads();
+  if (!holder) return;
+  const float sc = x8_piece_scale(x8_mag_value(max(mb, ex[16 * (s ^ 1) + n])));
+  const float inv = __builtin_amdgcn_rcpf(sc);
+  const int t = n, c = strip * 8 + 2 * g;  // output columns c, c + 1 (c even: the pair is contiguous)
+  if (t >= p.M) return;
+  _Float16* y = p.y16 + (p.yop ? xop_elem(t, c, p.yop) : (size_t)t * (p.N / 2) + c);
+  y[0] = x8_code(y0, inv);
+  y[1] = x8_code(y1, inv);
+  if ((strip & 1) == 0 && g == 0) p.ysc[(size_t)t * p.ysc_row + strip / 2] = sc;
 }
 
 // Token n's 4 piece scales of chunk c (p.x8 == 2).
@@ -850,6 +880,12 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     gemm_group_epilogue<TB>(p, acc, grp, s, S, kq == 0, lane, reinterpret_cast<float*>(xs));
     return;
   }
+  if constexpr (GS) {
+    if (p.ysc && p.epilogue == 1) {  // the gated epilogue with int8-x output (the same for every wave)
+      gemm_gated_x8_out(p, acc[0], strip, s, kq == 0 && live, lane, reinterpret_cast<uint32_t*>(xs));
+      return;
+    }
+  }
   if (kq != 0 || !live) return;
   if (p.bands > 1) {  // band b's scaled sums go to y32 + b M N (the consumer adds the bands in order)
     GemmParams q = p;
@@ -961,7 +997,8 @@ static size_t gemm_sliced_lds_bytes(const GemmParams& p, bool i8) {
   if (x && p.x8 == 2) x += (size_t)(bc + 3) / 4 * 1024;  // the band's int8-x piece scales after X^T
   const size_t red = (size_t)(p.kw - 1) * p.wpg * tb * 1024;
   const size_t tile = p.fuse ? (size_t)tb * 16 * (16 * p.wpg + 4) * sizeof(float) : 0;
-  return std::max(x, std::max(red, tile));
+  const size_t ex = p.ysc && p.epilogue == 1 ? (size_t)16 * p.wpg * sizeof(uint32_t) : 0;  // gemm_gated_x8_out
+  return std::max(std::max(x, ex), std::max(red, tile));
 }
 
 // Dynamic LDS above 64 KB (X^T passes of up to 128 KB): the kernel's limit is raised first (on the current device).
@@ -1200,6 +1237,14 @@ int gemm_launch(GemmParams& p, bool i8, hipStream_t s) {
   // group scales: the K-sliced kernel, one token block, whole 128-column groups in every band and range, X per wave or
   // the band's X^T in LDS at once, no row scales
   if (p.x8 && (!p.gscale || p.x8 > 2 || (p.x8 == 2 && (!p.xsc || p.xsc_row < p.K / 16)))) return DSPARK_EINVAL;
+  // int8-x output: the gated epilogue over whole strip pairs of one workgroup (one band), or the conv epilogue's
+  // 16-channel groups (one piece each, 15 waves)
+  if (p.ysc) {
+    const bool gated = p.epilogue == 1 && !p.fuse && p.kw > 0 && p.wpg % 2 == 0 && p.bands <= 1 && p.N % 32 == 0 &&
+                       !p.best_part && p.y16;
+    const bool conv = p.fuse == GEMM_FUSE_CONV && p.wpg == 3 && p.y16;
+    if (!p.gscale || (!gated && !conv) || p.ysc_row < (gated ? p.N / 32 : p.N / 48)) return DSPARK_EINVAL;
+  }
   if (p.gscale) {
     if (!i8 || p.kw <= 0 || p.M > 16 || p.K % 128 || p.scale) return DSPARK_EINVAL;
     const int bands = std::max(1, p.bands), bc = (p.K / 64 + bands - 1) / bands, cpk = (bc + p.kw - 1) / p.kw;

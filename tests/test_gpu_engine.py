@@ -86,7 +86,7 @@ def make_weights(eng, desc, seed, stop_half=False):
                                                            "h0", "h1", "x16", "mix", "q16", "gate", "y16", "vout", "a16",
                                                            "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys",
                                                            "ws_", "rope", "ring_table", "tap_x", "plant", "conv_state",
-                                                           "trace", "debug_layers", "x_scales"))]
+                                                           "trace", "debug_layers", "x_scales", "y_scales"))]
     for n in weight_names:
         nb = sizes[n]
         if n.endswith(".w") and not n.endswith("conv.w"):
@@ -390,3 +390,58 @@ def test_planted_rounds_commit_the_greedy_chain(dev, geom, seed, wrong):
             assert k == ((bad[0] - c + 1) if bad else nd + 1), (c, k, commits)
             c += k
     eng.close()
+
+
+# REF_X8 with FFNs whose gated GEMM (2 x 4608 rows) plans 4 strips per workgroup, so the gated epilogue writes a16 as
+# int8 codes too (at FFN 1024 its plan has one strip per workgroup and a16 stays fp16)
+REF_X8_WIDE = dict(REF_X8, ffn=4608, draft_ffn=4608)
+
+
+@pytest.mark.parametrize("geom,seed", [("ref_x8", 34), ("ref_x8_wide", 35)])
+def test_x8_producer_codes_bit_identical(dev, geom, seed, monkeypatch):
+    """int8 x (LFM3_X8): the attention merge, the conv epilogue and the gated epilogue write y16 / a16 as int8 codes
+    with their piece scales, which the out and w2 GEMMs read as given. The codes are the ones those GEMMs make of the
+    fp16 values as they load them (x_fill, dspark.hip:883-904): a round computed that way
+    (DSPARK_X8_PRODUCER_CODES=0 when the engine is created) is bit for bit the same round."""
+    torch = dev
+    host = load_host()
+    desc = host.model_desc(**(REF_X8_WIDE if geom == "ref_x8_wide" else REF_X8))
+    a, ctx_lo, ctx_new = 300, 150, 3
+    st0 = dict(a=a, anchor=STOP_ANCHOR, count=0, rounds_left=1 << 20, limit=a + 64, budget=512, eos=-1,
+               ctx_new=ctx_new, ctx_pos=a - ctx_new, ctx_lo=ctx_lo, run=1, skip_rounds=1, stop_at=a + 64,
+               ckpt_slot=-1, tokens=[STOP_ANCHOR])
+    out = {}
+    for form in ("1", "0"):
+        monkeypatch.setenv("DSPARK_X8_PRODUCER_CODES", form)
+        print(f"case x8 producer codes geom={geom} seed={seed} form={form}", flush=True)
+        eng = host.Engine(desc, 512)
+        make_weights(eng, desc, seed)
+        setup_caches(eng, host, desc, a, ctx_lo, seed + 100)
+        eng.set_state(**st0)
+        rounds = []
+        for _ in range(3):
+            eng.round(0, a)
+            torch.cuda.synchronize()
+            rounds.append(dict(st=tuple(getattr(eng.state(), f) for f in host.STATE_FIELDS),
+                               logits=eng.download("logits", np.uint32), base=eng.download("base", np.uint32),
+                               keys=eng.download("keys", np.uint64, (2 * desc.block,)),
+                               h=(eng.download("h0", np.uint32), eng.download("h1", np.uint32))))
+        y16 = eng.download("y16", np.uint16).view(np.float16).astype(np.float32)
+        a16 = eng.download("a16", np.uint16).view(np.float16).astype(np.float32)
+        out[form] = (rounds, y16, a16)
+        eng.close()
+    monkeypatch.delenv("DSPARK_X8_PRODUCER_CODES")
+    codes_rounds, y16c, a16c = out["1"]
+    load_rounds, y16f, a16f = out["0"]
+
+    def codes(x):
+        return bool(np.all(x == np.round(x)) and np.max(np.abs(x)) <= 127)
+    # the producers took the path under test: y16 (and a16 when the gated plan pairs strips) hold codes, and without
+    # producer codes they hold fp16 values
+    assert codes(y16c) and not codes(y16f)
+    assert codes(a16c) == (geom == "ref_x8_wide") and not codes(a16f)
+    for r, (p, q) in enumerate(zip(codes_rounds, load_rounds)):
+        assert p["st"] == q["st"], r
+        for k in ("logits", "base", "keys"):
+            assert np.array_equal(p[k], q[k]), (r, k)
+        assert all(np.array_equal(x, y) for x, y in zip(p["h"], q["h"])), r
