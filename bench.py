@@ -715,6 +715,59 @@ def bench_copy(args, torch):
     return {"workload": "copy", "bytes_per_copy": nbytes, "GBs_read_plus_write": round(2 * nbytes * args.steps / el / 1e9, 1)}
 
 
+def trace_summary(path):
+    """One round of a rocprofv3 kernel trace (the --kernel-trace --output-format csv file of a round workload): the
+    middle round of the longest run of back-to-back rounds with no host copy, trace mark or forced row count among
+    them (a round of a timed loop), as kernels by total time and GEMM launch shapes. Reads a CSV; no GPU."""
+    import csv
+    import collections
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    idx = [i for i, r in enumerate(rows) if "round_begin_kernel" in r["Kernel_Name"]]
+    runs, cur = [], []
+    for k in range(len(idx) - 1):
+        rnd = rows[idx[k]:idx[k + 1]]
+        names = [r["Kernel_Name"] for r in rnd]
+        if any("trace_mark" in n or "force_m" in n or "rocclr" in n for n in names):
+            if cur:
+                runs.append(cur)
+            cur = []
+            continue
+        cur.append(rnd)
+    if cur:
+        runs.append(cur)
+    if not runs:
+        return "no complete round in the trace"
+    best = max(runs, key=len)
+    rnd = best[len(best) // 2]
+
+    def name(r):
+        n = r["Kernel_Name"].replace("void ", "").replace("dspark::", "")
+        return n if n.startswith("_Z") else n.split("(dspark")[0].split("(")[0]
+    agg, shapes = collections.OrderedDict(), collections.OrderedDict()
+    for r in rnd:
+        n, d = name(r), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        a = agg.setdefault(n, [0, 0.0])
+        a[0] += 1
+        a[1] += d
+        if "gemm" in n:
+            key = f"{n} {int(r['Grid_Size_X']) // int(r['Workgroup_Size_X'])} x {r['Workgroup_Size_X']}"
+            b = shapes.setdefault(key, [0, 0.0])
+            b[0] += 1
+            b[1] += d
+    busy = sum(v[1] for v in agg.values())
+    nxt = rows[rows.index(rnd[-1]) + 1]
+    span = (int(nxt["Start_Timestamp"]) - int(rnd[0]["Start_Timestamp"])) / 1e3
+    out = [f"# round: {len(rnd)} kernels, kernel busy {busy:.1f} us, round_begin to next round_begin under the tracer "
+           f"{span:.1f} us (middle of {len(best)} back-to-back rounds)",
+           "# kernel, launches per round, total us, average us"]
+    for k, v in sorted(agg.items(), key=lambda x: -x[1][1]):
+        out.append(f"{k[:64]:64s} {v[0]:4d} {v[1]:8.1f} {v[1] / v[0]:7.2f}")
+    out.append("# GEMM launch shapes (workgroups x threads), launches, total us, average us:")
+    for k, v in sorted(shapes.items(), key=lambda x: -x[1][1]):
+        out.append(f"#   {k[:70]:70s} {v[0]:4d} {v[1]:8.1f} {v[1] / v[0]:7.2f}")
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -734,7 +787,12 @@ def main():
     ap.add_argument("--layers", type=int, default=2, help="attn workload: layers per step")
     ap.add_argument("--c2-only", action="store_true",
                     help="default workload without the headline tiers and the C5 and int8-record attention fields")
+    ap.add_argument("--trace-summary", default="", metavar="CSV",
+                    help="print one round of a rocprofv3 kernel-trace CSV of a round workload and exit (no GPU)")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)

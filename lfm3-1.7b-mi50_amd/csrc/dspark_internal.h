@@ -67,6 +67,11 @@ struct ResNormParams {
   // c / 16 of token t at t xsc_row + c / 16 (c the x column); nullptr: fp16 x
   float* xsc;
   int xsc_row;
+  // h_old from the embedding table instead (the first layer of a pass, embed_kernel's rows; h_old must be null): row
+  // t is embed[token(t)], token(t) = st->tokens[t] (embed_mode 0) or t == 0 ? st->anchor : mask_token (1); tokens
+  // outside the vocabulary read row 0
+  const _Float16* embed;
+  int embed_mode, mask_token, vocab;
 };
 
 struct QkRopeParams {

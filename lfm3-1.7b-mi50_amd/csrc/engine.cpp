@@ -114,10 +114,14 @@ struct dspark_engine {
   float *h[2] = {nullptr, nullptr}, *mix = nullptr, *vout = nullptr, *w2out = nullptr, *ctxv = nullptr, *ckvout = nullptr,
         *taps = nullptr, *logits = nullptr, *base = nullptr, *gate = nullptr;
   _Float16 *x16 = nullptr, *q16 = nullptr, *y16 = nullptr, *a16 = nullptr;
-  float* xsc = nullptr;  // x_format 1: the int8 codes' scales of the norm outputs in x16, [16 tbs][x_cols / 16]
+  // x_format 1: the int8 codes' scales of the norm outputs in x16; every scale buffer is [16 tbs][x_cols / 16]
+  float* xsc = nullptr;
   // x_format 1: the scales of the codes the attention merge, the conv epilogue and the gated epilogue write into y16
-  // or a16 (each read by the next GEMM before the other is written), [16 tbs][y_cols / 16]
+  // or a16 (each read by the next GEMM before the other is written)
   float* ysc = nullptr;
+  // the context projection's own norm outputs (tap norms, then the hidden norm) and their int8-x scales
+  _Float16* xc16 = nullptr;
+  float* xcsc = nullptr;
   // whether those producers write codes (else the out and w2 GEMMs quantize y16 / a16 as they load them: the same codes
   // and scales, so bit-identical rounds; DSPARK_X8_PRODUCER_CODES=0 at engine creation selects that form)
   bool y_codes = false;
@@ -128,7 +132,7 @@ struct dspark_engine {
   size_t ws_gemm_bytes = 0;
   void* ws_argmax = nullptr;
   size_t ws_argmax_bytes = 0;
-  int x_cols = 0, y_cols = 0, mix_cols = 0, crop_n = 0;
+  int x_cols = 0, mix_cols = 0, crop_n = 0;
   int tbs = 1;  // 16-token blocks of the round: x16, y16 and a16 hold 16 tbs token rows in the GEMMs' X operand order
   int cus = 256;
   dspark_state host_st;  // launch-time uploads stay alive until the stream has consumed them
@@ -226,13 +230,13 @@ __global__ void crop_ids_kernel(int32_t* ids, int n, int V) {
 // `bands` (optional): in, the most output bands the caller adds (y32 holds that many [M][N] blocks); out, the bands
 // the plan wrote.
 // `xop` false: x is row-major [M][K] (prompt projection) instead of the round's operand order.
-// int8 x (x_format 1): x16 holds the norm kernel's codes (scales in xsc); `x_codes`: x (y16 or a16) holds the codes a
-// producer wrote (scales in ysc); any other x is fp16, quantized as it is loaded. `y_codes` (optional): in, whether
-// the fp16 output y16 should be written as codes + ysc scales; out, whether it was (the gated epilogue needs strip
-// pairs inside a workgroup, the conv epilogue always can).
+// int8 x (x_format 1): x16 holds the norm kernel's codes (scales in xsc); `xsc_in`: x holds codes with these scales
+// (y16 / a16 from their producers, xc16 from the context's norms); any other x is fp16, quantized as it is loaded.
+// `y_codes` (optional): in, whether the fp16 output y16 should be written as codes + ysc scales; out, whether it was
+// (the gated epilogue needs strip pairs inside a workgroup, the conv epilogue always can).
 int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, const _Float16* s, int N, int epilogue,
          float* y32, _Float16* y16, hipStream_t st, const GemmParams* fuse = nullptr, int* bands = nullptr,
-         bool xop = true, bool x_codes = false, bool* y_codes = nullptr) {
+         bool xop = true, const float* xsc_in = nullptr, bool* y_codes = nullptr) {
   GemmParams p = {};
   p.st = e->ast;
   p.x = x;
@@ -250,9 +254,9 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
   p.yop = e->tbs;
   if (e->d.x_format == 1) {
     const bool norm_codes = x == e->x16 && xop;
-    p.x8 = norm_codes || x_codes ? 2 : 1;
-    p.xsc = x_codes && !norm_codes ? e->ysc : e->xsc;
-    p.xsc_row = x_codes && !norm_codes ? e->y_cols / 16 : e->x_cols / 16;
+    p.x8 = norm_codes || xsc_in ? 2 : 1;
+    p.xsc = xsc_in ? xsc_in : e->xsc;
+    p.xsc_row = e->x_cols / 16;
   }
   int wpg_req = 0;
   if (fuse) {
@@ -273,7 +277,7 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
     *y_codes = *y_codes && can;
     if (*y_codes) {
       p.ysc = e->ysc;
-      p.ysc_row = e->y_cols / 16;
+      p.ysc_row = e->x_cols / 16;
     }
   }
   p.bands = pl.bands;
@@ -296,11 +300,20 @@ int gemm(dspark_engine* e, const _Float16* x, int M, int K, const uint8_t* w, co
 }
 
 // Residual + RMS norm of M block rows (the bands of v are [M][H] each, as the GEMM of M rows wrote them).
+// embed_mode >= 0: h_old is the embedding of the pass's tokens (0: the State's tokens, 1: the drafter block's
+// anchor + mask tokens; h_old must be null). x16 / xsc: the outputs (default the round's x16 and its scales).
 int resnorm(dspark_engine* e, int M, const float* h_old, const float* v, int bands, const _Float16* post_w,
-            const _Float16* norm_w, int sandwich, float* dst, float* tap, hipStream_t s) {
+            const _Float16* norm_w, int sandwich, float* dst, float* tap, hipStream_t s, int embed_mode = -1,
+            _Float16* x16 = nullptr, float* xsc = nullptr) {
   ResNormParams p = {};
   p.st = e->ast;
   p.h_old = h_old;
+  if (embed_mode >= 0) {
+    p.embed = e->embed;
+    p.embed_mode = embed_mode;
+    p.mask_token = e->d.mask_token;
+    p.vocab = e->d.vocab;
+  }
   p.v = v;
   p.bands = bands;
   p.v_band_stride = (size_t)M * e->d.hidden;
@@ -310,11 +323,11 @@ int resnorm(dspark_engine* e, int M, const float* h_old, const float* v, int ban
   p.eps = e->d.eps;
   p.dst = dst;
   p.tap = tap;
-  p.x16 = e->x16;
+  p.x16 = x16 ? x16 : e->x16;
   p.x_row = e->d.hidden;
   p.H = e->d.hidden;
   p.xop = e->tbs;
-  p.xsc = e->xsc;
+  p.xsc = xsc ? xsc : e->xsc;
   p.xsc_row = e->x_cols / 16;
   return resnorm_launch(p, M, 1, s);
 }
@@ -334,7 +347,7 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   p.out_op = e->tbs;
   if (e->y_codes) {  // int8 x: the merge writes codes + scales for the out projection
     p.out_sc = e->ysc;
-    p.out_sc_row = e->y_cols / 16;
+    p.out_sc_row = e->x_cols / 16;
   }
   p.gate = gate;
   p.M = M;
@@ -406,8 +419,8 @@ int gemm_mix_conv(dspark_engine* e, const LayerW& W, int M, hipStream_t s) {
   f.conv_ring = W.conv_ring;
   f.conv_k = e->d.conv_kernel;
   bool codes = e->y_codes;  // int8 x: codes + scales for the out projection
-  return gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f, nullptr, true, false,
-              &codes);
+  return gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, nullptr, e->y16, s, &f, nullptr, true,
+              nullptr, &codes);
 }
 
 // Output bands the round's norm kernels add (the w2, out and fc GEMMs may split K over that many workgroups).
@@ -433,17 +446,20 @@ int mark(dspark_engine* e, int phase, hipStream_t s) {
 }
 
 // The context projection from its fc GEMM on (dspark.hip:2682-2705, 2487-2518; dspark.go:461-492): x_fc (the normed
-// taps of B positions, [B][n_taps * H]: the round's x16 in operand order, or row-major prompt taps) -> fc -> hidden
+// taps of B positions, [B][n_taps * H]: the round's xc16 in operand order, or row-major prompt taps) -> fc -> hidden
 // norm -> ckv -> per drafter layer k norm + RoPE, K/V rows into the drafter ring at positions State.ctx_pos + t for
-// t < State.ctx_new (of the active State).
+// t < State.ctx_new (of the active State). Its norm outputs go to xc16 (and, int8 x, xcsc), apart from the round's x16.
 int enqueue_context(dspark_engine* e, const _Float16* x_fc, bool x_op, hipStream_t s) {
   const dspark_model_desc& d = e->d;
   const int B = e->B, H = d.hidden;
+  const bool x8 = d.x_format == 1;
   int nb = ENGINE_BANDS;
-  CK(gemm(e, x_fc, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s, nullptr, &nb, x_op));
-  CK(resnorm(e, B, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s));
+  CK(gemm(e, x_fc, B, d.n_taps * H, e->fc_w, e->fc_s, H, 0, e->ctxv, nullptr, s, nullptr, &nb, x_op,
+          x8 && x_op ? e->xcsc : nullptr));
+  CK(resnorm(e, B, nullptr, e->ctxv, nb, nullptr, e->hidden_norm, 0, nullptr, nullptr, s, -1, e->xc16, e->xcsc));
   const int kvrow = 2 * d.kv_heads * d.head_dim;
-  CK(gemm(e, e->x16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s));
+  CK(gemm(e, e->xc16, B, H, e->ckv_w, e->ckv_s, d.draft_layers * kvrow, 0, e->ckvout, nullptr, s, nullptr, nullptr,
+          true, x8 ? e->xcsc : nullptr));
   for (int j0 = 0; j0 < d.draft_layers; j0 += QKROPE_BATCH) {  // one launch for up to 8 drafter layers
     QkRopeBatch b = {};
     b.n = std::min(QKROPE_BATCH, d.draft_layers - j0);
@@ -460,12 +476,16 @@ int enqueue_context(dspark_engine* e, const _Float16* x_fc, bool x_op, hipStream
 int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, hipStream_t s) {
   const dspark_model_desc& d = e->d;
   const int B = e->B, H = d.hidden, MV = mv;
-  const bool x8 = e->y_codes;  // the attention merge and the conv epilogue write y16 as int8 codes + scales
+  // int8 x: the attention merge and the conv epilogue write y16 as codes with these scales
+  float* const ysc = e->y_codes ? e->ysc : nullptr;
+  const bool x8 = e->y_codes;
   uint64_t* vbest = e->keys;
   uint64_t* mbest = e->keys + B;
   e->ast = e->st;
   CK(round_begin_launch(e->st, e->keys, 2 * B, e->seen, B, e->max_context + B, d.vocab, e->max_context + 2 * B, s));
   CK(mark(e, DSPARK_TRACE_BEGIN, s));
+  // the embedding folded into each pass's first norm (one launch fewer per pass), unless the layer dumps read it
+  const bool fold = !e->dump_on;
   if (force_m > 0) {
     CK(force_m_launch(e->st, force_m, s));
   } else {
@@ -478,40 +498,44 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       p.norm_w = e->tap_norms;
       p.norm_w_stride = H;
       p.eps = d.eps;
-      p.x16 = e->x16;
+      p.x16 = e->xc16;
       p.x_row = d.n_taps * H;
       p.x_group_stride = H;
       p.H = H;
       p.xop = e->tbs;
-      p.xsc = e->xsc;
+      p.xsc = e->xcsc;
       p.xsc_row = e->x_cols / 16;
       CK(resnorm_launch(p, B, d.n_taps, s));
     }
-    CK(enqueue_context(e, e->x16, true, s));
+    CK(enqueue_context(e, e->xc16, true, s));
     CK(mark(e, DSPARK_TRACE_CONTEXT, s));
   }
   if (skip) {
     CK(force_m_launch(e->st, 1, s));
   } else if (force_m <= 0) {
     // ---- drafter block
-    CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
+    if (!fold) CK(embed_launch(e->embed, e->st, 1, d.mask_token, B, H, d.vocab, e->h[0], s));
     int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
     for (int j = 0; j < d.draft_layers; ++j) {
       const LayerW& W = e->DL[j];
       CK(dump(e, j, e->h[cur], j ? e->w2out : nullptr, w2b, B, s));
-      CK(resnorm(e, B, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
+      if (j == 0 && fold)
+        CK(resnorm(e, B, nullptr, nullptr, 0, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s, 1));
+      else
+        CK(resnorm(e, B, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       CK(gemm_mix_qk(e, W, B, s));
       CK(attention(e, W, 1, plan_a, nullptr, B, s));
       int ob = ENGINE_BANDS;
-      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, x8));
+      CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, ysc));
       CK(resnorm(e, B, e->h[cur], e->vout, ob, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
       bool acodes = x8;
-      CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, nullptr, nullptr, true, false,
+      CK(gemm(e, e->x16, B, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, nullptr, nullptr, true, nullptr,
               &acodes));
       w2b = ENGINE_BANDS;
-      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b, true, acodes));
+      CK(gemm(e, e->a16, B, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b, true,
+              acodes ? e->ysc : nullptr));
     }
     CK(mark(e, DSPARK_TRACE_DRAFTER, s));
     CK(dump(e, d.draft_layers, e->h[cur], e->w2out, w2b, B, s));
@@ -544,15 +568,18 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
     CK(mark(e, DSPARK_TRACE_MARKOV, s));
   }
   // ---- verify (MV rows; rows past the State's M are computed and never committed)
-  CK(embed_launch(e->embed, e->st, 0, 0, MV, H, d.vocab, e->h[0], s));
+  if (!fold) CK(embed_launch(e->embed, e->st, 0, 0, MV, H, d.vocab, e->h[0], s));
   int cur = 0, w2b = 0;  // w2b: bands of the last w2 output
   for (int i = 0; i < d.n_layers; ++i) {
     const LayerW& W = e->L[i];
     const LayerW* P = i ? &e->L[i - 1] : nullptr;
     float* tap = (P && P->tap_slot >= 0) ? e->taps + (size_t)P->tap_slot * B * H : nullptr;
     CK(dump(e, d.draft_layers + 1 + i, e->h[cur], i ? e->w2out : nullptr, w2b, MV, s));
-    CK(resnorm(e, MV, e->h[cur], i ? e->w2out : nullptr, w2b, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
-               e->h[cur ^ 1], tap, s));
+    if (i == 0 && fold)
+      CK(resnorm(e, MV, nullptr, nullptr, 0, nullptr, W.op_norm, 1, e->h[cur ^ 1], nullptr, s, 0));
+    else
+      CK(resnorm(e, MV, e->h[cur], i ? e->w2out : nullptr, w2b, P ? P->post_ffn_norm : nullptr, W.op_norm, 1,
+                 e->h[cur ^ 1], tap, s));
     cur ^= 1;
     if (W.kind == 0) {
       CK(gemm_mix_conv(e, W, MV, s));
@@ -561,14 +588,15 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       CK(attention(e, W, 0, plan_a, e->gate, MV, s));
     }
     int ob = ENGINE_BANDS;
-    CK(gemm(e, e->y16, MV, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, x8));
+    CK(gemm(e, e->y16, MV, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, ysc));
     CK(resnorm(e, MV, e->h[cur], e->vout, ob, W.post_op_norm, W.ffn_norm, 1, e->h[cur ^ 1], nullptr, s));
     cur ^= 1;
     bool acodes = x8;
-    CK(gemm(e, e->x16, MV, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, nullptr, nullptr, true, false,
+    CK(gemm(e, e->x16, MV, H, W.w13_w, W.w13_s, 2 * W.ffn, 1, nullptr, e->a16, s, nullptr, nullptr, true, nullptr,
             &acodes));
     w2b = ENGINE_BANDS;
-    CK(gemm(e, e->a16, MV, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b, true, acodes));
+    CK(gemm(e, e->a16, MV, W.ffn, W.w2_w, W.w2_s, H, 0, e->w2out, nullptr, s, nullptr, &w2b, true,
+            acodes ? e->ysc : nullptr));
     CK(mark(e, DSPARK_TRACE_VERIFY_LAYER + i, s));
   }
   {
@@ -808,14 +836,15 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   e->h[1] = static_cast<float*>(e->alloc("h1", (size_t)B * H * 4, &err));
   e->tbs = (B + 15) / 16;
   e->x16 = h16("x16", (size_t)16 * e->tbs * e->x_cols);
-  e->y_cols = std::max(H, std::max(d.ffn, d.draft_ffn));
+  e->xc16 = h16("xc16", (size_t)16 * e->tbs * d.n_taps * H);
   {
     const char* v = std::getenv("DSPARK_X8_PRODUCER_CODES");
     e->y_codes = d.x_format == 1 && !(v && v[0] == '0');
   }
   if (d.x_format == 1) {
     e->xsc = static_cast<float*>(e->alloc("x_scales", (size_t)16 * e->tbs * (e->x_cols / 16) * sizeof(float), &err));
-    e->ysc = static_cast<float*>(e->alloc("y_scales", (size_t)16 * e->tbs * (e->y_cols / 16) * sizeof(float), &err));
+    e->ysc = static_cast<float*>(e->alloc("y_scales", (size_t)16 * e->tbs * (e->x_cols / 16) * sizeof(float), &err));
+    e->xcsc = static_cast<float*>(e->alloc("xc_scales", (size_t)16 * e->tbs * (e->x_cols / 16) * sizeof(float), &err));
   }
   e->mix = static_cast<float*>(e->alloc("mix", (size_t)B * e->mix_cols * 4, &err));
   e->q16 = h16("q16", (size_t)B * QH * D);

@@ -61,12 +61,23 @@ __global__ __launch_bounds__(256) void embed_kernel(const _Float16* embed, const
 // v = sum of `bands` inputs in band order; a = bands == 0 ? 0 : (sandwich ? rsqrt(mean(v^2) + eps) : 1);
 // h_new = h_old + a * v * post_w; x = fp16(h_new * rsqrt(mean(h_new^2) + eps) * norm_w).
 // One block per (row, group): blockIdx.y selects a group with its own inputs (the drafter's tap norms).
-template <int NK, bool HAS_H>
+// EMB: h_old is row token(t) of the embedding table (a pass's first layer, embed_kernel folded in).
+template <int NK, bool HAS_H, bool EMB = false>
 __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
   const int run = run_flag_load(p.st);  // tested after every load is in flight
   const int t = blockIdx.x, gi = blockIdx.y;
   const int H = p.H;
   const float* hold = HAS_H ? p.h_old + (size_t)gi * p.group_stride + (size_t)t * H : nullptr;
+  const _Float16* erow = nullptr;
+  if constexpr (EMB) {
+    // the token from the State (a vector load issued with the run flag), then its row
+    const int tok_v = state_word_load(p.st, p.embed_mode == 0 ? (int)offsetof(dspark_state, tokens) + 4 * t
+                                                              : (int)offsetof(dspark_state, anchor));
+    int tok = __builtin_amdgcn_readfirstlane(tok_v);
+    if (p.embed_mode != 0 && t != 0) tok = p.mask_token;
+    if (tok < 0 || tok >= p.vocab) tok = 0;
+    erow = p.embed + (size_t)tok * H;
+  }
   const _Float16* nw = p.norm_w + (size_t)gi * p.norm_w_stride;
   const _Float16* pw = p.post_w ? p.post_w : nw;  // no post_w: loaded from nw and replaced by 1 below
   // Four consecutive columns per thread per 1024 (NK = ceil(H / 1024) groups). Loads go to clamped, valid columns
@@ -80,7 +91,12 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
     const int i = 1024 * k + 4 * (int)threadIdx.x;
     ok[k] = i < H;
     col[k] = min(i, H - 4);
-    hv[k] = HAS_H ? ldg(reinterpret_cast<const f32x4*>(hold + col[k])) : f32x4{0, 0, 0, 0};
+    if constexpr (EMB) {
+      const half4 e4 = ldg(reinterpret_cast<const half4*>(erow + col[k]));
+      hv[k] = f32x4{(float)e4[0], (float)e4[1], (float)e4[2], (float)e4[3]};
+    } else {
+      hv[k] = HAS_H ? ldg(reinterpret_cast<const f32x4*>(hold + col[k])) : f32x4{0, 0, 0, 0};
+    }
     wn[k] = ldg(reinterpret_cast<const half4*>(nw + col[k]));
     wp[k] = ldg(reinterpret_cast<const half4*>(pw + col[k]));
     vv[k] = f32x4{0, 0, 0, 0};
@@ -616,7 +632,9 @@ int embed_launch(const void* embed, const dspark_state* st, int mode, int mask_t
 }
 template <int NK>
 static void resnorm_launch_nk(const ResNormParams& p, dim3 grid, hipStream_t s) {
-  if (p.h_old)
+  if (p.embed)
+    hipLaunchKernelGGL((resnorm_kernel<NK, false, true>), grid, dim3(256), 0, s, p);
+  else if (p.h_old)
     hipLaunchKernelGGL((resnorm_kernel<NK, true>), grid, dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((resnorm_kernel<NK, false>), grid, dim3(256), 0, s, p);
@@ -624,6 +642,7 @@ static void resnorm_launch_nk(const ResNormParams& p, dim3 grid, hipStream_t s) 
 
 int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) {
   if (p.H < 4 || p.H % 4 || p.H > 8192) return DSPARK_EINVAL;
+  if (p.embed && (p.h_old || !p.st || groups != 1 || p.vocab < 1)) return DSPARK_EINVAL;
   const dim3 grid(rows, groups);
   switch ((p.H + 1023) / 1024) {
     case 1: resnorm_launch_nk<1>(p, grid, s); break;
