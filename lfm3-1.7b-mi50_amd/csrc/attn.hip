@@ -417,6 +417,15 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
     __syncthreads();
   }
 
+  // Fresh block (p.mix): wave w's fresh row is token w's K/V, at position a + w (the host sends M <= waves).
+  constexpr int NE = D / 32;  // a fresh K/V row's dims per lane: lanes 0..31 hold dims l + 32 e, 32..63 repeat them
+  constexpr bool FRESH_OK = QB == 1 && D == 64;  // (the host sends a fresh block to these shapes only)
+  const bool fresh = FRESH_OK && p.mix != nullptr;
+  const int fpos = p.a + wave;
+  const int fpage = fpos / PAGE;
+  const bool fmine = fresh && wave < p.M && fpage >= pb && fpage < pe;  // wave-uniform
+  _Float16 fkh[NE], fvh[NE];  // the fresh K / V row's halves of this lane (dims l + 32 e)
+
   // Step `k`'s chunks into `slot`: chunk c of [0, PPS*CPG) goes to wave c % NW; every wave issues exactly LPW loads
   // (chunks past the step, or of pages past the split, become out-of-range loads into `trash`), so the counted waits
   // are compile-time constants.
@@ -449,6 +458,22 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
     if (k + RING - 1 < nsteps) issue(k + RING - 1, nxt);
+    // fresh positions in this step's pages: their K / V rows into the LDS copy (stale in the pool), then a barrier
+    if (fresh && p.a + p.M - 1 >= (pb + k * PPS) * PAGE && p.a < min(pe, pb + (k + 1) * PPS) * PAGE) {
+      if (fmine && (fpage - pb) / PPS == k && lane < 32) {
+        char* pg = const_cast<char*>(cur) + ((fpage - pb) % PPS) * PAGEB;
+        const int slot = fpos % PAGE;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+          const int d = lane + 32 * e;
+          *reinterpret_cast<_Float16*>(pg + 2 * k_page_elem(slot, d, D)) = fkh[e];
+          *reinterpret_cast<_Float16*>(pg + (CPG / 2 + d / 16) * 1024 + (16 * (slot / 8) + d % 16) * 16 + 2 * (slot % 8)) =
+              fvh[e];
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(LGKMCNT0_IMM);
+      __builtin_amdgcn_s_barrier();
+    }
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
       const int pp = j * PL + pl;
@@ -473,7 +498,52 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   // counter), so the wait for Q below leaves the first steps' pages in flight. Padding rows past G*M read the last
   // row (the merge never stores them).
   if (paged) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  if (pl == 0) {
+  // Fresh block: this wave's rows of Q and its fresh K/V row (token `wave`, when its position falls in this split)
+  // loaded from the mix rows first, so they are the oldest loads in the counter and the first step's wait covers them.
+  f32x4 fq[QB][D / 32][2];
+  half8 fqw[D / 32], fqc[D / 64], fqs[D / 64];
+  float fk[NE], fv[NE], fkw[NE], fkc[NE / 2], fks[NE / 2];
+  if (fresh) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int r = min((rg * QB + qb) * 16 + n, p.G * p.M - 1);
+      const float* qr = p.mix + (size_t)(r / p.G) * p.mix_row + (size_t)(h * p.G + r % p.G) * D + 8 * g;
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) {
+        fq[qb][s][0] = ldg(reinterpret_cast<const f32x4*>(qr + 32 * s));
+        fq[qb][s][1] = ldg(reinterpret_cast<const f32x4*>(qr + 32 * s + 4));
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) fqw[s] = ldg(reinterpret_cast<const half8*>(p.q_norm + 32 * s + 8 * g));
+    if (fmine) {
+      const float* row = p.mix + (size_t)wave * p.mix_row;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        const int d = (lane & 31) + 32 * e;
+        fk[e] = row[(size_t)(p.QH + h) * D + d];
+        fv[e] = row[(size_t)(p.QH + p.KVH + h) * D + d];
+        fkw[e] = (float)p.k_norm[d];
+      }
+#pragma unroll
+      for (int e = 0; e < NE / 2; ++e) {
+        const int i = (lane & 31) + 32 * e;
+        fkc[e] = (float)p.rope[(size_t)fpos * D + i];
+        fks[e] = (float)p.rope[(size_t)fpos * D + D / 2 + i];
+      }
+    }
+  }
+  if (fresh) {
+    // (the RoPE rows of the wave's tokens: a second round of loads, the token known only per row)
+#pragma unroll
+    for (int s = 0; s < D / 64; ++s) {
+      const int r = min(rg * QB * 16 + n, p.G * p.M - 1);
+      const _Float16* rt = p.rope + (size_t)(p.a + r / p.G) * D + 32 * s + 8 * g;
+      fqc[s] = ldg(reinterpret_cast<const half8*>(rt));
+      fqs[s] = ldg(reinterpret_cast<const half8*>(rt + D / 2));
+    }
+  }
+  if (pl == 0 && !fresh) {
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.q, (short)0, (int)((size_t)p.M * p.QH * D * 2), 0x00020000);
 #pragma unroll
@@ -498,21 +568,100 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   else
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __builtin_amdgcn_s_barrier();
+  if (fresh) {
+    // q/k norm + RoPE of the block (the q/k norm + RoPE kernel's arithmetic): row n's dims 32 s + 8 g + j sit in
+    // lane (n, g), so a row's sum of squares is four lanes and every RoPE pair (i, i + D / 2) is in one lane
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
+    for (int qb = 0; qb < QB; ++qb) {
+      float x[D / 32][8];
+      float ss = 0.f;
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) {
-      half8 q = *reinterpret_cast<const half8*>(q_lds + ((rg * QB + qb) * (D / 32) + s) * 1024 + lane * 16);
+      for (int s = 0; s < D / 32; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
-      qf.r[qb][s] = q;
+        for (int j = 0; j < 8; ++j) {
+          x[s][j] = fq[qb][s][j / 4][j % 4];
+          ss += x[s][j] * x[s][j];
+        }
+      ss += __shfl_xor(ss, 16);
+      ss += __shfl_xor(ss, 32);
+      const float inv = rsqrtf(ss / D + p.eps);
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[s][j] = x[s][j] * inv * (float)fqw[s][j];
+#pragma unroll
+      for (int s = 0; s < D / 64; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (32 * s + 8 * g + j < p.rot) {
+            const float c = (float)fqc[s][j], sn = (float)fqs[s][j];
+            const float x0 = x[s][j], x1 = x[s + D / 64][j];
+            x[s][j] = x0 * c - x1 * sn;
+            x[s + D / 64][j] = x1 * c + x0 * sn;
+          }
+        }
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) {
+        half8 q;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)(_Float16)x[s][j] * p.c);
+        qf.r[qb][s] = q;
+      }
     }
+    if (fmine) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) ss += fk[e] * fk[e];
+      ss = (lane < 32) ? ss : 0.f;
+      ss = wave_sum(ss);
+      const float inv = rsqrtf(ss / D + p.eps);
+      float r[NE];
+#pragma unroll
+      for (int e = 0; e < NE; ++e) r[e] = fk[e] * inv * fkw[e];
+#pragma unroll
+      for (int e = 0; e < NE / 2; ++e) {
+        if ((lane & 31) + 32 * e < p.rot) {
+          const float x0 = r[e], x1 = r[e + NE / 2];
+          r[e] = x0 * fkc[e] - x1 * fks[e];
+          r[e + NE / 2] = x1 * fkc[e] + x0 * fks[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        fkh[e] = (_Float16)r[e];
+        fvh[e] = (_Float16)fv[e];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) {
+        half8 q = *reinterpret_cast<const half8*>(q_lds + ((rg * QB + qb) * (D / 32) + s) * 1024 + lane * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = (_Float16)((float)q[j] * p.c);
+        qf.r[qb][s] = q;
+      }
+  }
   for (int k = 0; k < nsteps; k += RING) {
 #pragma unroll
     for (int u = 0; u < RING; ++u)
       if (k + u < nsteps) step(k + u, slots[u], slots[(u + RING - 1) % RING]);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // the fresh K / V row into the pools, for later rounds (nothing in this launch reads the pools' copy)
+  if (fmine && lane < 32) {
+    const int phys = paged ? sm_bt[fpage - pb] : fpage;
+    const int slot = fpos % PAGE;
+    _Float16* kb = const_cast<_Float16*>(p.kp) + ((size_t)phys * p.KVH + h) * (PAGE * D);
+    _Float16* vb = const_cast<_Float16*>(p.vp) + ((size_t)phys * p.KVH + h) * (D * PAGE);
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const int d = lane + 32 * e;
+      kb[k_page_elem(slot, d, D)] = fkh[e];
+      vb[d * PAGE + slot] = fvh[e];
+    }
+  }
 
   // Page lanes merge through LDS as a tree: at level `half` (PL / 2, ..., 1) lanes half .. 2 half - 1 store their
   // states and lane q < half folds in lane q + half's -- ((0 + 2) + (1 + 3)) for four lanes, a fixed order. The state
@@ -680,7 +829,7 @@ __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) 
   if (lane >= Q) return;
   float scale = l > 0.f ? 1.f / l : 0.f;
   const int t = row / p.G, qh = h * p.G + row % p.G;
-  if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * p.QH + qh)));
+  if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * (p.gate_stride > 0 ? p.gate_stride : p.QH) + qh)));
   {
 #pragma clang fp contract(off)  // the fp16 output is the fp32 output rounded (no product fused into the conversion)
     acc *= scale;

@@ -40,6 +40,19 @@ struct AttnParams {
   int qb, nrg;                // LDS-ring kernel: row blocks per wave, row groups (waves per page lane, nrg * qb >= nrb)
   int full_lo, full_hi;       // pages inside [full_lo, full_hi] need no mask
   float c;                    // log2(e) / sqrt(D)
+  int gate_stride;            // > 0: gate of (t, qh) at gate[t * gate_stride + qh] (else t * QH + qh)
+  // Fresh block (mix set; the LDS kernel with D = 64, one row block per wave and M <= waves): Q and the block's own
+  // K/V (positions a .. a + M - 1) from the attention-mix GEMM's rows instead of q and the pages -- per token
+  // `mix_row` floats, q heads at 0, k heads at QH D, v heads at (QH + KVH) D; the q/k RMS norm (q_norm / k_norm, eps)
+  // and RoPE (rope [positions][D]: cos | sin, pairs (i, i + D / 2) for i < rot) done here, as the q/k norm + RoPE
+  // kernel does. The split holding a fresh position patches its LDS copy of that page and writes the K/V rows into
+  // the pages for later rounds.
+  const float* mix;
+  int mix_row, rot;
+  const _Float16* q_norm;
+  const _Float16* k_norm;
+  const _Float16* rope;
+  float eps;
 };
 
 void attn_plan(AttnParams& p, int D, int cus);

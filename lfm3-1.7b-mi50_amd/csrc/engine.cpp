@@ -151,6 +151,9 @@ struct dspark_engine {
   float* dump = nullptr;
   bool dump_on = false;
   std::vector<void*> allocs;
+  // whether attention layers that can take their block fresh from the mix rows do (attn_fresh_ok); DSPARK_FRESH=0 at
+  // engine creation runs the q/k norm + RoPE kernel before every attention instead (for comparisons)
+  bool fresh = true;
 
   ~dspark_engine() {
     for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
@@ -332,7 +335,8 @@ int resnorm(dspark_engine* e, int M, const float* h_old, const float* v, int ban
   return resnorm_launch(p, M, 1, s);
 }
 
-int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const float* gate, int M, hipStream_t s) {
+// The attention launch parameters of layer Lw over M block rows, planned for position plan_a (workspace unbound).
+AttnParams attn_setup(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const float* gate, int M) {
   const dspark_model_desc& d = e->d;
   AttnParams p = {};
   p.st = e->ast;
@@ -369,6 +373,32 @@ int attention(dspark_engine* e, const LayerW& Lw, int drafter, int plan_a, const
   else
     attn_plan(p, d.head_dim, e->cus);
   if (drafter) p.window = d.draft_window;  // attn_range (device) derives start and drops the per-token window
+  return p;
+}
+
+// Whether the attention kernel takes the block fresh from the mix rows -- Q and the block's K/V normed and rotated in
+// the kernel, no q/k norm + RoPE launch before it: the LDS kernel over fp16 pages at D = 64 with one row block per
+// wave and at most one block token per wave.
+bool attn_fresh_ok(dspark_engine* e, const LayerW& Lw, const AttnParams& p) {
+  return e->fresh && !Lw.kv_rec && e->d.head_dim == 64 && p.lds == 1 && p.qb == 1 && p.M <= p.nrg * p.pl;
+}
+
+// Layer Lw's verify attention (attn_setup's parameters); fresh: the block from the mix rows (attn_fresh_ok).
+int attention(dspark_engine* e, const LayerW& Lw, AttnParams p, bool fresh, hipStream_t s) {
+  const dspark_model_desc& d = e->d;
+  if (fresh) {
+    p.mix = e->mix;
+    p.mix_row = Lw.mix_rows;
+    p.rot = Lw.kind == 2 ? e->rot_swa : d.rope_pairs;
+    p.q_norm = Lw.q_norm;
+    p.k_norm = Lw.k_norm;
+    p.rope = Lw.kind == 2 ? e->rope_swa : e->rope;
+    p.eps = d.eps;
+    if (p.gate) {  // the gate straight from the mix rows
+      p.gate = e->mix + (size_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
+      p.gate_stride = Lw.mix_rows;
+    }
+  }
   if (attn_workspace_bytes(p, d.head_dim) > e->ws_attn_bytes) return DSPARK_ENOSPACE;
   attn_bind_workspace(p, d.head_dim, e->ws_attn);
   return Lw.kv_rec ? attn_rec_launch(p, 3, s) : attn_launch(p, d.head_dim, 3, s);
@@ -406,9 +436,11 @@ QkRopeParams qk_params(dspark_engine* e, const LayerW& Lw, const float* mix, int
 // The attention mix GEMM, then the q/k norm + RoPE + K/V page write (qkrope). A fused epilogue needs one head per
 // workgroup: 49 workgroups for the C4 mix (10.6 us against 5.1 + 4.7 unfused) and 25 for the reference geometry's
 // 128-dim heads (14.5 us), so the two kernels are faster (measured on MI355X).
-int gemm_mix_qk(dspark_engine* e, const LayerW& W, int M, hipStream_t s) {
+// qk false: the attention takes the block fresh from the mix rows (attn_fresh_ok), no qkrope launch.
+int gemm_mix_qk(dspark_engine* e, const LayerW& W, int M, hipStream_t s, bool qk = true) {
   int rc = gemm(e, e->x16, M, e->d.hidden, W.mix_w, W.mix_s, W.mix_rows, 0, e->mix, nullptr, s);
-  return rc ? rc : qkrope_launch(qk_params(e, W, e->mix, W.mix_rows, true, false, M), s);
+  if (rc || !qk) return rc;
+  return qkrope_launch(qk_params(e, W, e->mix, W.mix_rows, true, false, M), s);
 }
 
 // The conv mix GEMM with the gated short conv fused into its epilogue (16 channels per group); output y16.
@@ -524,8 +556,10 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
       else
         CK(resnorm(e, B, e->h[cur], j ? e->w2out : nullptr, w2b, nullptr, W.op_norm, 0, e->h[cur ^ 1], nullptr, s));
       cur ^= 1;
-      CK(gemm_mix_qk(e, W, B, s));
-      CK(attention(e, W, 1, plan_a, nullptr, B, s));
+      const AttnParams ap = attn_setup(e, W, 1, plan_a, nullptr, B);
+      const bool fr = attn_fresh_ok(e, W, ap);
+      CK(gemm_mix_qk(e, W, B, s, !fr));
+      CK(attention(e, W, ap, fr, s));
       int ob = ENGINE_BANDS;
       CK(gemm(e, e->y16, B, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, ysc));
       CK(resnorm(e, B, e->h[cur], e->vout, ob, nullptr, W.ffn_norm, 0, e->h[cur ^ 1], nullptr, s));
@@ -584,8 +618,10 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
     if (W.kind == 0) {
       CK(gemm_mix_conv(e, W, MV, s));
     } else {
-      CK(gemm_mix_qk(e, W, MV, s));
-      CK(attention(e, W, 0, plan_a, e->gate, MV, s));
+      const AttnParams ap = attn_setup(e, W, 0, plan_a, e->gate, MV);
+      const bool fr = attn_fresh_ok(e, W, ap);
+      CK(gemm_mix_qk(e, W, MV, s, !fr));
+      CK(attention(e, W, ap, fr, s));
     }
     int ob = ENGINE_BANDS;
     CK(gemm(e, e->y16, MV, H, W.out_w, W.out_s, H, 0, e->vout, nullptr, s, nullptr, &ob, true, ysc));
@@ -827,6 +863,10 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
     err = DSPARK_ENOSPACE;
   }
   if (e->mirror) std::memset(e->mirror, 0, 16 * sizeof(int32_t));
+  {
+    const char* fv = std::getenv("DSPARK_FRESH");
+    e->fresh = !(fv && fv[0] == '0');
+  }
   e->trace = static_cast<uint64_t*>(e->alloc("trace", (size_t)(2 + 2 * DSPARK_TRACE_MAX_MARKS) * 8, &err));
   e->dump = static_cast<float*>(
       e->alloc("debug_layers", (size_t)(d.draft_layers + d.n_layers + 2) * 2 * B * H * sizeof(float), &err));
