@@ -199,14 +199,18 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
   }
 
   // Q of the wave's row blocks (padding rows past G*M read the last row; the store skips them)
+  constexpr bool FRESH_OK = QB == 1 && NRG <= 3;  // (the host sends a fresh block to these shapes only: 16 waves spill)
+  const bool fresh = FRESH_OK && p.mix != nullptr;  // the block from the mix rows (see below)
   u32x4 qraw[QB][4];
+  if (!fresh) {
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int r = min((rg * QB + qb) * 16 + n, p.G * p.M - 1);
-    const int t = r / p.G, qh = h * p.G + r % p.G;
-    const _Float16* qr = p.q + ((size_t)t * p.QH + qh) * REC_D + 8 * g;
+    for (int qb = 0; qb < QB; ++qb) {
+      const int r = min((rg * QB + qb) * 16 + n, p.G * p.M - 1);
+      const int t = r / p.G, qh = h * p.G + r % p.G;
+      const _Float16* qr = p.q + ((size_t)t * p.QH + qh) * REC_D + 8 * g;
 #pragma unroll
-    for (int grp = 0; grp < 4; ++grp) qraw[qb][grp] = ldg(reinterpret_cast<const u32x4*>(qr + 32 * grp));
+      for (int grp = 0; grp < 4; ++grp) qraw[qb][grp] = ldg(reinterpret_cast<const u32x4*>(qr + 32 * grp));
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // the Q loads stay ahead of the page loads, so waiting for Q drains no page
 
@@ -230,6 +234,137 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
   };
   if (nsteps > 0) issue(0, ring0);
   if (nsteps > 1) issue(1, ring1);
+
+  // Fresh block (p.mix): Q and the block's K/V records (positions a .. a + M - 1) from the attention-mix GEMM's rows,
+  // the q/k norm + RoPE (+ quantize_pair for the records) done here as the q/k norm + RoPE kernel does. Loaded after
+  // the first two pages are in flight (waiting for these loads waits for those pages too, which step 0 needs anyway,
+  // and keeps the raw rows out of registers while the pages are issued). Fresh pair i = (token i / 4, head i % 4) of
+  // this split's pages goes to wave i % NW; the records sit in registers until their page is in LDS.
+  constexpr int FPW = 4;  // fresh pairs per wave at most: 4 M pairs over 4 NRG waves, M <= 4 NRG (the host checks)
+  uint32_t fkq[FPW], fvq[FPW];  // lanes 0..31: the record's codes of dims l + 32 e, one byte per e
+  float fks[FPW], fvs[FPW];
+  int fslot[FPW], fpg[FPW];     // position's slot and page (-1: no pair)
+  if (fresh) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int r = min((rg * QB + qb) * 16 + n, p.G * p.M - 1);
+      const int t = r / p.G, qh = h * p.G + r % p.G;
+      const float* qr = p.mix + (size_t)t * p.mix_row + (size_t)qh * REC_D + 8 * g;
+      const _Float16* rt = p.rope + (size_t)(p.a + t) * REC_D + 8 * g;
+      float x[4][8];
+      float ss = 0.f;
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const f32x4 a0 = ldg(reinterpret_cast<const f32x4*>(qr + 32 * grp));
+        const f32x4 a1 = ldg(reinterpret_cast<const f32x4*>(qr + 32 * grp + 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[grp][j] = a0[j];
+          x[grp][4 + j] = a1[j];
+        }
+      }
+      half8 w[4], cs[2], sn[2];
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) w[grp] = ldg(reinterpret_cast<const half8*>(p.q_norm + 32 * grp + 8 * g));
+#pragma unroll
+      for (int grp = 0; grp < 2; ++grp) {
+        cs[grp] = ldg(reinterpret_cast<const half8*>(rt + 32 * grp));
+        sn[grp] = ldg(reinterpret_cast<const half8*>(rt + REC_D / 2 + 32 * grp));
+      }
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += x[grp][j] * x[grp][j];
+      ss += __shfl_xor(ss, 16);
+      ss += __shfl_xor(ss, 32);
+      const float inv = rsqrtf(ss / REC_D + p.eps);
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[grp][j] = x[grp][j] * inv * (float)w[grp][j];
+#pragma unroll
+      for (int grp = 0; grp < 2; ++grp)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (32 * grp + 8 * g + j < p.rot) {
+            const float c = (float)cs[grp][j], s_ = (float)sn[grp][j];
+            const float x0 = x[grp][j], x1 = x[grp + 2][j];
+            x[grp][j] = x0 * c - x1 * s_;
+            x[grp + 2][j] = x1 * c + x0 * s_;
+          }
+        }
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        half8 hq;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hq[j] = (_Float16)x[grp][j];
+        qraw[qb][grp] = __builtin_bit_cast(u32x4, hq);
+      }
+    }
+    // fresh records of this split's pages (the q/k norm + RoPE kernel's record branch, per pair)
+#pragma unroll
+    for (int f = 0; f < FPW; ++f) {
+      fpg[f] = -1;
+      const int i = wave + NW * f;
+      const int t = i / REC_KVH, hh = i % REC_KVH;
+      const int pos = p.a + t;
+      if (t >= p.M || pos / PAGE < pb || pos / PAGE >= pe) continue;  // wave-uniform
+      const float* row = p.mix + (size_t)t * p.mix_row;
+      float k[4], v[4], kw[4], kc[2], ksn[2];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = (lane & 31) + 32 * e;
+        k[e] = row[(size_t)(p.QH + hh) * REC_D + d];
+        v[e] = row[(size_t)(p.QH + p.KVH + hh) * REC_D + d];
+        kw[e] = (float)p.k_norm[d];
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int ii = (lane & 31) + 32 * e;
+        kc[e] = (float)p.rope[(size_t)pos * REC_D + ii];
+        ksn[e] = (float)p.rope[(size_t)pos * REC_D + REC_D / 2 + ii];
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += k[e] * k[e];
+      ss = (lane < 32) ? ss : 0.f;
+      ss = wave_sum(ss);
+      const float inv = rsqrtf(ss / REC_D + p.eps);
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = k[e] * inv * kw[e];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        if ((lane & 31) + 32 * e < p.rot) {
+          const float x0 = r[e], x1 = r[e + 2];
+          r[e] = x0 * kc[e] - x1 * ksn[e];
+          r[e + 2] = x1 * kc[e] + x0 * ksn[e];
+        }
+      }
+      float ak = 0.f, av = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ak = fmaxf(ak, fabsf(r[e]));
+        av = fmaxf(av, fabsf(v[e]));
+      }
+      ak = wave_max(ak);
+      av = wave_max(av);
+      const float ks = rec_scale(ak), vs = rec_scale(av);
+      const float ki = __fdiv_rn(1.f, ks), vi = __fdiv_rn(1.f, vs);
+      uint32_t kq = 0, vq = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kq |= (uint32_t)(rec_code(r[e], ki) & 255) << (8 * e);
+        vq |= (uint32_t)(rec_code(v[e], vi) & 255) << (8 * e);
+      }
+      fkq[f] = kq;
+      fvq[f] = vq;
+      fks[f] = ks;
+      fvs[f] = vs;
+      fslot[f] = (pos % PAGE) * REC_KVH + hh;
+      fpg[f] = pos / PAGE;
+    }
+  }
 
   RecQ qv[QB];
 #pragma unroll
@@ -256,6 +391,26 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();  // page k is in LDS; every wave is done with page k - 1 (its slot, vt, kvs)
     if (k + 2 < nsteps) issue(k + 2, nxt);
+    // fresh records of page k into its LDS copy (stale in the pool), then a barrier
+    if (fresh && p.a + p.M - 1 >= (pb + k) * PAGE && p.a < (pb + k + 1) * PAGE) {
+#pragma unroll
+      for (int f = 0; f < FPW; ++f) {
+        if (fpg[f] == pb + k && lane < 32) {
+          char* rec = const_cast<char*>(cur) + fslot[f] * REC_BYTES;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            rec[lane + 32 * e] = (char)((fkq[f] >> (8 * e)) & 255);
+            rec[REC_D + 4 + lane + 32 * e] = (char)((fvq[f] >> (8 * e)) & 255);
+          }
+          if (lane == 0) {
+            *reinterpret_cast<float*>(rec + REC_D) = fks[f];
+            *reinterpret_cast<float*>(rec + 2 * REC_D + 4) = fvs[f];
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(LGKMCNT0_IMM);
+      __builtin_amdgcn_s_barrier();
+    }
     rec_expand<NT>(cur, vt, kvs);
     __builtin_amdgcn_s_waitcnt(LGKMCNT0_IMM);
     __builtin_amdgcn_s_barrier();
@@ -362,6 +517,26 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
     if (k + 2 < nsteps) step(k + 2, ring2, ring1);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // the fresh records into the pool, for later rounds (nothing in this launch reads the pool's copy)
+  if (fresh) {
+#pragma unroll
+    for (int f = 0; f < FPW; ++f) {
+      if (fpg[f] >= 0 && lane < 32) {
+        const int phys = paged ? sm_bt[fpg[f] - pb] : fpg[f];
+        uint8_t* rec = reinterpret_cast<uint8_t*>(const_cast<_Float16*>(p.kp)) + (size_t)phys * REC_PAGE +
+                       (size_t)fslot[f] * REC_BYTES;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          rec[lane + 32 * e] = (uint8_t)((fkq[f] >> (8 * e)) & 255);
+          rec[REC_D + 4 + lane + 32 * e] = (uint8_t)((fvq[f] >> (8 * e)) & 255);
+        }
+        if (lane == 0) {
+          *reinterpret_cast<float*>(rec + REC_D) = fks[f];
+          *reinterpret_cast<float*>(rec + 2 * REC_D + 4) = fvs[f];
+        }
+      }
+    }
+  }
 
   // partials of this split: rows of KV head h, (max, sum) and acc / PSCALE
   // row-major partials ([head][row][split][D]; the head's region is R x S rows of D floats)

@@ -378,9 +378,13 @@ AttnParams attn_setup(dspark_engine* e, const LayerW& Lw, int drafter, int plan_
 
 // Whether the attention kernel takes the block fresh from the mix rows -- Q and the block's K/V normed and rotated in
 // the kernel, no q/k norm + RoPE launch before it: the LDS kernel over fp16 pages at D = 64 with one row block per
-// wave and at most one block token per wave.
+// wave and at most one block token per wave, or the record kernel with up to 3 row groups and splits of 8 pages or
+// more (its in-kernel Q and record work delays a split's first page by ~1-2 us: reference-build rounds measured
+// 1.645 -> 1.672 ms at 1k and 1.699 -> 1.713 at 32k with every record layer fused, 1.787 -> 1.769 at 128k).
 bool attn_fresh_ok(dspark_engine* e, const LayerW& Lw, const AttnParams& p) {
-  return e->fresh && !Lw.kv_rec && e->d.head_dim == 64 && p.lds == 1 && p.qb == 1 && p.M <= p.nrg * p.pl;
+  if (!e->fresh || p.qb != 1) return false;
+  if (Lw.kv_rec) return p.nrg <= 3 && p.M <= 4 * p.nrg && p.pps >= 8;
+  return e->d.head_dim == 64 && p.lds == 1 && p.M <= p.nrg * p.pl;
 }
 
 // Layer Lw's verify attention (attn_setup's parameters); fresh: the block from the mix rows (attn_fresh_ok).
