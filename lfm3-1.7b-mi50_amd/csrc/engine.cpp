@@ -154,6 +154,7 @@ struct dspark_engine {
   // whether attention layers that can take their block fresh from the mix rows do (attn_fresh_ok); DSPARK_FRESH=0 at
   // engine creation runs the q/k norm + RoPE kernel before every attention instead (for comparisons)
   bool fresh = true;
+  int fresh_rec_pps = 8;  // the record kernel's least pages per split for a fresh block (DSPARK_FRESH_REC_PPS)
 
   ~dspark_engine() {
     for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
@@ -383,7 +384,7 @@ AttnParams attn_setup(dspark_engine* e, const LayerW& Lw, int drafter, int plan_
 // 1.645 -> 1.672 ms at 1k and 1.699 -> 1.713 at 32k with every record layer fused, 1.787 -> 1.769 at 128k).
 bool attn_fresh_ok(dspark_engine* e, const LayerW& Lw, const AttnParams& p) {
   if (!e->fresh || p.qb != 1) return false;
-  if (Lw.kv_rec) return p.nrg <= 3 && p.M <= 4 * p.nrg && p.pps >= 8;
+  if (Lw.kv_rec) return p.nrg <= 3 && p.M <= 4 * p.nrg && p.pps >= e->fresh_rec_pps;
   return e->d.head_dim == 64 && p.lds == 1 && p.M <= p.nrg * p.pl;
 }
 
@@ -870,6 +871,8 @@ int dspark_engine_create(const dspark_model_desc* desc, int32_t max_context, dsp
   {
     const char* fv = std::getenv("DSPARK_FRESH");
     e->fresh = !(fv && fv[0] == '0');
+    const char* fr = std::getenv("DSPARK_FRESH_REC_PPS");
+    if (fr) e->fresh_rec_pps = std::max(1, std::atoi(fr));
   }
   e->trace = static_cast<uint64_t*>(e->alloc("trace", (size_t)(2 + 2 * DSPARK_TRACE_MAX_MARKS) * 8, &err));
   e->dump = static_cast<float*>(

@@ -66,7 +66,14 @@ REL_REC = 5e-3  # the same bar with int8 K/V records
 REL_X8 = 2.5e-2
 GEOMETRIES = {"small": SMALL, "ref_small": REF_SMALL, "small_stop": SMALL, "small_wide": SMALL_WIDE, "mid": MID,
               "mid24": MID24, "mid33": MID33, "mid64": MID64, "ref_rec": REF_REC, "small_ctxlo": SMALL,
-              "ref_x8": REF_X8}
+              "ref_x8": REF_X8, "ref_rec_fresh": REF_REC, "ref_x8_fresh": REF_X8}
+
+
+def fresh_records_everywhere(geom, monkeypatch):
+    """*_fresh geometries: the record kernel takes its block fresh from the mix rows at every split (it does from 8
+    pages per split otherwise, so at these contexts it would not)."""
+    if geom.endswith("_fresh"):
+        monkeypatch.setenv("DSPARK_FRESH_REC_PPS", "1")
 STOP_ANCHOR = 17
 
 
@@ -86,7 +93,8 @@ def make_weights(eng, desc, seed, stop_half=False):
                                                            "h0", "h1", "x16", "mix", "q16", "gate", "y16", "vout", "a16",
                                                            "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys",
                                                            "ws_", "rope", "ring_table", "tap_x", "plant", "conv_state",
-                                                           "trace", "debug_layers", "x_scales", "y_scales"))]
+                                                           "trace", "debug_layers", "x_scales", "y_scales", "xc16",
+                                                           "xc_scales"))]
     for n in weight_names:
         nb = sizes[n]
         if n.endswith(".w") and not n.endswith("conv.w"):
@@ -203,10 +211,12 @@ def near_tie_ok(values, got, want, rel=1e-3):
 @pytest.mark.parametrize("geom,seed", [("small", 11), ("small", 12), ("ref_small", 13), ("small_stop", 14),
                                        ("small_stop", 15), ("small_stop", 16), ("small_wide", 17), ("mid", 18),
                                        ("mid", 19), ("mid24", 20), ("mid33", 27), ("mid64", 30), ("ref_rec", 28),
-                                       ("small_ctxlo", 31), ("ref_x8", 32)])
-def test_engine_round_matches_oracle(dev, orc, geom, seed):
+                                       ("small_ctxlo", 31), ("ref_x8", 32), ("ref_rec_fresh", 38),
+                                       ("ref_x8_fresh", 39)])
+def test_engine_round_matches_oracle(dev, orc, geom, seed, monkeypatch):
     torch = dev
     host = load_host()
+    fresh_records_everywhere(geom, monkeypatch)
     from oracle import round as rnd
     desc = host.model_desc(**GEOMETRIES[geom])
     eng = host.Engine(desc, 512)
@@ -220,10 +230,18 @@ def test_engine_round_matches_oracle(dev, orc, geom, seed):
                ctx_pos=a - ctx_new, ctx_lo=ctx_lo, run=1, skip_rounds=1, stop_at=a + 64, ckpt_slot=-1,
                tokens=[anchor])
     eng.set_state(**st0)
+    # every attention layer takes its block fresh from the mix rows (mid: fp16 pages at D = 64, 9-token blocks; the
+    # *_fresh geometries: records at every split), so no q/k norm + RoPE launch writes q16
+    fused = geom.endswith("_fresh") or geom == "mid"
+    if fused:
+        q_sentinel = np.full(eng.tensor("q16")[1] // 2, 0x7E00, np.uint16)
+        eng.upload("q16", q_sentinel)
     torch.cuda.synchronize()
     print(f"case engine round geom={geom} seed={seed}", flush=True)
     eng.round(0, a)
     torch.cuda.synchronize()
+    if fused:
+        assert np.array_equal(eng.download("q16", np.uint16), q_sentinel)
     B, V, N = desc.block, desc.vocab, desc.crop_rows
     MV = min(B, 1 + desc.max_drafts)  # the verify pass's rows (drafts never exceed max_drafts)
     st = eng.state()
@@ -337,14 +355,16 @@ def _greedy_chain(eng, torch, st0, n):
 
 @pytest.mark.parametrize("geom,seed,wrong", [("small", 21, ()), ("small", 22, (3, 10, 11, 20)), ("ref_small", 23, ()),
                                              ("ref_small", 24, (0, 5, 13, 14)), ("mid", 25, (2, 9)),
-                                             ("ref_rec", 29, (4, 12)), ("ref_x8", 33, (3, 9))])
-def test_planted_rounds_commit_the_greedy_chain(dev, geom, seed, wrong):
+                                             ("ref_rec", 29, (4, 12)), ("ref_x8", 33, (3, 9)),
+                                             ("ref_rec_fresh", 40, (2, 11))])
+def test_planted_rounds_commit_the_greedy_chain(dev, geom, seed, wrong, monkeypatch):
     """Speculative rounds commit exactly the target's greedy chain, whatever the drafts: with drafts planted from the
     chain (force_m = -1), every round commits its drafts' accepted prefix plus the target's own next token. All
     drafts right: each round commits all of its drafts plus one. Chain positions listed in `wrong` are planted with a different
     token: the round stops there and commits the chain token as its bonus."""
     torch = dev
     host = load_host()
+    fresh_records_everywhere(geom, monkeypatch)
     desc = host.model_desc(**GEOMETRIES[geom])
     B = desc.block
     eng = host.Engine(desc, 512)

@@ -37,7 +37,7 @@ LAYER_REL_X8 = 2e-2
 LOGIT_TOL = 2e-3
 RUNTIME = ("kv.", "ring.", "conv.", "state", "seen", "out_tokens", "rep", "h0", "h1", "x16", "mix", "q16", "gate",
            "y16", "vout", "a16", "w2out", "ctx", "ckv_out", "taps", "logits", "base", "keys", "ws_", "rope",
-           "ring_table", "tap_x", "plant", "conv_state", "trace", "debug_layers", "x_scales", "y_scales")
+           "ring_table", "tap_x", "plant", "conv_state", "trace", "debug_layers", "x_scales", "y_scales", "xc16", "xc_scales")
 
 
 @pytest.fixture(scope="module")
