@@ -1,6 +1,6 @@
 // Elementwise and small kernels of the DSpark round: embedding, residual + RMS norms, q/k norm + RoPE + K/V page write
-// (the context projection's; the verify and drafter blocks run it in the mix GEMM's epilogue, as they do the gated
-// short conv), the drafter's Markov/confidence steps and the round's bookkeeping. Every kernel reads the
+// (the context projection's, and the verify and drafter blocks' where the attention kernel does not take the block
+// fresh from the mix rows), the drafter's Markov/confidence steps and the round's bookkeeping. Every kernel reads the
 // positions it needs (a, ctx_pos, ...) from the device State and returns at once when State.run is 0, so a whole
 // round is a fixed launch sequence that can be replayed without the host reading anything back.
 // Reference: norm_compute (dspark.hip:722-843), query_fresh + norm_rope (999-1061, 946-951),
