@@ -502,7 +502,10 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   // loaded from the mix rows first, so they are the oldest loads in the counter and the first step's wait covers them.
   f32x4 fq[QB][D / 32][2];
   half8 fqw[D / 32], fqc[D / 64], fqs[D / 64];
-  float fk[NE], fv[NE], fkw[NE], fkc[NE / 2], fks[NE / 2];
+  // (kept in their loaded types until the first barrier: a conversion next to its load would make the compiler wait
+  // for these loads, and every older one, before the pages are issued)
+  float fk[NE], fv[NE];
+  _Float16 fkw[NE], fkc[NE / 2], fks[NE / 2];
   if (fresh) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -523,13 +526,13 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
         const int d = (lane & 31) + 32 * e;
         fk[e] = row[(size_t)(p.QH + h) * D + d];
         fv[e] = row[(size_t)(p.QH + p.KVH + h) * D + d];
-        fkw[e] = (float)p.k_norm[d];
+        fkw[e] = p.k_norm[d];
       }
 #pragma unroll
       for (int e = 0; e < NE / 2; ++e) {
         const int i = (lane & 31) + 32 * e;
-        fkc[e] = (float)p.rope[(size_t)fpos * D + i];
-        fks[e] = (float)p.rope[(size_t)fpos * D + D / 2 + i];
+        fkc[e] = p.rope[(size_t)fpos * D + i];
+        fks[e] = p.rope[(size_t)fpos * D + D / 2 + i];
       }
     }
   }
@@ -559,8 +562,10 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   }
   char* const slots[4] = {ring0, ring1, ring2, ring3};
 #pragma unroll
-  for (int u = 0; u < RING - 1; ++u)
-    if (u < nsteps) issue(u, slots[u]);
+  // (every one of the first RING - 1 steps is issued, steps past the split as out-of-range loads into `trash`: a fixed
+  // count of younger loads, so the compiler's own wait for the raw rows above leaves the pages in flight; the counted
+  // waits stay right, the extra loads being the youngest)
+  for (int u = 0; u < RING - 1; ++u) issue(u, slots[u]);
   if (nsteps >= RING - 1)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((RING - 1) * LPW));
   else if (nsteps >= 1)
@@ -569,6 +574,22 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __builtin_amdgcn_s_barrier();
   if (fresh) {
+    // The raw rows are first used here: an empty asm that rewrites them keeps the compiler from moving any use (a
+    // conversion) up next to its load, where it would wait for the loads before the pages were issued.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) asm volatile("" : "+v"(fq[qb][s][0]), "+v"(fq[qb][s][1]));
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) asm volatile("" : "+v"(fqw[s]));
+#pragma unroll
+    for (int s = 0; s < D / 64; ++s) asm volatile("" : "+v"(fqc[s]), "+v"(fqs[s]));
+    if (fmine) {
+#pragma unroll
+      for (int e = 0; e < NE; ++e) asm volatile("" : "+v"(fk[e]), "+v"(fv[e]), "+v"(fkw[e]));
+#pragma unroll
+      for (int e = 0; e < NE / 2; ++e) asm volatile("" : "+v"(fkc[e]), "+v"(fks[e]));
+    }
     // q/k norm + RoPE of the block (the q/k norm + RoPE kernel's arithmetic): row n's dims 32 s + 8 g + j sit in
     // lane (n, g), so a row's sum of squares is four lanes and every RoPE pair (i, i + D / 2) is in one lane
 #pragma unroll
@@ -617,13 +638,13 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
       const float inv = rsqrtf(ss / D + p.eps);
       float r[NE];
 #pragma unroll
-      for (int e = 0; e < NE; ++e) r[e] = fk[e] * inv * fkw[e];
+      for (int e = 0; e < NE; ++e) r[e] = fk[e] * inv * (float)fkw[e];
 #pragma unroll
       for (int e = 0; e < NE / 2; ++e) {
         if ((lane & 31) + 32 * e < p.rot) {
-          const float x0 = r[e], x1 = r[e + NE / 2];
-          r[e] = x0 * fkc[e] - x1 * fks[e];
-          r[e + NE / 2] = x1 * fkc[e] + x0 * fks[e];
+          const float x0 = r[e], x1 = r[e + NE / 2], c = (float)fkc[e], sn = (float)fks[e];
+          r[e] = x0 * c - x1 * sn;
+          r[e + NE / 2] = x1 * c + x0 * sn;
         }
       }
 #pragma unroll
