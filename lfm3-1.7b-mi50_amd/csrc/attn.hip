@@ -363,7 +363,9 @@ constexpr int ATTN_CPOL_COHERENT = 16;  // buffer-store cache policy SC1: device
 // page lane pl = w / NRG. With QB > 1 fewer waves share each page (LDS reads per step fall by QB) and the waves can be
 // a multiple of four (one share per SIMD: 9 row blocks as 3 groups of 3 x 4 page lanes = 12 waves, where 9 waves of
 // one block each left one SIMD a third more work than the others).
-template <int D, int QB, int PL, int PPL, int LPW, int MAXW>
+// FR: the instantiation that takes a fresh block from the mix rows (p.mix; D = 64, QB = 1); the others are free of
+// that code, so the plain kernel's registers and load order stay its own.
+template <int D, int QB, int PL, int PPL, int LPW, int MAXW, bool FR = false>
 __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p) {
   constexpr int PAGEB = 4 * PAGE * D;  // K + V bytes of one (page, KV head)
   constexpr int CPG = PAGEB / 1024;    // 1 KB chunks per page: K chunks first, then V^T chunks
@@ -419,7 +421,7 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
 
   // Fresh block (p.mix): wave w's fresh row is token w's K/V, at position a + w (the host sends M <= waves).
   constexpr int NE = D / 32;  // a fresh K/V row's dims per lane: lanes 0..31 hold dims l + 32 e, 32..63 repeat them
-  constexpr bool FRESH_OK = QB == 1 && D == 64;  // (the host sends a fresh block to these shapes only)
+  constexpr bool FRESH_OK = FR && QB == 1 && D == 64;  // (the host sends a fresh block to these shapes only)
   const bool fresh = FRESH_OK && p.mix != nullptr;
   const int fpos = p.a + wave;
   const int fpage = fpos / PAGE;
@@ -562,10 +564,11 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   }
   char* const slots[4] = {ring0, ring1, ring2, ring3};
 #pragma unroll
-  // (every one of the first RING - 1 steps is issued, steps past the split as out-of-range loads into `trash`: a fixed
-  // count of younger loads, so the compiler's own wait for the raw rows above leaves the pages in flight; the counted
-  // waits stay right, the extra loads being the youngest)
-  for (int u = 0; u < RING - 1; ++u) issue(u, slots[u]);
+  // (with a fresh block every one of the first RING - 1 steps is issued, steps past the split as out-of-range loads
+  // into `trash`: a fixed count of younger loads, so the compiler's own wait for the raw rows above leaves the pages
+  // in flight; the counted waits stay right, the extra loads being the youngest)
+  for (int u = 0; u < RING - 1; ++u)
+    if (FRESH_OK || u < nsteps) issue(u, slots[u]);
   if (nsteps >= RING - 1)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((RING - 1) * LPW));
   else if (nsteps >= 1)
@@ -950,6 +953,15 @@ static void launch_attn(const AttnParams& p, hipStream_t s) {
 template <int D, int QB, int PL, int PPL, int LPW, int MAXW>
 static int launch_lds(const AttnParams& p, hipStream_t s) {
   if (p.nrg * PL > MAXW) return DSPARK_EUNSUPPORTED;
+  if constexpr (QB == 1 && D == 64) {
+    if (p.mix) {  // a fresh block: at most one block token per wave
+      if (p.M > p.nrg * PL) return DSPARK_EUNSUPPORTED;
+      hipLaunchKernelGGL((verify_attn_lds_kernel<D, QB, PL, PPL, LPW, MAXW, true>), dim3(p.KVH * p.S),
+                         dim3(p.nrg * PL * 64), 0, s, p);
+      return 0;
+    }
+  }
+  if (p.mix) return DSPARK_EUNSUPPORTED;
   hipLaunchKernelGGL((verify_attn_lds_kernel<D, QB, PL, PPL, LPW, MAXW>), dim3(p.KVH * p.S), dim3(p.nrg * PL * 64), 0, s,
                      p);
   return 0;
@@ -1077,6 +1089,7 @@ void attn_bind_workspace(AttnParams& p, int D, void* ws) {
 }
 
 static int launch_split(const AttnParams& p, int D, hipStream_t s) {
+  if (p.mix && !p.lds) return DSPARK_EUNSUPPORTED;  // (a fresh block goes to the LDS kernel only)
   if (p.lds) {
     // instantiated shapes (see lds_shape), as (PL, PPL, LPW): D = 64: (4, 1, 8 | 4 | 3 | 2), (2, 2, 4 | 3 | 2),
     // (1, 4, 4 | 3 | 2); D = 128: (2, 1, 16 | 8 | 6 | 4 | 3 | 2), (1, 1, 2 | 1)
