@@ -575,7 +575,7 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   const int run = run_flag_load(p.st);
   extern __shared__ u32x4 xs[];
   constexpr int WV = I8 ? 1 : 2;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int S = p.wpg, KW = p.kw;
   const int s = wave % S, kq = wave / S;
