@@ -131,7 +131,7 @@ template <int TB>
 __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int s, int S, bool holder,
                                     int lane, float* tile) {
   const int R = 16 * S, RS = R + 4;
-  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int grow0 = grp * R, r = 16 * s + 4 * g;
   f32x4 sc = {1.f, 1.f, 1.f, 1.f};
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   if (gemm_stopped(p)) return;
   extern __shared__ u32x4 xs[];
   constexpr int WV = I8 ? 1 : 2, PH = GEMM_PHASE_UNITS / TB;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int grp = blockIdx.x / p.ksplit, ks = blockIdx.x % p.ksplit;
   const int strips = p.N / 16;

@@ -113,12 +113,18 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
 #pragma unroll
       for (int k = 0; k < NK; ++k) lb[bb][k] = ldg(reinterpret_cast<const f32x4*>(vb + col[k]));
     }
+    // every load issued before the first add waits; a select, not a branch: under a branch the compiler sinks the
+    // second band's loads into it, behind the wait for the first band's values
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int bb = 0; bb < BB; ++bb)
-      if (b0 + bb < p.bands) {
+    for (int bb = 0; bb < BB; ++bb) {
+      const bool use = b0 + bb < p.bands;
 #pragma unroll
-        for (int k = 0; k < NK; ++k) vv[k] += lb[bb][k];
+      for (int k = 0; k < NK; ++k) {
+        const f32x4 sum = vv[k] + lb[bb][k];
+        vv[k] = use ? sum : vv[k];
       }
+    }
   };
   if (p.bands > 0) band_batch(0);
   for (int b0 = BB; b0 < p.bands; b0 += BB) band_batch(b0);
