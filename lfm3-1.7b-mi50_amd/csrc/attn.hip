@@ -185,10 +185,7 @@ __device__ __forceinline__ void page_accumulate(const Tile<D>& tl, RowState<D, Q
 
 template <int D, int QB, int PF, int OCC, bool QLDS>
 __global__ __launch_bounds__(256, OCC) void verify_attn_kernel(AttnParams p) {
-  if (p.st) {
-    if (p.st->run == 0) return;
-    attn_range(p);
-  }
+  if (p.st && !attn_state_range(p)) return;
   constexpr int R = 16 * QB;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: page indices stay scalar
@@ -380,10 +377,10 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   constexpr bool QRING = QBYTES <= PPS * PAGEB;
   __shared__ __attribute__((aligned(16))) char q_own[QRING ? 16 : QBYTES];
   char* const q_lds = QRING ? (RING > 3 ? ring3 : ring2) : q_own;
-  if (p.st) {
-    if (p.st->run == 0) return;
-    attn_range(p);
-  }
+  // The kernel arguments' last line (the fresh block's rope and eps) with the others in the first round trip: loaded
+  // later, with the arguments the block-table loads need, its miss would delay them.
+  if constexpr (FR) asm volatile("" ::"s"(p.rope));
+  if (p.st && !attn_state_range(p)) return;
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NRB = p.nrb, NRG = p.nrg, NW = NRG * PL;
@@ -415,7 +412,7 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
   // vector load (the direct-to-LDS loads count as possible clobbers), and its wait would drain the pages in flight.
   const bool paged = p.bt != nullptr;
   if (paged) {
-    for (int i = threadIdx.x; i < pe - pb; i += blockDim.x) sm_bt[i] = ldg(p.bt + pb + i);
+    for (int i = threadIdx.x; i < pe - pb; i += NW * 64) sm_bt[i] = ldg(p.bt + pb + i);
     __syncthreads();
   }
 
@@ -785,13 +782,26 @@ __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) 
   __shared__ f32x2 s_ml[W > 1 ? W - 1 : 1][Q];
   const int hr = blockIdx.y, h = hr / p.RG, rg = hr % p.RG, r = blockIdx.x;
   const int row = rg * p.R + r;
-  if (row >= p.G * p.M) return;  // the same for the whole workgroup
+  // Padding rows of the last row group (row >= G M, the same for the whole workgroup) load their partials (inside the
+  // workspace) and store nothing: returning before the loads would put the kernel arguments the loads need behind the
+  // test's own, one more dependent round trip for every row.
+  const bool live = row < p.G * p.M;
   const int run = run_flag_load(p.st);  // tested once the partial loads are in flight
+  // The gate word is loaded with the partials (a zero-length buffer when there is no gate: the load returns 0).
+  const int rowc = min(row, p.G * p.M - 1);
+  const int t = rowc / p.G, qh = h * p.G + rowc % p.G;
+  const int gstride = p.gate_stride > 0 ? p.gate_stride : p.QH;
+  const __amdgpu_buffer_rsrc_t rgate = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.gate, (short)0, p.gate ? (int)((size_t)p.M * gstride * sizeof(float)) : 0, 0x00020000);
+  const float gv = __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(rgate, (int)(((size_t)t * gstride + qh) * sizeof(float)), 0, 0));
   const int q = threadIdx.x % Q, j = threadIdx.x / Q;
   const size_t base = ((size_t)hr * p.R + r) * p.S;
   float m = -INFINITY, l = 0.f;
   f32x4 acc = {0, 0, 0, 0};
-  for (int b0 = 0; b0 < p.S; b0 += SL * PER) {
+  // Batches of SL x PER splits; the first is outside the loop (a loop head's wait, counted for the back edge, would hold
+  // its partial loads until the flag and gate words had arrived). Returns false when the workgroup stores nothing.
+  auto batch = [&](int b0) -> bool {
     f32x2 ml[PER];
     f32x4 av[PER];
 #pragma unroll
@@ -801,9 +811,9 @@ __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) 
       ml[i] = ok ? ldg(p.part_ml + base + sp) : f32x2{-INFINITY, 0.f};
       av[i] = ok ? ldg(reinterpret_cast<const f32x4*>(p.part_acc + (base + sp) * D) + q) : f32x4{0, 0, 0, 0};
     }
-    if (!run_flag_set(run)) {  // a stopped round writes nothing (the same for the whole workgroup)
+    if (!run_flag_set(run) || !live) {  // a stopped round or a padding row writes nothing (the whole workgroup)
       __builtin_amdgcn_s_waitcnt(0);
-      return;
+      return false;
     }
     float mb = m;
 #pragma unroll
@@ -820,7 +830,11 @@ __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) 
         acc += f * av[i];
       }
     }
-  }
+    return true;
+  };
+  if (!batch(0)) return;  // (S >= 1)
+  for (int b0 = SL * PER; b0 < p.S; b0 += SL * PER)
+    if (!batch(b0)) return;
   auto fold = [&](float mk, float lk, f32x4 ak) {
     const float mx = fmaxf(m, mk);
     if (mx > -INFINITY) {
@@ -852,8 +866,7 @@ __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) 
   }
   if (lane >= Q) return;
   float scale = l > 0.f ? 1.f / l : 0.f;
-  const int t = row / p.G, qh = h * p.G + row % p.G;
-  if (p.gate) scale *= 1.f / (1.f + expf(-ldg(p.gate + (size_t)t * (p.gate_stride > 0 ? p.gate_stride : p.QH) + qh)));
+  if (p.gate) scale *= 1.f / (1.f + expf(-gv));
   {
 #pragma clang fp contract(off)  // the fp16 output is the fp32 output rounded (no product fused into the conversion)
     acc *= scale;

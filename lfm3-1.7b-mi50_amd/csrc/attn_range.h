@@ -6,13 +6,13 @@
 
 namespace dspark {
 
-// The same plan evaluated on the device from the State's a: page range, pages per split, unmasked range.
-__device__ inline void attn_range(AttnParams& p) {
-  const int a = p.st->a;
+// The same plan evaluated on the device from the State's a (and, for the drafter, ctx_lo): page range, pages per
+// split, unmasked range.
+__device__ inline void attn_range(AttnParams& p, int a, int ctx_lo) {
   p.a = a;
   if (p.drafter) {
     // drafter ring: context [max(ctx_lo, a - window), a) for every block token, block keys in both directions
-    p.start = max(p.st->ctx_lo, a - p.window);
+    p.start = max(ctx_lo, a - p.window);
     p.window = 0;
     p.causal = 0;
   } else if (p.window > 0) {
@@ -26,6 +26,17 @@ __device__ inline void attn_range(AttnParams& p) {
   p.page0 = lo0 / PAGE;
   p.npages = hi_last / PAGE - p.page0 + 1;
   p.pps = (p.npages + p.S - 1) / p.S;
+}
+
+// A key-split kernel's prologue with a State: run, a and ctx_lo read in one round trip (scalar loads of one line; the
+// empty asm takes all three before the run test, which would otherwise put the other two behind it). Returns false
+// when the round is stopped.
+__device__ inline bool attn_state_range(AttnParams& p) {
+  const int run = p.st->run, a = p.st->a, lo = p.st->ctx_lo;
+  asm volatile("" ::"s"(run), "s"(a), "s"(lo));
+  if (run == 0) return false;
+  attn_range(p, a, lo);
+  return true;
 }
 
 }  // namespace dspark

@@ -178,10 +178,10 @@ __global__ __launch_bounds__(REC_KVH * NRG * 64) void verify_attn_rec_kernel(Att
   __shared__ __attribute__((aligned(16))) float kvs[REC_KVH * 2 * PAGE];
   __shared__ __attribute__((aligned(16))) char trash[1024];
   __shared__ int32_t sm_bt[REC_BT_MAX];
-  if (p.st) {
-    if (p.st->run == 0) return;
-    attn_range(p);
-  }
+  // Every line of the kernel arguments the prologue reads in the first round trip (the split bounds' line, 0xc0 on,
+  // would otherwise be read after the State's, one more dependent miss before the block-table loads).
+  asm volatile("" ::"s"(p.mix));
+  if (p.st && !attn_state_range(p)) return;
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = wave / NRG, rg = wave % NRG;

@@ -137,17 +137,28 @@ __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uin
                                                            int32_t* out_tokens, int out_cap, uint32_t* seen,
                                                            const uint64_t* part, int nchunks, int mfold,
                                                            int32_t* mirror) {
-  if (st->run == 0) return;
+  // The run word and the first batch of partial keys are requested together, and the keys are folded into LDS before
+  // run is tested (an early return ahead of the folding let the compiler move the key loads behind the State's round
+  // trip). Buffer loads: 0 -- no key -- past the keys, and for every load when there are none. A stopped round writes
+  // nothing.
+  const int run = run_flag_load(st);
+  const int n = part ? mfold * nchunks : 0;
+  constexpr int PB = 8;
+  const __amdgpu_buffer_rsrc_t rp =
+      __builtin_amdgcn_make_buffer_rsrc((void*)part, (short)0, n * (int)sizeof(uint64_t), 0x00020000);
+  u32x2 v0[PB];
+#pragma unroll
+  for (int i = 0; i < PB; ++i)
+    v0[i] = __builtin_amdgcn_raw_buffer_load_b64(rp, (64 * i + (int)threadIdx.x) * (int)sizeof(uint64_t), 0, 0);
   if (part) {
     __shared__ unsigned long long sb[64];
     sb[threadIdx.x] = 0;
     __syncthreads();
-    const int n = mfold * nchunks;
-    constexpr int PB = 8;
     for (int e0 = 0; e0 < n; e0 += 64 * PB) {
       uint64_t v[PB];
 #pragma unroll
-      for (int i = 0; i < PB; ++i) v[i] = ldg(part + min(e0 + 64 * i + (int)threadIdx.x, n - 1));
+      for (int i = 0; i < PB; ++i)
+        v[i] = e0 == 0 ? __builtin_bit_cast(uint64_t, v0[i]) : ldg(part + min(e0 + 64 * i + (int)threadIdx.x, n - 1));
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
         const int e = e0 + 64 * i + (int)threadIdx.x;
@@ -155,10 +166,10 @@ __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uin
       }
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
+    if (threadIdx.x != 0 || !run_flag_set(run)) return;
     for (int t = 0; t < mfold; ++t) best[t] = sb[t];  // the folded keys (thread 0 reads its own writes below)
   }
-  if (threadIdx.x != 0) return;
+  if (threadIdx.x != 0 || !run_flag_set(run)) return;
   if (m <= 0) m = st->M;  // rounds that drafted on the device: the verified count is in the State
   int acc = 0;
   for (int t = 0; t < m - 1; ++t) {

@@ -205,6 +205,9 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
 // base + t with base = st->a (verify, drafter block) or st->ctx_pos (context projection); tokens t >= count
 // (count = M, or st->ctx_new) are skipped.
 __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
+  // The parameters' three 64-byte lines (fields at 0, 64 and 132 bytes span any placement of the 136-byte struct) in
+  // one round trip: read where they are first used, behind the early-exit tests, they were four dependent misses.
+  asm volatile("" ::"s"(p.st), "s"(p.eps), "s"(p.count_from_ctx));
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int heads = p.QH + p.KVH;
