@@ -33,13 +33,24 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint32_t w0, uint32_t w1) {
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
 
 // Epilogue for one lane's 4 rows (row0 + 4g + i) of token t.
-__device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0, int g, f32x4 v) {
+// The per-row weight scales of rows r .. r + 3 as fp16 bits (1 without scales). The kernels load them with their first
+// loads (read in the epilogue, they were a dependent round trip after the main loop) and widen them in the epilogue,
+// behind an empty asm: widened where they are loaded, the conversion's wait would hold every weight load back.
+__device__ __forceinline__ u32x2 gemm_row_scales(const GemmParams& p, int r) {
+  if (!p.scale) return u32x2{0x3C003C00u, 0x3C003C00u};
+  return ldg(reinterpret_cast<const u32x2*>(p.scale + r));
+}
+__device__ __forceinline__ f32x4 gemm_row_scales_f32(u32x2 raw) {
+  asm volatile("" : "+v"(raw));
+  const half4 h = __builtin_bit_cast(half4, raw);
+  return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
+// sc: gemm_row_scales of rows row0 + 4 g .. (a product by 1 leaves the value unchanged)
+__device__ __forceinline__ void gemm_store(const GemmParams& p, int t, int row0, int g, f32x4 v, f32x4 sc) {
   if (t >= p.M) return;
   const int r = row0 + 4 * g;
-  if (p.scale) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] *= (float)ldg(p.scale + r + i);
-  }
+  v *= sc;
   if (p.epilogue == 1) {
     // rows (2i, 2i+1) = (gate, up): h[t][r/2 + i] = fp16(silu(gate) * up); r/2 is even, so the pair is contiguous
     _Float16* y = p.y16 + (p.yop ? xop_elem(t, r / 2, p.yop) : (size_t)t * (p.N / 2) + r / 2);
@@ -127,18 +138,14 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
 }
 
 // S strips per group; the waves with `holder` set hold strip s's sums (every wave of the workgroup finishes the group).
+// sc: the holder's row scales (gemm_row_scales of rows grow0 + r; strips past N hold rows no epilogue reads).
 template <int TB>
 __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int s, int S, bool holder,
-                                    int lane, float* tile) {
+                                    int lane, float* tile, f32x4 sc) {
   const int R = 16 * S, RS = R + 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int grow0 = grp * R, r = 16 * s + 4 * g;
-  f32x4 sc = {1.f, 1.f, 1.f, 1.f};
-  if (holder && p.scale && grow0 + r < p.N) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sc[i] = (float)ldg(p.scale + grow0 + r + i);
-  }
   __syncthreads();  // every wave is done with the LDS it used before
   if (holder) {
 #pragma unroll
@@ -155,7 +162,8 @@ __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB],
 // Finished sums of one strip (lane (n, g): rows 16 strip + 4 g + i of token 16 tb + n): the strip's row-argmax key
 // per token when the call asks for it, then the epilogue store.
 template <int TB>
-__device__ __forceinline__ void gemm_strip_out(const GemmParams& p, const f32x4 (&acc)[TB], int strip, int lane) {
+__device__ __forceinline__ void gemm_strip_out(const GemmParams& p, const f32x4 (&acc)[TB], int strip, int lane,
+                                               f32x4 sc) {
   const int n = lane & 15, g = lane >> 4, row0 = strip * 16;
   if (p.best_part) {
     // fold the lane's 4 rows, then the 4 row groups
@@ -176,7 +184,7 @@ __device__ __forceinline__ void gemm_strip_out(const GemmParams& p, const f32x4 
     }
   }
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) gemm_store(p, 16 * tb + n, row0, g, acc[tb]);
+  for (int tb = 0; tb < TB; ++tb) gemm_store(p, 16 * tb + n, row0, g, acc[tb], sc);
 }
 
 constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
@@ -208,6 +216,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
   const bool live = strip_raw < strips;
   const int strip = live ? strip_raw : strips - 1;
   const int row0 = strip * 16;
+  const u32x2 rsc = gemm_row_scales(p, row0 + 4 * g);  // first of the kernel's loads (the epilogue's)
   const int chunks = p.K / 64;
   const int cpk = (chunks + p.ksplit - 1) / p.ksplit;
   const int c0 = ks * cpk, c1 = min(chunks, c0 + cpk);
@@ -410,11 +419,11 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     }
   }
   if (p.fuse) {
-    gemm_group_epilogue<TB>(p, acc, grp, wave, nw, true, lane, reinterpret_cast<float*>(xs));
+    gemm_group_epilogue<TB>(p, acc, grp, wave, nw, true, lane, reinterpret_cast<float*>(xs), gemm_row_scales_f32(rsc));
     return;
   }
   if (!live) return;
-  gemm_strip_out<TB>(p, acc, strip, lane);
+  gemm_strip_out<TB>(p, acc, strip, lane, gemm_row_scales_f32(rsc));
 }
 
 // K-sliced GEMM for one workgroup of S x KW waves (S = wpg strips of 16 rows, KW = kw contiguous ranges of K): wave
@@ -586,6 +595,7 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   const bool live = strip_raw < strips;
   const int strip = live ? strip_raw : strips - 1;
   const int row0 = strip * 16;
+  const u32x2 rsc = gemm_row_scales(p, row0 + 4 * g);  // first of the kernel's loads (the epilogue's)
   const int chunks = p.K / 64;
   const int cpb_ = (chunks + p.bands - 1) / p.bands;  // chunks per band
   const int b0 = min(chunks, band * cpb_), b1 = min(chunks, b0 + cpb_);
@@ -877,7 +887,8 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     }
   }
   if (p.fuse) {
-    gemm_group_epilogue<TB>(p, acc, grp, s, S, kq == 0, lane, reinterpret_cast<float*>(xs));
+    gemm_group_epilogue<TB>(p, acc, grp, s, S, kq == 0, lane, reinterpret_cast<float*>(xs),
+                            gemm_row_scales_f32(rsc));
     return;
   }
   if constexpr (GS) {
@@ -890,10 +901,10 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   if (p.bands > 1) {  // band b's scaled sums go to y32 + b M N (the consumer adds the bands in order)
     GemmParams q = p;
     q.y32 = p.y32 + (size_t)band * p.M * p.N;
-    gemm_strip_out<TB>(q, acc, strip, lane);
+    gemm_strip_out<TB>(q, acc, strip, lane, gemm_row_scales_f32(rsc));
     return;
   }
-  gemm_strip_out<TB>(p, acc, strip, lane);
+  gemm_strip_out<TB>(p, acc, strip, lane, gemm_row_scales_f32(rsc));
 }
 
 // Split-K reduce in index order + epilogue: one thread per 4 rows of one token, partial loads in flight in batches.
@@ -903,6 +914,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
   const int groups = p.N / 4;
   if (idx >= p.M * groups) return;
   const int t = idx / groups, r = (idx % groups) * 4;
+  const u32x2 rsc = gemm_row_scales(p, r);
   f32x4 v = {0, 0, 0, 0};
   for (int k0 = 0; k0 < p.ksplit; k0 += GEMM_FIXUP_BATCH) {
     f32x4 b[GEMM_FIXUP_BATCH];
@@ -914,7 +926,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
       if (k0 + k < p.ksplit) v += b[k];
   }
   // gemm_store expects the lane's 4 rows at row0 + 4g: pass row0 = r, g = 0.
-  gemm_store(p, t, r, 0, v);
+  gemm_store(p, t, r, 0, v, gemm_row_scales_f32(rsc));
 }
 
 __global__ __launch_bounds__(64) void fold_strip_keys(const uint64_t* part, int strips, uint64_t* best,
