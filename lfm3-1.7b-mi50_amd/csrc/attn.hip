@@ -769,10 +769,11 @@ __global__ __launch_bounds__(MAXW * 64) void verify_attn_lds_kernel(AttnParams p
 // acc = sum f_s acc_s, f_s = exp2(m_s - m)); the split lanes of a wave then merge pairwise in a fixed xor tree and the
 // waves in wave order through LDS, so outputs are bit-identical run to run. o = acc / l (0 when nothing was visible),
 // times the optional sigmoid gate, stored fp16 and/or fp32. blockIdx = (row, KV head x row group); rows past G M (padding
-// of the last row block, never stored by the split kernels) are skipped. Measured on MI355X, graph-replayed with the
+// of the last row block, never stored by the split kernels) store nothing. Measured on MI355X, graph-replayed with the
 // partials in HBM: 256 splits at D 128 6.8 us (18.7 with the split-major layout and 32 lanes per output quad, whose
-// every load touched 32 cache lines), 64 splits 3.6 (4.9), C2's 24 splits at D 64 2.9 with 4 split lanes, one wave
-// per row (3.6; 3.3 with 8 lanes); 16 split lanes beyond 96 splits, 8 below (4 at D = 64 up to 32 splits). Reference
+// every load touched 32 cache lines), 64 splits 3.6 (4.9), C2's 24 splits at D 64 2.8 with 4 split lanes, one wave
+// per row (3.6; 3.3 with 8 lanes; 3.4 before the arguments, flag, gate and partials came in one round trip each);
+// 16 split lanes beyond 96 splits, 8 below (4 at D = 64 up to 32 splits). Reference
 // combine_phase, dspark.hip:2132-2185 (there the splits are the 60 workgroups' key ranges).
 template <int D, int SL>
 __global__ __launch_bounds__(SL * D / 4) void attn_combine_kernel(AttnParams p) {
