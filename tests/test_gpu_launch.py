@@ -424,3 +424,30 @@ def test_phase_trace(dev):
     clocks = [c for (_, _, c) in marks]
     assert all(b >= a for a, b in zip(clocks, clocks[1:])) and clocks[-1] > clocks[0]
     eng.close()
+
+
+@pytest.mark.parametrize("geom", ["small", "mid", "ref_rec", "ref_rec_fresh", "ref_x8"])
+def test_stopped_round_writes_nothing(dev, geom, monkeypatch):
+    """A round enqueued on a stopped State (run == 0) leaves every engine buffer as it was: pools, rings, conv state,
+    State, outputs and every scratch buffer (each kernel issues its first loads before it tests run, and must write
+    nothing when run == 0; dspark.hip:2438-2440 leaves the persistent loop at run == 0)."""
+    torch = dev
+    host = load_host()
+    if geom.endswith("_fresh"):
+        monkeypatch.setenv("DSPARK_FRESH_REC_PPS", "1")
+    desc = host.model_desc(**GEOMETRIES[geom])
+    eng = host.Engine(desc, 512)
+    make_weights(eng, desc, 47)
+    setup_caches(eng, host, desc, A0, CTX_LO, 147)
+    print(f"case stopped round {geom}", flush=True)
+    eng.set_state(a=A0, anchor=ANCHOR, count=0, rounds_left=3, limit=eng.max_context, budget=512, eos=-1, ctx_new=1,
+                  ctx_pos=A0 - 1, ctx_lo=CTX_LO, run=0, skip_rounds=1, stop_at=eng.max_context, ckpt_slot=-1,
+                  tokens=[ANCHOR])
+    torch.cuda.synchronize()
+    before = {n: eng.download(n, np.uint8) for n in eng.names()}
+    for m in (0, 1):  # a drafting round, and a verify-only round of one token
+        eng.round(m, A0)
+    torch.cuda.synchronize()
+    changed = [n for n in eng.names() if not np.array_equal(eng.download(n, np.uint8), before[n])]
+    assert not changed, changed
+    eng.close()
