@@ -78,6 +78,8 @@ __host__ __device__ inline int gemm_pass_tbs(int tb, int band_chunks) {
 // TB token blocks of 16. I8: weights biased int8, else fp16.
 __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st && p.st->run == 0; }
 
+constexpr int GEMM_VMCNT0 = 0x0F70;  // s_waitcnt vmcnt(0), other counters left unconstrained
+
 // ---------------------------------------------------------------- fused row-group epilogues
 // The workgroup's group of R = 16 * nw rows is complete (unsplit, or summed by the last split): every wave puts its
 // scaled products into an LDS tile [token][row] (stride RS = R + 4 floats), then the group's rows are finished there.
@@ -86,9 +88,17 @@ __device__ __forceinline__ bool gemm_stopped(const GemmParams& p) { return p.st 
 // 3c + 2. One thread per (token, channel): bx = fp16(B X); conv = w[K-1] bx + sum_{k<K-1} w[k] hist[pos-K+1+k] with the
 // history inside the block recomputed from the tile and before it read from the ring; y = fp16(C conv); ring[pos] = bx.
 // Ring slots written (a .. a+M-1) and read (a-K+1 .. a-1) are disjoint for M + K - 1 <= CONV_RING.
-__device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int grow0, int R, int nthreads) {
+// cs: the group's weights and ring history staged in LDS at the kernel's start (conv_stage_issue), or cs.ring null:
+// read from the global ring and weights here.
+struct ConvStage {
+  const _Float16* ring = nullptr;  // LDS [CONV_RING][16]: the group's 16 channels of every ring slot
+  const _Float16* w = nullptr;     // LDS [16][K] (+ padding to 128 halves)
+  int a = 0;                       // the State's a
+};
+__device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int grow0, int R, int nthreads, ConvStage cs) {
   const int H = p.N / 3, c0 = grow0 / 3, nch = R / 3, K = p.conv_k;
-  const int a = p.st->a;
+  const bool staged = cs.ring != nullptr;
+  const int a = staged ? cs.a : p.st->a;
   for (int e = threadIdx.x; e < p.M * nch; e += nthreads) {
     const int t = e / nch, cl = e % nch, c = c0 + cl;
     if (c >= H) continue;
@@ -100,7 +110,7 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
       w[k] = 0.f;
       bx[k] = 0.f;
       if (k < K) {
-        w[k] = (float)p.conv_w[(size_t)c * K + k];
+        w[k] = (float)(staged ? cs.w[cl * K + k] : p.conv_w[(size_t)c * K + k]);
         const int tt = t - (K - 1) + k;
         if (tt >= 0) {
           const float* m = tile + tt * RS + 3 * cl;
@@ -110,7 +120,8 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
             bx_t = bx[k];
           }
         } else {
-          bx[k] = (float)p.conv_ring[(size_t)((a + tt) & (CONV_RING - 1)) * H + c];
+          const int slot = (a + tt) & (CONV_RING - 1);
+          bx[k] = (float)(staged ? cs.ring[slot * 16 + cl] : p.conv_ring[(size_t)slot * H + c]);
         }
       }
     }
@@ -137,15 +148,37 @@ __device__ void epi_conv(const GemmParams& p, const float* tile, int RS, int gro
   }
 }
 
+// The conv epilogue's ring history and weights of the group's 16 channels c0 .. c0 + 15 into LDS, issued at the kernel's
+// start by direct-to-LDS loads (no registers, no waits; the epilogue waits for them before its first barrier): every
+// ring slot, since the slots read depend on the State's a, and the group's 16 x K weights (128 halves loaded). Read in
+// the epilogue, they were a dependent round trip after the main loop.
+__device__ __forceinline__ void conv_stage_issue(const GemmParams& p, int c0, int wave, int nw, int lane,
+                                                 _Float16* ring_lds, _Float16* w_lds) {
+  const int H = p.N / 3;
+  const __amdgpu_buffer_rsrc_t rr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.conv_ring, (short)0, CONV_RING * H * 2, 0x00020000);
+  for (int i = wave; i < CONV_RING / 8; i += nw)  // 8 slots x 16 channels (32 B each) per instruction
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (__attribute__((address_space(3))) void*)(ring_lds + i * 128), 4,
+                                             (uint32_t)(((8 * i + (lane >> 3)) * H + c0) * 2 + (lane & 7) * 4), 0,
+                                             0, 0);
+  if (wave == nw - 1) {
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.conv_w, (short)0, H * p.conv_k * 2, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)w_lds, 4,
+                                             (uint32_t)(c0 * p.conv_k * 2 + lane * 4), 0, 0, 0);
+  }
+}
+
 // S strips per group; the waves with `holder` set hold strip s's sums (every wave of the workgroup finishes the group).
 // sc: the holder's row scales (gemm_row_scales of rows grow0 + r; strips past N hold rows no epilogue reads).
 template <int TB>
 __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB], int grp, int s, int S, bool holder,
-                                    int lane, float* tile, f32x4 sc) {
+                                    int lane, float* tile, f32x4 sc, ConvStage cs = ConvStage{}) {
   const int R = 16 * S, RS = R + 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int grow0 = grp * R, r = 16 * s + 4 * g;
+  if (cs.ring) __builtin_amdgcn_s_waitcnt(GEMM_VMCNT0);  // this wave's staging loads are in LDS (the barrier: all)
   __syncthreads();  // every wave is done with the LDS it used before
   if (holder) {
 #pragma unroll
@@ -156,7 +189,7 @@ __device__ void gemm_group_epilogue(const GemmParams& p, const f32x4 (&acc)[TB],
   }
   __syncthreads();
   (void)wave;
-  epi_conv(p, tile, RS, grow0, R, 64 * nw);
+  epi_conv(p, tile, RS, grow0, R, 64 * nw, cs);
 }
 
 // Finished sums of one strip (lane (n, g): rows 16 strip + 4 g + i of token 16 tb + n): the strip's row-argmax key
@@ -188,7 +221,6 @@ __device__ __forceinline__ void gemm_strip_out(const GemmParams& p, const f32x4 
 }
 
 constexpr int GEMM_CPOL_COHERENT = 16;  // buffer-op cache policy SC1: device-scope coherent store / load
-constexpr int GEMM_VMCNT0 = 0x0F70;     // s_waitcnt vmcnt(0), other counters left unconstrained
 // s_waitcnt immediate: vmcnt(n) (6 bits, split low 4 / high 2), other counters left unconstrained
 #define GEMM_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
 #define GEMM_LGKMCNT0 0xC07F  // lgkmcnt(0), vmcnt and expcnt unconstrained
@@ -575,10 +607,11 @@ __device__ __forceinline__ f32x4 x8_scales_load(const GemmParams& p, int n, int 
 }
 
 // X8: 0 fp16 x; 1 int8 x quantized as it is loaded (p.x8 == 1); 2 int8 codes + scales given (p.x8 == 2).
-template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, int X8 = 0>
+template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, int X8 = 0, bool ONEB = false>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   static_assert(!GS || (TB == 1 && I8 && CPW % 2 == 0), "group scales: one token block, int8 weights, whole groups");
   static_assert(!X8 || GS, "int8 x goes with group scales");
+  static_assert(!ONEB || (XD && MAXT > 512), "the one-batch form is the 1024-thread X-per-wave kernel's");
   // The stop flag is loaded first and tested once the data loads are in flight and the products computed (before
   // anything is stored), so its latency overlaps theirs; a stopped round writes nothing.
   const int run = run_flag_load(p.st);
@@ -596,6 +629,14 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   const int strip = live ? strip_raw : strips - 1;
   const int row0 = strip * 16;
   const u32x2 rsc = gemm_row_scales(p, row0 + 4 * g);  // first of the kernel's loads (the epilogue's)
+  __shared__ __attribute__((aligned(16))) _Float16 conv_ring_lds[CONV_RING * 16];
+  __shared__ __attribute__((aligned(16))) _Float16 conv_w_lds[128];
+  const bool conv_st = p.fuse == GEMM_FUSE_CONV && p.st;
+  int conv_a = 0;  // the State's a, kept unread until the epilogue
+  if (conv_st) {
+    conv_a = state_word_load(p.st, (int)offsetof(dspark_state, a));
+    conv_stage_issue(p, grp * 16, wave, nw, lane, conv_ring_lds, conv_w_lds);
+  }
   const int chunks = p.K / 64;
   const int cpb_ = (chunks + p.bands - 1) / p.bands;  // chunks per band
   const int b0 = min(chunks, band * cpb_), b1 = min(chunks, b0 + cpb_);
@@ -673,6 +714,9 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
       }
       if constexpr (GS) gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
       load(w, cb);
+      // the one-batch form: every load of the batch issued before the first product (the scheduler would otherwise
+      // reuse a consumed chunk's registers for the last loads, a round trip after the first products)
+      if constexpr (ONEB) __builtin_amdgcn_sched_barrier(0);
       if constexpr (X8) {
         f32x4 accg = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -716,6 +760,10 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     if constexpr (MAXT <= 512) {  // with 128 VGPRs (1024 threads) the peeled copy spills: keep the plain loop there
       if (c0 < c1) batch(c0);
       for (int cb = c0 + CPW; cb < c1; cb += CPW) batch(cb);
+    } else if constexpr (ONEB) {
+      // one batch per range (the host checked): no loop, so no loop-head waits -- counted for the back edge, they
+      // would hold the batch's later weight loads behind the loads issued before it (stop flag, scales, conv staging)
+      if (c0 < c1) batch(c0);
     } else {
       for (int cb = c0; cb < c1; cb += CPW) batch(cb);
     }
@@ -887,8 +935,18 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
     }
   }
   if (p.fuse) {
+    ConvStage cs;  // (fields set one by one: an aggregate of LDS addresses would become a constant initializer)
+    cs.ring = nullptr;
+    cs.w = nullptr;
+    cs.a = 0;
+    if (conv_st) {
+      cs.ring = conv_ring_lds;
+      cs.w = conv_w_lds;
+      asm volatile("" : "+v"(conv_a));
+      cs.a = __builtin_amdgcn_readfirstlane(conv_a);
+    }
     gemm_group_epilogue<TB>(p, acc, grp, s, S, kq == 0, lane, reinterpret_cast<float*>(xs),
-                            gemm_row_scales_f32(rsc));
+                            gemm_row_scales_f32(rsc), cs);
     return;
   }
   if constexpr (GS) {
@@ -1066,6 +1124,8 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
     if (TB == 1 && gemm_sliced_xd(p, I8)) {
       if (block.x <= 512)  // up to 8 waves: twice the registers per wave (no spills with the first batch peeled)
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512>), grid, block, lds, s, p);
+      else if (cpk <= 8)  // every range one batch (w13, the conv mix)
+        hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 1024, false, 0, true>), grid, block, lds, s, p);
       else
         hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true>), grid, block, lds, s, p);
       return;
