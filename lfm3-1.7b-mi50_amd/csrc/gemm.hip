@@ -714,9 +714,9 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
       }
       if constexpr (GS) gscale_load<CPW>(p, gsr, cb, c1, row0 + 4 * g);
       load(w, cb);
-      // the one-batch form: every load of the batch issued before the first product (the scheduler would otherwise
-      // reuse a consumed chunk's registers for the last loads, a round trip after the first products)
-      if constexpr (ONEB) __builtin_amdgcn_sched_barrier(0);
+      // every load of the batch issued before its first product (the scheduler would otherwise reuse a consumed
+      // chunk's registers for the last loads, a round trip after the first products)
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (X8) {
         f32x4 accg = f32x4{0, 0, 0, 0};
 #pragma unroll
