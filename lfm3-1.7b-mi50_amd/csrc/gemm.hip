@@ -607,7 +607,10 @@ __device__ __forceinline__ f32x4 x8_scales_load(const GemmParams& p, int n, int 
 }
 
 // X8: 0 fp16 x; 1 int8 x quantized as it is loaded (p.x8 == 1); 2 int8 codes + scales given (p.x8 == 2).
-template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, int X8 = 0, bool ONEB = false>
+// TO (int8 x): tile-major weights only -- with the row-major form also compiled in, whose chunk is four loads against
+// one, the compiler cannot count a batch's loads past the layout test and waits for all of them before the first product.
+template <int TB, bool I8, int CPW, bool XD, int MAXT = 1024, bool GS = false, int X8 = 0, bool ONEB = false,
+          bool TO = false>
 __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
   static_assert(!GS || (TB == 1 && I8 && CPW % 2 == 0), "group scales: one token block, int8 weights, whole groups");
   static_assert(!X8 || GS, "int8 x goes with group scales");
@@ -647,7 +650,7 @@ __global__ __launch_bounds__(MAXT) void gemm_sliced_kernel(GemmParams p) {
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0, 0, 0, 0};
 
-  const bool tiled = I8 && p.tiled;
+  const bool tiled = I8 && (TO || p.tiled);
   const uint8_t* wrow = tiled ? reinterpret_cast<const uint8_t*>(p.w) + (size_t)strip * chunks * 1024 + lane * 16
                               : reinterpret_cast<const uint8_t*>(p.w) + (size_t)(row0 + n) * p.K * (I8 ? 1 : 2) + 16 * g;
   const int cstride = tiled ? 1024 : 64;
@@ -1079,6 +1082,17 @@ static void allow_lds(F* kernel, size_t lds) {
                               (int)lds);
 }
 
+// int8 x with group scales: X per wave (<= 8 waves) or X^T of the band through LDS; TO: tile-major weights only.
+template <bool I8, int X8, bool TO>
+static void launch_sliced_x8(const GemmParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  if (gemm_sliced_xd(p, I8)) {
+    hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, X8, false, TO>), grid, block, lds, s, p);
+  } else {
+    allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, X8, false, TO>, lds);
+    hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, X8, false, TO>), grid, block, lds, s, p);
+  }
+}
+
 template <int TB, bool I8>
 static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   const int groups = (p.N / 16 + p.wpg - 1) / p.wpg;
@@ -1088,20 +1102,18 @@ static void launch_sliced_tb(const GemmParams& p, hipStream_t s) {
   if constexpr (I8 && TB == 1) {
     if (p.gscale) {  // group scales: X per wave, or X^T of the band in LDS at once (gemm_launch checked)
       if (p.x8 == 1) {  // int8 x (LFM3_X8), quantized as it is loaded
-        if (gemm_sliced_xd(p, I8)) {
-          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, 1>), grid, block, lds, s, p);
+        if (p.tiled) {
+          launch_sliced_x8<I8, 1, true>(p, grid, block, lds, s);
         } else {
-          allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, 1>, lds);
-          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, 1>), grid, block, lds, s, p);
+          launch_sliced_x8<I8, 1, false>(p, grid, block, lds, s);
         }
         return;
       }
       if (p.x8 == 2) {  // int8 codes + scales from the norm kernel
-        if (gemm_sliced_xd(p, I8)) {
-          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, true, 512, true, 2>), grid, block, lds, s, p);
+        if (p.tiled) {
+          launch_sliced_x8<I8, 2, true>(p, grid, block, lds, s);
         } else {
-          allow_lds(gemm_sliced_kernel<1, I8, 8, false, 1024, true, 2>, lds);
-          hipLaunchKernelGGL((gemm_sliced_kernel<1, I8, 8, false, 1024, true, 2>), grid, block, lds, s, p);
+          launch_sliced_x8<I8, 2, false>(p, grid, block, lds, s);
         }
         return;
       }
