@@ -146,16 +146,16 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
   for (int k = 0; k < NK; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s_vv += vv[k][j] * vv[k][j];
-  __shared__ float red[8];
-  auto block_sum = [&](float x) -> float {
+  // one LDS slot set per sum (the kernel takes two), so a sum needs one barrier, not one more to guard a reused set
+  __shared__ float red[2][4];
+  auto block_sum = [&](int k, float x) -> float {
     x = wave_sum(x);
+    if ((threadIdx.x & 63) == 0) red[k][threadIdx.x >> 6] = x;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
+    return (red[k][0] + red[k][1]) + (red[k][2] + red[k][3]);
   };
   float a = 0.f;
-  if (p.bands > 0) a = p.sandwich ? rsqrtf(block_sum(s_vv) / H + p.eps) : 1.f;
+  if (p.bands > 0) a = p.sandwich ? rsqrtf(block_sum(0, s_vv) / H + p.eps) : 1.f;
   float s_hh = 0.f;
 #pragma unroll
   for (int k = 0; k < NK; ++k)
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
       hv[k][j] = fmaf(vv[k][j] * a, (float)wp[k][j], hv[k][j]);
       s_hh += hv[k][j] * hv[k][j];
     }
-  const float inv = rsqrtf(block_sum(s_hh) / H + p.eps);
+  const float inv = rsqrtf(block_sum(1, s_hh) / H + p.eps);
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const int i = 1024 * k + 4 * (int)threadIdx.x;
