@@ -204,6 +204,9 @@ __global__ __launch_bounds__(256) void resnorm_kernel(ResNormParams p) {
 // per token: q [QH*D] | k [KVH*D] | v [KVH*D] | gate [QH] (gate optional), `row` floats apart. Position of token t:
 // base + t with base = st->a (verify, drafter block) or st->ctx_pos (context projection); tokens t >= count
 // (count = M, or st->ctx_new) are skipped.
+// D (64 or 128, p.D) as a template argument: the per-lane dims loops unroll, so the row loads go out together (with
+// D a run-time value, each pass of the loads loop waited for the previous one's: four round trips at D = 128).
+template <int D>
 __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   // The parameters' three 64-byte lines (fields at 0, 64 and 132 bytes span any placement of the 136-byte struct) in
   // one round trip: read where they are first used, behind the early-exit tests, they were four dependent misses.
@@ -222,16 +225,16 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   const int base_v = state_word_load(p.st, p.pos_from_ctx ? (int)offsetof(dspark_state, ctx_pos)
                                                            : (int)offsetof(dspark_state, a));
   const int count_v = p.count_from_ctx ? state_word_load(p.st, (int)offsetof(dspark_state, ctx_new)) : p.M;
-  const int D = p.D, half = D / 2;
+  constexpr int half = D / 2;
   const float* row = p.mix + (size_t)t * p.row;
   const float* src = isq ? row + (size_t)hh * D : row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)(hh - p.QH) * D;
   const _Float16* nw = isq ? p.q_norm : p.k_norm;
   const int kvh = hh - p.QH;
   const float* vsrc = row + (size_t)p.QH * D * (p.q16 ? 1 : 0) + (size_t)p.KVH * D + (size_t)kvh * D;
   // lane l holds dims l and l + 32 (D = 64) or l, l+32, l+64, l+96 (D = 128): pairs (i, i + D/2) share a lane
-  constexpr int MAXE = 4;
-  const int ne = D / 32;  // 2 or 4
-  float v[MAXE], vv[MAXE], wn[MAXE];
+  constexpr int ne = D / 32;  // 2 or 4
+  float v[ne], vv[ne], wn[ne];
+#pragma unroll
   for (int e = 0; e < ne; ++e) {
     const int d = (lane & 31) + 32 * e;
     v[e] = src[d];
@@ -247,7 +250,8 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   const int pos = __builtin_amdgcn_readfirstlane(base_v) + t;
   // RoPE: pair (i, i + half) for i < rot, cos/sin from the table row of `pos` (cos | sin, D halves)
   const _Float16* rt = p.rope + (size_t)pos * D;
-  float cs[MAXE / 2], sn[MAXE / 2];
+  float cs[ne / 2], sn[ne / 2];
+#pragma unroll
   for (int e = 0; e < ne / 2; ++e) {
     const int i = (lane & 31) + 32 * e;  // i < half
     cs[e] = (float)rt[i];
@@ -256,14 +260,18 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   const int lp = pos / PAGE, slot = pos % PAGE;
   const int phys = isq ? 0 : (p.bt ? p.bt[lp] : lp);
   float ss = 0.f;
+#pragma unroll
   for (int e = 0; e < ne; ++e) ss += v[e] * v[e];
   // lanes 32..63 duplicate lanes 0..31; sum over the first 32 lanes
   ss = (lane < 32) ? ss : 0.f;
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / D + p.eps);
+#pragma unroll
   for (int e = 0; e < ne; ++e) v[e] = v[e] * inv * wn[e];
-  float r[MAXE];
+  float r[ne];
+#pragma unroll
   for (int e = 0; e < ne; ++e) r[e] = v[e];
+#pragma unroll
   for (int e = 0; e < ne / 2; ++e) {
     const int i = (lane & 31) + 32 * e;  // i < half
     if (i < p.rot) {
@@ -277,6 +285,7 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
     // int8 record of (pos, kvh) (D = 128: lanes 0..31 hold dims l, l + 32, l + 64, l + 96; lanes 32..63 repeat
     // them): quantize_pair of K (normed, rotated, fp32) and of V (fp32), kernels/ops.hip:212-251
     float ak = 0.f, av = 0.f;
+#pragma unroll
     for (int e = 0; e < ne; ++e) {
       ak = fmaxf(ak, fabsf(r[e]));
       av = fmaxf(av, fabsf(vv[e]));
@@ -287,6 +296,7 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
     uint8_t* rb = p.rec + (size_t)phys * ((size_t)PAGE * p.KVH * 264) + ((size_t)slot * p.KVH + kvh) * 264;
     const float ks = rec_scale(ak), vs = rec_scale(av);
     const float ki = __fdiv_rn(1.f, ks), vi = __fdiv_rn(1.f, vs);
+#pragma unroll
     for (int e = 0; e < ne; ++e) {
       const int d = (lane & 31) + 32 * e;
       rb[d] = (uint8_t)rec_code(r[e], ki);
@@ -301,6 +311,7 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   if (lane >= 32) return;
   if (isq) {
     _Float16* q = p.q16 + ((size_t)t * p.QH + hh) * D;
+#pragma unroll
     for (int e = 0; e < ne; ++e) q[(lane & 31) + 32 * e] = (_Float16)r[e];
     if (p.gate && p.gate_in_mix) {
       if (lane == 0) p.gate[(size_t)t * p.QH + hh] = row[(size_t)(p.QH + 2 * p.KVH) * D + hh];
@@ -310,6 +321,7 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   // K (normed, rotated) and V (as is) into the pages at `pos`
   _Float16* kb = p.kp + ((size_t)phys * p.KVH + kvh) * (PAGE * D);
   _Float16* vb = p.vp + ((size_t)phys * p.KVH + kvh) * (D * PAGE);
+#pragma unroll
   for (int e = 0; e < ne; ++e) {
     const int d = (lane & 31) + 32 * e;
     kb[k_page_elem(slot, d, D)] = (_Float16)r[e];
@@ -317,10 +329,12 @@ __device__ __forceinline__ void qkrope_body(const QkRopeParams& p) {
   }
 }
 
-__global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) { qkrope_body(p); }
+template <int D>
+__global__ __launch_bounds__(256) void qkrope_kernel(QkRopeParams p) { qkrope_body<D>(p); }
 
 // Several layers of the same shape in one launch (the context projection's drafter layers): layer blockIdx.y.
-__global__ __launch_bounds__(256) void qkrope_batch_kernel(QkRopeBatch b) { qkrope_body(b.l[blockIdx.y]); }
+template <int D>
+__global__ __launch_bounds__(256) void qkrope_batch_kernel(QkRopeBatch b) { qkrope_body<D>(b.l[blockIdx.y]); }
 
 // ---------------------------------------------------------------- drafter: Markov + confidence (markov_phase)
 // Step j (0-based) proposes draft j+1 from prev = (j == 0 ? anchor : the token of step j-1's argmax key):
@@ -666,8 +680,12 @@ int resnorm_launch(const ResNormParams& p, int rows, int groups, hipStream_t s) 
   return (int)hipGetLastError();
 }
 int qkrope_launch(const QkRopeParams& p, hipStream_t s) {
+  if (p.D != 64 && p.D != 128) return DSPARK_EINVAL;
   const int tasks = p.M * (p.QH + p.KVH);
-  hipLaunchKernelGGL(qkrope_kernel, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
+  if (p.D == 64)
+    hipLaunchKernelGGL(qkrope_kernel<64>, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(qkrope_kernel<128>, dim3((tasks + 3) / 4), dim3(256), 0, s, p);
   return (int)hipGetLastError();
 }
 
@@ -676,8 +694,14 @@ int qkrope_batch_launch(const QkRopeBatch& b, hipStream_t s) {
   const QkRopeParams& p = b.l[0];
   for (int j = 1; j < b.n; ++j)
     if (b.l[j].M != p.M || b.l[j].QH != p.QH || b.l[j].KVH != p.KVH) return DSPARK_EINVAL;
+  if (p.D != 64 && p.D != 128) return DSPARK_EINVAL;
+  for (int j = 1; j < b.n; ++j)
+    if (b.l[j].D != p.D) return DSPARK_EINVAL;
   const int tasks = p.M * (p.QH + p.KVH);
-  hipLaunchKernelGGL(qkrope_batch_kernel, dim3((tasks + 3) / 4, b.n), dim3(256), 0, s, b);
+  if (p.D == 64)
+    hipLaunchKernelGGL(qkrope_batch_kernel<64>, dim3((tasks + 3) / 4, b.n), dim3(256), 0, s, b);
+  else
+    hipLaunchKernelGGL(qkrope_batch_kernel<128>, dim3((tasks + 3) / 4, b.n), dim3(256), 0, s, b);
   return (int)hipGetLastError();
 }
 int markov_launch(const MarkovParams& p, hipStream_t s) {
