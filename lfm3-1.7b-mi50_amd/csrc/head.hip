@@ -133,15 +133,32 @@ __device__ __forceinline__ int key_token(uint64_t k) { return (int)(0xffffffffu 
 // mirror (optional): host memory the launch loop polls; after the books, words 1.. get the State's run, a, count,
 // rounds_left, skip, miss, accepted, verified, and words 0 (last, release) and 15 (first) the State's rounds_done, so
 // a reader that finds word 15 == word 0 has read one round's values (system-scope stores: visible to the host).
+//
+// The books run on the whole wave: lane l holds the State's header word l, tokens[l], tokens[l + 1] and key l, all
+// requested in the kernel's first round with the run flag and the first batch of partial keys. Acceptance is a ballot
+// over the lanes (lane t < m - 1 misses when token(key t) != tokens[t + 1]; acc = the first miss, else m - 1); lanes
+// 1..acc store the accepted drafts and lane 0 the bonus token, each setting its own seen bit; the header words the
+// books change are stored by lane 0 from registers. No value is read back from memory after the first round.
 __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uint64_t* best, int m, int skip_now,
                                                            int32_t* out_tokens, int out_cap, uint32_t* seen,
                                                            const uint64_t* part, int nchunks, int mfold,
                                                            int32_t* mirror) {
-  // The run word and the first batch of partial keys are requested together, and the keys are folded into LDS before
-  // run is tested (an early return ahead of the folding let the compiler move the key loads behind the State's round
-  // trip). Buffer loads: 0 -- no key -- past the keys, and for every load when there are none. A stopped round writes
-  // nothing.
-  const int run = run_flag_load(st);
+  // Buffer loads: 0 past the end of each buffer (past the keys, and for every key load of the buffer that is not
+  // read). A stopped round writes nothing.
+  const int lane = (int)threadIdx.x;
+  asm volatile("" ::"s"(mirror));  // the kernarg line past the first: fetched with the first
+  constexpr int NH = (int)(offsetof(dspark_state, tokens) / sizeof(int32_t));  // header words
+  static_assert(NH <= 64 && DSPARK_MT_MAX == 64, "one header word and one token per lane");
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)st, (short)0, (int)sizeof(dspark_state), 0x00020000);
+  const int run = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)offsetof(dspark_state, run), 0, 0);
+  const int hw = __builtin_amdgcn_raw_buffer_load_b32(rs, min(lane, NH - 1) * 4, 0, 0);
+  const int tk = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)offsetof(dspark_state, tokens) + lane * 4, 0, 0);
+  const int tn =
+      __builtin_amdgcn_raw_buffer_load_b32(rs, (int)offsetof(dspark_state, tokens) + min(lane + 1, 63) * 4, 0, 0);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)best, (short)0, part ? 0 : max(m, 0) * (int)sizeof(uint64_t), 0x00020000);
+  const u32x2 kb = __builtin_amdgcn_raw_buffer_load_b64(rb, lane * (int)sizeof(uint64_t), 0, 0);
   const int n = part ? mfold * nchunks : 0;
   constexpr int PB = 8;
   const __amdgpu_buffer_rsrc_t rp =
@@ -149,81 +166,91 @@ __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uin
   u32x2 v0[PB];
 #pragma unroll
   for (int i = 0; i < PB; ++i)
-    v0[i] = __builtin_amdgcn_raw_buffer_load_b64(rp, (64 * i + (int)threadIdx.x) * (int)sizeof(uint64_t), 0, 0);
+    v0[i] = __builtin_amdgcn_raw_buffer_load_b64(rp, (64 * i + lane) * (int)sizeof(uint64_t), 0, 0);
+  __shared__ unsigned long long sb[64];
   if (part) {
-    __shared__ unsigned long long sb[64];
-    sb[threadIdx.x] = 0;
+    sb[lane] = 0;
     __syncthreads();
     for (int e0 = 0; e0 < n; e0 += 64 * PB) {
       uint64_t v[PB];
 #pragma unroll
       for (int i = 0; i < PB; ++i)
-        v[i] = e0 == 0 ? __builtin_bit_cast(uint64_t, v0[i]) : ldg(part + min(e0 + 64 * i + (int)threadIdx.x, n - 1));
+        v[i] = e0 == 0 ? __builtin_bit_cast(uint64_t, v0[i]) : ldg(part + min(e0 + 64 * i + lane, n - 1));
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
-        const int e = e0 + 64 * i + (int)threadIdx.x;
+        const int e = e0 + 64 * i + lane;
         if (e < n) atomicMax(&sb[e / nchunks], (unsigned long long)v[i]);
       }
     }
     __syncthreads();
-    if (threadIdx.x != 0 || !run_flag_set(run)) return;
-    for (int t = 0; t < mfold; ++t) best[t] = sb[t];  // the folded keys (thread 0 reads its own writes below)
   }
-  if (threadIdx.x != 0 || !run_flag_set(run)) return;
-  if (m <= 0) m = st->M;  // rounds that drafted on the device: the verified count is in the State
-  int acc = 0;
-  for (int t = 0; t < m - 1; ++t) {
-    if (key_token(best[t]) != st->tokens[t + 1]) break;
-    ++acc;
-  }
+  if (!run_flag_set(run)) return;
+  const uint64_t key = part ? (uint64_t)sb[lane] : __builtin_bit_cast(uint64_t, kb);
+  if (part && lane < mfold) best[lane] = key;  // the folded keys
+  auto hdr = [&](size_t off) { return __builtin_amdgcn_readlane(hw, (int)(off / sizeof(int32_t))); };
+  if (m <= 0) m = hdr(offsetof(dspark_state, M));  // rounds that drafted on the device: the verified count is in the State
+  const uint64_t miss = __builtin_amdgcn_ballot_w64(lane < m - 1 && key_token(key) != tn);
+  const int acc = miss ? (int)__builtin_ctzll(miss) : max(m - 1, 0);
   const int commit = acc + 1;
-  const int bonus = key_token(best[acc]);
-  const int aa = st->a;
-  int count = st->count;
+  const int bonus = key_token((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, acc));  // the token is the low word
+  const int aa = hdr(offsetof(dspark_state, a));
+  const int count = hdr(offsetof(dspark_state, count));
   if (count < 0 || count + commit > out_cap) {  // no room for the commit: write nothing and stop
-    st->run = 0;
+    if (lane == 0) st->run = 0;
     return;
   }
-  for (int i = 1; i <= acc; ++i) out_tokens[count++] = st->tokens[i];
-  out_tokens[count++] = bonus;
-  for (int i = 1; i <= acc; ++i) {
-    const int tk = st->tokens[i];
-    seen[tk >> 5] |= 1u << (tk & 31);
+  // lanes 1..acc: the accepted drafts tokens[1..acc] at count..count+acc-1; lane 0: the bonus token after them
+  const int val = lane == 0 ? bonus : tk;
+  const bool mine = lane <= acc;
+  if (mine) {
+    out_tokens[lane == 0 ? count + acc : count + lane - 1] = val;
+    atomicOr(&seen[val >> 5], 1u << (val & 31));
   }
-  seen[bonus >> 5] |= 1u << (bonus & 31);
-  bool stop = false;
-  if (st->eos >= 0)
-    for (int i = count - commit; i < count; ++i) stop = stop || out_tokens[i] == st->eos;
-  st->count = count;
-  st->ctx_new = commit;
-  st->ctx_pos = aa;
-  st->a = aa + commit;
-  st->anchor = bonus;
-  st->accepted += acc;
-  st->verified += m;
+  const int eos = hdr(offsetof(dspark_state, eos));
+  const bool stop = eos >= 0 && __builtin_amdgcn_ballot_w64(mine && val == eos) != 0;
+  if (lane != 0) return;
+  const int count1 = count + commit, a1 = aa + commit;
+  const int accepted = hdr(offsetof(dspark_state, accepted)) + acc;
+  const int verified = hdr(offsetof(dspark_state, verified)) + m;
+  int skip = hdr(offsetof(dspark_state, skip)), miss_n = hdr(offsetof(dspark_state, miss));
   if (skip_now > 0) {
-    st->skip -= 1;
+    skip -= 1;
   } else if (acc == 0) {
-    st->miss += 1;
-    if (st->skip_after > 0 && st->miss >= st->skip_after) {
-      st->skip = st->skip_rounds;
-      st->miss = 0;
+    miss_n += 1;
+    const int skip_after = hdr(offsetof(dspark_state, skip_after));
+    if (skip_after > 0 && miss_n >= skip_after) {
+      skip = hdr(offsetof(dspark_state, skip_rounds));
+      miss_n = 0;
     }
   } else {
-    st->miss = 0;
+    miss_n = 0;
   }
+  const int rounds_done = hdr(offsetof(dspark_state, rounds_done)) + 1;
+  const int rounds_left = hdr(offsetof(dspark_state, rounds_left)) - 1;
+  const int run1 = (!stop && rounds_left > 0 && a1 < hdr(offsetof(dspark_state, stop_at)) &&
+                    count1 < hdr(offsetof(dspark_state, budget)))
+                       ? 1
+                       : 0;
+  st->count = count1;
+  st->ctx_new = commit;
+  st->ctx_pos = aa;
+  st->a = a1;
+  st->anchor = bonus;
+  st->accepted = accepted;
+  st->verified = verified;
+  st->skip = skip;
+  st->miss = miss_n;
   st->tokens[0] = bonus;
-  st->rounds_done += 1;
-  st->rounds_left -= 1;
-  st->run = (!stop && st->rounds_left > 0 && st->a < st->stop_at && count < st->budget) ? 1 : 0;
+  st->rounds_done = rounds_done;
+  st->rounds_left = rounds_left;
+  st->run = run1;
   if (mirror) {
-    const int seq = st->rounds_done;
-    const int words[8] = {st->run, st->a, st->count, st->rounds_left, st->skip, st->miss, st->accepted, st->verified};
-    __hip_atomic_store(mirror + 15, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int words[8] = {run1, a1, count1, rounds_left, skip, miss_n, accepted, verified};
+    __hip_atomic_store(mirror + 15, rounds_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __atomic_thread_fence(__ATOMIC_RELEASE);  // word 15 before the values
 #pragma unroll
     for (int i = 0; i < 8; ++i) __hip_atomic_store(mirror + 1 + i, words[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(mirror, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(mirror, rounds_done, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
