@@ -129,6 +129,9 @@ struct MarkovParams {
   const float* table;           // [N][N] w1q[crop_ids[c]] . w2q[r] (markov_table_launch), or nullptr: steps dot w2q
   const float* c2c;             // [N] c2[crop_ids[c]]
   const float* s1c;             // [N] w1s[crop_ids[c]]
+  // Planted drafts (benchmarks of a set acceptance rate on random-init models), or nullptr: after the drafter's own
+  // drafts, tokens[1 .. cap] = plant[a + 1 .. a + cap] and M = 1 + cap (the cap markov_kernel applies)
+  const int32_t* plant;
 };
 
 int embed_launch(const void* embed, const struct ::dspark_state* st, int mode, int mask_token, int M, int H, int V, float* h,

@@ -602,8 +602,8 @@ int enqueue_round(dspark_engine* e, int force_m, int plan_a, int mv, bool skip, 
     mp.table = e->mtab;
     mp.c2c = e->mc2c;
     mp.s1c = e->ms1c;
+    mp.plant = force_m < 0 ? e->plant : nullptr;  // planted rounds: the Markov launch applies the plant
     CK(markov_launch(mp, s));
-    if (force_m < 0) CK(plant_launch(e->st, e->plant, B, d.max_drafts, reinterpret_cast<const int32_t*>(e->rep + 2), s));
     CK(mark(e, DSPARK_TRACE_MARKOV, s));
   }
   // ---- verify (MV rows; rows past the State's M are computed and never committed)

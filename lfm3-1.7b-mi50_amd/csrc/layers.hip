@@ -571,6 +571,20 @@ __global__ __launch_bounds__(1024) void markov_chain_kernel(MarkovParams p) {
     for (int i = 0; i < CHAIN_ROWS / 4; ++i) bv[i] = bn[i];
     bconf = bnconf;
   }
+  if (p.plant) {
+    // Planted drafts replace the chain's (the plant kernel's books, one launch fewer): after a barrier that orders them
+    // behind thread 0's chain stores, lane j of wave 0 loads plant[a + j] and stores tokens[j] (one load and one store
+    // each, instead of a load-store chain on one thread), lane 0 the anchor and M.
+    __syncthreads();
+    if (wave != 0) return;
+    const int a = st->a, drafts = max(cap, 0);
+    if (lane >= 1 && lane <= drafts) st->tokens[lane] = ldg(p.plant + a + lane);
+    if (lane == 0) {
+      st->tokens[0] = st->anchor;
+      st->M = drafts + 1;
+    }
+    return;
+  }
   if (tid != 0) return;
   st->tokens[0] = st->anchor;
   if (M != 0) return;  // stopped by confidence: tokens and M already written
@@ -708,11 +722,12 @@ int markov_launch(const MarkovParams& p, hipStream_t s) {
   const int blocks = (p.N + 255) / 256;
   if (p.table && p.N <= CHAIN_MAX_N) {
     if (p.block >= 2) hipLaunchKernelGGL(markov_kernel, dim3(blocks), dim3(256), 0, s, p, 0);
-    hipLaunchKernelGGL(markov_chain_kernel, dim3(1), dim3(CHAIN_THREADS), 0, s, p);
+    hipLaunchKernelGGL(markov_chain_kernel, dim3(1), dim3(CHAIN_THREADS), 0, s, p);  // (applies p.plant itself)
     return (int)hipGetLastError();
   }
   for (int j = 0; j < p.block - 1; ++j) hipLaunchKernelGGL(markov_kernel, dim3(blocks), dim3(256), 0, s, p, j);
   hipLaunchKernelGGL(markov_finalize, dim3(1), dim3(64), 0, s, p);
+  if (p.plant) return plant_launch(p.st, p.plant, p.block, p.max_drafts, p.max_drafts_dev, s);
   return (int)hipGetLastError();
 }
 int markov_table_launch(const int8_t* w1q, const float* w1s, const float* c2, const int8_t* w2q, const int32_t* crop_ids,
