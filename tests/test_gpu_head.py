@@ -111,6 +111,84 @@ def test_commit_stop_rules_on_device(dev, orc):
             assert getattr(gst, f) == getattr(ost, f), (kw, f)
 
 
+COMMIT_EDGE = {
+    # name: (State tokens[0..m-1], the verify argmax tokens best[0..m-1], State fields, skip_now)
+    "mid_miss": ([5, 10, 11, 12], [10, 99, 12, 13], {}, 0),                      # acc 1: the second draft misses
+    "miss_to_skip": ([5, 10, 11, 12], [7, 8, 9, 13], dict(miss=1, skip_after=2, skip_rounds=3), 0),  # acc 0
+    "eos_bonus": ([5, 10, 11, 12], [10, 11, 77, 13], dict(eos=77), 0),           # the bonus token is eos
+    "eos_first_draft": ([5, 77, 11, 12], [77, 11, 12, 13], dict(eos=77), 0),     # an accepted draft is eos
+    "one_row": ([5], [42], {}, 0),                                               # m = 1: the bonus alone
+    "all_64": ([5] + [100 + j for j in range(1, 64)], [100 + j for j in range(1, 64)] + [999], {}, 0),
+    "same_word": ([5, 40, 40, 41], [40, 40, 41, 63], {}, 0),                     # one seen word, a token twice
+    "skip_round": ([5, 10, 11, 12], [7, 8, 9, 13], dict(skip=2, miss=1, skip_after=2), 1),
+    "count_carried": ([5, 10, 11, 12], [10, 11, 12, 13], dict(count=17, accepted=40, verified=90), 0),
+}
+
+
+@pytest.mark.parametrize("case", sorted(COMMIT_EDGE))
+def test_commit_edge_cases_on_device(dev, orc, case):
+    """Acceptance + commit on the device against the oracle's books: misses at every position, the skip/miss
+    counters, eos among the drafts and as the bonus, one row, all 64 rows accepted, several committed tokens in one
+    seen word (the same token twice), a skip round, counters carried in. Every State field, the State's tokens, the
+    emitted tokens and the seen bitmap are compared."""
+    torch = dev
+    host = load_host()
+    V = 4096
+    tokens, best_tok, fields, skip_now = COMMIT_EDGE[case]
+    m = len(tokens)
+    base = dict(a=1024, anchor=tokens[0], tokens=tokens, rounds_left=32, budget=4096, eos=-1, stop_at=4096, run=1,
+                skip_rounds=1, skip_after=0, miss=0)
+    base.update(fields)
+    keys = np.array([orc.argmax_key(1.0, t) for t in best_tok], np.uint64)
+    st = host.state_tensor(**base)
+    best = torch.from_numpy(keys.view(np.int64)).cuda()
+    out = torch.full((128,), -7, dtype=torch.int32, device="cuda")
+    seen0 = np.zeros(V // 32, np.uint32)
+    seen0[3] = 0x80000001  # bits already set stay set
+    seen = torch.from_numpy(seen0.view(np.int32).copy()).cuda()
+    host.accept_commit(st, best, m, out, seen, skip_now=skip_now)
+    torch.cuda.synchronize()
+    gst = host.state_from_tensor(st)
+    ost = orc.new_state(**base)
+    oout = np.full(128, -7, np.int32)
+    oseen = seen0.copy()
+    acc = orc.accept_commit(ost, np.array(best_tok, np.int32), m, oout, oseen, skip_now=skip_now)
+    for f in host.STATE_FIELDS:
+        assert getattr(gst, f) == getattr(ost, f), (case, f, getattr(gst, f), getattr(ost, f))
+    assert [gst.tokens[i] for i in range(64)] == [ost.tokens[i] for i in range(64)], case
+    np.testing.assert_array_equal(out.cpu().numpy(), oout, err_msg=case)
+    np.testing.assert_array_equal(seen.cpu().numpy().view(np.uint32), oseen, err_msg=case)
+    expect_acc = {"mid_miss": 1, "miss_to_skip": 0, "eos_bonus": 2, "eos_first_draft": 3, "one_row": 0, "all_64": 63,
+                  "same_word": 3, "skip_round": 0, "count_carried": 3}[case]
+    assert acc == expect_acc, (case, acc)
+
+
+def test_commit_refuses_a_full_output_buffer(dev, orc):
+    """A commit that would write past out_cap writes nothing and stops the run: State.run = 0, every other State
+    word, the emitted tokens and the seen bitmap unchanged."""
+    torch = dev
+    host = load_host()
+    V = 4096
+    base = dict(a=1024, anchor=5, tokens=[5, 10, 11, 12], rounds_left=32, budget=4096, eos=-1, stop_at=4096, run=1,
+                count=2)
+    keys = np.array([orc.argmax_key(1.0, t) for t in (10, 11, 99, 13)], np.uint64)  # acc 2: 3 tokens to commit
+    st = host.state_tensor(**base)
+    before = host.state_from_tensor(st)
+    best = torch.from_numpy(keys.view(np.int64)).cuda()
+    out = torch.full((4,), -7, dtype=torch.int32, device="cuda")  # out_cap 4 < count 2 + 3
+    seen = torch.zeros(V // 32, dtype=torch.int32, device="cuda")
+    host.accept_commit(st, best, 4, out, seen)
+    torch.cuda.synchronize()
+    after = host.state_from_tensor(st)
+    assert after.run == 0
+    for f in host.STATE_FIELDS:
+        if f != "run":
+            assert getattr(after, f) == getattr(before, f), f
+    assert [after.tokens[i] for i in range(4)] == [5, 10, 11, 12]
+    assert out.cpu().tolist() == [-7, -7, -7, -7]
+    assert int(seen.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("M,N,K,epilogue", [
     (16, 12288, 2048, 0),   # K-sliced, 4 strips x 4 ranges, X^T in LDS
     (16, 2048, 8192, 0),    # long K: split across workgroups
