@@ -143,8 +143,8 @@ __global__ __launch_bounds__(64) void accept_commit_kernel(dspark_state* st, uin
                                                            int32_t* out_tokens, int out_cap, uint32_t* seen,
                                                            const uint64_t* part, int nchunks, int mfold,
                                                            int32_t* mirror) {
-  // Buffer loads: 0 past the end of each buffer (past the keys, and for every key load of the buffer that is not
-  // read). A stopped round writes nothing.
+  // Buffer loads return 0 past a buffer's end: past the partial keys, and for every load of best[] when the keys
+  // come folded from part (best's buffer is then given length 0). A stopped round writes nothing.
   const int lane = (int)threadIdx.x;
   asm volatile("" ::"s"(mirror));  // the kernarg line past the first: fetched with the first
   constexpr int NH = (int)(offsetof(dspark_state, tokens) / sizeof(int32_t));  // header words
